@@ -1,0 +1,198 @@
+"""GPU parity of the whole path on the tiny qwen3 pair (Q8_0, d 512, 4 / 2 layers, vocab 32000): logits against the
+oracle (zerollm's RefModel restated), batched = sequential, KV rollback, device sampling, and speculative decoding."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from zerollm_amd import model as Mdl
+from zerollm_amd.generate import generate
+from zerollm_amd.sampler import HipSampler
+from zerollm_amd.speculative import generate_speculative
+
+pytestmark = pytest.mark.gpu
+
+# logits tolerance of the parity contract (fp32 results; the path reproduces the reference's rounding points, so the
+# observed differences are far below it)
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+
+
+def prompt(n, seed=1, vocab=32000):
+    r = O.Rng(seed)
+    return [int(r() * vocab) for _ in range(n)]
+
+
+@pytest.mark.parametrize("kv", ["f32", "f16"])
+def test_logits_match_oracle(gpu, tiny_files, kv):
+    toks = prompt(40)
+    ref = O.OracleModel(tiny_files[0], ctx=128, kv=kv)
+    want = np.stack([ref.forward(t) for t in toks])
+    m = Mdl.HipModel.load(tiny_files[0], ctx=128, kv=kv)
+    got = np.stack([m.forward(t).copy() for t in toks])
+    m.close()
+    diff = np.abs(got - want)
+    assert diff.max() <= MAX_ABS and diff.mean() <= MEAN_ABS, (diff.max(), diff.mean())
+    print(f"kv={kv}: max-abs {diff.max():.3g}, mean-abs {diff.mean():.3g}, bit-exact {np.mean(got == want):.4f}")
+    assert (got.argmax(1) == want.argmax(1)).all()
+
+
+def test_forward_batch_all_equals_sequential(gpu, tiny_files):
+    toks = prompt(24, seed=2)
+    a = Mdl.HipModel.load(tiny_files[0], ctx=128, kv="f16")
+    seq = np.stack([a.forward(t).copy() for t in toks])
+    b = Mdl.HipModel.load(tiny_files[0], ctx=128, kv="f16")
+    rows = []
+    for chunk in (toks[:5], toks[5:6], toks[6:15], toks[15:24]):
+        rows.append(b.forward_batch(chunk, logits="all").copy())
+    bat = np.concatenate(rows)
+    assert (bat.view(np.uint32) == seq.view(np.uint32)).all()
+    last = b.forward_batch([toks[0], toks[1]], logits="last").copy()
+    assert b.pos == 26
+    a.forward(toks[0])
+    assert (last.view(np.uint32) == a.forward(toks[1]).view(np.uint32)).all()
+    a.close()
+    b.close()
+
+
+def test_rollback_equals_fresh_run(gpu, tiny_files):
+    """50 random accept/reject cycles leave the same state as a fresh sequential run (test/spec-logits.test.js:97-139)."""
+    rng = np.random.default_rng(4)
+    m = Mdl.HipModel.load(tiny_files[0], ctx=512, kv="f16")
+    seq = prompt(8, seed=3)
+    m.forward_batch(seq, logits=False)
+    for _ in range(50):
+        k = int(rng.integers(1, 6))
+        cand = [int(x) for x in rng.integers(0, 32000, k)]
+        m.forward_batch(cand, logits="all")
+        keep = int(rng.integers(0, k + 1))
+        seq += cand[:keep]
+        m.truncate(len(seq))
+    fresh = Mdl.HipModel.load(tiny_files[0], ctx=512, kv="f16")
+    for i in range(0, len(seq) - 1, 16):
+        fresh.forward_batch(seq[i:min(i + 16, len(seq) - 1)], logits=False)
+    a = fresh.forward(seq[-1]).copy()
+    m.truncate(len(seq) - 1)
+    b = m.forward(seq[-1]).copy()
+    assert (a.view(np.uint32) == b.view(np.uint32)).all()
+    m.close()
+    fresh.close()
+
+
+def test_errors_carry_reference_messages(gpu, tiny_files):
+    m = Mdl.HipModel.load(tiny_files[0], ctx=8, max_batch=4, logits_batch=2)
+    with pytest.raises(Exception, match="out of range"):
+        m.forward(32000)
+    with pytest.raises(Exception, match=r"batch of 5 tokens \(max 4\)"):
+        m.forward_batch([1, 2, 3, 4, 5])
+    with pytest.raises(Exception, match="logitsBatch"):
+        m.forward_batch([1, 2, 3], logits="all")
+    m.forward_batch([1, 2, 3, 4], logits=False)
+    m.forward_batch([1, 2, 3, 4], logits=False)
+    with pytest.raises(Exception, match=r"context full \(8 tokens\)"):
+        m.forward(1)
+    m.close()
+    m.close()
+    with pytest.raises(Exception, match="model is closed"):
+        m.forward(1)
+
+
+def test_device_sampler_matches_oracle(gpu, tiny_files):
+    m = Mdl.HipModel.load(tiny_files[0], ctx=64)
+    toks = prompt(6, seed=8)
+    for cfg in [dict(temperature=0.7, top_k=40, top_p=0.9), dict(temperature=1.0, top_k=5, top_p=1.0, min_p=0.05),
+                dict(temperature=0.8, top_k=40, top_p=0.95, repeat_penalty=1.3, presence_penalty=0.2, frequency_penalty=0.1),
+                dict(temperature=0)]:
+        ds = HipSampler(seed=77, **cfg)
+        hs = O.Sampler(seed=77, **cfg)
+        for t in toks:
+            logits = m.forward(t).copy()
+            hist = toks[:3]
+            dd = ds.distribution(m, 0, hist)
+            hd = hs.distribution(logits, hist)
+            assert list(dd.ids) == list(hd.ids)
+            assert np.allclose(dd.probs, hd.probs, rtol=1e-14, atol=0)
+            assert dd.greedy == hd.greedy
+            assert ds.sample(m, 0, hist) == hs.sample(logits, hist)
+        m.reset()
+    m.close()
+
+
+@pytest.mark.parametrize("k", [1, 2, 4, 7])
+def test_greedy_speculative_equals_plain_greedy(gpu, tiny_files, k):
+    """test/spec-generate.test.js:29-59: greedy speculative output is plain greedy output."""
+    p = prompt(64, seed=5)
+    t = Mdl.HipModel.load(tiny_files[0], ctx=512, kv="f16")
+    d = Mdl.HipModel.load(tiny_files[1], ctx=512, kv="f16")
+    st = {}
+    spec = list(generate_speculative(t, d, p, k=k, max_tokens=48, stats=st))
+    plain_m = Mdl.HipModel.load(tiny_files[0], ctx=512, kv="f16")
+    plain = list(generate(plain_m, p, max_tokens=48))
+    assert spec == plain
+    assert st["speculative"]["cycles"] > 0 and st["generated"] == 48
+    for x in (t, d, plain_m):
+        x.close()
+
+
+def test_oracle_draft_accepts_everything(gpu, tiny_files):
+    """A draft identical to the target is always right (test/spec-generate.test.js:29-59)."""
+    p = prompt(16, seed=6)
+    t = Mdl.HipModel.load(tiny_files[0], ctx=256)
+    d = Mdl.HipModel.load(tiny_files[0], ctx=256)
+    st = {}
+    out = list(generate_speculative(t, d, p, k=4, max_tokens=21, stats=st))
+    assert len(out) == 21
+    assert st["speculative"]["acceptRate"] == 1.0
+    t.close()
+    d.close()
+
+
+def test_greedy_stream_matches_oracle(gpu, tiny_files):
+    """Tiny config: 64-token prompt, greedy, k=4, f32 KV; the device stream equals the oracle's plain greedy stream."""
+    p = prompt(64, seed=9)
+    ref = O.OracleModel(tiny_files[0], ctx=256)
+    logits = None
+    for tok in p:
+        logits = ref.forward(tok)
+    want = []
+    for _ in range(32):
+        nxt = int(np.argmax(logits))
+        want.append(nxt)
+        logits = ref.forward(nxt)
+    t = Mdl.HipModel.load(tiny_files[0], ctx=256)
+    d = Mdl.HipModel.load(tiny_files[1], ctx=256)
+    got = list(generate_speculative(t, d, p, k=4, max_tokens=32))
+    assert got == want
+    t.close()
+    d.close()
+
+
+def test_stop_token_and_limits(gpu, tiny_files):
+    p = prompt(20, seed=10)
+    t = Mdl.HipModel.load(tiny_files[0], ctx=64)
+    d = Mdl.HipModel.load(tiny_files[1], ctx=64)
+    plain_m = Mdl.HipModel.load(tiny_files[0], ctx=64)
+    plain = list(generate(plain_m, p, max_tokens=10))
+    stop = plain[3]
+    st = {}
+    got = list(generate_speculative(t, d, p, k=4, max_tokens=10, stop_ids={stop}, stats=st))
+    assert got == plain[:plain.index(stop)]
+    assert st["stopReason"] == "stop"
+    st = {}
+    got = list(generate_speculative(t, d, p, k=4, max_tokens=200, stats=st))
+    assert len(got) == 64 - 20 + 1 and st["stopReason"] == "context"
+    for x in (t, d, plain_m):
+        x.close()
+
+
+def test_sampled_speculative_is_reproducible_and_uses_target_distribution(gpu, tiny_files):
+    p = prompt(32, seed=11)
+    runs = []
+    for _ in range(2):
+        t = Mdl.HipModel.load(tiny_files[0], ctx=256, kv="f16")
+        d = Mdl.HipModel.load(tiny_files[1], ctx=256, kv="f16")
+        s = HipSampler(temperature=0.7, top_k=40, top_p=0.9, seed=1234)
+        st = {}
+        runs.append(list(generate_speculative(t, d, p, k=4, max_tokens=40, sample=s, stats=st)))
+        t.close()
+        d.close()
+    assert runs[0] == runs[1]
+    assert len(runs[0]) == 40

@@ -1,0 +1,115 @@
+"""CPU tests of the host side: the C-ABI library loads and exports every symbol the header declares (no compute calls
+without a GPU), the GGUF reader/writer round trip, and the synthetic generator and quantisers."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from zerollm_amd import _lib, gguf as G, synth
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    src = open(os.path.join(ROOT, "include", "zerollm_hip.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(zl_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = C.CDLL(_lib.LIB_PATH)
+    names = header_functions()
+    assert len(names) >= 30
+    for n in names:
+        assert hasattr(L, n), n
+    # and the Python binding covers them all
+    bound = {s[0] for s in _lib.SIGNATURES}
+    assert set(names) <= bound, set(names) - bound
+
+
+def test_errors_without_gpu_are_reported_not_crashing():
+    """A bad path fails with a status code and a message (no GPU is touched before the file is parsed)."""
+    h = C.c_void_p()
+    o = _lib.zl_model_opts()
+    rc = _lib.lib().zl_model_load(b"/nonexistent/x.gguf", C.byref(o), C.byref(h))
+    assert rc != 0
+    assert _lib.lib().zl_last_error()
+
+
+def test_gguf_round_trip(tmp_path):
+    M = G.MetaKV
+    meta = [M("general.architecture", G.STRING, "qwen3"), M("qwen3.block_count", G.UINT32, 2),
+            M("qwen3.attention.layer_norm_rms_epsilon", G.FLOAT32, 1e-6), M("x.arr", G.ARRAY, [1, 2, 3], G.INT32),
+            M("x.strs", G.ARRAY, ["a", "bc"], G.STRING), M("x.b", G.BOOL, True), M("x.f64", G.FLOAT64, 0.125)]
+    a = np.arange(64, dtype=np.float32)
+    b = np.arange(34 * 4, dtype=np.uint8)
+    p = str(tmp_path / "t.gguf")
+    G.write_gguf(p, meta, [("a", [64], G.F32, a), ("b", [128], G.Q8_0, b)], alignment=64)
+    g = G.read_gguf(p)
+    assert g.get("general.architecture") == "qwen3" and g.get("qwen3.block_count") == 2
+    assert g.get("qwen3.attention.layer_norm_rms_epsilon") == float(np.float32(1e-6))
+    assert g.get("x.arr") == [1, 2, 3] and g.get("x.strs") == ["a", "bc"] and g.get("x.b") is True
+    assert g.alignment == 64 and g.data_start % 64 == 0
+    assert (g.floats("a") == a).all() and (np.asarray(g.data("b")) == b).all()
+    assert g.tensor("b").abs_offset % 64 == 0
+
+
+def test_gguf_rejects_bad_files(tmp_path):
+    p = tmp_path / "bad.gguf"
+    p.write_bytes(b"GGML" + b"\0" * 20)
+    with pytest.raises(ValueError, match="not a GGUF file"):
+        G.read_gguf(str(p))
+    p.write_bytes(b"GGUF" + (3).to_bytes(4, "little") + (1).to_bytes(8, "little") + (0).to_bytes(8, "little"))
+    with pytest.raises(ValueError):
+        G.read_gguf(str(p))
+
+
+def test_synth_is_deterministic_and_normal():
+    t = synth.TensorSpec("w", G.F32, 64, 1024, seed=42, std=1.0)
+    a = synth.tensor_bytes(t).view(np.float32)
+    b = synth.tensor_bytes(t).view(np.float32)
+    assert (a == b).all()
+    assert abs(a.mean()) < 0.02 and abs(a.std() - 1) < 0.02
+    # kurtosis of a normal is 3; tails present
+    k = ((a - a.mean()) ** 4).mean() / a.var() ** 2
+    assert abs(k - 3) < 0.15 and np.abs(a).max() > 3.5
+    # a column window of a wider tensor takes the same deviates
+    w = synth.TensorSpec("w", G.F32, 64, 256, seed=42, std=1.0, src_cols=1024, col0=0)
+    assert (synth.tensor_bytes(w).view(np.float32).reshape(64, 256) == a.reshape(64, 1024)[:, :256]).all()
+
+
+@pytest.mark.parametrize("type_,tol", [(G.Q8_0, 0.51 / 127), (G.Q4_K, 1.02 / 15), (G.Q5_K, 1.02 / 31), (G.Q6_K, 1.01 / 32),
+                                       (G.Q5_0, 1.01 / 16), (G.Q4_0, 1.01 / 8)])
+def test_quantisers_round_trip(type_, tol):
+    """The library's quantisers against the oracle's dequantisation of what they write: error within half a step
+    (the K-quant affine step is range/qmax with range <= 2*amax; Q4_0/Q5_0/Q6_K map +max exactly and clamp -max)."""
+    rows, cols = 16, 512
+    f = synth.TensorSpec("w", G.F32, rows, cols, seed=7, std=0.02)
+    x = synth.tensor_bytes(f).view(np.float32).reshape(rows, cols)
+    q = synth.TensorSpec("w", type_, rows, cols, seed=7, std=0.02)
+    y = O.dequant(type_, synth.tensor_bytes(q), rows, cols)
+    amax = np.abs(x).max()
+    assert np.abs(x - y).max() <= tol * amax * 1.05 + 1e-6, np.abs(x - y).max() / amax
+    if type_ == G.Q8_0:
+        # Q8_0 follows the reference's quantizeQ8_0 exactly
+        assert (synth.tensor_bytes(q) == O.quantize_q8_0(x.reshape(-1))).all()
+    if type_ == G.Q4_0:
+        assert (synth.tensor_bytes(q) == O.quantize_q4_0(x.reshape(-1))).all()
+
+
+def test_named_configs():
+    t, d = synth.tiny_pair()
+    assert t.weight_bytes == 30777344 and d.weight_bytes == 24092672
+    names_t = {x.name: x for x in t.tensors}
+    names_d = {x.name: x for x in d.tensors}
+    # the tiny draft is the target's first 2 layers and the same head: identical tensor specs
+    for n, x in names_d.items():
+        assert names_t[n] == x
+    T, D = synth.qwen3_8b_pair()
+    assert T.weight_bytes == 4923568128 and D.weight_bytes == 633233408
+    e_t = {x.name: x for x in T.tensors}["output.weight"]
+    e_d = {x.name: x for x in D.tensors}["output.weight"]
+    assert e_d.seed == e_t.seed and e_d.src_cols == 4096 and e_d.cols == 1024 and e_d.type == G.Q8_0

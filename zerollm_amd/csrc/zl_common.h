@@ -1,0 +1,82 @@
+// Shared definitions of the zerollm MI355X library: ggml type ids, the repacked weight layout, error handling and
+// small device helpers. Target: gfx950 (CDNA4), wave64.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stdexcept>
+#include <string>
+
+#include "zerollm_hip.h"  // status codes (ZL_OK, ZL_ERR_*)
+
+namespace zl {
+
+// ggml tensor type ids (zerollm src/gguf/types.js:10-15)
+enum : int { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q5_0 = 6, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_BF16 = 30 };
+
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string &m) : std::runtime_error(m), code(c) {}
+};
+
+
+#define ZL_HIP(x)                                                                                 \
+  do {                                                                                            \
+    hipError_t e_ = (x);                                                                          \
+    if (e_ != hipSuccess) throw ::zl::Error(ZL_ERR_HIP, std::string(#x) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+#define ZL_REQUIRE(cond, code, msg)               \
+  do {                                            \
+    if (!(cond)) throw ::zl::Error((code), (msg)); \
+  } while (0)
+
+// ---------------------------------------------------------------------------------------------- repacked weights
+// Every quantised matrix is stored as row-major planes of 64-value "slabs" (cols padded to a multiple of 64 with zero
+// blocks), so that one lane's unit of work is contiguous, 16-byte aligned and the same size for every format:
+//   qs  packed low bits, QB bytes per slab:
+//        Q8_0 64 (int8), Q4_0/Q5_0/Q4_K/Q5_K 32 (byte j: low nibble = value j, high nibble = value j+32),
+//        Q6_K 32 (same nibble layout, the low 4 of 6 bits)
+//   qx  extra high bits per slab: Q5_0/Q5_K 8 bytes (bit j of word w = 5th bit of value 32w+j),
+//        Q6_K 16 bytes (byte j: bits 2i..2i+1 = top 2 bits of value j + 16i)
+//   sc  4 bytes per slab: Q4_K/Q5_K scale codes of the two 32-value sub-blocks, then their min codes;
+//        Q6_K the four int8 16-value group scales
+//   dd  f16 scales: Q8_0/Q4_0/Q5_0 two per slab (one per 32-block); Q4_K/Q5_K (d, dmin) per 256-value super-block;
+//        Q6_K d per super-block
+// F32/F16/BF16 matrices keep their row-major values in qs.
+struct DevMat {
+  int type = -1, rows = 0, cols = 0, nslab = 0;
+  uint8_t *qs = nullptr, *qx = nullptr, *sc = nullptr;
+  uint16_t *dd = nullptr;
+};
+
+inline int qs_bytes(int t) { return t == T_Q8_0 ? 64 : 32; }
+inline int qx_bytes(int t) { return (t == T_Q5_0 || t == T_Q5_K) ? 8 : t == T_Q6_K ? 16 : 0; }
+inline int sc_bytes(int t) { return (t == T_Q4_K || t == T_Q5_K || t == T_Q6_K) ? 4 : 0; }
+inline bool is_quant(int t) { return t == T_Q8_0 || t == T_Q4_0 || t == T_Q5_0 || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
+inline bool is_kquant(int t) { return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
+
+// ---------------------------------------------------------------------------------------------- device helpers
+__device__ inline float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+__device__ inline uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
+
+__device__ inline int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+template <typename T>
+__device__ inline T wave_sum_xor(T v, int width) {
+  for (int o = 1; o < width; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Order-preserving key of a float (larger float -> larger key); -0 is folded onto +0 so that equal values have equal keys.
+__device__ inline uint32_t fkey(float f) {
+  uint32_t u = __float_as_uint(f);
+  if (u == 0x80000000u) u = 0;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ inline float keyf(uint32_t k) {
+  uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(u);
+}
+
+}  // namespace zl

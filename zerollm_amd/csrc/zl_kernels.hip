@@ -1,0 +1,836 @@
+// Forward-pass kernels for gfx950: weight repack, dequantisation, RMSNorm + int8 activation quantisation, the k-quant
+// GEMV family (M = 1..64 tokens), per-head q/k RMSNorm + RoPE + KV append, and causal GQA attention.
+//
+// Numerics follow zerollm's reference path (src/model/forward.js:184-248, src/compute/ref-kernels.js): integer block
+// dots are exact; every scale combination, norm, softmax and RoPE step is done in f64 with the reference's rounding
+// points (f32 stores); the attention weighted sum accumulates in f32 in position order, one fused multiply-add per
+// position, as the reference's `attOut[i] += p * V[i]` does. The only freedom taken is the order of f64 sums (block
+// partials across lanes, softmax denominators), which moves results by ~1e-16 relative before the f32 rounding.
+// The whole library is built with -ffp-contract=off; fusions are written out explicitly.
+#include "zl_kernels.h"
+
+namespace zl {
+
+// ================================================================================================ repack
+// Raw ggml blocks of one matrix (rows x rawRowBytes) -> slab planes (see DevMat in zl_common.h).
+
+__device__ inline void q6_value(const uint8_t *blk, int e, int &lo4, int &hi2) {
+  int h = e >> 7, e2 = e & 127, qq = e2 >> 5, l = e2 & 31;
+  int byte = blk[64 * h + ((qq & 1) ? 32 : 0) + l];
+  lo4 = (qq < 2) ? (byte & 15) : (byte >> 4);
+  hi2 = (blk[128 + 32 * h + l] >> (2 * qq)) & 3;
+}
+
+__global__ void k_repack(int type, const uint8_t *__restrict__ raw, long rawRowBytes, int rows, int cols, int nslab,
+                         uint8_t *qs, uint8_t *qx, uint8_t *sc, uint16_t *dd) {
+  long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)rows * nslab) return;
+  int r = (int)(idx / nslab), s = (int)(idx % nslab);
+  const uint8_t *row = raw + (long)r * rawRowBytes;
+  if (type == T_Q8_0 || type == T_Q4_0 || type == T_Q5_0) {
+    int nb = cols / 32;
+    int bsz = type == T_Q8_0 ? 34 : type == T_Q4_0 ? 18 : 22;
+    uint8_t *oq = qs + idx * (type == T_Q8_0 ? 64 : 32);
+    for (int half = 0; half < 2; half++) {
+      int b = 2 * s + half;
+      const uint8_t *blk = b < nb ? row + (long)b * bsz : nullptr;
+      dd[idx * 2 + half] = blk ? (uint16_t)(blk[0] | (blk[1] << 8)) : 0;
+      if (type == T_Q8_0) {
+        for (int i = 0; i < 32; i++) oq[32 * half + i] = blk ? blk[2 + i] : 0;
+      } else {
+        const uint8_t *nib = blk ? blk + (type == T_Q4_0 ? 2 : 6) : nullptr;
+        // block value j: j < 16 low nibble of byte j, else high nibble of byte j-16; slab byte j holds value j (low
+        // nibble, from block 2s) and value j+32 (high nibble, from block 2s+1)
+        for (int j = 0; j < 32; j++) {
+          int v = nib ? (j < 16 ? (nib[j] & 15) : (nib[j - 16] >> 4)) : 0;
+          if (half == 0) oq[j] = (uint8_t)((oq[j] & 0xF0) | v);
+          else oq[j] = (uint8_t)((oq[j] & 0x0F) | (v << 4));
+        }
+        if (type == T_Q5_0) {
+          uint32_t h = blk ? ((uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) | ((uint32_t)blk[5] << 24)) : 0u;
+          uint8_t *ox = qx + idx * 8 + 4 * half;
+          ox[0] = h & 0xff; ox[1] = (h >> 8) & 0xff; ox[2] = (h >> 16) & 0xff; ox[3] = (h >> 24) & 0xff;
+        }
+      }
+    }
+    return;
+  }
+  if (type == T_Q4_K || type == T_Q5_K) {
+    int five = type == T_Q5_K;
+    int sb = s >> 2, c = s & 3;
+    const uint8_t *blk = row + (long)sb * (five ? 176 : 144);
+    const uint8_t *src = blk + (five ? 48 : 16) + 32 * c;
+    uint8_t *oq = qs + idx * 32;
+    for (int l = 0; l < 32; l++) oq[l] = src[l];
+    const uint8_t *S = blk + 4;
+    int scv[8], mnv[8];
+    for (int j = 0; j < 4; j++) {
+      scv[j] = S[j] & 63; mnv[j] = S[j + 4] & 63;
+      scv[j + 4] = (S[j + 8] & 0x0f) | ((S[j] >> 6) << 4);
+      mnv[j + 4] = (S[j + 8] >> 4) | ((S[j + 4] >> 6) << 4);
+    }
+    uint8_t *os = sc + idx * 4;
+    os[0] = (uint8_t)scv[2 * c]; os[1] = (uint8_t)scv[2 * c + 1]; os[2] = (uint8_t)mnv[2 * c]; os[3] = (uint8_t)mnv[2 * c + 1];
+    if (c == 0) {
+      long di = ((long)r * (nslab >> 2) + sb) * 2;
+      dd[di] = (uint16_t)(blk[0] | (blk[1] << 8));
+      dd[di + 1] = (uint16_t)(blk[2] | (blk[3] << 8));
+    }
+    if (five) {
+      uint32_t w0 = 0, w1 = 0;
+      for (int l = 0; l < 32; l++) {
+        w0 |= (uint32_t)((blk[16 + l] >> (2 * c)) & 1) << l;
+        w1 |= (uint32_t)((blk[16 + l] >> (2 * c + 1)) & 1) << l;
+      }
+      uint8_t *ox = qx + idx * 8;
+      for (int i = 0; i < 4; i++) { ox[i] = (w0 >> (8 * i)) & 0xff; ox[4 + i] = (w1 >> (8 * i)) & 0xff; }
+    }
+    return;
+  }
+  if (type == T_Q6_K) {
+    int sb = s >> 2, u = s & 3;
+    const uint8_t *blk = row + (long)sb * 210;
+    uint8_t *oq = qs + idx * 32, *ox = qx + idx * 16;
+    for (int j = 0; j < 32; j++) {
+      int lo0, hi0, lo1, hi1;
+      q6_value(blk, 64 * u + j, lo0, hi0);
+      q6_value(blk, 64 * u + 32 + j, lo1, hi1);
+      oq[j] = (uint8_t)(lo0 | (lo1 << 4));
+    }
+    for (int j = 0; j < 16; j++) {
+      int b = 0;
+      for (int i = 0; i < 4; i++) { int lo, hi; q6_value(blk, 64 * u + j + 16 * i, lo, hi); b |= hi << (2 * i); }
+      ox[j] = (uint8_t)b;
+    }
+    uint8_t *os = sc + idx * 4;
+    for (int g = 0; g < 4; g++) os[g] = blk[192 + 4 * u + g];
+    if (u == 0) dd[(long)r * (nslab >> 2) + sb] = (uint16_t)(blk[208] | (blk[209] << 8));
+    return;
+  }
+}
+
+// ================================================================================================ dequantisation
+// One slab (64 values) of one row, with the reference's dequantisation arithmetic (src/compute/quant.js:33-202).
+__device__ void dequant_slab(const MatView m, int r, int s, float *out) {
+  long idx = (long)r * m.nslab + s;
+  const int t = m.type;
+  if (t == T_F32 || t == T_F16 || t == T_BF16) {
+    for (int i = 0; i < 64; i++) {
+      int c = 64 * s + i;
+      if (c >= m.cols) { out[i] = 0; continue; }
+      long e = (long)r * m.cols + c;
+      if (t == T_F32) out[i] = ((const float *)m.qs)[e];
+      else if (t == T_F16) out[i] = h2f(((const uint16_t *)m.qs)[e]);
+      else out[i] = __uint_as_float((uint32_t)((const uint16_t *)m.qs)[e] << 16);
+    }
+    return;
+  }
+  if (t == T_Q8_0) {
+    const int8_t *q = (const int8_t *)(m.qs + idx * 64);
+    for (int h = 0; h < 2; h++) {
+      double d = (double)h2f(m.dd[idx * 2 + h]);
+      for (int i = 0; i < 32; i++) out[32 * h + i] = (float)(d * (double)q[32 * h + i]);
+    }
+    return;
+  }
+  const uint8_t *q = m.qs + idx * 32;
+  if (t == T_Q4_0 || t == T_Q5_0) {
+    const uint8_t *x = m.qx + idx * 8;
+    for (int h = 0; h < 2; h++) {
+      double d = (double)h2f(m.dd[idx * 2 + h]);
+      uint32_t hb = t == T_Q5_0 ? ((uint32_t)x[4 * h] | ((uint32_t)x[4 * h + 1] << 8) | ((uint32_t)x[4 * h + 2] << 16) | ((uint32_t)x[4 * h + 3] << 24)) : 0;
+      for (int j = 0; j < 32; j++) {
+        int v = h == 0 ? (q[j] & 15) : (q[j] >> 4);
+        int val = t == T_Q4_0 ? v - 8 : (v | (((hb >> j) & 1) << 4)) - 16;
+        out[32 * h + j] = (float)(d * (double)val);
+      }
+    }
+    return;
+  }
+  if (t == T_Q4_K || t == T_Q5_K) {
+    long di = ((long)r * (m.nslab >> 2) + (s >> 2)) * 2;
+    double d = (double)h2f(m.dd[di]), dmin = (double)h2f(m.dd[di + 1]);
+    const uint8_t *S = m.sc + idx * 4;
+    const uint8_t *x = m.qx + idx * 8;
+    for (int h = 0; h < 2; h++) {
+      int sc = S[h], mn = S[2 + h];
+      uint32_t hb = t == T_Q5_K ? ((uint32_t)x[4 * h] | ((uint32_t)x[4 * h + 1] << 8) | ((uint32_t)x[4 * h + 2] << 16) | ((uint32_t)x[4 * h + 3] << 24)) : 0;
+      for (int j = 0; j < 32; j++) {
+        int v = h == 0 ? (q[j] & 15) : (q[j] >> 4);
+        if (t == T_Q5_K) v |= ((hb >> j) & 1) << 4;
+        out[32 * h + j] = (float)(d * (double)sc * (double)v - dmin * (double)mn);
+      }
+    }
+    return;
+  }
+  if (t == T_Q6_K) {
+    double d = (double)h2f(m.dd[(long)r * (m.nslab >> 2) + (s >> 2)]);
+    const int8_t *S = (const int8_t *)(m.sc + idx * 4);
+    const uint8_t *x = m.qx + idx * 16;
+    for (int v = 0; v < 64; v++) {
+      int lo = v < 32 ? (q[v] & 15) : (q[v - 32] >> 4);
+      int j = v & 15, i = v >> 4;
+      int hi = (x[j] >> (2 * i)) & 3;
+      int val = (lo | (hi << 4)) - 32;
+      out[v] = (float)(d * (double)S[v >> 4] * (double)val);
+    }
+    return;
+  }
+}
+
+__global__ void k_dequant_rows(const MatView m, const int *rowIds, int nrows, float *out, int ldo) {
+  int rr = blockIdx.x;
+  if (rr >= nrows) return;
+  int r = rowIds[rr];
+  float buf[64];
+  for (int s = threadIdx.x; s < m.nslab; s += blockDim.x) {
+    dequant_slab(m, r, s, buf);
+    int n = min(64, m.cols - 64 * s);
+    for (int i = 0; i < n; i++) out[(long)rr * ldo + 64 * s + i] = buf[i];
+  }
+}
+
+// Embedding lookup: x[b] = dequant(token_embd row step.tokens[b]) (src/model/forward.js:195).
+__global__ void k_embed(const MatView m, const Step *step, float *x, int ldx) {
+  int b = blockIdx.x;
+  if (b >= step->B) return;
+  int tok = step->tokens[b];
+  float buf[64];
+  for (int s = threadIdx.x; s < m.nslab; s += blockDim.x) {
+    dequant_slab(m, tok, s, buf);
+    int n = min(64, m.cols - 64 * s);
+    for (int i = 0; i < n; i++) x[(long)b * ldx + 64 * s + i] = buf[i];
+  }
+}
+
+// ================================================================================================ activation quantisation
+// 32 consecutive lanes own one 32-value block: d = amax/127 (f64, stored f32), q = round-half-away(x * (1/d)), sums of
+// the block and of each 16-value half (src/compute/ref-kernels.js:44-62).
+__device__ inline void quant_block32(float v, int i, int8_t *xq, float *xd, int32_t *xs, int32_t *xs16) {
+  float a = fabsf(v);
+  for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+  double scale = (double)a / 127.0;
+  double inv = scale != 0.0 ? 1.0 / scale : 0.0;
+  int q = (int)round((double)v * inv);
+  xq[i] = (int8_t)q;
+  int s16 = q;
+  for (int o = 1; o < 16; o <<= 1) s16 += __shfl_xor(s16, o, 64);
+  int s32 = s16 + __shfl_xor(s16, 16, 64);
+  if ((i & 15) == 0) xs16[i >> 4] = s16;
+  if ((i & 31) == 0) { xd[i >> 5] = (float)scale; xs[i >> 5] = s32; }
+}
+
+// RMSNorm (optional) + quantisation of rows x[row0 + blockIdx.x] (length n) into activation row blockIdx.x
+// (length npad >= n, zero padded). rmsnorm: s = 1/sqrt(mean(x^2) + eps), xb = x*s*w (src/compute/ref-kernels.js:305-310).
+__global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x, int ldx, int row0, const float *__restrict__ w,
+                                                    double eps, int n, int npad, Act act) {
+  __shared__ double red[4];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const float *xr = x + (long)(row0 + b) * ldx;
+  double s = 1.0;
+  if (w) {
+    double ss = 0;
+    for (int i = tid; i < n; i += 256) { double v = (double)xr[i]; ss += v * v; }
+    ss = wave_sum_xor(ss, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    ss = (red[0] + red[1]) + (red[2] + red[3]);
+    s = 1.0 / sqrt(ss / (double)n + eps);
+  }
+  int8_t *xq = act.q + (long)b * act.ld;
+  float *xd = act.d + (long)b * (act.ld >> 5);
+  int32_t *xs = act.s + (long)b * (act.ld >> 5);
+  int32_t *xs16 = act.s16 + (long)b * (act.ld >> 4);
+  for (int i = tid; i < npad; i += 256) {
+    float v = 0.f;
+    if (i < n) v = w ? (float)((double)xr[i] * s * (double)w[i]) : xr[i];
+    if (act.f) act.f[(long)b * act.ld + i] = v;
+    quant_block32(v, i, xq, xd, xs, xs16);
+  }
+}
+
+// ================================================================================================ GEMV
+// y[t][r] = sum over the row's blocks of the reference's per-block term (src/compute/ref-kernels.js:132-277), for
+// M tokens at once. Mapping: `lpr` lanes share a row and take its 64-value slabs round robin (lane j: slabs j, j+lpr,
+// ...), each lane adds its blocks' f64 terms in slab order, then a butterfly over the lpr lanes. The per-(row, token)
+// arithmetic does not depend on M, so a batched pass gives the same bits as token-by-token passes. Int8 activations
+// of MT tokens are staged in LDS one K-window at a time (window = multiple of 64*lpr, so the slab order is kept).
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// weights are read once per pass: non-temporal loads keep them from displacing activations in the caches
+__device__ inline u32x4 ldnt4(const void *p) { return __builtin_nontemporal_load((const u32x4 *)p); }
+__device__ inline u32x2 ldnt2(const void *p) { return __builtin_nontemporal_load((const u32x2 *)p); }
+
+template <int FMT>
+struct Slab {
+  uint32_t w[16];  // 64 unsigned/signed 8-bit values, slab order
+  uint32_t scw;    // scale codes (K-quants)
+  float d0, d1;    // Q8_0/Q4_0/Q5_0: block scales; Q4_K/Q5_K: d, dmin; Q6_K: d
+};
+
+template <int FMT>
+__device__ inline void load_slab(const MatView &m, long idx, int r, int s, Slab<FMT> &o) {
+  if (FMT == T_Q8_0) {
+    const uint8_t *p = m.qs + idx * 64;
+    #pragma unroll
+    for (int i = 0; i < 4; i++) { u32x4 v = ldnt4(p + 16 * i); o.w[4 * i] = v.x; o.w[4 * i + 1] = v.y; o.w[4 * i + 2] = v.z; o.w[4 * i + 3] = v.w; }
+    uint32_t dw = __builtin_nontemporal_load((const uint32_t *)(m.dd + idx * 2));
+    o.d0 = h2f(dw & 0xffff); o.d1 = h2f(dw >> 16);
+    return;
+  }
+  const uint8_t *p = m.qs + idx * 32;
+  u32x4 a = ldnt4(p), b = ldnt4(p + 16);
+  uint32_t L[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  if (FMT == T_Q4_0 || FMT == T_Q4_K || FMT == T_Q5_0 || FMT == T_Q5_K) {
+    #pragma unroll
+    for (int i = 0; i < 8; i++) { o.w[i] = L[i] & 0x0F0F0F0Fu; o.w[8 + i] = (L[i] >> 4) & 0x0F0F0F0Fu; }
+    if (FMT == T_Q5_0 || FMT == T_Q5_K) {
+      u32x2 h = ldnt2(m.qx + idx * 8);
+      #pragma unroll
+      for (int i = 0; i < 8; i++) {
+        o.w[i] |= (((h.x >> (4 * i)) & 15u) * 0x00204081u & 0x01010101u) << 4;
+        o.w[8 + i] |= (((h.y >> (4 * i)) & 15u) * 0x00204081u & 0x01010101u) << 4;
+      }
+    }
+    if (FMT == T_Q4_0 || FMT == T_Q5_0) {
+      uint32_t dw = __builtin_nontemporal_load((const uint32_t *)(m.dd + idx * 2));
+      o.d0 = h2f(dw & 0xffff); o.d1 = h2f(dw >> 16);
+    } else {
+      o.scw = __builtin_nontemporal_load((const uint32_t *)(m.sc + idx * 4));
+      uint32_t dw = __builtin_nontemporal_load((const uint32_t *)(m.dd + ((long)r * (m.nslab >> 2) + (s >> 2)) * 2));
+      o.d0 = h2f(dw & 0xffff); o.d1 = h2f(dw >> 16);
+    }
+    return;
+  }
+  if (FMT == T_Q6_K) {
+    u32x4 h = ldnt4(m.qx + idx * 16);
+    uint32_t Hq[4] = {h.x, h.y, h.z, h.w};
+    #pragma unroll
+    for (int i = 0; i < 4; i++) {
+      o.w[i] = (L[i] & 0x0F0F0F0Fu) | ((Hq[i] & 0x03030303u) << 4);
+      o.w[4 + i] = (L[4 + i] & 0x0F0F0F0Fu) | ((Hq[i] & 0x0C0C0C0Cu) << 2);
+      o.w[8 + i] = ((L[i] >> 4) & 0x0F0F0F0Fu) | (Hq[i] & 0x30303030u);
+      o.w[12 + i] = ((L[4 + i] >> 4) & 0x0F0F0F0Fu) | ((Hq[i] & 0xC0C0C0C0u) >> 2);
+    }
+    o.scw = __builtin_nontemporal_load((const uint32_t *)(m.sc + idx * 4));
+    o.d0 = h2f(__builtin_nontemporal_load(m.dd + (long)r * (m.nslab >> 2) + (s >> 2)));
+    return;
+  }
+}
+
+// acc += this slab's terms for one token, in the reference's order and rounding.
+template <int FMT>
+__device__ inline double slab_terms(const Slab<FMT> &o, const uint32_t *X, const float *xd, const int32_t *xs,
+                                    const int32_t *xs16, double acc) {
+  if (FMT == T_Q6_K) {
+    int g[4];
+    #pragma unroll
+    for (int k = 0; k < 4; k++) {
+      int a = 0;
+      #pragma unroll
+      for (int i = 0; i < 4; i++) a = sdot4((int)o.w[4 * k + i], (int)X[4 * k + i], a);
+      g[k] = a - 32 * xs16[k];
+    }
+    double d = (double)o.d0;
+    #pragma unroll
+    for (int k = 0; k < 4; k++) {
+      double sc = (double)(int8_t)((o.scw >> (8 * k)) & 0xff);
+      acc = acc + (double)xd[k >> 1] * d * sc * (double)g[k];  // (((xd*d)*scale)*gsum)
+    }
+    return acc;
+  }
+  int lo = 0, hi = 0;
+  #pragma unroll
+  for (int i = 0; i < 8; i++) lo = sdot4((int)o.w[i], (int)X[i], lo);
+  #pragma unroll
+  for (int i = 8; i < 16; i++) hi = sdot4((int)o.w[i], (int)X[i], hi);
+  if (FMT == T_Q8_0) {
+    acc = acc + (double)lo * (double)o.d0 * (double)xd[0];
+    acc = acc + (double)hi * (double)o.d1 * (double)xd[1];
+    return acc;
+  }
+  if (FMT == T_Q4_0 || FMT == T_Q5_0) {
+    const int off = FMT == T_Q4_0 ? 8 : 16;
+    acc = acc + (double)(lo - off * xs[0]) * (double)o.d0 * (double)xd[0];
+    acc = acc + (double)(hi - off * xs[1]) * (double)o.d1 * (double)xd[1];
+    return acc;
+  }
+  // Q4_K / Q5_K: xd * (d*sc*sum(q*xq) - dmin*mn*sum(xq))
+  double d = (double)o.d0, dm = (double)o.d1;
+  double sc0 = (double)(o.scw & 0xff), sc1 = (double)((o.scw >> 8) & 0xff);
+  double mn0 = (double)((o.scw >> 16) & 0xff), mn1 = (double)(o.scw >> 24);
+  acc = acc + (double)xd[0] * (d * sc0 * (double)lo - dm * mn0 * (double)xs[0]);
+  acc = acc + (double)xd[1] * (d * sc1 * (double)hi - dm * mn1 * (double)xs[1]);
+  return acc;
+}
+
+template <int FMT, int MT, int EPI>
+__global__ __launch_bounds__(256) void k_gemv(const GemvArgs a) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lpr = a.lpr, slots = 64 / lpr, slot = lane / lpr, j = lane % lpr;
+  const int unit = (blockIdx.x * 4 + wave) * slots + slot;
+  // two rows per lane: a gate/up pair for SWIGLU, else two consecutive rows of the concatenated segments
+  int grow[2];
+  if (EPI == EPI_SWIGLU) { grow[0] = unit; grow[1] = a.rows_total + unit; }
+  else { grow[0] = 2 * unit; grow[1] = 2 * unit + 1; }
+  const int lim = EPI == EPI_SWIGLU ? a.rows_total : a.rows_total;
+  const bool valid0 = (EPI == EPI_SWIGLU ? unit : grow[0]) < lim;
+  const bool valid1 = EPI == EPI_SWIGLU ? valid0 : grow[1] < lim;
+  int segi[2], lrow[2];
+  MatView mv[2];
+  #pragma unroll
+  for (int r = 0; r < 2; r++) {
+    int g = grow[r];
+    int si = 0, base = 0;
+    if (EPI != EPI_SWIGLU) {
+      if (g >= lim) g = lim - 1;
+      while (si + 1 < a.nseg && g >= base + a.seg[si].rows) { base += a.seg[si].rows; si++; }
+    } else {
+      si = r; base = r ? a.rows_total : 0;
+      if (unit >= lim) g = base + lim - 1;
+    }
+    segi[r] = si; lrow[r] = g - base;
+    mv[r] = a.seg[si].m;
+  }
+  const int nslab = a.nslab, K = nslab * 64;
+  for (int t0 = 0; t0 < a.M; t0 += MT) {
+    const int mt = min(MT, a.M - t0);
+    double acc[2][MT];
+    #pragma unroll
+    for (int r = 0; r < 2; r++)
+      #pragma unroll
+      for (int t = 0; t < MT; t++) acc[r][t] = 0.0;
+    for (int k0 = 0; k0 < K; k0 += a.wk) {
+      const int kw = min(a.wk, K - k0);
+      __syncthreads();
+      // stage int8 activations [mt][kw] (16-byte pieces)
+      const int pieces = kw >> 4;
+      for (int p = threadIdx.x; p < mt * pieces; p += 256) {
+        int t = p / pieces, c = p % pieces;
+        *(uint4 *)(lds + (long)t * kw + 16 * c) = *(const uint4 *)(a.act.q + (long)(t0 + t) * a.act.ld + k0 + 16 * c);
+      }
+      __syncthreads();
+      for (int s = (k0 >> 6) + j; s < ((k0 + kw) >> 6); s += lpr) {
+        Slab<FMT> sl[2];
+        #pragma unroll
+        for (int r = 0; r < 2; r++) load_slab<FMT>(mv[r], (long)lrow[r] * nslab + s, lrow[r], s, sl[r]);
+        const int ls = (s << 6) - k0;
+        #pragma unroll
+        for (int t = 0; t < MT; t++) {
+          if (t < mt) {
+            uint32_t X[16];
+            const uint4 *xp = (const uint4 *)(lds + (long)t * kw + ls);
+            #pragma unroll
+            for (int i = 0; i < 4; i++) { uint4 v = xp[i]; X[4 * i] = v.x; X[4 * i + 1] = v.y; X[4 * i + 2] = v.z; X[4 * i + 3] = v.w; }
+            const long tb = (long)(t0 + t);
+            const float *xd = a.act.d + tb * (a.act.ld >> 5) + 2 * s;
+            const int32_t *xs = a.act.s + tb * (a.act.ld >> 5) + 2 * s;
+            const int32_t *xs16 = a.act.s16 + tb * (a.act.ld >> 4) + 4 * s;
+            #pragma unroll
+            for (int r = 0; r < 2; r++) acc[r][t] = slab_terms<FMT>(sl[r], X, xd, xs, xs16, acc[r][t]);
+          }
+        }
+      }
+    }
+    // butterfly over the lpr lanes of this row slot
+    #pragma unroll
+    for (int r = 0; r < 2; r++)
+      #pragma unroll
+      for (int t = 0; t < MT; t++)
+        for (int o = 1; o < lpr; o <<= 1) acc[r][t] += __shfl_xor(acc[r][t], o, 64);
+    if (j == 0) {
+      #pragma unroll
+      for (int t = 0; t < MT; t++) {
+        if (t >= mt) continue;
+        const long tb = t0 + t;
+        if (EPI == EPI_SWIGLU) {
+          if (!valid0) continue;
+          double g = (double)(float)acc[0][t], u = (double)(float)acc[1][t];
+          double silu = g / (1.0 + exp(-g));  // src/compute/ref-kernels.js:322
+          a.hb[tb * a.ldh + unit] = (float)(silu * u);
+        } else {
+          #pragma unroll
+          for (int r = 0; r < 2; r++) {
+            if (r == 0 ? !valid0 : !valid1) continue;
+            const GemvSeg &sg = a.seg[segi[r]];
+            float y = (float)acc[r][t];
+            if (EPI == EPI_RESID) {
+              float *xp = a.resid + tb * a.ldr + lrow[r];
+              *xp = (float)((double)*xp + (double)y);
+            } else {
+              if (sg.bias) y = (float)((double)y + (double)sg.bias[lrow[r]]);
+              sg.out[tb * sg.ldo + lrow[r]] = y;
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// Float weights (F32/F16/BF16) use the f32 activation (src/compute/ref-kernels.js:278-299): one wave per row,
+// sequential f64 sum per lane over a strided subset, then a butterfly.
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemv_float(const GemvArgs a, const float *__restrict__ xf, int ldx) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row = blockIdx.x * 4 + wave;
+  const bool swig = EPI == EPI_SWIGLU;
+  if (row >= a.rows_total) return;
+  for (int t = 0; t < a.M; t++) {
+    double accs[2] = {0.0, 0.0};
+    for (int r = 0; r < (swig ? 2 : 1); r++) {
+      int g = swig ? row : row, si = swig ? r : 0, base = 0;
+      if (!swig) while (si + 1 < a.nseg && g >= base + a.seg[si].rows) { base += a.seg[si].rows; si++; }
+      const MatView &m = a.seg[si].m;
+      int lr = g - base;
+      double acc = 0;
+      for (int c = lane; c < m.cols; c += 64) {
+        long e = (long)lr * m.cols + c;
+        float wv = m.type == T_F32 ? ((const float *)m.qs)[e] : m.type == T_F16 ? h2f(((const uint16_t *)m.qs)[e])
+                                                                                : __uint_as_float((uint32_t)((const uint16_t *)m.qs)[e] << 16);
+        acc = acc + (double)wv * (double)xf[(long)t * ldx + c];
+      }
+      acc = wave_sum_xor(acc, 64);
+      accs[r] = acc;
+      if (!swig && lane == 0) {
+        const GemvSeg &sg = a.seg[si];
+        float y = (float)acc;
+        if (EPI == EPI_RESID) { float *xp = a.resid + (long)t * a.ldr + lr; *xp = (float)((double)*xp + (double)y); }
+        else { if (sg.bias) y = (float)((double)y + (double)sg.bias[lr]); sg.out[(long)t * sg.ldo + lr] = y; }
+      }
+    }
+    if (swig && lane == 0) {
+      double g = (double)(float)accs[0], u = (double)(float)accs[1];
+      a.hb[(long)t * a.ldh + row] = (float)(g / (1.0 + exp(-g)) * u);
+    }
+  }
+}
+
+// ================================================================================================ q/k norm, RoPE, KV append
+// One wave per (token, head). Heads [0, nHead) are query heads (normed, rotated, written back), heads
+// [nHead, nHead + nHeadKv) are KV heads (k normed and rotated, k and v appended to the cache at step.pos0 + b).
+// Order as src/model/forward.js:203-211: bias (added by the GEMV), per-head RMSNorm, RoPE, store.
+__global__ __launch_bounds__(64) void k_qk_rope_kv(const RopeArgs a) {
+  __shared__ float v[512];
+  const int b = blockIdx.x, hh = blockIdx.y, lane = threadIdx.x;
+  const Step *st = a.step;
+  if (b >= st->B) return;
+  const int pos = st->pos0 + b;
+  const bool isq = hh < a.nHead;
+  const int head = isq ? hh : hh - a.nHead;
+  const int hd = a.hd;
+  float *src = isq ? a.q + (long)b * a.ldq + (long)head * hd : a.k + (long)b * a.ldkv + (long)head * hd;
+  const float *nw = isq ? a.qNorm : a.kNorm;
+  for (int i = lane; i < hd; i += 64) v[i] = src[i];
+  __syncthreads();
+  if (nw) {
+    double ss = 0;
+    for (int i = lane; i < hd; i += 64) { double x = (double)v[i]; ss += x * x; }
+    ss = wave_sum_xor(ss, 64);
+    double s = 1.0 / sqrt(ss / (double)hd + a.eps);
+    for (int i = lane; i < hd; i += 64) v[i] = (float)((double)v[i] * s * (double)nw[i]);
+    __syncthreads();
+  }
+  const int half = a.nRot / 2;
+  for (int i = lane; i < half; i += 64) {
+    int i0 = a.neox ? i : 2 * i, i1 = a.neox ? i + half : 2 * i + 1;
+    double c = (double)a.cosT[(long)pos * half + i], sn = (double)a.sinT[(long)pos * half + i];
+    double x0 = (double)v[i0], x1 = (double)v[i1];
+    v[i0] = (float)(x0 * c - x1 * sn);  // pairs are disjoint across lanes
+    v[i1] = (float)(x0 * sn + x1 * c);
+  }
+  __syncthreads();
+  if (isq) {
+    for (int i = lane; i < hd; i += 64) src[i] = v[i];
+    return;
+  }
+  const long off = (((long)a.layer * a.nHeadKv + head) * a.ctx + pos) * hd;
+  const float *vs = a.v + (long)b * a.ldkv + (long)head * hd;
+  if (a.kvF16) {
+    uint16_t *kc = (uint16_t *)a.kcache + off, *vc = (uint16_t *)a.vcache + off;
+    for (int i = lane; i < hd; i += 64) { kc[i] = f2h(v[i]); vc[i] = f2h(vs[i]); }
+  } else {
+    float *kc = (float *)a.kcache + off, *vc = (float *)a.vcache + off;
+    for (int i = lane; i < hd; i += 64) { kc[i] = v[i]; vc[i] = vs[i]; }
+  }
+}
+
+// ================================================================================================ attention
+// Causal GQA attention for token b (position step.pos0 + b) and HPB query heads sharing one KV head, with the
+// reference's arithmetic (src/model/forward.js:213-230): scores s = sum_i q_i K_i (f64, in i order), stored f32 after
+// *1/sqrt(hd); softmax with f64 exp and sum, probabilities stored f32; out_i accumulated in f32 over positions in
+// order. The head output is quantised for the output projection in the same kernel, and also stored in f32.
+template <int HPB, int HD, bool F16KV>
+__global__ __launch_bounds__(HPB * HD) void k_attention(const AttnArgs a) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int NT = HPB * HD, NW = NT / 64;
+  const int b = blockIdx.x, hg = blockIdx.y, tid = threadIdx.x;
+  const Step *st = a.step;
+  if (b >= st->B) return;
+  const int npos = st->pos0 + b + 1;
+  const int h0 = hg * HPB;
+  const int kvh = h0 / (a.nHead / a.nHeadKv);
+  float *qs = (float *)lds;              // [HPB][HD]
+  float *p = qs + HPB * HD;              // [HPB][pstride]
+  const int ps = a.pstride;
+  __shared__ double red[HPB * NW];
+  __shared__ float redf[HPB * NW];
+  for (int i = tid; i < HPB * HD; i += NT) qs[i] = a.q[(long)b * a.ldq + (long)h0 * HD + i];
+  __syncthreads();
+  const long kvoff = ((long)a.layer * a.nHeadKv + kvh) * a.ctx * HD;
+  const double scale = a.scale;
+  // scores: one position per thread, dot products in f64 in element order (exact products, one rounding per step)
+  float lmax[HPB];
+  #pragma unroll
+  for (int h = 0; h < HPB; h++) lmax[h] = -INFINITY;
+  for (int t = tid; t < npos; t += NT) {
+    double s[HPB];
+    #pragma unroll
+    for (int h = 0; h < HPB; h++) s[h] = 0.0;
+    if (F16KV) {
+      const uint16_t *kr = (const uint16_t *)a.kcache + kvoff + (long)t * HD;
+      for (int i = 0; i < HD; i += 8) {
+        uint4 u = *(const uint4 *)(kr + i);
+        uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+        #pragma unroll
+        for (int c = 0; c < 8; c++) {
+          double kv = (double)h2f((uint16_t)((w4[c >> 1] >> (16 * (c & 1))) & 0xffff));
+          #pragma unroll
+          for (int h = 0; h < HPB; h++) s[h] = fma((double)qs[h * HD + i + c], kv, s[h]);
+        }
+      }
+    } else {
+      const float *kr = (const float *)a.kcache + kvoff + (long)t * HD;
+      for (int i = 0; i < HD; i += 4) {
+        float4 u = *(const float4 *)(kr + i);
+        float w4[4] = {u.x, u.y, u.z, u.w};
+        #pragma unroll
+        for (int c = 0; c < 4; c++)
+          #pragma unroll
+          for (int h = 0; h < HPB; h++) s[h] = fma((double)qs[h * HD + i + c], (double)w4[c], s[h]);
+      }
+    }
+    #pragma unroll
+    for (int h = 0; h < HPB; h++) {
+      float v = (float)(s[h] * scale);
+      p[h * ps + t] = v;
+      lmax[h] = fmaxf(lmax[h], v);
+    }
+  }
+  #pragma unroll
+  for (int h = 0; h < HPB; h++) {
+    float m = lmax[h];
+    for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if ((tid & 63) == 0) redf[h * NW + (tid >> 6)] = m;
+  }
+  __syncthreads();
+  double mx[HPB], sum[HPB];
+  #pragma unroll
+  for (int h = 0; h < HPB; h++) {
+    float m = redf[h * NW];
+    for (int w = 1; w < NW; w++) m = fmaxf(m, redf[h * NW + w]);
+    mx[h] = (double)m;
+    sum[h] = 0.0;
+  }
+  // softmax (src/compute/ref-kernels.js:313-320): e = exp(s - max) stored f32, sum of the unrounded e, then p = e * (1/sum)
+  for (int t = tid; t < npos; t += NT) {
+    #pragma unroll
+    for (int h = 0; h < HPB; h++) {
+      double e = exp((double)p[h * ps + t] - mx[h]);
+      p[h * ps + t] = (float)e;
+      sum[h] += e;
+    }
+  }
+  #pragma unroll
+  for (int h = 0; h < HPB; h++) {
+    double sm = wave_sum_xor(sum[h], 64);
+    if ((tid & 63) == 0) red[h * NW + (tid >> 6)] = sm;
+  }
+  __syncthreads();
+  double inv[HPB];
+  #pragma unroll
+  for (int h = 0; h < HPB; h++) {
+    double sm = red[h * NW];
+    for (int w = 1; w < NW; w++) sm += red[h * NW + w];
+    inv[h] = 1.0 / sm;
+  }
+  for (int t = tid; t < npos; t += NT) {
+    #pragma unroll
+    for (int h = 0; h < HPB; h++) p[h * ps + t] = (float)((double)p[h * ps + t] * inv[h]);
+  }
+  __syncthreads();
+  // weighted sum of V: thread -> (head tid / HD, dim tid % HD); f32 accumulation in position order
+  const int h = tid / HD, i = tid % HD;
+  const float *ph = p + h * ps;
+  float o = 0.f;
+  if (F16KV) {
+    const uint16_t *vb = (const uint16_t *)a.vcache + kvoff + i;
+    int t = 0;
+    for (; t + 4 <= npos; t += 4) {
+      float v0 = h2f(vb[(long)t * HD]), v1 = h2f(vb[(long)(t + 1) * HD]), v2 = h2f(vb[(long)(t + 2) * HD]), v3 = h2f(vb[(long)(t + 3) * HD]);
+      float4 pp = *(const float4 *)(ph + t);
+      o = fmaf(pp.x, v0, o); o = fmaf(pp.y, v1, o); o = fmaf(pp.z, v2, o); o = fmaf(pp.w, v3, o);
+    }
+    for (; t < npos; t++) o = fmaf(ph[t], h2f(vb[(long)t * HD]), o);
+  } else {
+    const float *vb = (const float *)a.vcache + kvoff + i;
+    int t = 0;
+    for (; t + 4 <= npos; t += 4) {
+      float v0 = vb[(long)t * HD], v1 = vb[(long)(t + 1) * HD], v2 = vb[(long)(t + 2) * HD], v3 = vb[(long)(t + 3) * HD];
+      float4 pp = *(const float4 *)(ph + t);
+      o = fmaf(pp.x, v0, o); o = fmaf(pp.y, v1, o); o = fmaf(pp.z, v2, o); o = fmaf(pp.w, v3, o);
+    }
+    for (; t < npos; t++) o = fmaf(ph[t], vb[(long)t * HD], o);
+  }
+  const int col = (h0 + h) * HD + i;
+  if (a.out) a.out[(long)b * a.ldo + col] = o;
+  Act act = a.act;
+  quant_block32(o, col, act.q + (long)b * act.ld, act.d + (long)b * (act.ld >> 5), act.s + (long)b * (act.ld >> 5),
+                act.s16 + (long)b * (act.ld >> 4));
+}
+
+// ================================================================================================ synthetic weights
+// Raw ggml blocks of a synthetic tensor generated in place (zerollm_amd/csrc/synth.h): one thread per block.
+__global__ void k_synth(int type, uint64_t seed, double std, uint64_t srcCols, uint64_t col0, int rows, int cols,
+                        uint8_t *out) {
+  int bv = zl_synth::block_values(type), bb = zl_synth::block_bytes(type);
+  long nbr = cols / bv;
+  long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)rows * nbr) return;
+  long r = idx / nbr, b = idx % nbr;
+  zl_synth::synth_block(type, seed, std, srcCols, col0, (uint64_t)r, (uint64_t)b, out + idx * bb);
+}
+
+__global__ void k_fill_f32(float *p, long n, float v) {
+  long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// ================================================================================================ launch helpers
+template <int FMT, int MT>
+static void launch_gemv_fmt(const GemvArgs &a, int epi, int blocks, size_t ldsBytes, hipStream_t st) {
+  if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemv<FMT, MT, EPI_STORE>), dim3(blocks), dim3(256), ldsBytes, st, a);
+  else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemv<FMT, MT, EPI_RESID>), dim3(blocks), dim3(256), ldsBytes, st, a);
+  else hipLaunchKernelGGL((k_gemv<FMT, MT, EPI_SWIGLU>), dim3(blocks), dim3(256), ldsBytes, st, a);
+}
+
+template <int MT>
+static void launch_gemv_mt(int fmt, const GemvArgs &a, int epi, int blocks, size_t ldsBytes, hipStream_t st) {
+  switch (fmt) {
+    case T_Q8_0: launch_gemv_fmt<T_Q8_0, MT>(a, epi, blocks, ldsBytes, st); break;
+    case T_Q4_0: launch_gemv_fmt<T_Q4_0, MT>(a, epi, blocks, ldsBytes, st); break;
+    case T_Q5_0: launch_gemv_fmt<T_Q5_0, MT>(a, epi, blocks, ldsBytes, st); break;
+    case T_Q4_K: launch_gemv_fmt<T_Q4_K, MT>(a, epi, blocks, ldsBytes, st); break;
+    case T_Q5_K: launch_gemv_fmt<T_Q5_K, MT>(a, epi, blocks, ldsBytes, st); break;
+    case T_Q6_K: launch_gemv_fmt<T_Q6_K, MT>(a, epi, blocks, ldsBytes, st); break;
+    default: throw Error(ZL_ERR_UNSUPPORTED, "gemv: unsupported weight type");
+  }
+}
+
+int gemv_lpr(int nslab) {
+  int l = 64;
+  while (l > 8 && l > nslab) l >>= 1;
+  return l;
+}
+
+void launch_gemv(const GemvArgs &a0, int epi, const float *xf, int ldx, hipStream_t st) {
+  GemvArgs a = a0;
+  const int fmt = a.seg[0].m.type;
+  for (int i = 1; i < a.nseg; i++) ZL_REQUIRE(a.seg[i].m.type == fmt && a.seg[i].m.nslab == a.nslab, ZL_ERR_ARG, "gemv: segments differ in type or width");
+  if (!is_quant(fmt)) {
+    int rows = a.rows_total;
+    int blocks = (rows + 3) / 4;
+    if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemv_float<EPI_STORE>), dim3(blocks), dim3(256), 0, st, a, xf, ldx);
+    else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemv_float<EPI_RESID>), dim3(blocks), dim3(256), 0, st, a, xf, ldx);
+    else hipLaunchKernelGGL((k_gemv_float<EPI_SWIGLU>), dim3(blocks), dim3(256), 0, st, a, xf, ldx);
+    ZL_HIP(hipGetLastError());
+    return;
+  }
+  const int lpr = a.lpr;
+  const int slots = 64 / lpr;
+  const int units = epi == EPI_SWIGLU ? a.rows_total : (a.rows_total + 1) / 2;
+  const int blocks = (units + 4 * slots - 1) / (4 * slots);
+  const int MT = a.M <= 1 ? 1 : a.M <= 2 ? 2 : a.M <= 4 ? 4 : a.M <= 8 ? 8 : 16;
+  // K window: all of K if it fits 64 KB of LDS for MT tokens, else the largest multiple of 64*lpr that does
+  const int K = a.nslab * 64;
+  const int step = 64 * lpr;
+  int wk = (65536 / MT) / step * step;
+  if (wk < step) wk = step;
+  if (wk > K) wk = K;
+  a.wk = wk;
+  const size_t ldsBytes = (size_t)MT * wk;
+  switch (MT) {
+    case 1: launch_gemv_mt<1>(fmt, a, epi, blocks, ldsBytes, st); break;
+    case 2: launch_gemv_mt<2>(fmt, a, epi, blocks, ldsBytes, st); break;
+    case 4: launch_gemv_mt<4>(fmt, a, epi, blocks, ldsBytes, st); break;
+    case 8: launch_gemv_mt<8>(fmt, a, epi, blocks, ldsBytes, st); break;
+    default: launch_gemv_mt<16>(fmt, a, epi, blocks, ldsBytes, st); break;
+  }
+  ZL_HIP(hipGetLastError());
+}
+
+template <int HPB, int HD>
+static void launch_attn_hd(const AttnArgs &a, dim3 grid, size_t lds, hipStream_t st) {
+  if (a.kvF16) hipLaunchKernelGGL((k_attention<HPB, HD, true>), grid, dim3(HPB * HD), lds, st, a);
+  else hipLaunchKernelGGL((k_attention<HPB, HD, false>), grid, dim3(HPB * HD), lds, st, a);
+}
+
+void launch_attention(const AttnArgs &a, int B, int ctxMax, int hpb, hipStream_t st) {
+  (void)ctxMax;
+  const size_t lds = (size_t)hpb * a.hd * 4 + (size_t)hpb * a.pstride * 4;
+  dim3 grid(B, a.nHead / hpb);
+  if (hpb == 2) {
+    if (a.hd == 64) launch_attn_hd<2, 64>(a, grid, lds, st);
+    else if (a.hd == 128) launch_attn_hd<2, 128>(a, grid, lds, st);
+    else launch_attn_hd<2, 256>(a, grid, lds, st);
+  } else {
+    if (a.hd == 64) launch_attn_hd<1, 64>(a, grid, lds, st);
+    else if (a.hd == 128) launch_attn_hd<1, 128>(a, grid, lds, st);
+    else launch_attn_hd<1, 256>(a, grid, lds, st);
+  }
+  ZL_HIP(hipGetLastError());
+}
+
+void launch_norm_quant(const float *x, int ldx, int row0, int nrows, const float *w, double eps, int n, int npad,
+                       const Act &act, hipStream_t st) {
+  hipLaunchKernelGGL(k_norm_quant, dim3(nrows), dim3(256), 0, st, x, ldx, row0, w, eps, n, npad, act);
+  ZL_HIP(hipGetLastError());
+}
+
+void launch_rope(const RopeArgs &a, int B, hipStream_t st) {
+  hipLaunchKernelGGL(k_qk_rope_kv, dim3(B, a.nHead + a.nHeadKv), dim3(64), 0, st, a);
+  ZL_HIP(hipGetLastError());
+}
+
+void launch_embed(const MatView &m, const Step *step, int B, float *x, int ldx, hipStream_t st) {
+  hipLaunchKernelGGL(k_embed, dim3(B), dim3(64), 0, st, m, step, x, ldx);
+  ZL_HIP(hipGetLastError());
+}
+
+void launch_dequant_rows(const MatView &m, const int *rowIds, int nrows, float *out, int ldo, hipStream_t st) {
+  hipLaunchKernelGGL(k_dequant_rows, dim3(nrows), dim3(64), 0, st, m, rowIds, nrows, out, ldo);
+  ZL_HIP(hipGetLastError());
+}
+
+void launch_repack(int type, const uint8_t *raw, long rawRowBytes, int rows, int cols, int nslab, DevMat &m, hipStream_t st) {
+  long n = (long)rows * nslab;
+  hipLaunchKernelGGL(k_repack, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, type, raw, rawRowBytes, rows, cols, nslab,
+                     m.qs, m.qx, m.sc, m.dd);
+  ZL_HIP(hipGetLastError());
+}
+
+void launch_synth(int type, uint64_t seed, double std, uint64_t srcCols, uint64_t col0, int rows, int cols, uint8_t *out,
+                  hipStream_t st) {
+  long n = (long)rows * (cols / zl_synth::block_values(type));
+  hipLaunchKernelGGL(k_synth, dim3((unsigned)((n + 127) / 128)), dim3(128), 0, st, type, seed, std, srcCols, col0, rows, cols, out);
+  ZL_HIP(hipGetLastError());
+}
+
+void launch_fill(float *p, long n, float v, hipStream_t st) {
+  hipLaunchKernelGGL(k_fill_f32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p, n, v);
+  ZL_HIP(hipGetLastError());
+}
+
+}  // namespace zl

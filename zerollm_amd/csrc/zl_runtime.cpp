@@ -1,0 +1,1184 @@
+// Runtime of the zerollm MI355X library: model construction (GGUF or synthetic) with weight repacking, the forward
+// pass as one captured HIP graph per (batch, logits mode), the on-device speculative cycle, and the C ABI
+// (include/zerollm_hip.h).
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <chrono>
+#include <map>
+#include <memory>
+#include <thread>
+#include <vector>
+
+#include "zerollm_hip.h"
+#include "gguf.h"
+#include "zl_kernels.h"
+
+namespace zl {
+
+static thread_local std::string g_err;
+static int g_device = -1;
+
+static void ensure_init() {
+  if (g_device < 0) {
+    int n = 0;
+    ZL_HIP(hipGetDeviceCount(&n));
+    ZL_REQUIRE(n > 0, ZL_ERR_HIP, "no GPU visible");
+    ZL_HIP(hipSetDevice(0));
+    g_device = 0;
+  }
+}
+
+static int pad64(int n) { return (n + 63) / 64 * 64; }
+
+// ---------------------------------------------------------------------------------------------- allocations
+struct Arena {
+  std::vector<void *> ptrs;
+  int64_t bytes = 0;
+  void *alloc(size_t n) {
+    void *p = nullptr;
+    if (n == 0) n = 16;
+    ZL_HIP(hipMalloc(&p, n));
+    ptrs.push_back(p);
+    bytes += (int64_t)n;
+    return p;
+  }
+  void release() {
+    for (void *p : ptrs) hipFree(p);
+    ptrs.clear();
+    bytes = 0;
+  }
+};
+
+// Allocate the planes of a rows x cols matrix of `type` and repack raw ggml rows (device pointer) into them.
+static DevMat make_mat(Arena &ar, int type, int rows, int cols, const uint8_t *draw, hipStream_t st) {
+  DevMat m;
+  m.type = type; m.rows = rows; m.cols = cols;
+  m.nslab = (cols + 63) / 64;
+  int64_t rb = ggml_row_bytes(type, cols);
+  ZL_REQUIRE(rb > 0, ZL_ERR_UNSUPPORTED, "unsupported tensor type " + std::to_string(type) + " for " + std::to_string(cols) + " columns");
+  if (!is_quant(type)) {
+    ZL_REQUIRE(type == T_F32 || type == T_F16 || type == T_BF16, ZL_ERR_UNSUPPORTED,
+               "reference kernels: unsupported tensor type " + std::to_string(type) + " (supported: F32, F16, BF16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)");
+    m.qs = (uint8_t *)ar.alloc((size_t)rb * rows);
+    ZL_HIP(hipMemcpyAsync(m.qs, draw, (size_t)rb * rows, hipMemcpyDeviceToDevice, st));
+    return m;
+  }
+  const long ns = (long)rows * m.nslab;
+  m.qs = (uint8_t *)ar.alloc(ns * qs_bytes(type));
+  if (qx_bytes(type)) m.qx = (uint8_t *)ar.alloc(ns * qx_bytes(type));
+  if (sc_bytes(type)) m.sc = (uint8_t *)ar.alloc(ns * sc_bytes(type));
+  long nd = (type == T_Q4_K || type == T_Q5_K) ? (long)rows * (m.nslab / 4) * 2 : type == T_Q6_K ? (long)rows * (m.nslab / 4) : ns * 2;
+  m.dd = (uint16_t *)ar.alloc(nd * 2);
+  launch_repack(type, draw, rb, rows, cols, m.nslab, m, st);
+  return m;
+}
+
+// ---------------------------------------------------------------------------------------------- model
+struct Layer {
+  DevMat wq, wk, wv, wo, wgate, wup, wdown;
+  float *attnNorm = nullptr, *ffnNorm = nullptr, *qNorm = nullptr, *kNorm = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr;
+};
+
+}  // namespace zl
+
+struct zl_model {
+  zl_config cfg{};
+  int ctx = 0, kvF16 = 0, maxBatch = 16, logitsBatch = 16;
+  bool closed = false;
+  zl::Arena ar;
+  int64_t weightBytes = 0;
+  zl::DevMat tokEmbd, output;
+  float *outputNorm = nullptr;
+  std::vector<zl::Layer> layers;
+  float *cosT = nullptr, *sinT = nullptr;
+  void *kcache = nullptr, *vcache = nullptr;
+  float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *hb = nullptr, *logits = nullptr;
+  zl::Act act{};
+  zl::Step *dstep = nullptr;
+  hipStream_t st = nullptr;
+  hipStream_t cst = nullptr;  // graphs are captured on their own stream
+  std::vector<int> tokens;
+  std::map<int, hipGraphExec_t> graphs;
+  std::map<int, hipGraph_t> graphDefs;
+  // timing probe
+  int probeLayer = -1, probeWhich = -1;
+  hipEvent_t probeA = nullptr, probeB = nullptr;
+  double probeMs = 0;
+  int64_t probeCount = 0, probeBytes = 0;
+  int lastLaunchHadProbe = 0;
+  ~zl_model();
+};
+
+struct zl_sampler {
+  zl::SamplerParams sp{};
+  zl::Arena ar;
+  zl::SpecState *ss = nullptr;      // device
+  zl::SpecState *hss = nullptr;     // pinned host mirror
+  zl::DevDist *pdist = nullptr, *qdist = nullptr, *tmpdist = nullptr;
+  zl::DevDist *hdist = nullptr;     // pinned
+  int *dhist = nullptr;             // device history (tail + drafted)
+  int *dstop = nullptr;
+  int *dtok = nullptr, *htok = nullptr;
+  float *scratch = nullptr;
+  int scratchVocab = 0;
+  hipStream_t st = nullptr;
+  ~zl_sampler();
+};
+
+struct zl_mat {
+  zl::Arena ar;
+  std::vector<zl::DevMat> copies;
+  hipStream_t st = nullptr;
+  ~zl_mat() {
+    if (st) hipStreamSynchronize(st);
+    ar.release();
+    if (st) hipStreamDestroy(st);
+  }
+};
+
+zl_model::~zl_model() {
+  if (st) hipStreamSynchronize(st);
+  for (auto &g : graphs) hipGraphExecDestroy(g.second);
+  for (auto &g : graphDefs) hipGraphDestroy(g.second);
+  if (probeA) hipEventDestroy(probeA);
+  if (probeB) hipEventDestroy(probeB);
+  ar.release();
+  if (st) hipStreamDestroy(st);
+  if (cst) hipStreamDestroy(cst);
+}
+
+zl_sampler::~zl_sampler() {
+  if (st) hipStreamSynchronize(st);
+  ar.release();
+  if (hss) hipHostFree(hss);
+  if (hdist) hipHostFree(hdist);
+  if (htok) hipHostFree(htok);
+  if (st) hipStreamDestroy(st);
+}
+
+namespace zl {
+
+// Small kernels that set per-pass state from kernel arguments (no host buffer has to outlive an async copy).
+__global__ void k_set_step(Step *d, Step h) { if (threadIdx.x == 0) *d = h; }
+struct HistArgs { int n; int ids[128]; };
+__global__ void k_set_hist(int *d, HistArgs h) {
+  for (int i = threadIdx.x; i < h.n; i += blockDim.x) d[i] = h.ids[i];
+}
+struct StopArgs { int n; int ids[64]; };
+__global__ void k_set_stop(int *d, StopArgs h) {
+  for (int i = threadIdx.x; i < h.n; i += blockDim.x) d[i] = h.ids[i];
+}
+__global__ void k_spec_reset(SpecState *ss) {
+  if (threadIdx.x == 0) { ss->kk = 0; ss->stopped = 0; ss->a = 0; ss->tok = -1; }
+}
+__global__ void k_set_rng(SpecState *ss, uint32_t v) { if (threadIdx.x == 0) ss->rng = v; }
+
+static void set_step(zl_model *m, int pos0, const int *toks, int B) {
+  Step h;
+  memset(&h, 0, sizeof(h));
+  h.pos0 = pos0; h.B = B;
+  for (int i = 0; i < B; i++) h.tokens[i] = toks[i];
+  hipLaunchKernelGGL(k_set_step, dim3(1), dim3(64), 0, m->st, m->dstep, h);
+  ZL_HIP(hipGetLastError());
+}
+
+static int qdim(const zl_model *m) { return m->cfg.n_head * m->cfg.head_dim; }
+static int kvdim(const zl_model *m) { return m->cfg.n_head_kv * m->cfg.head_dim; }
+
+static int64_t mat_bytes(const DevMat &mm) { int64_t rb = ggml_row_bytes(mm.type, mm.cols); return rb < 0 ? 0 : rb * mm.rows; }
+
+// Allocate KV cache, activations, RoPE tables; compute pass bytes.
+static void finish_model(zl_model *m, const float *ropeFreqs) {
+  const zl_config &c = m->cfg;
+  ZL_REQUIRE(c.head_dim == 128 || c.head_dim == 64 || c.head_dim == 256, ZL_ERR_UNSUPPORTED,
+             "head_dim " + std::to_string(c.head_dim) + " is not supported (64, 128 or 256)");
+  ZL_REQUIRE(c.n_head % c.n_head_kv == 0, ZL_ERR_UNSUPPORTED, "n_head must be a multiple of n_head_kv");
+  const int half = c.n_rot / 2;
+  // RoPE tables exactly as ropeTables (src/compute/ref-kernels.js:329-342), in f64 on the host, stored f32
+  std::vector<float> cs((size_t)m->ctx * half), sn((size_t)m->ctx * half);
+  for (int i = 0; i < half; i++) {
+    double freq = pow((double)c.rope_base, (-2.0 * i) / c.n_rot);
+    if (ropeFreqs) freq /= (double)ropeFreqs[i];
+    for (int p = 0; p < m->ctx; p++) {
+      cs[(size_t)p * half + i] = (float)cos(p * freq);
+      sn[(size_t)p * half + i] = (float)sin(p * freq);
+    }
+  }
+  m->cosT = (float *)m->ar.alloc(cs.size() * 4);
+  m->sinT = (float *)m->ar.alloc(sn.size() * 4);
+  ZL_HIP(hipMemcpy(m->cosT, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+  ZL_HIP(hipMemcpy(m->sinT, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+  const size_t kvElems = (size_t)c.n_layer * c.n_head_kv * m->ctx * c.head_dim;
+  m->kcache = m->ar.alloc(kvElems * (m->kvF16 ? 2 : 4));
+  m->vcache = m->ar.alloc(kvElems * (m->kvF16 ? 2 : 4));
+  ZL_HIP(hipMemset(m->kcache, 0, kvElems * (m->kvF16 ? 2 : 4)));
+  ZL_HIP(hipMemset(m->vcache, 0, kvElems * (m->kvF16 ? 2 : 4)));
+  const int B = m->maxBatch;
+  m->x = (float *)m->ar.alloc((size_t)B * c.n_embd * 4);
+  m->q = (float *)m->ar.alloc((size_t)B * qdim(m) * 4);
+  m->k = (float *)m->ar.alloc((size_t)B * kvdim(m) * 4);
+  m->v = (float *)m->ar.alloc((size_t)B * kvdim(m) * 4);
+  m->hb = (float *)m->ar.alloc((size_t)B * c.n_ff * 4);
+  m->logits = (float *)m->ar.alloc((size_t)m->logitsBatch * c.vocab * 4);
+  const int ld = pad64(std::max(c.n_embd, std::max(qdim(m), c.n_ff)));
+  m->act.ld = ld;
+  m->act.q = (int8_t *)m->ar.alloc((size_t)B * ld);
+  m->act.d = (float *)m->ar.alloc((size_t)B * (ld / 32) * 4);
+  m->act.s = (int32_t *)m->ar.alloc((size_t)B * (ld / 32) * 4);
+  m->act.s16 = (int32_t *)m->ar.alloc((size_t)B * (ld / 16) * 4);
+  m->act.f = (float *)m->ar.alloc((size_t)B * ld * 4);
+  ZL_HIP(hipMemset(m->act.q, 0, (size_t)B * ld));
+  m->dstep = (Step *)m->ar.alloc(sizeof(Step));
+  ZL_HIP(hipMemset(m->dstep, 0, sizeof(Step)));
+  int64_t wb = 0;
+  for (auto &L : m->layers) wb += mat_bytes(L.wq) + mat_bytes(L.wk) + mat_bytes(L.wv) + mat_bytes(L.wo) + mat_bytes(L.wgate) + mat_bytes(L.wup) + mat_bytes(L.wdown);
+  wb += mat_bytes(m->output);
+  m->weightBytes = wb;
+  ZL_HIP(hipStreamSynchronize(m->st));
+}
+
+// ---------------------------------------------------------------------------------------------- forward pass
+struct SegSpec { const DevMat *m; float *out; int ldo; const float *bias; };
+
+static void gemv_group(zl_model *m, const std::vector<SegSpec> &segs, int B, int epi, bool probe) {
+  GemvArgs a;
+  memset(&a, 0, sizeof(a));
+  a.nseg = (int)segs.size();
+  a.rows_total = 0;
+  for (int i = 0; i < a.nseg; i++) {
+    a.seg[i].m = view(*segs[i].m);
+    a.seg[i].rows = segs[i].m->rows;
+    a.seg[i].out = segs[i].out;
+    a.seg[i].ldo = segs[i].ldo;
+    a.seg[i].bias = segs[i].bias;
+    if (epi != EPI_SWIGLU || i == 0) a.rows_total += segs[i].m->rows;
+  }
+  a.nslab = segs[0].m->nslab;
+  a.act = m->act;
+  a.M = B;
+  a.lpr = gemv_lpr(a.nslab);
+  a.resid = m->x;
+  a.ldr = m->cfg.n_embd;
+  a.hb = m->hb;
+  a.ldh = m->cfg.n_ff;
+  if (probe) ZL_HIP(hipEventRecord(m->probeA, m->st));
+  launch_gemv(a, epi, m->act.f, m->act.ld, m->st);
+  if (probe) ZL_HIP(hipEventRecord(m->probeB, m->st));
+}
+
+// Enqueue one forward pass of B tokens (tokens and positions from m->dstep). want: 0 none, 1 last, 2 all.
+static void enqueue_forward(zl_model *m, int B, int want, bool withProbe) {
+  const zl_config &c = m->cfg;
+  const int d = c.n_embd, qd = qdim(m), kvd = kvdim(m), ff = c.n_ff;
+  const double eps = (double)c.rms_eps;
+  launch_embed(view(m->tokEmbd), m->dstep, B, m->x, d, m->st);
+  for (int l = 0; l < c.n_layer; l++) {
+    Layer &L = m->layers[l];
+    auto P = [&](int which) { return withProbe && m->probeLayer == l && m->probeWhich == which; };
+    launch_norm_quant(m->x, d, 0, B, L.attnNorm, eps, d, pad64(d), m->act, m->st);
+    // q, k, v: consecutive matrices of one type share a launch
+    SegSpec qkv[3] = {{&L.wq, m->q, qd, L.bq}, {&L.wk, m->k, kvd, L.bk}, {&L.wv, m->v, kvd, L.bv}};
+    int i0 = 0;
+    while (i0 < 3) {
+      int i1 = i0 + 1;
+      while (i1 < 3 && qkv[i1].m->type == qkv[i0].m->type) i1++;
+      gemv_group(m, std::vector<SegSpec>(qkv + i0, qkv + i1), B, EPI_STORE, P(0) && i0 == 0);
+      i0 = i1;
+    }
+    RopeArgs ra;
+    ra.q = m->q; ra.k = m->k; ra.v = m->v; ra.ldq = qd; ra.ldkv = kvd;
+    ra.qNorm = L.qNorm; ra.kNorm = L.kNorm; ra.eps = eps;
+    ra.cosT = m->cosT; ra.sinT = m->sinT;
+    ra.nRot = c.n_rot; ra.neox = c.neox; ra.nHead = c.n_head; ra.nHeadKv = c.n_head_kv; ra.hd = c.head_dim;
+    ra.ctx = m->ctx; ra.layer = l; ra.kvF16 = m->kvF16; ra.kcache = m->kcache; ra.vcache = m->vcache; ra.step = m->dstep;
+    launch_rope(ra, B, m->st);
+    AttnArgs aa;
+    aa.q = m->q; aa.ldq = qd; aa.kcache = m->kcache; aa.vcache = m->vcache;
+    aa.nHead = c.n_head; aa.nHeadKv = c.n_head_kv; aa.hd = c.head_dim; aa.ctx = m->ctx; aa.layer = l; aa.kvF16 = m->kvF16;
+    aa.pstride = (m->ctx + 3) / 4 * 4;
+    aa.scale = 1.0 / sqrt((double)c.head_dim);
+    aa.step = m->dstep; aa.out = m->act.f; aa.ldo = m->act.ld; aa.act = m->act;
+    const int group = c.n_head / c.n_head_kv;
+    int hpb = (group % 2 == 0 && (size_t)2 * (c.head_dim + aa.pstride) * 4 <= 65536) ? 2 : 1;
+    ZL_REQUIRE((size_t)hpb * (c.head_dim + aa.pstride) * 4 <= 65536, ZL_ERR_UNSUPPORTED, "context too long for the attention kernel");
+    launch_attention(aa, B, m->ctx, hpb, m->st);
+    gemv_group(m, {{&L.wo, nullptr, 0, nullptr}}, B, EPI_RESID, P(1));
+    launch_norm_quant(m->x, d, 0, B, L.ffnNorm, eps, d, pad64(d), m->act, m->st);
+    ZL_REQUIRE(L.wgate.type == L.wup.type, ZL_ERR_UNSUPPORTED, "ffn_gate and ffn_up must share a type");
+    gemv_group(m, {{&L.wgate, nullptr, 0, nullptr}, {&L.wup, nullptr, 0, nullptr}}, B, EPI_SWIGLU, P(2));
+    launch_norm_quant(m->hb, ff, 0, B, nullptr, eps, ff, pad64(ff), m->act, m->st);
+    gemv_group(m, {{&L.wdown, nullptr, 0, nullptr}}, B, EPI_RESID, P(3));
+  }
+  if (want == 2) {
+    launch_norm_quant(m->x, d, 0, B, m->outputNorm, eps, d, pad64(d), m->act, m->st);
+    gemv_group(m, {{&m->output, m->logits, c.vocab, nullptr}}, B, EPI_STORE, withProbe && m->probeWhich == 4);
+  } else if (want == 1) {
+    launch_norm_quant(m->x, d, B - 1, 1, m->outputNorm, eps, d, pad64(d), m->act, m->st);
+    gemv_group(m, {{&m->output, m->logits, c.vocab, nullptr}}, 1, EPI_STORE, withProbe && m->probeWhich == 4);
+  }
+}
+
+static hipGraphExec_t graph_for(zl_model *m, int B, int want) {
+  const int key = B * 4 + want;
+  auto it = m->graphs.find(key);
+  if (it != m->graphs.end()) return it->second;
+  const bool probe = m->probeWhich >= 0;
+  hipGraph_t g = nullptr;
+  hipStream_t run = m->st;
+  m->st = m->cst;
+  struct Back { zl_model *m; hipStream_t s; ~Back() { m->st = s; } } back{m, run};
+  ZL_HIP(hipStreamBeginCapture(m->cst, hipStreamCaptureModeThreadLocal));
+  try {
+    enqueue_forward(m, B, want, probe);
+  } catch (...) {
+    hipStreamEndCapture(m->cst, &g);
+    if (g) hipGraphDestroy(g);
+    throw;
+  }
+  ZL_HIP(hipStreamEndCapture(m->cst, &g));
+  hipGraphExec_t ex;
+  ZL_HIP(hipGraphInstantiate(&ex, g, nullptr, nullptr, 0));
+  m->graphs[key] = ex;
+  m->graphDefs[key] = g;
+  return ex;
+}
+
+static bool graph_has_probe(zl_model *m, int B, int want) {
+  if (m->probeWhich < 0) return false;
+  if (m->probeWhich == 4) return want != 0;
+  (void)B;
+  return m->probeLayer >= 0 && m->probeLayer < m->cfg.n_layer;
+}
+
+// One pass; the caller has set m->dstep. Accumulates the probe after the pass if requested.
+static void launch_pass(zl_model *m, int B, int want) {
+  ZL_HIP(hipGraphLaunch(graph_for(m, B, want), m->st));
+  m->lastLaunchHadProbe = graph_has_probe(m, B, want);
+}
+
+static void collect_probe(zl_model *m) {
+  if (!m->lastLaunchHadProbe) return;
+  ZL_HIP(hipEventSynchronize(m->probeB));
+  float ms = 0;
+  ZL_HIP(hipEventElapsedTime(&ms, m->probeA, m->probeB));
+  m->probeMs += ms;
+  m->probeCount++;
+  m->lastLaunchHadProbe = 0;
+}
+
+// PoolModel.forwardBatch checks (src/compute/pool.js:146-155), same messages.
+static void check_batch(zl_model *m, const int32_t *tokens, int B, int want) {
+  ZL_REQUIRE(!m->closed, ZL_ERR_STATE, "model is closed");
+  ZL_REQUIRE(B >= 1 && B <= m->maxBatch, ZL_ERR_BATCH, "batch of " + std::to_string(B) + " tokens (max " + std::to_string(m->maxBatch) + ")");
+  const int pos = (int)m->tokens.size();
+  ZL_REQUIRE(pos + B <= m->ctx, ZL_ERR_CONTEXT, "context full (" + std::to_string(m->ctx) + " tokens)");
+  for (int i = 0; i < B; i++)
+    ZL_REQUIRE(tokens[i] >= 0 && tokens[i] < m->cfg.vocab, ZL_ERR_TOKEN, "token id " + std::to_string(tokens[i]) + " out of range");
+  ZL_REQUIRE(!(want == 2 && B > m->logitsBatch), ZL_ERR_BATCH,
+             "logits for all positions of a batch of " + std::to_string(B) + " tokens (this pool supports " + std::to_string(m->logitsBatch) +
+                 "; raise the logitsBatch option)");
+}
+
+static void forward(zl_model *m, const int32_t *tokens, int B, int want) {
+  check_batch(m, tokens, B, want);
+  set_step(m, (int)m->tokens.size(), tokens, B);
+  launch_pass(m, B, want);
+  for (int i = 0; i < B; i++) m->tokens.push_back(tokens[i]);
+}
+
+// ---------------------------------------------------------------------------------------------- construction
+static zl_model *new_model(const zl_model_opts *o) {
+  std::unique_ptr<zl_model> m(new zl_model());
+  int mb = o && o->max_batch > 0 ? o->max_batch : 16;
+  m->maxBatch = std::max(1, std::min(mb, 64));
+  int lb = o && o->logits_batch > 0 ? o->logits_batch : 16;
+  m->logitsBatch = std::max(1, std::min(lb, m->maxBatch));
+  m->kvF16 = o ? (o->kv_f16 ? 1 : 0) : 0;
+  ZL_HIP(hipStreamCreateWithFlags(&m->st, hipStreamNonBlocking));
+  ZL_HIP(hipStreamCreateWithFlags(&m->cst, hipStreamNonBlocking));
+  ZL_HIP(hipEventCreate(&m->probeA));
+  ZL_HIP(hipEventCreate(&m->probeB));
+  return m.release();
+}
+
+static void check_config(const zl_config &c) {
+  ZL_REQUIRE(c.n_embd > 0 && c.n_layer > 0 && c.n_ff > 0 && c.n_head > 0 && c.n_head_kv > 0 && c.head_dim > 0 && c.vocab > 0,
+             ZL_ERR_ARG, "bad model config");
+  ZL_REQUIRE(c.n_rot > 0 && c.n_rot <= c.head_dim && c.n_rot % 2 == 0, ZL_ERR_ARG, "bad rope dimension count");
+}
+
+static float *upload_vec(zl_model *m, const std::vector<float> &v) {
+  float *p = (float *)m->ar.alloc(v.size() * 4);
+  ZL_HIP(hipMemcpy(p, v.data(), v.size() * 4, hipMemcpyHostToDevice));
+  return p;
+}
+
+// ---- from GGUF (modelConfig, src/model/config.js:275-325; tensors as RefModel, src/model/forward.js:114-132)
+static zl_model *load_gguf(const char *path, const zl_model_opts *o) {
+  GGUF g = read_gguf(path);
+  const GGUFValue *av = g.get("general.architecture");
+  ZL_REQUIRE(av && av->type == 8, ZL_ERR_FORMAT, "GGUF has no general.architecture");
+  const std::string arch = av->str;
+  int archId = arch == "llama" ? 0 : arch == "qwen2" ? 1 : arch == "qwen3" ? 2 : -1;
+  ZL_REQUIRE(archId >= 0, ZL_ERR_UNSUPPORTED, "architecture \"" + arch + "\" is not supported by the HIP path (supported: llama, qwen2, qwen3)");
+  auto need = [&](const std::string &k) {
+    const GGUFValue *v = g.get(arch + "." + k);
+    ZL_REQUIRE(v != nullptr, ZL_ERR_FORMAT, "GGUF is missing metadata key " + arch + "." + k);
+    return v->num;
+  };
+  zl_config c{};
+  c.arch = archId;
+  c.n_embd = (int)need("embedding_length");
+  c.n_head = (int)need("attention.head_count");
+  c.n_head_kv = (int)g.num(arch + ".attention.head_count_kv", c.n_head);
+  double hd = g.num(arch + ".attention.key_length", (double)c.n_embd / c.n_head);
+  ZL_REQUIRE(hd == (double)(int)hd, ZL_ERR_FORMAT, "cannot determine integer head_dim");
+  c.head_dim = (int)hd;
+  const GGUFTensor *te = g.tensor("token_embd.weight");
+  const GGUFValue *toks = g.get("tokenizer.ggml.tokens");
+  double vs = g.num(arch + ".vocab_size", -1);
+  if (vs < 0) vs = toks && toks->type == 9 ? (double)toks->arrLen : te ? (double)te->dims[1] : -1;
+  ZL_REQUIRE(vs > 0, ZL_ERR_FORMAT, "cannot determine vocab size");
+  c.vocab = (int)vs;
+  c.n_layer = (int)need("block_count");
+  c.n_ctx_train = (int)need("context_length");
+  c.n_ff = (int)need("feed_forward_length");
+  c.n_rot = (int)g.num(arch + ".rope.dimension_count", c.head_dim);
+  c.rms_eps = (float)g.num(arch + ".attention.layer_norm_rms_epsilon", 1e-5);
+  c.rope_base = (float)g.num(arch + ".rope.freq_base", 10000);
+  c.neox = archId != 0;
+  c.qk_norm = g.tensor("blk.0.attn_q_norm.weight") != nullptr;
+  c.qkv_bias = g.tensor("blk.0.attn_q.bias") != nullptr;
+  c.tied = g.tensor("output.weight") == nullptr;
+  c.has_rope_freqs = g.tensor("rope_freqs.weight") != nullptr;
+  check_config(c);
+
+  std::unique_ptr<zl_model> m(new_model(o));
+  m->cfg = c;
+  int want_ctx = o && o->ctx > 0 ? o->ctx : 2048;
+  m->ctx = std::min(want_ctx, c.n_ctx_train);
+  FILE *f = fopen(path, "rb");
+  ZL_REQUIRE(f != nullptr, ZL_ERR_IO, std::string("cannot open ") + path);
+  struct Closer { FILE *f; ~Closer() { fclose(f); } } closer{f};
+  // staging: pinned host chunk + device buffer sized for the largest tensor
+  uint64_t maxBytes = 0;
+  for (auto &t : g.tensors) maxBytes = std::max(maxBytes, t.nBytes);
+  uint8_t *dstage = (uint8_t *)nullptr;
+  ZL_HIP(hipMalloc(&dstage, std::max<uint64_t>(maxBytes, 16)));
+  const size_t CH = 64u << 20;
+  uint8_t *hst = nullptr;
+  ZL_HIP(hipHostMalloc(&hst, CH));
+  struct Freer { uint8_t *d, *h; ~Freer() { hipFree(d); hipHostFree(h); } } freer{dstage, hst};
+  auto read_dev = [&](const GGUFTensor &t) {
+    for (uint64_t off = 0; off < t.nBytes; off += CH) {
+      size_t n = (size_t)std::min<uint64_t>(CH, t.nBytes - off);
+      ZL_HIP(hipStreamSynchronize(m->st));
+      if (fseeko(f, (off_t)(t.absOffset + off), SEEK_SET) != 0 || fread(hst, 1, n, f) != n)
+        throw Error(ZL_ERR_IO, "tensor " + t.name + ": unexpected end of file");
+      ZL_HIP(hipMemcpyAsync(dstage + off, hst, n, hipMemcpyHostToDevice, m->st));
+    }
+    ZL_HIP(hipStreamSynchronize(m->st));
+  };
+  auto req = [&](const std::string &n) -> const GGUFTensor & {
+    const GGUFTensor *t = g.tensor(n);
+    ZL_REQUIRE(t != nullptr, ZL_ERR_FORMAT, "tensor not found in GGUF: " + n);
+    return *t;
+  };
+  auto W = [&](const std::string &n, int rows, int cols) {
+    const GGUFTensor &t = req(n);
+    ZL_REQUIRE(t.dims.size() >= 2 && (int)t.dims[0] == cols && (int)t.dims[1] == rows, ZL_ERR_FORMAT, "tensor " + n + " has unexpected shape");
+    read_dev(t);
+    DevMat mm = make_mat(m->ar, t.type, rows, cols, dstage, m->st);
+    ZL_HIP(hipStreamSynchronize(m->st));
+    return mm;
+  };
+  auto V = [&](const std::string &n, int len) -> float * {
+    const GGUFTensor &t = req(n);
+    ZL_REQUIRE((int)t.dims[0] == len, ZL_ERR_FORMAT, "tensor " + n + " has unexpected length");
+    std::vector<uint8_t> raw(t.nBytes);
+    if (fseeko(f, (off_t)t.absOffset, SEEK_SET) != 0 || fread(raw.data(), 1, t.nBytes, f) != t.nBytes) throw Error(ZL_ERR_IO, "tensor " + n + ": read failed");
+    std::vector<float> v(len);
+    if (t.type == T_F32) memcpy(v.data(), raw.data(), (size_t)len * 4);
+    else throw Error(ZL_ERR_UNSUPPORTED, "vector tensor " + n + " must be F32");
+    return upload_vec(m.get(), v);
+  };
+  auto Vopt = [&](const std::string &n, int len) -> float * { return g.tensor(n) ? V(n, len) : nullptr; };
+  const int qd = c.n_head * c.head_dim, kvd = c.n_head_kv * c.head_dim;
+  m->tokEmbd = W("token_embd.weight", c.vocab, c.n_embd);
+  m->outputNorm = V("output_norm.weight", c.n_embd);
+  m->output = c.tied ? m->tokEmbd : W("output.weight", c.vocab, c.n_embd);
+  std::vector<float> ropeFreqs;
+  if (c.has_rope_freqs) {
+    const GGUFTensor &t = req("rope_freqs.weight");
+    ropeFreqs.resize(t.dims[0]);
+    if (fseeko(f, (off_t)t.absOffset, SEEK_SET) != 0 || fread(ropeFreqs.data(), 4, t.dims[0], f) != t.dims[0]) throw Error(ZL_ERR_IO, "rope_freqs read failed");
+  }
+  for (int l = 0; l < c.n_layer; l++) {
+    const std::string p = "blk." + std::to_string(l) + ".";
+    Layer L;
+    L.attnNorm = V(p + "attn_norm.weight", c.n_embd);
+    L.wq = W(p + "attn_q.weight", qd, c.n_embd);
+    L.wk = W(p + "attn_k.weight", kvd, c.n_embd);
+    L.wv = W(p + "attn_v.weight", kvd, c.n_embd);
+    L.wo = W(p + "attn_output.weight", c.n_embd, qd);
+    L.bq = Vopt(p + "attn_q.bias", qd); L.bk = Vopt(p + "attn_k.bias", kvd); L.bv = Vopt(p + "attn_v.bias", kvd);
+    L.qNorm = Vopt(p + "attn_q_norm.weight", c.head_dim); L.kNorm = Vopt(p + "attn_k_norm.weight", c.head_dim);
+    L.ffnNorm = V(p + "ffn_norm.weight", c.n_embd);
+    L.wgate = W(p + "ffn_gate.weight", c.n_ff, c.n_embd);
+    L.wup = W(p + "ffn_up.weight", c.n_ff, c.n_embd);
+    L.wdown = W(p + "ffn_down.weight", c.n_embd, c.n_ff);
+    m->layers.push_back(L);
+  }
+  finish_model(m.get(), c.has_rope_freqs ? ropeFreqs.data() : nullptr);
+  return m.release();
+}
+
+// ---- synthetic
+static void synth_to_device(const zl_synth_tensor &t, uint8_t *out, hipStream_t st) {
+  ZL_REQUIRE(zl_synth::block_values(t.type) > 0, ZL_ERR_UNSUPPORTED, "synthetic tensors support F32, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K");
+  ZL_REQUIRE(t.cols % zl_synth::block_values(t.type) == 0, ZL_ERR_ARG, std::string("synthetic tensor ") + (t.name ? t.name : "") + ": cols not a whole number of blocks");
+  launch_synth(t.type, t.seed, t.std, (uint64_t)(t.src_cols > 0 ? t.src_cols : t.cols), (uint64_t)t.col0, (int)t.rows, (int)t.cols, out, st);
+}
+
+static zl_model *build_synth(const zl_config *cfg, const zl_synth_tensor *ts, int n, const zl_model_opts *o) {
+  zl_config c = *cfg;
+  check_config(c);
+  std::map<std::string, const zl_synth_tensor *> byName;
+  for (int i = 0; i < n; i++) byName[ts[i].name] = &ts[i];
+  std::unique_ptr<zl_model> m(new_model(o));
+  m->cfg = c;
+  int want_ctx = o && o->ctx > 0 ? o->ctx : 2048;
+  m->ctx = std::min(want_ctx, c.n_ctx_train);
+  size_t maxBytes = 16;
+  for (int i = 0; i < n; i++) if (!ts[i].fill) maxBytes = std::max(maxBytes, (size_t)ggml_row_bytes(ts[i].type, ts[i].cols) * (size_t)ts[i].rows);
+  uint8_t *dstage = nullptr;
+  ZL_HIP(hipMalloc(&dstage, maxBytes));
+  struct Freer { uint8_t *d; ~Freer() { hipFree(d); } } freer{dstage};
+  auto req = [&](const std::string &nm) -> const zl_synth_tensor & {
+    auto it = byName.find(nm);
+    ZL_REQUIRE(it != byName.end(), ZL_ERR_ARG, "synthetic model has no tensor " + nm);
+    return *it->second;
+  };
+  auto W = [&](const std::string &nm, int rows, int cols) {
+    const zl_synth_tensor &t = req(nm);
+    ZL_REQUIRE(t.rows == rows && t.cols == cols && !t.fill, ZL_ERR_ARG, "synthetic tensor " + nm + " has unexpected shape");
+    synth_to_device(t, dstage, m->st);
+    DevMat mm = make_mat(m->ar, t.type, rows, cols, dstage, m->st);
+    ZL_HIP(hipStreamSynchronize(m->st));
+    return mm;
+  };
+  auto V = [&](const std::string &nm, int len) -> float * {
+    const zl_synth_tensor &t = req(nm);
+    ZL_REQUIRE(t.rows * t.cols == len, ZL_ERR_ARG, "synthetic vector " + nm + " has unexpected length");
+    if (t.fill) return upload_vec(m.get(), std::vector<float>(len, t.fill_value));
+    ZL_REQUIRE(t.type == T_F32, ZL_ERR_ARG, "synthetic vector " + nm + " must be F32");
+    float *p = (float *)m->ar.alloc((size_t)len * 4);
+    synth_to_device(t, (uint8_t *)p, m->st);
+    return p;
+  };
+  auto Vopt = [&](const std::string &nm, int len) -> float * { return byName.count(nm) ? V(nm, len) : nullptr; };
+  const int qd = c.n_head * c.head_dim, kvd = c.n_head_kv * c.head_dim;
+  m->tokEmbd = W("token_embd.weight", c.vocab, c.n_embd);
+  m->outputNorm = V("output_norm.weight", c.n_embd);
+  m->output = c.tied ? m->tokEmbd : W("output.weight", c.vocab, c.n_embd);
+  for (int l = 0; l < c.n_layer; l++) {
+    const std::string p = "blk." + std::to_string(l) + ".";
+    Layer L;
+    L.attnNorm = V(p + "attn_norm.weight", c.n_embd);
+    L.wq = W(p + "attn_q.weight", qd, c.n_embd);
+    L.wk = W(p + "attn_k.weight", kvd, c.n_embd);
+    L.wv = W(p + "attn_v.weight", kvd, c.n_embd);
+    L.wo = W(p + "attn_output.weight", c.n_embd, qd);
+    L.bq = Vopt(p + "attn_q.bias", qd); L.bk = Vopt(p + "attn_k.bias", kvd); L.bv = Vopt(p + "attn_v.bias", kvd);
+    L.qNorm = Vopt(p + "attn_q_norm.weight", c.head_dim); L.kNorm = Vopt(p + "attn_k_norm.weight", c.head_dim);
+    L.ffnNorm = V(p + "ffn_norm.weight", c.n_embd);
+    L.wgate = W(p + "ffn_gate.weight", c.n_ff, c.n_embd);
+    L.wup = W(p + "ffn_up.weight", c.n_ff, c.n_embd);
+    L.wdown = W(p + "ffn_down.weight", c.n_embd, c.n_ff);
+    m->layers.push_back(L);
+  }
+  ZL_REQUIRE(!c.has_rope_freqs, ZL_ERR_UNSUPPORTED, "synthetic models do not take rope_freqs");
+  finish_model(m.get(), nullptr);
+  return m.release();
+}
+
+// ---------------------------------------------------------------------------------------------- sampler
+static zl_sampler *new_sampler(const zl_sampler_opts *o) {
+  std::unique_ptr<zl_sampler> s(new zl_sampler());
+  SamplerParams &p = s->sp;
+  p.temperature = o->temperature; p.topP = o->top_p; p.minP = o->min_p; p.repeatPenalty = o->repeat_penalty;
+  p.presence = o->presence_penalty; p.frequency = o->frequency_penalty; p.topK = o->top_k; p.repeatLastN = o->repeat_last_n;
+  p.penalized = (p.repeatPenalty != 1.0 || p.presence != 0.0 || p.frequency != 0.0) ? 1 : 0;
+  p.greedyArgmax = o->greedy_argmax ? 1 : 0;
+  if (!(p.temperature <= 0.0) && !p.greedyArgmax)
+    ZL_REQUIRE(p.topK >= 1 && p.topK <= KCAP, ZL_ERR_UNSUPPORTED, "top_k must be 1.." + std::to_string(KCAP) + " on the GPU sampler");
+  ZL_REQUIRE(p.repeatLastN >= 0 && p.repeatLastN <= 64, ZL_ERR_UNSUPPORTED, "repeat_last_n must be 0..64 on the GPU sampler");
+  ZL_HIP(hipStreamCreateWithFlags(&s->st, hipStreamNonBlocking));
+  s->ss = (SpecState *)s->ar.alloc(sizeof(SpecState));
+  ZL_HIP(hipMemset(s->ss, 0, sizeof(SpecState)));
+  ZL_HIP(hipHostMalloc((void **)&s->hss, sizeof(SpecState)));
+  s->pdist = (DevDist *)s->ar.alloc(sizeof(DevDist) * 65);
+  s->qdist = (DevDist *)s->ar.alloc(sizeof(DevDist) * 64);
+  s->tmpdist = (DevDist *)s->ar.alloc(sizeof(DevDist));
+  ZL_HIP(hipHostMalloc((void **)&s->hdist, sizeof(DevDist)));
+  s->dhist = (int *)s->ar.alloc(sizeof(int) * 256);
+  s->dstop = (int *)s->ar.alloc(sizeof(int) * 64);
+  s->dtok = (int *)s->ar.alloc(sizeof(int) * 4);
+  ZL_HIP(hipHostMalloc((void **)&s->htok, sizeof(int) * 4));
+  hipLaunchKernelGGL(k_set_rng, dim3(1), dim3(64), 0, s->st, s->ss, o->seed);
+  ZL_HIP(hipGetLastError());
+  ZL_HIP(hipStreamSynchronize(s->st));
+  return s.release();
+}
+
+static void ensure_scratch(zl_sampler *s, int vocab) {
+  if (!s->sp.penalized || s->scratchVocab >= vocab) return;
+  s->scratch = (float *)s->ar.alloc((size_t)65 * vocab * 4);
+  s->scratchVocab = vocab;
+}
+
+// Upload the last repeatLastN ids of a history (only those can matter) and return how many were kept.
+static int upload_hist(zl_sampler *s, hipStream_t st, const int32_t *hist, int nh) {
+  if (!s->sp.penalized || !hist || nh <= 0) return 0;
+  int keep = std::min(nh, s->sp.repeatLastN);
+  HistArgs h;
+  h.n = keep;
+  for (int i = 0; i < keep; i++) h.ids[i] = hist[nh - keep + i];
+  hipLaunchKernelGGL(k_set_hist, dim3(1), dim3(128), 0, st, s->dhist, h);
+  ZL_HIP(hipGetLastError());
+  return keep;
+}
+
+// Make stream `a` wait for the work already queued on stream `b`.
+static void stream_wait(hipStream_t a, hipStream_t b) {
+  if (a == b) return;
+  hipEvent_t e;
+  ZL_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  ZL_HIP(hipEventRecord(e, b));
+  ZL_HIP(hipStreamWaitEvent(a, e, 0));
+  ZL_HIP(hipEventDestroy(e));
+}
+
+static void dist_of_row(zl_sampler *s, zl_model *m, int row, const int32_t *hist, int nh, DevDist *out) {
+  ZL_REQUIRE(!m->closed, ZL_ERR_STATE, "model is closed");
+  ZL_REQUIRE(row >= 0 && row < m->logitsBatch, ZL_ERR_ARG, "logits row out of range");
+  ensure_scratch(s, m->cfg.vocab);
+  const int keep = upload_hist(s, m->st, hist, nh);
+  launch_dist_rows(m->logits + (size_t)row * m->cfg.vocab, m->cfg.vocab, 1, m->cfg.vocab, s->sp, keep ? s->dhist : nullptr, keep, 0,
+                   s->scratch, out, m->st);
+}
+
+// ---------------------------------------------------------------------------------------------- speculative cycle
+static void spec_cycle(zl_model *T, zl_model *D, zl_sampler *s, const int32_t *feed, int nFeed, int pending, int kk,
+                       const int32_t *stopIds, int nStop, const int32_t *hist, int nh, zl_spec_result *out) {
+  ZL_REQUIRE(!T->closed && !D->closed, ZL_ERR_STATE, "model is closed");
+  ZL_REQUIRE(T->cfg.vocab == D->cfg.vocab, ZL_ERR_ARG, "draft vocabulary differs from the target's");
+  ZL_REQUIRE(kk >= 0 && kk <= 63 && kk + 1 <= T->logitsBatch && kk + 1 <= T->maxBatch, ZL_ERR_BATCH, "kk + 1 exceeds the target's verify limit");
+  ZL_REQUIRE(nStop >= 0 && nStop <= 64, ZL_ERR_ARG, "at most 64 stop ids");
+  ZL_REQUIRE(pending >= 0 && pending < T->cfg.vocab, ZL_ERR_TOKEN, "token id " + std::to_string(pending) + " out of range");
+  ZL_REQUIRE((int)T->tokens.size() + kk + 1 <= T->ctx, ZL_ERR_CONTEXT, "context full (" + std::to_string(T->ctx) + " tokens)");
+  if (kk > 0) {
+    ZL_REQUIRE(nFeed >= 1, ZL_ERR_ARG, "the draft must be fed at least the pending token");
+    ZL_REQUIRE((int)D->tokens.size() + nFeed + kk - 1 <= D->ctx, ZL_ERR_CONTEXT, "context full (" + std::to_string(D->ctx) + " tokens)");
+    for (int i = 0; i < nFeed; i++) ZL_REQUIRE(feed[i] >= 0 && feed[i] < D->cfg.vocab, ZL_ERR_TOKEN, "token id " + std::to_string(feed[i]) + " out of range");
+  }
+  ensure_scratch(s, T->cfg.vocab);
+  // everything runs on the target's stream, in order
+  hipStream_t st = T->st;
+  stream_wait(st, D->st);
+  stream_wait(st, s->st);
+  hipStream_t dst = D->st;
+  D->st = st;  // draft graphs launch on this stream for the cycle (graphs do not bind a stream)
+  struct Restore { zl_model *D; hipStream_t s; ~Restore() { D->st = s; } } restore{D, dst};
+  hipEvent_t e0, e1;
+  ZL_HIP(hipEventCreate(&e0));
+  ZL_HIP(hipEventCreate(&e1));
+  struct EvFree { hipEvent_t a, b; ~EvFree() { hipEventDestroy(a); hipEventDestroy(b); } } evf{e0, e1};
+  ZL_HIP(hipEventRecord(e0, st));
+  // target verify step: [pending, x_1..x_kk] at the target's position; drafts are written by the draws
+  {
+    Step h;
+    memset(&h, 0, sizeof(h));
+    h.pos0 = (int)T->tokens.size(); h.B = kk + 1; h.tokens[0] = pending;
+    hipLaunchKernelGGL(k_set_step, dim3(1), dim3(64), 0, st, T->dstep, h);
+  }
+  hipLaunchKernelGGL(k_spec_reset, dim3(1), dim3(64), 0, st, s->ss);
+  const int keep = upload_hist(s, st, hist, nh);
+  {
+    StopArgs sa;
+    sa.n = nStop;
+    for (int i = 0; i < nStop; i++) sa.ids[i] = stopIds[i];
+    if (nStop) hipLaunchKernelGGL(k_set_stop, dim3(1), dim3(64), 0, st, s->dstop, sa);
+  }
+  ZL_HIP(hipGetLastError());
+  const int *dh = s->sp.penalized ? s->dhist : nullptr;
+  if (kk > 0) {
+    // feedLogits (src/model/speculative.js:51-61): chunks of maxBatch, logits of the last one
+    int lastChunk = 1;
+    for (int i = 0; i < nFeed;) {
+      int c = std::min(D->maxBatch, nFeed - i);
+      bool last = i + c == nFeed;
+      check_batch(D, feed + i, c, last ? 1 : 0);
+      set_step(D, (int)D->tokens.size(), feed + i, c);
+      launch_pass(D, c, last ? 1 : 0);
+      for (int t = 0; t < c; t++) D->tokens.push_back(feed[i + t]);
+      lastChunk = c;
+      i += c;
+    }
+    for (int j = 0; j < kk; j++) {
+      launch_dist_rows(D->logits, D->cfg.vocab, 1, D->cfg.vocab, s->sp, dh, keep + j, 0, s->scratch, s->qdist + j, st);
+      launch_draft_draw(s->qdist + j, s->ss, j, s->dstop, nStop, D->dstep, j == 0 ? lastChunk : 1, T->dstep, s->dhist, keep, st);
+      if (j < kk - 1) launch_pass(D, 1, 1);
+    }
+  }
+  launch_pass(T, kk + 1, 2);
+  launch_dist_rows(T->logits, T->cfg.vocab, kk + 1, T->cfg.vocab, s->sp, dh, keep, 1, s->scratch, s->pdist, st);
+  launch_accept(s->pdist, s->qdist, s->ss, (s->sp.temperature <= 0.0 || s->sp.greedyArgmax) ? 1 : 0, st);
+  ZL_HIP(hipEventRecord(e1, st));
+  ZL_HIP(hipMemcpyAsync(s->hss, s->ss, sizeof(SpecState), hipMemcpyDeviceToHost, st));
+  ZL_HIP(hipStreamSynchronize(st));
+  collect_probe(T);
+  const SpecState &r = *s->hss;
+  const int kkA = kk > 0 ? r.kk : 0;
+  out->kk = kkA;
+  out->accepted = r.a;
+  out->token = r.tok;
+  for (int j = 0; j < kkA; j++) out->drafted[j] = r.drafted[j];
+  float ms = 0;
+  ZL_HIP(hipEventElapsedTime(&ms, e0, e1));
+  out->ms_total = ms;
+  // bookkeeping as the reference's calls leave it: the draft processed x_1..x_{kk-1} (the last draft is not fed,
+  // nor anything after a stop token); the target processed [pending, x_1..x_kk]
+  for (int j = 0; j + 1 < kkA; j++) D->tokens.push_back(r.drafted[j]);
+  T->tokens.push_back(pending);
+  for (int j = 0; j < kkA; j++) T->tokens.push_back(r.drafted[j]);
+}
+
+}  // namespace zl
+
+// ================================================================================================ C ABI
+using namespace zl;
+
+#define ZL_API_BEGIN try {
+#define ZL_API_END                              \
+  g_err.clear();                                \
+  return ZL_OK;                                 \
+  }                                             \
+  catch (const zl::Error &e) {                  \
+    g_err = e.what();                           \
+    return e.code;                              \
+  }                                             \
+  catch (const std::exception &e) {             \
+    g_err = e.what();                           \
+    return ZL_ERR_HIP;                          \
+  }
+
+extern "C" {
+
+const char *zl_last_error(void) { return g_err.c_str(); }
+
+int zl_init(int device) {
+  ZL_API_BEGIN
+  int n = 0;
+  ZL_HIP(hipGetDeviceCount(&n));
+  ZL_REQUIRE(device >= 0 && device < n, ZL_ERR_ARG, "no such GPU: " + std::to_string(device));
+  ZL_HIP(hipSetDevice(device));
+  g_device = device;
+  ZL_API_END
+}
+
+int zl_device_query(zl_device_info *out) {
+  ZL_API_BEGIN
+  ensure_init();
+  hipDeviceProp_t p;
+  ZL_HIP(hipGetDeviceProperties(&p, g_device));
+  memset(out, 0, sizeof(*out));
+  snprintf(out->name, sizeof(out->name), "%s", p.gcnArchName);
+  out->compute_units = p.multiProcessorCount;
+  out->hbm_bytes = (int64_t)p.totalGlobalMem;
+  out->lds_per_block = (int)p.sharedMemPerBlock;
+  out->clock_khz = p.clockRate;
+  out->mem_clock_khz = p.memoryClockRate;
+  out->mem_bus_width = p.memoryBusWidth;
+  ZL_API_END
+}
+
+int zl_model_load(const char *path, const zl_model_opts *opts, zl_model **out) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(path && out, ZL_ERR_ARG, "null argument");
+  ensure_init();
+  *out = load_gguf(path, opts);
+  ZL_API_END
+}
+
+int zl_model_synth(const zl_config *cfg, const zl_synth_tensor *tensors, int n, const zl_model_opts *opts, zl_model **out) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(cfg && tensors && out && n > 0, ZL_ERR_ARG, "null argument");
+  ensure_init();
+  *out = build_synth(cfg, tensors, n, opts);
+  ZL_API_END
+}
+
+int zl_model_config(const zl_model *m, zl_config *out) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(m && out, ZL_ERR_ARG, "null argument");
+  *out = m->cfg;
+  ZL_API_END
+}
+
+int zl_model_info_get(const zl_model *m, zl_model_info *out) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(m && out, ZL_ERR_ARG, "null argument");
+  out->ctx = m->ctx; out->max_batch = m->maxBatch; out->logits_batch = m->logitsBatch; out->kv_f16 = m->kvF16;
+  out->weight_bytes = m->weightBytes; out->device_bytes = m->ar.bytes;
+  ZL_API_END
+}
+
+int zl_model_free(zl_model *m) {
+  ZL_API_BEGIN
+  delete m;
+  ZL_API_END
+}
+
+int zl_forward(zl_model *m, const int32_t *tokens, int n, int logits_mode, float *host_logits) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(m && tokens, ZL_ERR_ARG, "null argument");
+  ZL_REQUIRE(logits_mode >= 0 && logits_mode <= 2, ZL_ERR_ARG, "logits_mode must be 0, 1 or 2");
+  forward(m, tokens, n, logits_mode);
+  if (host_logits && logits_mode) {
+    size_t rows = logits_mode == 2 ? (size_t)n : 1;
+    ZL_HIP(hipMemcpyAsync(host_logits, m->logits, rows * m->cfg.vocab * 4, hipMemcpyDeviceToHost, m->st));
+  }
+  if (host_logits || m->lastLaunchHadProbe) {
+    ZL_HIP(hipStreamSynchronize(m->st));
+    collect_probe(m);
+  }
+  ZL_API_END
+}
+
+int zl_model_logits(const zl_model *m, int row0, int nrows, float *host_out) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(m && host_out, ZL_ERR_ARG, "null argument");
+  ZL_REQUIRE(row0 >= 0 && nrows >= 0 && row0 + nrows <= m->logitsBatch, ZL_ERR_ARG, "logits rows out of range");
+  ZL_HIP(hipMemcpyAsync(host_out, m->logits + (size_t)row0 * m->cfg.vocab, (size_t)nrows * m->cfg.vocab * 4, hipMemcpyDeviceToHost, m->st));
+  ZL_HIP(hipStreamSynchronize(m->st));
+  ZL_API_END
+}
+
+int zl_truncate(zl_model *m, int n) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(m, ZL_ERR_ARG, "null argument");
+  if (n < 0) n = 0;
+  if (n < (int)m->tokens.size()) m->tokens.resize(n);
+  ZL_API_END
+}
+
+int zl_mark_rollback(zl_model *m) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(m, ZL_ERR_ARG, "null argument");
+  ZL_API_END
+}
+
+int zl_reset(zl_model *m) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(m, ZL_ERR_ARG, "null argument");
+  m->tokens.clear();
+  ZL_API_END
+}
+
+int zl_model_pos(const zl_model *m) { return m ? (int)m->tokens.size() : -1; }
+
+int zl_model_tokens(const zl_model *m, int32_t *out, int cap) {
+  if (!m) return -1;
+  int n = (int)m->tokens.size();
+  for (int i = 0; i < n && i < cap; i++) out[i] = m->tokens[i];
+  return n;
+}
+
+int zl_synth_tensor_bytes(const zl_synth_tensor *t, int use_device, void *host_out) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(t && host_out, ZL_ERR_ARG, "null argument");
+  if (t->fill) {
+    for (int64_t i = 0; i < t->rows * t->cols; i++) ((float *)host_out)[i] = t->fill_value;
+    return ZL_OK;
+  }
+  const int bv = zl_synth::block_values(t->type), bb = zl_synth::block_bytes(t->type);
+  ZL_REQUIRE(bv > 0 && t->cols % bv == 0, ZL_ERR_UNSUPPORTED, "unsupported synthetic tensor type/shape");
+  const int64_t nbr = t->cols / bv;
+  const size_t bytes = (size_t)(t->rows * nbr) * bb;
+  const uint64_t src = (uint64_t)(t->src_cols > 0 ? t->src_cols : t->cols);
+  if (use_device) {
+    ensure_init();
+    uint8_t *d = nullptr;
+    ZL_HIP(hipMalloc(&d, bytes));
+    struct F { uint8_t *d; ~F() { hipFree(d); } } fr{d};
+    launch_synth(t->type, t->seed, t->std, src, (uint64_t)t->col0, (int)t->rows, (int)t->cols, d, nullptr);
+    ZL_HIP(hipMemcpy(host_out, d, bytes, hipMemcpyDeviceToHost));
+  } else {
+    uint8_t *o = (uint8_t *)host_out;
+    const int64_t total = t->rows * nbr;
+    int nt = (int)std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    if (total < 4096) nt = 1;
+    std::vector<std::thread> th;
+    for (int w = 0; w < nt; w++) {
+      th.emplace_back([=]() {
+        for (int64_t i = total * w / nt; i < total * (w + 1) / nt; i++)
+          zl_synth::synth_block(t->type, t->seed, t->std, src, (uint64_t)t->col0, (uint64_t)(i / nbr), (uint64_t)(i % nbr), o + i * bb);
+      });
+    }
+    for (auto &x : th) x.join();
+  }
+  ZL_API_END
+}
+
+int zl_sampler_create(const zl_sampler_opts *opts, zl_sampler **out) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(opts && out, ZL_ERR_ARG, "null argument");
+  ensure_init();
+  *out = new_sampler(opts);
+  ZL_API_END
+}
+
+int zl_sampler_free(zl_sampler *s) {
+  ZL_API_BEGIN
+  delete s;
+  ZL_API_END
+}
+
+int zl_sampler_get_rng(zl_sampler *s, uint32_t *state) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(s && state, ZL_ERR_ARG, "null argument");
+  ZL_HIP(hipDeviceSynchronize());
+  ZL_HIP(hipMemcpy(state, &s->ss->rng, 4, hipMemcpyDeviceToHost));
+  ZL_API_END
+}
+
+int zl_sampler_set_rng(zl_sampler *s, uint32_t state) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(s, ZL_ERR_ARG, "null argument");
+  ZL_HIP(hipDeviceSynchronize());
+  hipLaunchKernelGGL(k_set_rng, dim3(1), dim3(64), 0, s->st, s->ss, state);
+  ZL_HIP(hipStreamSynchronize(s->st));
+  ZL_API_END
+}
+
+int zl_sample(zl_sampler *s, zl_model *m, int row, const int32_t *hist, int n_hist, int32_t *token) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(s && m && token, ZL_ERR_ARG, "null argument");
+  stream_wait(m->st, s->st);
+  dist_of_row(s, m, row, hist, n_hist, s->tmpdist);
+  launch_draw_one(s->tmpdist, &s->ss->rng, s->dtok, m->st);
+  ZL_HIP(hipMemcpyAsync(s->htok, s->dtok, 4, hipMemcpyDeviceToHost, m->st));
+  ZL_HIP(hipStreamSynchronize(m->st));
+  *token = s->htok[0];
+  ZL_API_END
+}
+
+int zl_distribution(zl_sampler *s, zl_model *m, int row, const int32_t *hist, int n_hist, int32_t *ids, double *probs,
+                    int cap, int *n, double *total, int *greedy) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(s && m && ids && probs && n && total && greedy, ZL_ERR_ARG, "null argument");
+  stream_wait(m->st, s->st);
+  dist_of_row(s, m, row, hist, n_hist, s->tmpdist);
+  ZL_HIP(hipMemcpyAsync(s->hdist, s->tmpdist, sizeof(DevDist), hipMemcpyDeviceToHost, m->st));
+  ZL_HIP(hipStreamSynchronize(m->st));
+  const DevDist &d = *s->hdist;
+  ZL_REQUIRE(d.n <= cap, ZL_ERR_ARG, "distribution capacity too small");
+  for (int i = 0; i < d.n; i++) { ids[i] = d.ids[i]; probs[i] = d.probs[i]; }
+  *n = d.n; *total = d.total; *greedy = d.greedy;
+  ZL_API_END
+}
+
+int zl_spec_cycle(zl_model *target, zl_model *draft, zl_sampler *s, const int32_t *feed, int n_feed, int32_t pending, int kk,
+                  const int32_t *stop_ids, int n_stop, const int32_t *hist, int n_hist, zl_spec_result *out) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(target && draft && s && out, ZL_ERR_ARG, "null argument");
+  spec_cycle(target, draft, s, feed, n_feed, pending, kk, stop_ids, n_stop, hist, n_hist, out);
+  ZL_API_END
+}
+
+// ---- kernel probes
+int zl_mat_upload(int type, const void *raw, int64_t rows, int64_t cols, zl_mat **out) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(raw && out && rows > 0 && cols > 0, ZL_ERR_ARG, "bad argument");
+  ensure_init();
+  int64_t rb = ggml_row_bytes(type, cols);
+  ZL_REQUIRE(rb > 0, ZL_ERR_UNSUPPORTED, "unsupported type/shape");
+  std::unique_ptr<zl_mat> m(new zl_mat());
+  ZL_HIP(hipStreamCreateWithFlags(&m->st, hipStreamNonBlocking));
+  uint8_t *d = nullptr;
+  ZL_HIP(hipMalloc(&d, (size_t)rb * rows));
+  struct F { uint8_t *d; ~F() { hipFree(d); } } fr{d};
+  ZL_HIP(hipMemcpy(d, raw, (size_t)rb * rows, hipMemcpyHostToDevice));
+  m->copies.push_back(make_mat(m->ar, type, (int)rows, (int)cols, d, m->st));
+  ZL_HIP(hipStreamSynchronize(m->st));
+  *out = m.release();
+  ZL_API_END
+}
+
+int zl_mat_synth(int type, int64_t rows, int64_t cols, uint64_t seed, double stdv, int copies, zl_mat **out) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(out && rows > 0 && cols > 0 && copies >= 1, ZL_ERR_ARG, "bad argument");
+  ensure_init();
+  int64_t rb = ggml_row_bytes(type, cols);
+  ZL_REQUIRE(rb > 0 && zl_synth::block_values(type) > 0, ZL_ERR_UNSUPPORTED, "unsupported type/shape");
+  std::unique_ptr<zl_mat> m(new zl_mat());
+  ZL_HIP(hipStreamCreateWithFlags(&m->st, hipStreamNonBlocking));
+  uint8_t *d = nullptr;
+  ZL_HIP(hipMalloc(&d, (size_t)rb * rows));
+  struct F { uint8_t *d; ~F() { hipFree(d); } } fr{d};
+  for (int c = 0; c < copies; c++) {
+    launch_synth(type, seed + (uint64_t)c * 0x9E3779B97F4A7C15ull, stdv, (uint64_t)cols, 0, (int)rows, (int)cols, d, m->st);
+    m->copies.push_back(make_mat(m->ar, type, (int)rows, (int)cols, d, m->st));
+    ZL_HIP(hipStreamSynchronize(m->st));
+  }
+  *out = m.release();
+  ZL_API_END
+}
+
+int zl_mat_free(zl_mat *m) {
+  ZL_API_BEGIN
+  delete m;
+  ZL_API_END
+}
+
+int zl_mat_dequant(zl_mat *m, int64_t row0, int64_t nrows, float *out) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(m && out && row0 >= 0 && nrows > 0 && row0 + nrows <= m->copies[0].rows, ZL_ERR_ARG, "bad argument");
+  const DevMat &mm = m->copies[0];
+  std::vector<int> ids(nrows);
+  for (int64_t i = 0; i < nrows; i++) ids[i] = (int)(row0 + i);
+  int *dids = nullptr;
+  float *dout = nullptr;
+  ZL_HIP(hipMalloc(&dids, nrows * 4));
+  ZL_HIP(hipMalloc(&dout, (size_t)nrows * mm.nslab * 64 * 4));
+  struct F { int *a; float *b; ~F() { hipFree(a); hipFree(b); } } fr{dids, dout};
+  ZL_HIP(hipMemcpy(dids, ids.data(), nrows * 4, hipMemcpyHostToDevice));
+  launch_dequant_rows(view(mm), dids, (int)nrows, dout, mm.cols, m->st);
+  ZL_HIP(hipStreamSynchronize(m->st));
+  ZL_HIP(hipMemcpy(out, dout, (size_t)nrows * mm.cols * 4, hipMemcpyDeviceToHost));
+  ZL_API_END
+}
+
+// activations for probes: quantise M rows of x (host) on the device
+struct ProbeAct {
+  Arena ar;
+  Act act{};
+  float *x = nullptr;
+};
+static void probe_act(ProbeAct &pa, const float *x, int64_t K, int M, hipStream_t st) {
+  const int ld = pad64((int)K);
+  pa.act.ld = ld;
+  pa.act.q = (int8_t *)pa.ar.alloc((size_t)M * ld);
+  pa.act.d = (float *)pa.ar.alloc((size_t)M * (ld / 32) * 4);
+  pa.act.s = (int32_t *)pa.ar.alloc((size_t)M * (ld / 32) * 4);
+  pa.act.s16 = (int32_t *)pa.ar.alloc((size_t)M * (ld / 16) * 4);
+  pa.act.f = (float *)pa.ar.alloc((size_t)M * ld * 4);
+  pa.x = (float *)pa.ar.alloc((size_t)M * K * 4);
+  if (x) ZL_HIP(hipMemcpy(pa.x, x, (size_t)M * K * 4, hipMemcpyHostToDevice));
+  else launch_fill(pa.x, (long)M * K, 0.5f, st);
+  launch_norm_quant(pa.x, (int)K, 0, M, nullptr, 0.0, (int)K, ld, pa.act, st);
+}
+
+static void probe_gemv(const DevMat &mm, const Act &act, int M, float *y, hipStream_t st) {
+  GemvArgs a;
+  memset(&a, 0, sizeof(a));
+  a.nseg = 1;
+  a.seg[0].m = view(mm); a.seg[0].rows = mm.rows; a.seg[0].out = y; a.seg[0].ldo = mm.rows;
+  a.rows_total = mm.rows; a.nslab = mm.nslab; a.act = act; a.M = M; a.lpr = gemv_lpr(mm.nslab);
+  launch_gemv(a, EPI_STORE, act.f, act.ld, st);
+}
+
+int zl_mat_gemv(zl_mat *m, const float *x, int M, float *y) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(m && x && y && M >= 1 && M <= 64, ZL_ERR_ARG, "bad argument");
+  const DevMat &mm = m->copies[0];
+  ProbeAct pa;
+  struct R { ProbeAct *p; ~R() { p->ar.release(); } } rel{&pa};
+  probe_act(pa, x, mm.cols, M, m->st);
+  float *dy = (float *)pa.ar.alloc((size_t)M * mm.rows * 4);
+  probe_gemv(mm, pa.act, M, dy, m->st);
+  ZL_HIP(hipStreamSynchronize(m->st));
+  ZL_HIP(hipMemcpy(y, dy, (size_t)M * mm.rows * 4, hipMemcpyDeviceToHost));
+  ZL_API_END
+}
+
+int zl_mat_gemv_time(zl_mat *m, int M, int iters, float *ms_per_call) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(m && ms_per_call && M >= 1 && M <= 64 && iters >= 1, ZL_ERR_ARG, "bad argument");
+  const DevMat &m0 = m->copies[0];
+  ProbeAct pa;
+  struct R { ProbeAct *p; ~R() { p->ar.release(); } } rel{&pa};
+  probe_act(pa, nullptr, m0.cols, M, m->st);
+  float *dy = (float *)pa.ar.alloc((size_t)M * m0.rows * 4);
+  const int nc = (int)m->copies.size();
+  for (int i = 0; i < nc; i++) probe_gemv(m->copies[i], pa.act, M, dy, m->st);  // warm-up
+  hipEvent_t a, b;
+  ZL_HIP(hipEventCreate(&a));
+  ZL_HIP(hipEventCreate(&b));
+  struct E { hipEvent_t a, b; ~E() { hipEventDestroy(a); hipEventDestroy(b); } } ev{a, b};
+  ZL_HIP(hipEventRecord(a, m->st));
+  for (int i = 0; i < iters; i++) probe_gemv(m->copies[i % nc], pa.act, M, dy, m->st);
+  ZL_HIP(hipEventRecord(b, m->st));
+  ZL_HIP(hipEventSynchronize(b));
+  float ms = 0;
+  ZL_HIP(hipEventElapsedTime(&ms, a, b));
+  *ms_per_call = ms / iters;
+  ZL_API_END
+}
+
+int zl_quant_act(const float *x, int64_t K, int M, int8_t *q, float *d, int32_t *s) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(x && q && d && s && K > 0 && K % 32 == 0 && M >= 1, ZL_ERR_ARG, "bad argument");
+  ensure_init();
+  hipStream_t st;
+  ZL_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+  struct S { hipStream_t s; ~S() { hipStreamDestroy(s); } } ss{st};
+  ProbeAct pa;
+  struct R { ProbeAct *p; ~R() { p->ar.release(); } } rel{&pa};
+  probe_act(pa, x, K, M, st);
+  ZL_HIP(hipStreamSynchronize(st));
+  const int ld = pa.act.ld;
+  for (int t = 0; t < M; t++) {
+    ZL_HIP(hipMemcpy(q + t * K, pa.act.q + (size_t)t * ld, K, hipMemcpyDeviceToHost));
+    ZL_HIP(hipMemcpy(d + t * (K / 32), pa.act.d + (size_t)t * (ld / 32), (K / 32) * 4, hipMemcpyDeviceToHost));
+    ZL_HIP(hipMemcpy(s + t * (K / 32), pa.act.s + (size_t)t * (ld / 32), (K / 32) * 4, hipMemcpyDeviceToHost));
+  }
+  ZL_API_END
+}
+
+int zl_probe_set(zl_model *m, int layer, int which) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(m, ZL_ERR_ARG, "null argument");
+  ZL_REQUIRE(which >= -1 && which <= 4, ZL_ERR_ARG, "which must be -1..4");
+  ZL_HIP(hipStreamSynchronize(m->st));
+  for (auto &g : m->graphs) hipGraphExecDestroy(g.second);
+  for (auto &g : m->graphDefs) hipGraphDestroy(g.second);
+  m->graphs.clear();
+  m->graphDefs.clear();
+  m->probeLayer = layer;
+  m->probeWhich = which;
+  m->probeMs = 0;
+  m->probeCount = 0;
+  m->lastLaunchHadProbe = 0;
+  const Layer *L = (layer >= 0 && layer < (int)m->layers.size()) ? &m->layers[layer] : nullptr;
+  int64_t b = 0;
+  if (which == 4) b = mat_bytes(m->output);
+  else if (L) b = which == 0 ? mat_bytes(L->wq) : which == 1 ? mat_bytes(L->wo) : which == 2 ? mat_bytes(L->wgate) + mat_bytes(L->wup) : which == 3 ? mat_bytes(L->wdown) : 0;
+  m->probeBytes = b;
+  ZL_API_END
+}
+
+int zl_probe_read(zl_model *m, double *ms_total, int64_t *count, int64_t *bytes_per_launch) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(m && ms_total && count && bytes_per_launch, ZL_ERR_ARG, "null argument");
+  *ms_total = m->probeMs;
+  *count = m->probeCount;
+  *bytes_per_launch = m->probeBytes;
+  ZL_API_END
+}
+
+}  // extern "C"

@@ -1,0 +1,316 @@
+// On-device sampling for the speculative step: the sampler's distribution() and draw(), the draft's proposal draws,
+// and the acceptance test with residual / bonus draws, so that only accepted token ids leave the GPU.
+//
+// Semantics follow zerollm's createSampler (src/sampling/sampler.js:81-155), generateSpeculative's accept block
+// (src/model/speculative.js:192-209), probOf (:64-67) and drawResidual (:75-87). The f64 arithmetic after the
+// candidate selection is sequential in one lane, in the reference's order, so a seeded run consumes the same uniforms
+// and takes the same decisions as the reference given the same logits.
+#include "zl_kernels.h"
+
+namespace zl {
+
+// mulberry32 (src/util/rng.js:4-13)
+__device__ inline double rng_next(uint32_t &a) {
+  a = a + 0x6d2b79f5u;
+  uint32_t t = a;
+  t = (t ^ (t >> 15)) * (t | 1u);
+  t ^= t + (t ^ (t >> 7)) * (t | 61u);
+  return (double)(t ^ (t >> 14)) / 4294967296.0;
+}
+
+// Exact zerollm heap (src/sampling/sampler.js:21-43) for the rare case of ties at the k-th value: which of the tied
+// candidates survive depends on the heap's history, so it is replayed literally. One thread; out holds k entries.
+__device__ int heap_topk(const float *l, int n, int k, int *ids, double *vals) {
+  int size = 0;
+  for (int i = 0; i < n; i++) {
+    double v = (double)l[i];
+    if (size < k) {
+      ids[size] = i; vals[size] = v; size++;
+      int j = size - 1;
+      while (j > 0) {
+        int p = (j - 1) >> 1;
+        if (vals[j] >= vals[p]) break;
+        int ti = ids[j]; ids[j] = ids[p]; ids[p] = ti; double tv = vals[j]; vals[j] = vals[p]; vals[p] = tv;
+        j = p;
+      }
+    } else if (v > vals[0]) {
+      ids[0] = i; vals[0] = v;
+      int j = 0;
+      for (;;) {
+        int le = 2 * j + 1, ri = le + 1, m = j;
+        if (le < size && vals[le] < vals[m]) m = le;
+        if (ri < size && vals[ri] < vals[m]) m = ri;
+        if (m == j) break;
+        int ti = ids[j]; ids[j] = ids[m]; ids[m] = ti; double tv = vals[j]; vals[j] = vals[m]; vals[m] = tv;
+        j = m;
+      }
+    }
+  }
+  return size;
+}
+
+constexpr int DT = 1024;  // threads of the distribution kernel
+
+// distribution(logits row, history) for nrows rows (src/sampling/sampler.js:94-142).
+__global__ __launch_bounds__(DT) void k_dist_rows(const float *__restrict__ logits, int ldl, int vocab, SamplerParams sp,
+                                                 const int *hist, int histLen0, int histInc, float *scratch, DevDist *out) {
+  __shared__ uint32_t hcount[256];
+  __shared__ int s_ids[KCAP];
+  __shared__ double s_vals[KCAP];
+  __shared__ int o_ids[KCAP];
+  __shared__ double o_vals[KCAP];
+  __shared__ uint32_t s_prefix, s_mask, s_remaining, s_eqcount;
+  __shared__ int s_ncand;
+  __shared__ float s_bestv[DT / 64];
+  __shared__ int s_besti[DT / 64];
+  const int r = blockIdx.x, tid = threadIdx.x;
+  const float *l = logits + (long)r * ldl;
+  DevDist *D = out + r;
+  // ---- penalties on a private copy (the reference modifies and restores the caller's buffer)
+  const int hl = hist ? histLen0 + r * histInc : 0;
+  if (sp.penalized && hl > 0) {
+    float *cp = scratch + (long)r * vocab;
+    for (int i = tid; i < vocab; i += DT) cp[i] = l[i];
+    __syncthreads();
+    if (tid == 0) {
+      int start = hl - sp.repeatLastN;
+      if (start < 0) start = 0;
+      for (int i = start; i < hl; i++) {
+        int t = hist[i];
+        bool seen = false;
+        for (int j = start; j < i; j++) if (hist[j] == t) { seen = true; break; }
+        if (seen) continue;
+        int c = 0;
+        for (int j = i; j < hl; j++) c += hist[j] == t;
+        double lv = (double)cp[t];
+        double v = sp.repeatPenalty != 1.0 ? (lv > 0 ? lv / sp.repeatPenalty : lv * sp.repeatPenalty) : lv;
+        v -= (double)c * sp.frequency + sp.presence;
+        cp[t] = (float)v;
+      }
+    }
+    __syncthreads();
+    __threadfence_block();
+    l = cp;
+  }
+  // ---- greedy: first maximum (src/sampling/sampler.js:46-50)
+  if (sp.temperature <= 0.0 || sp.greedyArgmax) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = tid; i < vocab; i += DT) {
+      float v = l[i];
+      if (v > bv) { bv = v; bi = i; }
+    }
+    for (int o = 1; o < 64; o <<= 1) {
+      float ov = __shfl_xor(bv, o, 64);
+      int oi = __shfl_xor(bi, o, 64);
+      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if ((tid & 63) == 0) { s_bestv[tid >> 6] = bv; s_besti[tid >> 6] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+      float b = s_bestv[0];
+      int id = s_besti[0];
+      for (int w = 1; w < DT / 64; w++)
+        if (s_bestv[w] > b || (s_bestv[w] == b && s_besti[w] < id)) { b = s_bestv[w]; id = s_besti[w]; }
+      if (id == 0x7fffffff) id = 0;  // every logit NaN: the reference's argmax also returns 0
+      D->n = 1; D->greedy = 1; D->total = 1.0; D->ids[0] = id; D->probs[0] = 1.0;
+    }
+    return;
+  }
+  const int K = sp.topK;
+  // ---- radix select of the K-th largest key
+  if (tid == 0) { s_prefix = 0; s_mask = 0; s_remaining = (uint32_t)K; }
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = tid; i < 256; i += DT) hcount[i] = 0;
+    __syncthreads();
+    const uint32_t prefix = s_prefix, mask = s_mask;
+    for (int i = tid; i < vocab; i += DT) {
+      uint32_t k = fkey(l[i]);
+      if ((k & mask) == prefix) atomicAdd(&hcount[(k >> shift) & 255], 1u);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t rem = s_remaining, above = 0;
+      int d = 255;
+      for (; d > 0; d--) {
+        if (above + hcount[d] >= rem) break;
+        above += hcount[d];
+      }
+      s_remaining = rem - above;
+      s_eqcount = hcount[d];
+      s_prefix = prefix | ((uint32_t)d << shift);
+      s_mask = mask | (255u << shift);
+    }
+    __syncthreads();
+  }
+  const uint32_t T = s_prefix;
+  const bool tie = s_eqcount != s_remaining;
+  if (tid == 0) s_ncand = 0;
+  __syncthreads();
+  if (!tie) {
+    for (int i = tid; i < vocab; i += DT) {
+      uint32_t k = fkey(l[i]);
+      if (k >= T) {
+        int p = atomicAdd(&s_ncand, 1);
+        if (p < KCAP) { s_ids[p] = i; s_vals[p] = (double)l[i]; }
+      }
+    }
+  } else if (tid == 0) {
+    s_ncand = heap_topk(l, vocab, K, s_ids, s_vals);
+  }
+  __syncthreads();
+  const int m = min(s_ncand, K);
+  // ---- sort by value desc, id asc (rank sort)
+  for (int i = tid; i < m; i += DT) {
+    double vi = s_vals[i];
+    int ii = s_ids[i], rank = 0;
+    for (int j = 0; j < m; j++) {
+      double vj = s_vals[j];
+      rank += (vj > vi) || (vj == vi && s_ids[j] < ii);
+    }
+    o_ids[rank] = ii; o_vals[rank] = vi;
+  }
+  __syncthreads();
+  // ---- softmax with temperature, min-p, top-p (one lane, the reference's order)
+  if (tid == 0) {
+    double mx = o_vals[0], sum = 0;
+    for (int i = 0; i < m; i++) { double pr = exp((o_vals[i] - mx) / sp.temperature); D->probs[i] = pr; sum += pr; }
+    for (int i = 0; i < m; i++) D->probs[i] = D->probs[i] / sum;
+    int keep = m;
+    if (sp.minP > 0) {
+      double thr = sp.minP * D->probs[0];
+      keep = 1;
+      while (keep < m && D->probs[keep] >= thr) keep++;
+    }
+    if (sp.topP < 1) {
+      double c = 0;
+      int i = 0;
+      while (i < keep) { c += D->probs[i]; i++; if (c >= sp.topP) break; }
+      keep = i > 1 ? i : 1;
+    }
+    double total = 0;
+    for (int i = 0; i < keep; i++) total += D->probs[i];
+    for (int i = 0; i < keep; i++) D->ids[i] = o_ids[i];
+    D->n = keep; D->greedy = 0; D->total = total;
+  }
+}
+
+// draw(dist) (src/sampling/sampler.js:145-151)
+__device__ inline int draw_dist(const DevDist &d, uint32_t &rng) {
+  if (d.greedy) return d.ids[0];
+  double r = rng_next(rng) * d.total;
+  for (int i = 0; i < d.n; i++) {
+    r -= d.probs[i];
+    if (r <= 0) return d.ids[i];
+  }
+  return d.ids[d.n - 1];
+}
+
+// probOf (src/model/speculative.js:64-67)
+__device__ inline double prob_of(const DevDist &d, int id) {
+  for (int i = 0; i < d.n; i++) if (d.ids[i] == id) return d.probs[i] / d.total;
+  return 0.0;
+}
+
+// drawResidual (src/model/speculative.js:75-87); the dense scratch of the reference is a lookup into q's support
+__device__ int draw_residual(const DevDist &p, const DevDist &q, uint32_t &rng) {
+  double res[KCAP];
+  double sum = 0;
+  for (int i = 0; i < p.n; i++) {
+    double qv = 0.0;
+    for (int j = 0; j < q.n; j++) if (q.ids[j] == p.ids[i]) { qv = q.probs[j] / q.total; break; }
+    double v = p.probs[i] / p.total - qv;
+    res[i] = 0.0;
+    if (v > 0) { res[i] = v; sum += v; }
+  }
+  if (!(sum > 0)) return draw_dist(p, rng);
+  double r = rng_next(rng) * sum;
+  int last = 0;
+  for (int i = 0; i < p.n; i++) {
+    if (res[i] > 0) {
+      last = i;
+      r -= res[i];
+      if (r <= 0) return p.ids[i];
+    }
+  }
+  return p.ids[last];
+}
+
+// Draft proposal j (src/model/speculative.js:169-177): draw x_j from the draft's distribution, record it, stop after a
+// stop token (later calls in the same cycle do nothing, as the reference's loop has ended), and make x_j the next
+// draft input and the (j+1)-th verify token.
+__global__ void k_draft_draw(const DevDist *dist, SpecState *ss, int j, const int *stopIds, int nStop, Step *draftStep,
+                             int advance, Step *targetStep, int *hist, int histLen0) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  if (ss->stopped) return;
+  uint32_t rng = ss->rng;
+  int x = draw_dist(*dist, rng);
+  ss->rng = rng;
+  ss->drafted[j] = x;
+  ss->kk = j + 1;
+  for (int i = 0; i < nStop; i++) if (stopIds[i] == x) ss->stopped = 1;
+  draftStep->tokens[0] = x;
+  draftStep->pos0 += advance;
+  draftStep->B = 1;
+  targetStep->tokens[1 + j] = x;
+  if (hist) hist[histLen0 + j] = x;
+}
+
+// Acceptance (src/model/speculative.js:192-209): greedy compare, or accept with probability min(1, p/q) and on the first
+// rejection draw from the residual; when every draft is accepted the bonus token comes from the last row.
+__global__ void k_accept(const DevDist *pdist, const DevDist *qdist, SpecState *ss, int greedy) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  uint32_t rng = ss->rng;
+  const int kk = ss->kk;
+  int a = 0, tok = -1;
+  for (int j = 0; j < kk; j++) {
+    const DevDist &P = pdist[j];
+    const int x = ss->drafted[j];
+    if (greedy) {
+      int t = P.ids[0];
+      if (t == x) { a++; continue; }
+      tok = t;
+      break;
+    }
+    double px = prob_of(P, x), qx = prob_of(qdist[j], x);
+    if (rng_next(rng) * qx < px) { a++; continue; }
+    tok = draw_residual(P, qdist[j], rng);
+    break;
+  }
+  if (a == kk) tok = draw_dist(pdist[kk], rng);
+  ss->a = a;
+  ss->tok = tok;
+  ss->rng = rng;
+}
+
+__global__ void k_draw_one(const DevDist *dist, uint32_t *rng, int *out) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  uint32_t s = *rng;
+  *out = draw_dist(*dist, s);
+  *rng = s;
+}
+
+void launch_dist_rows(const float *logits, int ldl, int nrows, int vocab, const SamplerParams &sp, const int *hist,
+                      int histLen0, int histInc, float *scratch, DevDist *out, hipStream_t st) {
+  hipLaunchKernelGGL(k_dist_rows, dim3(nrows), dim3(DT), 0, st, logits, ldl, vocab, sp, hist, histLen0, histInc, scratch, out);
+  ZL_HIP(hipGetLastError());
+}
+
+void launch_draft_draw(const DevDist *dist, SpecState *ss, int j, const int *stopIds, int nStop, Step *draftStep,
+                       int advance, Step *targetStep, int *hist, int histLen0, hipStream_t st) {
+  hipLaunchKernelGGL(k_draft_draw, dim3(1), dim3(64), 0, st, dist, ss, j, stopIds, nStop, draftStep, advance, targetStep,
+                     hist, histLen0);
+  ZL_HIP(hipGetLastError());
+}
+
+void launch_accept(const DevDist *pdist, const DevDist *qdist, SpecState *ss, int greedy, hipStream_t st) {
+  hipLaunchKernelGGL(k_accept, dim3(1), dim3(64), 0, st, pdist, qdist, ss, greedy);
+  ZL_HIP(hipGetLastError());
+}
+
+void launch_draw_one(const DevDist *dist, uint32_t *rng, int *out, hipStream_t st) {
+  hipLaunchKernelGGL(k_draw_one, dim3(1), dim3(64), 0, st, dist, rng, out);
+  ZL_HIP(hipGetLastError());
+}
+
+}  // namespace zl
