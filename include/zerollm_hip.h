@@ -145,6 +145,7 @@ typedef struct {
   int token;       /* correction (first rejection) or bonus token */
   int32_t drafted[64];
   float ms_total;  /* device time of the cycle */
+  float ms_draft;  /* device time of the draft phase (feed + proposals); the rest is verification + acceptance */
 } zl_spec_result;
 
 /* One cycle of generateSpeculative (src/model/speculative.js:155-209) on the GPU: feed `feed` to the draft
@@ -174,10 +175,11 @@ int zl_mat_gemv_time(zl_mat *m, int M, int iters, float *ms_per_call);
 int zl_quant_act(const float *x, int64_t K, int M, int8_t *q, float *d, int32_t *s);
 
 /* ---------------------------------------------------------------------------------------------- timing probe */
-/* Events around one GEMV launch inside the captured forward graph (layer `layer`, which: 0 qkv, 1 wo, 2 gate+up,
- * 3 down, 4 output head); graphs are rebuilt. zl_probe_read returns the accumulated ms and launch count. */
-int zl_probe_set(zl_model *m, int layer, int which);
-int zl_probe_read(zl_model *m, double *ms_total, int64_t *count, int64_t *bytes_per_launch);
+/* Mean duration of `iters` back-to-back launches of one GEMV of the forward pass (which: 0 first q/k/v group, 1 wo,
+ * 2 gate+up, 3 down, 4 output head) with M tokens, cycling through the layers' weights, timed with HIP events on the
+ * model's stream; also the weight bytes one launch streams. Measurement aid (the reference times its kernels with
+ * tools/kbench.mjs). */
+int zl_probe_gemv(zl_model *m, int which, int M, int iters, float *ms_per_launch, int64_t *bytes_per_launch);
 
 #ifdef __cplusplus
 }

@@ -328,3 +328,37 @@ class OracleModel:
             self.close()
         except Exception:
             pass
+
+
+class ArraySource:
+    """A GGUF-like view (get / tensor / data / floats) over in-memory raw tensors of a synthetic model spec
+    (zerollm_amd.synth.ModelSpec), so the oracle can run a model that only exists in memory."""
+
+    class _T:
+        def __init__(self, name, type_, dims):
+            self.name, self.type, self.dims = name, type_, dims
+
+    def __init__(self, spec, arrays):
+        a = spec.arch
+        self.meta = {
+            "general.architecture": a, f"{a}.embedding_length": spec.n_embd, f"{a}.attention.head_count": spec.n_head,
+            f"{a}.attention.head_count_kv": spec.n_head_kv, f"{a}.attention.key_length": spec.head_dim,
+            f"{a}.vocab_size": spec.vocab, f"{a}.block_count": spec.n_layer, f"{a}.feed_forward_length": spec.n_ff,
+            f"{a}.rope.dimension_count": spec.head_dim, f"{a}.context_length": spec.ctx_train,
+            f"{a}.attention.layer_norm_rms_epsilon": float(np.float32(spec.rms_eps)),
+            f"{a}.rope.freq_base": float(np.float32(spec.rope_base)),
+        }
+        self.arrays = arrays
+        self.tensors = {t.name: self._T(t.name, t.type, t.dims) for t in spec.tensors}
+
+    def get(self, k, default=None):
+        return self.meta.get(k, default)
+
+    def tensor(self, name):
+        return self.tensors.get(name)
+
+    def data(self, name):
+        return self.arrays[name]
+
+    def floats(self, name):
+        return self.arrays[name].view(np.float32)

@@ -53,7 +53,8 @@ class zl_sampler_opts(C.Structure):
 
 
 class zl_spec_result(C.Structure):
-    _fields_ = [("kk", C.c_int), ("accepted", C.c_int), ("token", C.c_int), ("drafted", C.c_int32 * 64), ("ms_total", C.c_float)]
+    _fields_ = [("kk", C.c_int), ("accepted", C.c_int), ("token", C.c_int), ("drafted", C.c_int32 * 64), ("ms_total", C.c_float),
+                ("ms_draft", C.c_float)]
 
 
 P = C.c_void_p
@@ -93,8 +94,7 @@ SIGNATURES = [
     ("zl_mat_gemv", C.c_int, [P, F32P, C.c_int, F32P]),
     ("zl_mat_gemv_time", C.c_int, [P, C.c_int, C.c_int, F32P]),
     ("zl_quant_act", C.c_int, [F32P, C.c_int64, C.c_int, C.POINTER(C.c_int8), F32P, I32P]),
-    ("zl_probe_set", C.c_int, [P, C.c_int, C.c_int]),
-    ("zl_probe_read", C.c_int, [P, F64P, C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
+    ("zl_probe_gemv", C.c_int, [P, C.c_int, C.c_int, C.c_int, F32P, C.POINTER(C.c_int64)]),
 ]
 
 _lib = None

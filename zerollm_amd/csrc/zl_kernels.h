@@ -81,9 +81,10 @@ struct AttnArgs {
   Act act;
 };
 
-int gemv_lpr(int nslab);
+int gemv_lpr(int rows, int nslab);
 void launch_gemv(const GemvArgs &a, int epi, const float *xf, int ldx, hipStream_t st);
 void launch_attention(const AttnArgs &a, int B, int ctxMax, int hpb, hipStream_t st);
+size_t attention_lds(int hpb, int hd, int pstride);
 void launch_norm_quant(const float *x, int ldx, int row0, int nrows, const float *w, double eps, int n, int npad,
                        const Act &act, hipStream_t st);
 void launch_rope(const RopeArgs &a, int B, hipStream_t st);

@@ -220,12 +220,15 @@ __device__ inline void quant_block32(float v, int i, int8_t *xq, float *xd, int3
   if ((i & 31) == 0) { xd[i >> 5] = (float)scale; xs[i >> 5] = s32; }
 }
 
-// RMSNorm (optional) + quantisation of rows x[row0 + blockIdx.x] (length n) into activation row blockIdx.x
-// (length npad >= n, zero padded). rmsnorm: s = 1/sqrt(mean(x^2) + eps), xb = x*s*w (src/compute/ref-kernels.js:305-310).
+// RMSNorm (optional) + quantisation of rows x[row0 + blockIdx.y] (length n) into activation row blockIdx.y (length
+// npad >= n, zero padded). rmsnorm: s = 1/sqrt(mean(x^2) + eps), xb = x*s*w (src/compute/ref-kernels.js:305-310).
+// Block blockIdx.x quantises elements [512*blockIdx.x, +512); every block of a row computes the same sum of squares
+// (same order), so they all use the same s.
+constexpr int NQ_CHUNK = 512;
 __global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x, int ldx, int row0, const float *__restrict__ w,
                                                     double eps, int n, int npad, Act act) {
   __shared__ double red[4];
-  const int b = blockIdx.x, tid = threadIdx.x;
+  const int b = blockIdx.y, tid = threadIdx.x;
   const float *xr = x + (long)(row0 + b) * ldx;
   double s = 1.0;
   if (w) {
@@ -241,7 +244,8 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x,
   float *xd = act.d + (long)b * (act.ld >> 5);
   int32_t *xs = act.s + (long)b * (act.ld >> 5);
   int32_t *xs16 = act.s16 + (long)b * (act.ld >> 4);
-  for (int i = tid; i < npad; i += 256) {
+  const int c0 = blockIdx.x * NQ_CHUNK, c1 = min(npad, c0 + NQ_CHUNK);
+  for (int i = c0 + tid; i < c1; i += 256) {
     float v = 0.f;
     if (i < n) v = w ? (float)((double)xr[i] * s * (double)w[i]) : xr[i];
     if (act.f) act.f[(long)b * act.ld + i] = v;
@@ -256,212 +260,247 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x,
 // arithmetic does not depend on M, so a batched pass gives the same bits as token-by-token passes. Int8 activations
 // of MT tokens are staged in LDS one K-window at a time (window = multiple of 64*lpr, so the slab order is kept).
 
+constexpr int GEMV_LDS_MAX = 96 * 1024;  // staged activations per block (MT tokens x K-window int8)
+constexpr int GEMV_MAX_BLOCKS = 1024;     // row-pair blocks beyond this stride over the rows
+
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // weights are read once per pass: non-temporal loads keep them from displacing activations in the caches
 __device__ inline u32x4 ldnt4(const void *p) { return __builtin_nontemporal_load((const u32x4 *)p); }
 __device__ inline u32x2 ldnt2(const void *p) { return __builtin_nontemporal_load((const u32x2 *)p); }
 
-template <int FMT>
-struct Slab {
-  uint32_t w[16];  // 64 unsigned/signed 8-bit values, slab order
+// Raw planes of one slab as loaded (unpacked only when used, so the next slab's loads stay in flight meanwhile).
+struct SlabRaw {
+  uint32_t L[16];  // Q8_0: 16 words of int8; others: 8 words of nibbles
+  uint32_t H[4];   // Q5_0/Q5_K: 2 words of 5th bits; Q6_K: 4 words of top-2 bits
   uint32_t scw;    // scale codes (K-quants)
-  float d0, d1;    // Q8_0/Q4_0/Q5_0: block scales; Q4_K/Q5_K: d, dmin; Q6_K: d
+  uint32_t dw;     // f16 scales: (d0 | d1 << 16) for Q8_0/Q4_0/Q5_0, (d | dmin << 16) for Q4_K/Q5_K, d for Q6_K
 };
 
 template <int FMT>
-__device__ inline void load_slab(const MatView &m, long idx, int r, int s, Slab<FMT> &o) {
+__device__ inline void load_raw(const MatView &m, long idx, int r, int s, SlabRaw &o) {
   if (FMT == T_Q8_0) {
     const uint8_t *p = m.qs + idx * 64;
     #pragma unroll
-    for (int i = 0; i < 4; i++) { u32x4 v = ldnt4(p + 16 * i); o.w[4 * i] = v.x; o.w[4 * i + 1] = v.y; o.w[4 * i + 2] = v.z; o.w[4 * i + 3] = v.w; }
-    uint32_t dw = __builtin_nontemporal_load((const uint32_t *)(m.dd + idx * 2));
-    o.d0 = h2f(dw & 0xffff); o.d1 = h2f(dw >> 16);
+    for (int i = 0; i < 4; i++) { u32x4 v = ldnt4(p + 16 * i); o.L[4 * i] = v.x; o.L[4 * i + 1] = v.y; o.L[4 * i + 2] = v.z; o.L[4 * i + 3] = v.w; }
+    o.dw = __builtin_nontemporal_load((const uint32_t *)(m.dd + idx * 2));
     return;
   }
   const uint8_t *p = m.qs + idx * 32;
   u32x4 a = ldnt4(p), b = ldnt4(p + 16);
-  uint32_t L[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  if (FMT == T_Q4_0 || FMT == T_Q4_K || FMT == T_Q5_0 || FMT == T_Q5_K) {
-    #pragma unroll
-    for (int i = 0; i < 8; i++) { o.w[i] = L[i] & 0x0F0F0F0Fu; o.w[8 + i] = (L[i] >> 4) & 0x0F0F0F0Fu; }
-    if (FMT == T_Q5_0 || FMT == T_Q5_K) {
-      u32x2 h = ldnt2(m.qx + idx * 8);
-      #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        o.w[i] |= (((h.x >> (4 * i)) & 15u) * 0x00204081u & 0x01010101u) << 4;
-        o.w[8 + i] |= (((h.y >> (4 * i)) & 15u) * 0x00204081u & 0x01010101u) << 4;
-      }
-    }
-    if (FMT == T_Q4_0 || FMT == T_Q5_0) {
-      uint32_t dw = __builtin_nontemporal_load((const uint32_t *)(m.dd + idx * 2));
-      o.d0 = h2f(dw & 0xffff); o.d1 = h2f(dw >> 16);
-    } else {
-      o.scw = __builtin_nontemporal_load((const uint32_t *)(m.sc + idx * 4));
-      uint32_t dw = __builtin_nontemporal_load((const uint32_t *)(m.dd + ((long)r * (m.nslab >> 2) + (s >> 2)) * 2));
-      o.d0 = h2f(dw & 0xffff); o.d1 = h2f(dw >> 16);
-    }
-    return;
+  o.L[0] = a.x; o.L[1] = a.y; o.L[2] = a.z; o.L[3] = a.w; o.L[4] = b.x; o.L[5] = b.y; o.L[6] = b.z; o.L[7] = b.w;
+  if (FMT == T_Q5_0 || FMT == T_Q5_K) { u32x2 h = ldnt2(m.qx + idx * 8); o.H[0] = h.x; o.H[1] = h.y; }
+  if (FMT == T_Q6_K) { u32x4 h = ldnt4(m.qx + idx * 16); o.H[0] = h.x; o.H[1] = h.y; o.H[2] = h.z; o.H[3] = h.w; }
+  if (FMT == T_Q4_0 || FMT == T_Q5_0) o.dw = __builtin_nontemporal_load((const uint32_t *)(m.dd + idx * 2));
+  if (FMT == T_Q4_K || FMT == T_Q5_K) {
+    o.scw = __builtin_nontemporal_load((const uint32_t *)(m.sc + idx * 4));
+    o.dw = __builtin_nontemporal_load((const uint32_t *)(m.dd + ((long)r * (m.nslab >> 2) + (s >> 2)) * 2));
   }
   if (FMT == T_Q6_K) {
-    u32x4 h = ldnt4(m.qx + idx * 16);
-    uint32_t Hq[4] = {h.x, h.y, h.z, h.w};
-    #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      o.w[i] = (L[i] & 0x0F0F0F0Fu) | ((Hq[i] & 0x03030303u) << 4);
-      o.w[4 + i] = (L[4 + i] & 0x0F0F0F0Fu) | ((Hq[i] & 0x0C0C0C0Cu) << 2);
-      o.w[8 + i] = ((L[i] >> 4) & 0x0F0F0F0Fu) | (Hq[i] & 0x30303030u);
-      o.w[12 + i] = ((L[4 + i] >> 4) & 0x0F0F0F0Fu) | ((Hq[i] & 0xC0C0C0C0u) >> 2);
-    }
     o.scw = __builtin_nontemporal_load((const uint32_t *)(m.sc + idx * 4));
-    o.d0 = h2f(__builtin_nontemporal_load(m.dd + (long)r * (m.nslab >> 2) + (s >> 2)));
-    return;
+    o.dw = __builtin_nontemporal_load(m.dd + (long)r * (m.nslab >> 2) + (s >> 2));
   }
 }
 
-// acc += this slab's terms for one token, in the reference's order and rounding.
+// 64 values of the slab as int8 lanes (natural value order), unsigned codes for the offset formats.
 template <int FMT>
-__device__ inline double slab_terms(const Slab<FMT> &o, const uint32_t *X, const float *xd, const int32_t *xs,
-                                    const int32_t *xs16, double acc) {
+__device__ inline void unpack(const SlabRaw &o, uint32_t *w) {
+  if (FMT == T_Q8_0) {
+    #pragma unroll
+    for (int i = 0; i < 16; i++) w[i] = o.L[i];
+    return;
+  }
+  if (FMT == T_Q6_K) {
+    #pragma unroll
+    for (int i = 0; i < 4; i++) {
+      w[i] = (o.L[i] & 0x0F0F0F0Fu) | ((o.H[i] & 0x03030303u) << 4);
+      w[4 + i] = (o.L[4 + i] & 0x0F0F0F0Fu) | ((o.H[i] & 0x0C0C0C0Cu) << 2);
+      w[8 + i] = ((o.L[i] >> 4) & 0x0F0F0F0Fu) | (o.H[i] & 0x30303030u);
+      w[12 + i] = ((o.L[4 + i] >> 4) & 0x0F0F0F0Fu) | ((o.H[i] & 0xC0C0C0C0u) >> 2);
+    }
+    return;
+  }
+  #pragma unroll
+  for (int i = 0; i < 8; i++) { w[i] = o.L[i] & 0x0F0F0F0Fu; w[8 + i] = (o.L[i] >> 4) & 0x0F0F0F0Fu; }
+  if (FMT == T_Q5_0 || FMT == T_Q5_K) {
+    #pragma unroll
+    for (int i = 0; i < 8; i++) {
+      w[i] |= (((o.H[0] >> (4 * i)) & 15u) * 0x00204081u & 0x01010101u) << 4;
+      w[8 + i] |= (((o.H[1] >> (4 * i)) & 15u) * 0x00204081u & 0x01010101u) << 4;
+    }
+  }
+}
+
+// acc += this slab's terms for one token, in the reference's order and rounding (src/compute/ref-kernels.js:132-277).
+template <int FMT>
+__device__ inline double slab_terms(const uint32_t *w, const SlabRaw &o, const uint32_t *X, const float *xd,
+                                    const int32_t *xs, const int32_t *xs16, double acc) {
+  const float d0 = h2f(o.dw & 0xffff), d1 = h2f(o.dw >> 16);
   if (FMT == T_Q6_K) {
     int g[4];
     #pragma unroll
     for (int k = 0; k < 4; k++) {
       int a = 0;
       #pragma unroll
-      for (int i = 0; i < 4; i++) a = sdot4((int)o.w[4 * k + i], (int)X[4 * k + i], a);
+      for (int i = 0; i < 4; i++) a = sdot4((int)w[4 * k + i], (int)X[4 * k + i], a);
       g[k] = a - 32 * xs16[k];
     }
-    double d = (double)o.d0;
+    const double d = (double)d0;
     #pragma unroll
     for (int k = 0; k < 4; k++) {
       double sc = (double)(int8_t)((o.scw >> (8 * k)) & 0xff);
-      acc = acc + (double)xd[k >> 1] * d * sc * (double)g[k];  // (((xd*d)*scale)*gsum)
+      acc = acc + (double)xd[k >> 1] * d * sc * (double)g[k];  // ((xd*d)*scale)*gsum
     }
     return acc;
   }
   int lo = 0, hi = 0;
   #pragma unroll
-  for (int i = 0; i < 8; i++) lo = sdot4((int)o.w[i], (int)X[i], lo);
+  for (int i = 0; i < 8; i++) lo = sdot4((int)w[i], (int)X[i], lo);
   #pragma unroll
-  for (int i = 8; i < 16; i++) hi = sdot4((int)o.w[i], (int)X[i], hi);
+  for (int i = 8; i < 16; i++) hi = sdot4((int)w[i], (int)X[i], hi);
   if (FMT == T_Q8_0) {
-    acc = acc + (double)lo * (double)o.d0 * (double)xd[0];
-    acc = acc + (double)hi * (double)o.d1 * (double)xd[1];
+    acc = acc + (double)lo * (double)d0 * (double)xd[0];
+    acc = acc + (double)hi * (double)d1 * (double)xd[1];
     return acc;
   }
   if (FMT == T_Q4_0 || FMT == T_Q5_0) {
     const int off = FMT == T_Q4_0 ? 8 : 16;
-    acc = acc + (double)(lo - off * xs[0]) * (double)o.d0 * (double)xd[0];
-    acc = acc + (double)(hi - off * xs[1]) * (double)o.d1 * (double)xd[1];
+    acc = acc + (double)(lo - off * xs[0]) * (double)d0 * (double)xd[0];
+    acc = acc + (double)(hi - off * xs[1]) * (double)d1 * (double)xd[1];
     return acc;
   }
   // Q4_K / Q5_K: xd * (d*sc*sum(q*xq) - dmin*mn*sum(xq))
-  double d = (double)o.d0, dm = (double)o.d1;
-  double sc0 = (double)(o.scw & 0xff), sc1 = (double)((o.scw >> 8) & 0xff);
-  double mn0 = (double)((o.scw >> 16) & 0xff), mn1 = (double)(o.scw >> 24);
+  const double d = (double)d0, dm = (double)d1;
+  const double sc0 = (double)(o.scw & 0xff), sc1 = (double)((o.scw >> 8) & 0xff);
+  const double mn0 = (double)((o.scw >> 16) & 0xff), mn1 = (double)(o.scw >> 24);
   acc = acc + (double)xd[0] * (d * sc0 * (double)lo - dm * mn0 * (double)xs[0]);
   acc = acc + (double)xd[1] * (d * sc1 * (double)hi - dm * mn1 * (double)xs[1]);
   return acc;
 }
 
+// y[t][r] = sum over the row's blocks of the reference's per-block term, for M tokens at once.
+// Mapping: `lpr` lanes share a pair of rows (a gate/up pair for SWIGLU) and take the row's 64-value slabs round robin
+// (lane j: slabs j, j+lpr, ...); each lane adds its blocks' f64 terms in slab order, then a butterfly over the lpr
+// lanes. lpr is fixed per matrix, so the per-(row, token) arithmetic does not depend on M: a batched pass gives the
+// same bits as token-by-token passes. The int8 activations of MT tokens are staged in LDS (one K-window when they fit,
+// else windows that are multiples of 64*lpr, which keeps the slab order). Blocks stride over row pairs; the next
+// slab's planes are loaded while the current one is computed.
 template <int FMT, int MT, int EPI>
 __global__ __launch_bounds__(256) void k_gemv(const GemvArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lpr = a.lpr, slots = 64 / lpr, slot = lane / lpr, j = lane % lpr;
-  const int unit = (blockIdx.x * 4 + wave) * slots + slot;
-  // two rows per lane: a gate/up pair for SWIGLU, else two consecutive rows of the concatenated segments
-  int grow[2];
-  if (EPI == EPI_SWIGLU) { grow[0] = unit; grow[1] = a.rows_total + unit; }
-  else { grow[0] = 2 * unit; grow[1] = 2 * unit + 1; }
-  const int lim = EPI == EPI_SWIGLU ? a.rows_total : a.rows_total;
-  const bool valid0 = (EPI == EPI_SWIGLU ? unit : grow[0]) < lim;
-  const bool valid1 = EPI == EPI_SWIGLU ? valid0 : grow[1] < lim;
-  int segi[2], lrow[2];
-  MatView mv[2];
-  #pragma unroll
-  for (int r = 0; r < 2; r++) {
-    int g = grow[r];
-    int si = 0, base = 0;
-    if (EPI != EPI_SWIGLU) {
-      if (g >= lim) g = lim - 1;
-      while (si + 1 < a.nseg && g >= base + a.seg[si].rows) { base += a.seg[si].rows; si++; }
-    } else {
-      si = r; base = r ? a.rows_total : 0;
-      if (unit >= lim) g = base + lim - 1;
-    }
-    segi[r] = si; lrow[r] = g - base;
-    mv[r] = a.seg[si].m;
-  }
+  const int nunits = EPI == EPI_SWIGLU ? a.rows_total : (a.rows_total + 1) / 2;
+  const int upb = 4 * slots;  // units per block per iteration
   const int nslab = a.nslab, K = nslab * 64;
+  const bool windowed = a.wk < K;
   for (int t0 = 0; t0 < a.M; t0 += MT) {
     const int mt = min(MT, a.M - t0);
-    double acc[2][MT];
-    #pragma unroll
-    for (int r = 0; r < 2; r++)
-      #pragma unroll
-      for (int t = 0; t < MT; t++) acc[r][t] = 0.0;
-    for (int k0 = 0; k0 < K; k0 += a.wk) {
-      const int kw = min(a.wk, K - k0);
+    auto stage = [&](int k0, int kw) {
       __syncthreads();
-      // stage int8 activations [mt][kw] (16-byte pieces)
       const int pieces = kw >> 4;
       for (int p = threadIdx.x; p < mt * pieces; p += 256) {
         int t = p / pieces, c = p % pieces;
         *(uint4 *)(lds + (long)t * kw + 16 * c) = *(const uint4 *)(a.act.q + (long)(t0 + t) * a.act.ld + k0 + 16 * c);
       }
       __syncthreads();
-      for (int s = (k0 >> 6) + j; s < ((k0 + kw) >> 6); s += lpr) {
-        Slab<FMT> sl[2];
+    };
+    if (!windowed) stage(0, K);
+    for (int ub = blockIdx.x * upb; ub < nunits; ub += gridDim.x * upb) {
+      const int unit = ub + wave * slots + slot;
+      const bool valid = unit < nunits;
+      const int u = valid ? unit : nunits - 1;
+      int segi[2], lrow[2];
+      MatView mv[2];
+      #pragma unroll
+      for (int r = 0; r < 2; r++) {
+        int si = 0, base = 0, g;
+        if (EPI == EPI_SWIGLU) { si = r; g = u; }
+        else {
+          g = min(2 * u + r, a.rows_total - 1);
+          while (si + 1 < a.nseg && g >= base + a.seg[si].rows) { base += a.seg[si].rows; si++; }
+          g -= base;
+        }
+        segi[r] = si; lrow[r] = g;
+        mv[r] = a.seg[si].m;
+      }
+      double acc[2][MT];
+      #pragma unroll
+      for (int r = 0; r < 2; r++)
         #pragma unroll
-        for (int r = 0; r < 2; r++) load_slab<FMT>(mv[r], (long)lrow[r] * nslab + s, lrow[r], s, sl[r]);
-        const int ls = (s << 6) - k0;
-        #pragma unroll
-        for (int t = 0; t < MT; t++) {
-          if (t < mt) {
-            uint32_t X[16];
-            const uint4 *xp = (const uint4 *)(lds + (long)t * kw + ls);
+        for (int t = 0; t < MT; t++) acc[r][t] = 0.0;
+      for (int k0 = 0; k0 < K; k0 += a.wk) {
+        const int kw = min(a.wk, K - k0);
+        if (windowed) stage(k0, kw);
+        const int send = (k0 + kw) >> 6;
+        int s = (k0 >> 6) + j;
+        SlabRaw cur[2], nxt[2];
+        if (s < send) {
+          #pragma unroll
+          for (int r = 0; r < 2; r++) load_raw<FMT>(mv[r], (long)lrow[r] * nslab + s, lrow[r], s, cur[r]);
+        }
+        while (s < send) {
+          const int sn = s + lpr;
+          if (sn < send) {
             #pragma unroll
-            for (int i = 0; i < 4; i++) { uint4 v = xp[i]; X[4 * i] = v.x; X[4 * i + 1] = v.y; X[4 * i + 2] = v.z; X[4 * i + 3] = v.w; }
-            const long tb = (long)(t0 + t);
-            const float *xd = a.act.d + tb * (a.act.ld >> 5) + 2 * s;
-            const int32_t *xs = a.act.s + tb * (a.act.ld >> 5) + 2 * s;
-            const int32_t *xs16 = a.act.s16 + tb * (a.act.ld >> 4) + 4 * s;
-            #pragma unroll
-            for (int r = 0; r < 2; r++) acc[r][t] = slab_terms<FMT>(sl[r], X, xd, xs, xs16, acc[r][t]);
+            for (int r = 0; r < 2; r++) load_raw<FMT>(mv[r], (long)lrow[r] * nslab + sn, lrow[r], sn, nxt[r]);
           }
+          uint32_t w[2][16];
+          #pragma unroll
+          for (int r = 0; r < 2; r++) unpack<FMT>(cur[r], w[r]);
+          const int ls = (s << 6) - k0;
+          const int lw = windowed ? kw : K;
+          #pragma unroll
+          for (int t = 0; t < MT; t++) {
+            if (t < mt) {
+              uint32_t X[16];
+              const uint4 *xp = (const uint4 *)(lds + (long)t * lw + ls);
+              #pragma unroll
+              for (int i = 0; i < 4; i++) { uint4 v = xp[i]; X[4 * i] = v.x; X[4 * i + 1] = v.y; X[4 * i + 2] = v.z; X[4 * i + 3] = v.w; }
+              const long tb = (long)(t0 + t);
+              const float *xd = a.act.d + tb * (a.act.ld >> 5) + 2 * s;
+              const int32_t *xs = a.act.s + tb * (a.act.ld >> 5) + 2 * s;
+              const int32_t *xs16 = a.act.s16 + tb * (a.act.ld >> 4) + 4 * s;
+              #pragma unroll
+              for (int r = 0; r < 2; r++) acc[r][t] = slab_terms<FMT>(w[r], cur[r], X, xd, xs, xs16, acc[r][t]);
+            }
+          }
+          #pragma unroll
+          for (int r = 0; r < 2; r++) cur[r] = nxt[r];
+          s = sn;
         }
       }
-    }
-    // butterfly over the lpr lanes of this row slot
-    #pragma unroll
-    for (int r = 0; r < 2; r++)
-      #pragma unroll
-      for (int t = 0; t < MT; t++)
-        for (int o = 1; o < lpr; o <<= 1) acc[r][t] += __shfl_xor(acc[r][t], o, 64);
-    if (j == 0) {
+      // butterfly over the lpr lanes of this row pair (live tokens only)
       #pragma unroll
       for (int t = 0; t < MT; t++) {
-        if (t >= mt) continue;
-        const long tb = t0 + t;
-        if (EPI == EPI_SWIGLU) {
-          if (!valid0) continue;
-          double g = (double)(float)acc[0][t], u = (double)(float)acc[1][t];
-          double silu = g / (1.0 + exp(-g));  // src/compute/ref-kernels.js:322
-          a.hb[tb * a.ldh + unit] = (float)(silu * u);
-        } else {
+        if (t < mt) {
           #pragma unroll
-          for (int r = 0; r < 2; r++) {
-            if (r == 0 ? !valid0 : !valid1) continue;
-            const GemvSeg &sg = a.seg[segi[r]];
-            float y = (float)acc[r][t];
-            if (EPI == EPI_RESID) {
-              float *xp = a.resid + tb * a.ldr + lrow[r];
-              *xp = (float)((double)*xp + (double)y);
-            } else {
-              if (sg.bias) y = (float)((double)y + (double)sg.bias[lrow[r]]);
-              sg.out[tb * sg.ldo + lrow[r]] = y;
+          for (int r = 0; r < 2; r++)
+            for (int o = 1; o < lpr; o <<= 1) acc[r][t] += __shfl_xor(acc[r][t], o, 64);
+        }
+      }
+      if (j == 0 && valid) {
+        #pragma unroll
+        for (int t = 0; t < MT; t++) {
+          if (t >= mt) continue;
+          const long tb = t0 + t;
+          if (EPI == EPI_SWIGLU) {
+            double g = (double)(float)acc[0][t], uu = (double)(float)acc[1][t];
+            double silu = g / (1.0 + exp(-g));  // src/compute/ref-kernels.js:322
+            a.hb[tb * a.ldh + unit] = (float)(silu * uu);
+          } else {
+            #pragma unroll
+            for (int r = 0; r < 2; r++) {
+              if (2 * unit + r >= a.rows_total) continue;
+              const GemvSeg &sg = a.seg[segi[r]];
+              float y = (float)acc[r][t];
+              if (EPI == EPI_RESID) {
+                float *xp = a.resid + tb * a.ldr + lrow[r];
+                *xp = (float)((double)*xp + (double)y);
+              } else {
+                if (sg.bias) y = (float)((double)y + (double)sg.bias[lrow[r]]);
+                sg.out[tb * sg.ldo + lrow[r]] = y;
+              }
             }
           }
         }
@@ -566,57 +605,58 @@ template <int HPB, int HD, bool F16KV>
 __global__ __launch_bounds__(HPB * HD) void k_attention(const AttnArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int NT = HPB * HD, NW = NT / 64;
+  constexpr int VB = F16KV ? 2 : 4;           // bytes per cached value
+  constexpr int CH = 16384 / (HD * VB);       // positions per staged V chunk (16 KB)
+  constexpr int EPL = 16 / VB;                // K values per lane per 16-byte load
+  constexpr int LP = HD / EPL;                // lanes per position in the score dots
+  constexpr int PPI = NT / LP;                // positions per score iteration
   const int b = blockIdx.x, hg = blockIdx.y, tid = threadIdx.x;
   const Step *st = a.step;
   if (b >= st->B) return;
   const int npos = st->pos0 + b + 1;
   const int h0 = hg * HPB;
   const int kvh = h0 / (a.nHead / a.nHeadKv);
-  float *qs = (float *)lds;              // [HPB][HD]
-  float *p = qs + HPB * HD;              // [HPB][pstride]
   const int ps = a.pstride;
+  float *qs = (float *)lds;                                   // [HPB][HD]
+  float *p = qs + HPB * HD;                                   // [HPB][ps]
+  uint8_t *vbuf = (uint8_t *)(p + HPB * ps);                  // [2][CH][HD] cached values
   __shared__ double red[HPB * NW];
   __shared__ float redf[HPB * NW];
   for (int i = tid; i < HPB * HD; i += NT) qs[i] = a.q[(long)b * a.ldq + (long)h0 * HD + i];
   __syncthreads();
   const long kvoff = ((long)a.layer * a.nHeadKv + kvh) * a.ctx * HD;
-  const double scale = a.scale;
-  // scores: one position per thread, dot products in f64 in element order (exact products, one rounding per step)
+  const uint8_t *kbase = (const uint8_t *)a.kcache + kvoff * VB;
+  const uint8_t *vbase = (const uint8_t *)a.vcache + kvoff * VB;
+  // ---- scores: LP lanes per position, each an exact-product f64 partial dot over EPL elements, then a butterfly
+  const int part = tid % LP;
   float lmax[HPB];
   #pragma unroll
   for (int h = 0; h < HPB; h++) lmax[h] = -INFINITY;
-  for (int t = tid; t < npos; t += NT) {
+  for (int t0 = 0; t0 < npos; t0 += PPI) {
+    const int t = t0 + tid / LP;
     double s[HPB];
     #pragma unroll
     for (int h = 0; h < HPB; h++) s[h] = 0.0;
-    if (F16KV) {
-      const uint16_t *kr = (const uint16_t *)a.kcache + kvoff + (long)t * HD;
-      for (int i = 0; i < HD; i += 8) {
-        uint4 u = *(const uint4 *)(kr + i);
-        uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+    if (t < npos) {
+      uint4 u = *(const uint4 *)(kbase + ((long)t * HD + part * EPL) * VB);
+      uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+      #pragma unroll
+      for (int e = 0; e < EPL; e++) {
+        double kv = F16KV ? (double)h2f((uint16_t)((w4[e >> 1] >> (16 * (e & 1))) & 0xffff)) : (double)__uint_as_float(w4[e]);
         #pragma unroll
-        for (int c = 0; c < 8; c++) {
-          double kv = (double)h2f((uint16_t)((w4[c >> 1] >> (16 * (c & 1))) & 0xffff));
-          #pragma unroll
-          for (int h = 0; h < HPB; h++) s[h] = fma((double)qs[h * HD + i + c], kv, s[h]);
-        }
-      }
-    } else {
-      const float *kr = (const float *)a.kcache + kvoff + (long)t * HD;
-      for (int i = 0; i < HD; i += 4) {
-        float4 u = *(const float4 *)(kr + i);
-        float w4[4] = {u.x, u.y, u.z, u.w};
-        #pragma unroll
-        for (int c = 0; c < 4; c++)
-          #pragma unroll
-          for (int h = 0; h < HPB; h++) s[h] = fma((double)qs[h * HD + i + c], (double)w4[c], s[h]);
+        for (int h = 0; h < HPB; h++) s[h] = fma((double)qs[h * HD + part * EPL + e], kv, s[h]);
       }
     }
     #pragma unroll
-    for (int h = 0; h < HPB; h++) {
-      float v = (float)(s[h] * scale);
-      p[h * ps + t] = v;
-      lmax[h] = fmaxf(lmax[h], v);
+    for (int h = 0; h < HPB; h++)
+      for (int o = 1; o < LP; o <<= 1) s[h] += __shfl_xor(s[h], o, 64);
+    if (part == 0 && t < npos) {
+      #pragma unroll
+      for (int h = 0; h < HPB; h++) {
+        float v = (float)(s[h] * a.scale);
+        p[h * ps + t] = v;
+        lmax[h] = fmaxf(lmax[h], v);
+      }
     }
   }
   #pragma unroll
@@ -634,7 +674,7 @@ __global__ __launch_bounds__(HPB * HD) void k_attention(const AttnArgs a) {
     mx[h] = (double)m;
     sum[h] = 0.0;
   }
-  // softmax (src/compute/ref-kernels.js:313-320): e = exp(s - max) stored f32, sum of the unrounded e, then p = e * (1/sum)
+  // ---- softmax (src/compute/ref-kernels.js:313-320): e = exp(s - max) stored f32, sum of the unrounded e, p = e * (1/sum)
   for (int t = tid; t < npos; t += NT) {
     #pragma unroll
     for (int h = 0; h < HPB; h++) {
@@ -660,29 +700,59 @@ __global__ __launch_bounds__(HPB * HD) void k_attention(const AttnArgs a) {
     #pragma unroll
     for (int h = 0; h < HPB; h++) p[h * ps + t] = (float)((double)p[h * ps + t] * inv[h]);
   }
-  __syncthreads();
-  // weighted sum of V: thread -> (head tid / HD, dim tid % HD); f32 accumulation in position order
+  // ---- weighted sum of V: thread -> (head tid / HD, dim tid % HD), f32 accumulation in position order. V is staged
+  // through LDS in chunks of CH positions (double buffered: the next chunk's loads are in flight during the chain).
+  constexpr int CB = CH * HD * VB;                            // chunk bytes
+  constexpr int LPT = (CB / 16 + NT - 1) / NT;                // 16-byte loads per thread per chunk
   const int h = tid / HD, i = tid % HD;
   const float *ph = p + h * ps;
+  const int nch = (npos + CH - 1) / CH;
+  uint4 pre[LPT];
+  auto fetch = [&](int c) {
+    const long base = (long)c * CH * HD * VB;
+    const long lim = (long)npos * HD * VB;                    // rows past the last position are not read
+    #pragma unroll
+    for (int k = 0; k < LPT; k++) {
+      const int off = (k * NT + tid) * 16;
+      pre[k] = (off < CB && base + off < lim) ? *(const uint4 *)(vbase + base + off) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store = [&](int buf) {
+    #pragma unroll
+    for (int k = 0; k < LPT; k++) {
+      const int off = (k * NT + tid) * 16;
+      if (off < CB) *(uint4 *)(vbuf + buf * CB + off) = pre[k];
+    }
+  };
+  fetch(0);
+  __syncthreads();
+  store(0);
+  __syncthreads();
   float o = 0.f;
-  if (F16KV) {
-    const uint16_t *vb = (const uint16_t *)a.vcache + kvoff + i;
-    int t = 0;
-    for (; t + 4 <= npos; t += 4) {
-      float v0 = h2f(vb[(long)t * HD]), v1 = h2f(vb[(long)(t + 1) * HD]), v2 = h2f(vb[(long)(t + 2) * HD]), v3 = h2f(vb[(long)(t + 3) * HD]);
-      float4 pp = *(const float4 *)(ph + t);
+  for (int c = 0; c < nch; c++) {
+    if (c + 1 < nch) fetch(c + 1);
+    const int t0 = c * CH, cnt = min(CH, npos - t0);
+    const uint8_t *vb = vbuf + (c & 1) * CB;
+    int tt = 0;
+    for (; tt + 4 <= cnt; tt += 4) {
+      float4 pp = *(const float4 *)(ph + t0 + tt);
+      float v0, v1, v2, v3;
+      if (F16KV) {
+        v0 = h2f(((const uint16_t *)vb)[(tt + 0) * HD + i]); v1 = h2f(((const uint16_t *)vb)[(tt + 1) * HD + i]);
+        v2 = h2f(((const uint16_t *)vb)[(tt + 2) * HD + i]); v3 = h2f(((const uint16_t *)vb)[(tt + 3) * HD + i]);
+      } else {
+        v0 = ((const float *)vb)[(tt + 0) * HD + i]; v1 = ((const float *)vb)[(tt + 1) * HD + i];
+        v2 = ((const float *)vb)[(tt + 2) * HD + i]; v3 = ((const float *)vb)[(tt + 3) * HD + i];
+      }
       o = fmaf(pp.x, v0, o); o = fmaf(pp.y, v1, o); o = fmaf(pp.z, v2, o); o = fmaf(pp.w, v3, o);
     }
-    for (; t < npos; t++) o = fmaf(ph[t], h2f(vb[(long)t * HD]), o);
-  } else {
-    const float *vb = (const float *)a.vcache + kvoff + i;
-    int t = 0;
-    for (; t + 4 <= npos; t += 4) {
-      float v0 = vb[(long)t * HD], v1 = vb[(long)(t + 1) * HD], v2 = vb[(long)(t + 2) * HD], v3 = vb[(long)(t + 3) * HD];
-      float4 pp = *(const float4 *)(ph + t);
-      o = fmaf(pp.x, v0, o); o = fmaf(pp.y, v1, o); o = fmaf(pp.z, v2, o); o = fmaf(pp.w, v3, o);
+    for (; tt < cnt; tt++) {
+      float v = F16KV ? h2f(((const uint16_t *)vb)[tt * HD + i]) : ((const float *)vb)[tt * HD + i];
+      o = fmaf(ph[t0 + tt], v, o);
     }
-    for (; t < npos; t++) o = fmaf(ph[t], vb[(long)t * HD], o);
+    __syncthreads();
+    if (c + 1 < nch) store((c + 1) & 1);
+    __syncthreads();
   }
   const int col = (h0 + h) * HD + i;
   if (a.out) a.out[(long)b * a.ldo + col] = o;
@@ -709,11 +779,21 @@ __global__ void k_fill_f32(float *p, long n, float v) {
 }
 
 // ================================================================================================ launch helpers
+template <int FMT, int MT, int EPI>
+static void launch_gemv_k(const GemvArgs &a, int blocks, size_t ldsBytes, hipStream_t st) {
+  static bool attr = false;
+  if (!attr) {
+    ZL_HIP(hipFuncSetAttribute((const void *)k_gemv<FMT, MT, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize, GEMV_LDS_MAX));
+    attr = true;
+  }
+  hipLaunchKernelGGL((k_gemv<FMT, MT, EPI>), dim3(blocks), dim3(256), ldsBytes, st, a);
+}
+
 template <int FMT, int MT>
 static void launch_gemv_fmt(const GemvArgs &a, int epi, int blocks, size_t ldsBytes, hipStream_t st) {
-  if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemv<FMT, MT, EPI_STORE>), dim3(blocks), dim3(256), ldsBytes, st, a);
-  else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemv<FMT, MT, EPI_RESID>), dim3(blocks), dim3(256), ldsBytes, st, a);
-  else hipLaunchKernelGGL((k_gemv<FMT, MT, EPI_SWIGLU>), dim3(blocks), dim3(256), ldsBytes, st, a);
+  if (epi == EPI_STORE) launch_gemv_k<FMT, MT, EPI_STORE>(a, blocks, ldsBytes, st);
+  else if (epi == EPI_RESID) launch_gemv_k<FMT, MT, EPI_RESID>(a, blocks, ldsBytes, st);
+  else launch_gemv_k<FMT, MT, EPI_SWIGLU>(a, blocks, ldsBytes, st);
 }
 
 template <int MT>
@@ -729,10 +809,14 @@ static void launch_gemv_mt(int fmt, const GemvArgs &a, int epi, int blocks, size
   }
 }
 
-int gemv_lpr(int nslab) {
-  int l = 64;
-  while (l > 8 && l > nslab) l >>= 1;
-  return l;
+// Lanes per row pair: enough lanes in total to keep the GPU's memory pipes full (about 2^19 lanes), at most 64, at
+// least 8, never more than the row's slabs. Depends only on the matrix shape (rows of the launch, columns).
+int gemv_lpr(int rows, int nslab) {
+  int want = 8;
+  while (want < 64 && (long)want * rows < (1L << 19)) want <<= 1;
+  int cap = 8;
+  while (cap * 2 <= nslab && cap < 64) cap <<= 1;
+  return want < cap ? want : cap;
 }
 
 void launch_gemv(const GemvArgs &a0, int epi, const float *xf, int ldx, hipStream_t st) {
@@ -751,16 +835,17 @@ void launch_gemv(const GemvArgs &a0, int epi, const float *xf, int ldx, hipStrea
   const int lpr = a.lpr;
   const int slots = 64 / lpr;
   const int units = epi == EPI_SWIGLU ? a.rows_total : (a.rows_total + 1) / 2;
-  const int blocks = (units + 4 * slots - 1) / (4 * slots);
   const int MT = a.M <= 1 ? 1 : a.M <= 2 ? 2 : a.M <= 4 ? 4 : a.M <= 8 ? 8 : 16;
-  // K window: all of K if it fits 64 KB of LDS for MT tokens, else the largest multiple of 64*lpr that does
+  // K window: all of K when MT rows of it fit the LDS budget, else the largest multiple of 64*lpr that does
   const int K = a.nslab * 64;
   const int step = 64 * lpr;
-  int wk = (65536 / MT) / step * step;
+  int wk = (GEMV_LDS_MAX / MT) / step * step;
   if (wk < step) wk = step;
   if (wk > K) wk = K;
   a.wk = wk;
   const size_t ldsBytes = (size_t)MT * wk;
+  int blocks = (units + 4 * slots - 1) / (4 * slots);
+  if (wk == K && blocks > GEMV_MAX_BLOCKS) blocks = GEMV_MAX_BLOCKS;
   switch (MT) {
     case 1: launch_gemv_mt<1>(fmt, a, epi, blocks, ldsBytes, st); break;
     case 2: launch_gemv_mt<2>(fmt, a, epi, blocks, ldsBytes, st); break;
@@ -773,29 +858,41 @@ void launch_gemv(const GemvArgs &a0, int epi, const float *xf, int ldx, hipStrea
 
 template <int HPB, int HD>
 static void launch_attn_hd(const AttnArgs &a, dim3 grid, size_t lds, hipStream_t st) {
+  static size_t attrSet[2] = {64 * 1024, 64 * 1024};  // dynamic LDS above 64 KB must be requested per kernel
+  if (lds > attrSet[a.kvF16]) {
+    if (a.kvF16) ZL_HIP(hipFuncSetAttribute((const void *)k_attention<HPB, HD, true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    else ZL_HIP(hipFuncSetAttribute((const void *)k_attention<HPB, HD, false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    attrSet[a.kvF16] = lds;
+  }
   if (a.kvF16) hipLaunchKernelGGL((k_attention<HPB, HD, true>), grid, dim3(HPB * HD), lds, st, a);
   else hipLaunchKernelGGL((k_attention<HPB, HD, false>), grid, dim3(HPB * HD), lds, st, a);
 }
 
+size_t attention_lds(int hpb, int hd, int pstride) { return (size_t)hpb * hd * 4 + (size_t)hpb * pstride * 4 + 2 * 16384; }
+constexpr size_t ATTN_LDS_MAX = 150 * 1024;  // dynamic LDS of one attention block (the kernel's static LDS is < 1 KB)
+
 void launch_attention(const AttnArgs &a, int B, int ctxMax, int hpb, hipStream_t st) {
   (void)ctxMax;
-  const size_t lds = (size_t)hpb * a.hd * 4 + (size_t)hpb * a.pstride * 4;
+  const size_t lds = attention_lds(hpb, a.hd, a.pstride);
+  ZL_REQUIRE(lds <= ATTN_LDS_MAX, ZL_ERR_UNSUPPORTED, "context too long for the attention kernel");
   dim3 grid(B, a.nHead / hpb);
-  if (hpb == 2) {
-    if (a.hd == 64) launch_attn_hd<2, 64>(a, grid, lds, st);
-    else if (a.hd == 128) launch_attn_hd<2, 128>(a, grid, lds, st);
-    else launch_attn_hd<2, 256>(a, grid, lds, st);
-  } else {
-    if (a.hd == 64) launch_attn_hd<1, 64>(a, grid, lds, st);
-    else if (a.hd == 128) launch_attn_hd<1, 128>(a, grid, lds, st);
-    else launch_attn_hd<1, 256>(a, grid, lds, st);
+  switch (hpb * 1000 + a.hd) {
+    case 1064: launch_attn_hd<1, 64>(a, grid, lds, st); break;
+    case 1128: launch_attn_hd<1, 128>(a, grid, lds, st); break;
+    case 1256: launch_attn_hd<1, 256>(a, grid, lds, st); break;
+    case 2064: launch_attn_hd<2, 64>(a, grid, lds, st); break;
+    case 2128: launch_attn_hd<2, 128>(a, grid, lds, st); break;
+    case 2256: launch_attn_hd<2, 256>(a, grid, lds, st); break;
+    case 4064: launch_attn_hd<4, 64>(a, grid, lds, st); break;
+    case 4128: launch_attn_hd<4, 128>(a, grid, lds, st); break;
+    default: throw Error(ZL_ERR_UNSUPPORTED, "attention: unsupported heads-per-block / head_dim");
   }
   ZL_HIP(hipGetLastError());
 }
 
 void launch_norm_quant(const float *x, int ldx, int row0, int nrows, const float *w, double eps, int n, int npad,
                        const Act &act, hipStream_t st) {
-  hipLaunchKernelGGL(k_norm_quant, dim3(nrows), dim3(256), 0, st, x, ldx, row0, w, eps, n, npad, act);
+  hipLaunchKernelGGL(k_norm_quant, dim3((npad + NQ_CHUNK - 1) / NQ_CHUNK, nrows), dim3(256), 0, st, x, ldx, row0, w, eps, n, npad, act);
   ZL_HIP(hipGetLastError());
 }
 

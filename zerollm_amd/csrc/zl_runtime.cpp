@@ -3,6 +3,7 @@
 // (include/zerollm_hip.h).
 #include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -103,12 +104,6 @@ struct zl_model {
   std::vector<int> tokens;
   std::map<int, hipGraphExec_t> graphs;
   std::map<int, hipGraph_t> graphDefs;
-  // timing probe
-  int probeLayer = -1, probeWhich = -1;
-  hipEvent_t probeA = nullptr, probeB = nullptr;
-  double probeMs = 0;
-  int64_t probeCount = 0, probeBytes = 0;
-  int lastLaunchHadProbe = 0;
   ~zl_model();
 };
 
@@ -143,8 +138,6 @@ zl_model::~zl_model() {
   if (st) hipStreamSynchronize(st);
   for (auto &g : graphs) hipGraphExecDestroy(g.second);
   for (auto &g : graphDefs) hipGraphDestroy(g.second);
-  if (probeA) hipEventDestroy(probeA);
-  if (probeB) hipEventDestroy(probeB);
   ar.release();
   if (st) hipStreamDestroy(st);
   if (cst) hipStreamDestroy(cst);
@@ -243,7 +236,7 @@ static void finish_model(zl_model *m, const float *ropeFreqs) {
 // ---------------------------------------------------------------------------------------------- forward pass
 struct SegSpec { const DevMat *m; float *out; int ldo; const float *bias; };
 
-static void gemv_group(zl_model *m, const std::vector<SegSpec> &segs, int B, int epi, bool probe) {
+static void gemv_group(zl_model *m, const std::vector<SegSpec> &segs, int B, int epi) {
   GemvArgs a;
   memset(&a, 0, sizeof(a));
   a.nseg = (int)segs.size();
@@ -259,25 +252,22 @@ static void gemv_group(zl_model *m, const std::vector<SegSpec> &segs, int B, int
   a.nslab = segs[0].m->nslab;
   a.act = m->act;
   a.M = B;
-  a.lpr = gemv_lpr(a.nslab);
+  a.lpr = gemv_lpr(epi == EPI_SWIGLU ? 2 * a.rows_total : a.rows_total, a.nslab);
   a.resid = m->x;
   a.ldr = m->cfg.n_embd;
   a.hb = m->hb;
   a.ldh = m->cfg.n_ff;
-  if (probe) ZL_HIP(hipEventRecord(m->probeA, m->st));
   launch_gemv(a, epi, m->act.f, m->act.ld, m->st);
-  if (probe) ZL_HIP(hipEventRecord(m->probeB, m->st));
 }
 
 // Enqueue one forward pass of B tokens (tokens and positions from m->dstep). want: 0 none, 1 last, 2 all.
-static void enqueue_forward(zl_model *m, int B, int want, bool withProbe) {
+static void enqueue_forward(zl_model *m, int B, int want) {
   const zl_config &c = m->cfg;
   const int d = c.n_embd, qd = qdim(m), kvd = kvdim(m), ff = c.n_ff;
   const double eps = (double)c.rms_eps;
   launch_embed(view(m->tokEmbd), m->dstep, B, m->x, d, m->st);
   for (int l = 0; l < c.n_layer; l++) {
     Layer &L = m->layers[l];
-    auto P = [&](int which) { return withProbe && m->probeLayer == l && m->probeWhich == which; };
     launch_norm_quant(m->x, d, 0, B, L.attnNorm, eps, d, pad64(d), m->act, m->st);
     // q, k, v: consecutive matrices of one type share a launch
     SegSpec qkv[3] = {{&L.wq, m->q, qd, L.bq}, {&L.wk, m->k, kvd, L.bk}, {&L.wv, m->v, kvd, L.bv}};
@@ -285,7 +275,7 @@ static void enqueue_forward(zl_model *m, int B, int want, bool withProbe) {
     while (i0 < 3) {
       int i1 = i0 + 1;
       while (i1 < 3 && qkv[i1].m->type == qkv[i0].m->type) i1++;
-      gemv_group(m, std::vector<SegSpec>(qkv + i0, qkv + i1), B, EPI_STORE, P(0) && i0 == 0);
+      gemv_group(m, std::vector<SegSpec>(qkv + i0, qkv + i1), B, EPI_STORE);
       i0 = i1;
     }
     RopeArgs ra;
@@ -301,23 +291,26 @@ static void enqueue_forward(zl_model *m, int B, int want, bool withProbe) {
     aa.pstride = (m->ctx + 3) / 4 * 4;
     aa.scale = 1.0 / sqrt((double)c.head_dim);
     aa.step = m->dstep; aa.out = m->act.f; aa.ldo = m->act.ld; aa.act = m->act;
+    // heads per block: the whole GQA group when it fits (K and V are then read once per group)
     const int group = c.n_head / c.n_head_kv;
-    int hpb = (group % 2 == 0 && (size_t)2 * (c.head_dim + aa.pstride) * 4 <= 65536) ? 2 : 1;
-    ZL_REQUIRE((size_t)hpb * (c.head_dim + aa.pstride) * 4 <= 65536, ZL_ERR_UNSUPPORTED, "context too long for the attention kernel");
+    int hpb = 1;
+    for (int cand : {4, 2}) {
+      if (group % cand == 0 && cand * c.head_dim <= 512 && attention_lds(cand, c.head_dim, aa.pstride) <= 150 * 1024) { hpb = cand; break; }
+    }
     launch_attention(aa, B, m->ctx, hpb, m->st);
-    gemv_group(m, {{&L.wo, nullptr, 0, nullptr}}, B, EPI_RESID, P(1));
+    gemv_group(m, {{&L.wo, nullptr, 0, nullptr}}, B, EPI_RESID);
     launch_norm_quant(m->x, d, 0, B, L.ffnNorm, eps, d, pad64(d), m->act, m->st);
     ZL_REQUIRE(L.wgate.type == L.wup.type, ZL_ERR_UNSUPPORTED, "ffn_gate and ffn_up must share a type");
-    gemv_group(m, {{&L.wgate, nullptr, 0, nullptr}, {&L.wup, nullptr, 0, nullptr}}, B, EPI_SWIGLU, P(2));
+    gemv_group(m, {{&L.wgate, nullptr, 0, nullptr}, {&L.wup, nullptr, 0, nullptr}}, B, EPI_SWIGLU);
     launch_norm_quant(m->hb, ff, 0, B, nullptr, eps, ff, pad64(ff), m->act, m->st);
-    gemv_group(m, {{&L.wdown, nullptr, 0, nullptr}}, B, EPI_RESID, P(3));
+    gemv_group(m, {{&L.wdown, nullptr, 0, nullptr}}, B, EPI_RESID);
   }
   if (want == 2) {
     launch_norm_quant(m->x, d, 0, B, m->outputNorm, eps, d, pad64(d), m->act, m->st);
-    gemv_group(m, {{&m->output, m->logits, c.vocab, nullptr}}, B, EPI_STORE, withProbe && m->probeWhich == 4);
+    gemv_group(m, {{&m->output, m->logits, c.vocab, nullptr}}, B, EPI_STORE);
   } else if (want == 1) {
     launch_norm_quant(m->x, d, B - 1, 1, m->outputNorm, eps, d, pad64(d), m->act, m->st);
-    gemv_group(m, {{&m->output, m->logits, c.vocab, nullptr}}, 1, EPI_STORE, withProbe && m->probeWhich == 4);
+    gemv_group(m, {{&m->output, m->logits, c.vocab, nullptr}}, 1, EPI_STORE);
   }
 }
 
@@ -325,14 +318,13 @@ static hipGraphExec_t graph_for(zl_model *m, int B, int want) {
   const int key = B * 4 + want;
   auto it = m->graphs.find(key);
   if (it != m->graphs.end()) return it->second;
-  const bool probe = m->probeWhich >= 0;
   hipGraph_t g = nullptr;
   hipStream_t run = m->st;
   m->st = m->cst;
   struct Back { zl_model *m; hipStream_t s; ~Back() { m->st = s; } } back{m, run};
   ZL_HIP(hipStreamBeginCapture(m->cst, hipStreamCaptureModeThreadLocal));
   try {
-    enqueue_forward(m, B, want, probe);
+    enqueue_forward(m, B, want);
   } catch (...) {
     hipStreamEndCapture(m->cst, &g);
     if (g) hipGraphDestroy(g);
@@ -346,27 +338,69 @@ static hipGraphExec_t graph_for(zl_model *m, int B, int want) {
   return ex;
 }
 
-static bool graph_has_probe(zl_model *m, int B, int want) {
-  if (m->probeWhich < 0) return false;
-  if (m->probeWhich == 4) return want != 0;
-  (void)B;
-  return m->probeLayer >= 0 && m->probeLayer < m->cfg.n_layer;
+// Graph capture can be switched off (ZEROLLM_HIP_GRAPHS=0): the same kernels are then launched one by one, which
+// some tracing tools need.
+static bool use_graphs() {
+  static int v = -1;
+  if (v < 0) {
+    const char *e = getenv("ZEROLLM_HIP_GRAPHS");
+    v = (e && e[0] == '0') ? 0 : 1;
+  }
+  return v == 1;
 }
 
-// One pass; the caller has set m->dstep. Accumulates the probe after the pass if requested.
+// One pass; the caller has set m->dstep.
 static void launch_pass(zl_model *m, int B, int want) {
-  ZL_HIP(hipGraphLaunch(graph_for(m, B, want), m->st));
-  m->lastLaunchHadProbe = graph_has_probe(m, B, want);
+  if (use_graphs()) ZL_HIP(hipGraphLaunch(graph_for(m, B, want), m->st));
+  else enqueue_forward(m, B, want);
 }
 
-static void collect_probe(zl_model *m) {
-  if (!m->lastLaunchHadProbe) return;
-  ZL_HIP(hipEventSynchronize(m->probeB));
-  float ms = 0;
-  ZL_HIP(hipEventElapsedTime(&ms, m->probeA, m->probeB));
-  m->probeMs += ms;
-  m->probeCount++;
-  m->lastLaunchHadProbe = 0;
+// Time `iters` back-to-back launches of one GEMV of the pass (which: 0 first q/k/v group, 1 wo, 2 gate+up, 3 down,
+// 4 output head) with M tokens, cycling through the layers' weights (cache-cold), between two events on the model's
+// stream. Uses the model's activation buffers as the last pass left them.
+static void probe_gemv(zl_model *m, int which, int M, int iters, float *ms, int64_t *bytes) {
+  ZL_REQUIRE(!m->closed, ZL_ERR_STATE, "model is closed");
+  ZL_REQUIRE(which >= 0 && which <= 4 && M >= 1 && M <= m->maxBatch && iters >= 1, ZL_ERR_ARG, "bad probe arguments");
+  const zl_config &c = m->cfg;
+  auto segs_of = [&](int l) -> std::vector<SegSpec> {
+    Layer &L = m->layers[l];
+    switch (which) {
+      case 0: {
+        std::vector<SegSpec> v{{&L.wq, m->q, qdim(m), nullptr}};
+        if (L.wk.type == L.wq.type) v.push_back({&L.wk, m->k, kvdim(m), nullptr});
+        if (L.wk.type == L.wq.type && L.wv.type == L.wq.type) v.push_back({&L.wv, m->v, kvdim(m), nullptr});
+        return v;
+      }
+      case 1: return {{&L.wo, nullptr, 0, nullptr}};
+      case 2: return {{&L.wgate, nullptr, 0, nullptr}, {&L.wup, nullptr, 0, nullptr}};
+      case 3: return {{&L.wdown, nullptr, 0, nullptr}};
+      default: return {{&m->output, m->logits, c.vocab, nullptr}};
+    }
+  };
+  const int epi = which == 1 || which == 3 ? EPI_RESID : which == 2 ? EPI_SWIGLU : EPI_STORE;
+  int64_t b = 0;
+  for (auto &sg : segs_of(0)) b += mat_bytes(*sg.m);
+  *bytes = b;
+  // the residual epilogues accumulate into x: keep a copy and restore it afterwards
+  float *xsave = (float *)nullptr;
+  const size_t xb = (size_t)m->maxBatch * c.n_embd * 4;
+  ZL_HIP(hipMalloc(&xsave, xb));
+  struct F { float *p; ~F() { hipFree(p); } } fr{xsave};
+  ZL_HIP(hipMemcpyAsync(xsave, m->x, xb, hipMemcpyDeviceToDevice, m->st));
+  for (int l = 0; l < std::min(c.n_layer, iters); l++) gemv_group(m, segs_of(which == 4 ? 0 : l), M, epi);  // warm-up
+  hipEvent_t a, e;
+  ZL_HIP(hipEventCreate(&a));
+  ZL_HIP(hipEventCreate(&e));
+  struct E { hipEvent_t a, b; ~E() { hipEventDestroy(a); hipEventDestroy(b); } } ev{a, e};
+  ZL_HIP(hipEventRecord(a, m->st));
+  for (int i = 0; i < iters; i++) gemv_group(m, segs_of(which == 4 ? 0 : i % c.n_layer), M, epi);
+  ZL_HIP(hipEventRecord(e, m->st));
+  ZL_HIP(hipEventSynchronize(e));
+  float t = 0;
+  ZL_HIP(hipEventElapsedTime(&t, a, e));
+  *ms = t / iters;
+  ZL_HIP(hipMemcpyAsync(m->x, xsave, xb, hipMemcpyDeviceToDevice, m->st));
+  ZL_HIP(hipStreamSynchronize(m->st));
 }
 
 // PoolModel.forwardBatch checks (src/compute/pool.js:146-155), same messages.
@@ -399,8 +433,6 @@ static zl_model *new_model(const zl_model_opts *o) {
   m->kvF16 = o ? (o->kv_f16 ? 1 : 0) : 0;
   ZL_HIP(hipStreamCreateWithFlags(&m->st, hipStreamNonBlocking));
   ZL_HIP(hipStreamCreateWithFlags(&m->cst, hipStreamNonBlocking));
-  ZL_HIP(hipEventCreate(&m->probeA));
-  ZL_HIP(hipEventCreate(&m->probeB));
   return m.release();
 }
 
@@ -693,10 +725,11 @@ static void spec_cycle(zl_model *T, zl_model *D, zl_sampler *s, const int32_t *f
   hipStream_t dst = D->st;
   D->st = st;  // draft graphs launch on this stream for the cycle (graphs do not bind a stream)
   struct Restore { zl_model *D; hipStream_t s; ~Restore() { D->st = s; } } restore{D, dst};
-  hipEvent_t e0, e1;
+  hipEvent_t e0, e1, em;
   ZL_HIP(hipEventCreate(&e0));
   ZL_HIP(hipEventCreate(&e1));
-  struct EvFree { hipEvent_t a, b; ~EvFree() { hipEventDestroy(a); hipEventDestroy(b); } } evf{e0, e1};
+  ZL_HIP(hipEventCreate(&em));
+  struct EvFree { hipEvent_t a, b, c; ~EvFree() { hipEventDestroy(a); hipEventDestroy(b); hipEventDestroy(c); } } evf{e0, e1, em};
   ZL_HIP(hipEventRecord(e0, st));
   // target verify step: [pending, x_1..x_kk] at the target's position; drafts are written by the draws
   {
@@ -734,22 +767,24 @@ static void spec_cycle(zl_model *T, zl_model *D, zl_sampler *s, const int32_t *f
       if (j < kk - 1) launch_pass(D, 1, 1);
     }
   }
+  ZL_HIP(hipEventRecord(em, st));
   launch_pass(T, kk + 1, 2);
   launch_dist_rows(T->logits, T->cfg.vocab, kk + 1, T->cfg.vocab, s->sp, dh, keep, 1, s->scratch, s->pdist, st);
   launch_accept(s->pdist, s->qdist, s->ss, (s->sp.temperature <= 0.0 || s->sp.greedyArgmax) ? 1 : 0, st);
   ZL_HIP(hipEventRecord(e1, st));
   ZL_HIP(hipMemcpyAsync(s->hss, s->ss, sizeof(SpecState), hipMemcpyDeviceToHost, st));
   ZL_HIP(hipStreamSynchronize(st));
-  collect_probe(T);
   const SpecState &r = *s->hss;
   const int kkA = kk > 0 ? r.kk : 0;
   out->kk = kkA;
   out->accepted = r.a;
   out->token = r.tok;
   for (int j = 0; j < kkA; j++) out->drafted[j] = r.drafted[j];
-  float ms = 0;
+  float ms = 0, md = 0;
   ZL_HIP(hipEventElapsedTime(&ms, e0, e1));
+  ZL_HIP(hipEventElapsedTime(&md, e0, em));
   out->ms_total = ms;
+  out->ms_draft = md;
   // bookkeeping as the reference's calls leave it: the draft processed x_1..x_{kk-1} (the last draft is not fed,
   // nor anything after a stop token); the target processed [pending, x_1..x_kk]
   for (int j = 0; j + 1 < kkA; j++) D->tokens.push_back(r.drafted[j]);
@@ -852,10 +887,7 @@ int zl_forward(zl_model *m, const int32_t *tokens, int n, int logits_mode, float
     size_t rows = logits_mode == 2 ? (size_t)n : 1;
     ZL_HIP(hipMemcpyAsync(host_logits, m->logits, rows * m->cfg.vocab * 4, hipMemcpyDeviceToHost, m->st));
   }
-  if (host_logits || m->lastLaunchHadProbe) {
-    ZL_HIP(hipStreamSynchronize(m->st));
-    collect_probe(m);
-  }
+  if (host_logits) ZL_HIP(hipStreamSynchronize(m->st));
   ZL_API_END
 }
 
@@ -1088,7 +1120,7 @@ static void probe_gemv(const DevMat &mm, const Act &act, int M, float *y, hipStr
   memset(&a, 0, sizeof(a));
   a.nseg = 1;
   a.seg[0].m = view(mm); a.seg[0].rows = mm.rows; a.seg[0].out = y; a.seg[0].ldo = mm.rows;
-  a.rows_total = mm.rows; a.nslab = mm.nslab; a.act = act; a.M = M; a.lpr = gemv_lpr(mm.nslab);
+  a.rows_total = mm.rows; a.nslab = mm.nslab; a.act = act; a.M = M; a.lpr = gemv_lpr(mm.rows, mm.nslab);
   launch_gemv(a, EPI_STORE, act.f, act.ld, st);
 }
 
@@ -1150,34 +1182,10 @@ int zl_quant_act(const float *x, int64_t K, int M, int8_t *q, float *d, int32_t 
   ZL_API_END
 }
 
-int zl_probe_set(zl_model *m, int layer, int which) {
+int zl_probe_gemv(zl_model *m, int which, int M, int iters, float *ms_per_launch, int64_t *bytes_per_launch) {
   ZL_API_BEGIN
-  ZL_REQUIRE(m, ZL_ERR_ARG, "null argument");
-  ZL_REQUIRE(which >= -1 && which <= 4, ZL_ERR_ARG, "which must be -1..4");
-  ZL_HIP(hipStreamSynchronize(m->st));
-  for (auto &g : m->graphs) hipGraphExecDestroy(g.second);
-  for (auto &g : m->graphDefs) hipGraphDestroy(g.second);
-  m->graphs.clear();
-  m->graphDefs.clear();
-  m->probeLayer = layer;
-  m->probeWhich = which;
-  m->probeMs = 0;
-  m->probeCount = 0;
-  m->lastLaunchHadProbe = 0;
-  const Layer *L = (layer >= 0 && layer < (int)m->layers.size()) ? &m->layers[layer] : nullptr;
-  int64_t b = 0;
-  if (which == 4) b = mat_bytes(m->output);
-  else if (L) b = which == 0 ? mat_bytes(L->wq) : which == 1 ? mat_bytes(L->wo) : which == 2 ? mat_bytes(L->wgate) + mat_bytes(L->wup) : which == 3 ? mat_bytes(L->wdown) : 0;
-  m->probeBytes = b;
-  ZL_API_END
-}
-
-int zl_probe_read(zl_model *m, double *ms_total, int64_t *count, int64_t *bytes_per_launch) {
-  ZL_API_BEGIN
-  ZL_REQUIRE(m && ms_total && count && bytes_per_launch, ZL_ERR_ARG, "null argument");
-  *ms_total = m->probeMs;
-  *count = m->probeCount;
-  *bytes_per_launch = m->probeBytes;
+  ZL_REQUIRE(m && ms_per_launch && bytes_per_launch, ZL_ERR_ARG, "null argument");
+  probe_gemv(m, which, M, iters, ms_per_launch, bytes_per_launch);
   ZL_API_END
 }
 

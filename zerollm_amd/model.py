@@ -150,18 +150,15 @@ class HipModel:
     def logitsBatch(self):
         return self.logits_batch
 
-    # ---- timing probe (events around one GEMV launch inside the captured pass)
+    # ---- timing probe
     PROBE = {"qkv": 0, "wo": 1, "gate_up": 2, "down": 3, "output": 4}
 
-    def set_probe(self, layer: int, which: str | None):
-        call("zl_probe_set", self._h, int(layer), -1 if which is None else self.PROBE[which])
-
-    def read_probe(self):
-        ms = C.c_double()
-        n = C.c_int64()
+    def probe_gemv(self, which: str, M: int, iters: int):
+        """(ms per launch, weight bytes per launch) of one GEMV of the pass, launched back to back over the layers."""
+        ms = C.c_float()
         b = C.c_int64()
-        call("zl_probe_read", self._h, C.byref(ms), C.byref(n), C.byref(b))
-        return ms.value, n.value, b.value
+        call("zl_probe_gemv", self._h, self.PROBE[which], int(M), int(iters), C.byref(ms), C.byref(b))
+        return ms.value, b.value
 
 
 def verify_limit(model) -> int:

@@ -58,7 +58,7 @@ def generate_speculative(target, draft, prompt_ids, k=4, max_tokens=256, sample=
     draft.truncate(d_reuse)
     stats.update(promptTokens=n0, cachedTokens=reuse, generated=0, stopReason="length")
     spec = stats["speculative"] = {"k": k_max, "cycles": 0, "drafted": 0, "accepted": 0, "acceptRate": 0.0,
-                                   "tokensPerCycle": 0.0, "cycleMs": 0.0, "otherMs": 0.0,
+                                   "tokensPerCycle": 0.0, "cycleMs": 0.0, "draftMs": 0.0, "verifyMs": 0.0, "otherMs": 0.0,
                                    "acceptedHist": [0] * (k_max + 1), "draftCachedTokens": d_reuse, "draftPrefillMs": 0.0}
     t0 = time.perf_counter()
     _, aborted = prefill_tokens(target, body, start=reuse, want_logits=False, signal=signal)
@@ -107,6 +107,8 @@ def generate_speculative(target, draft, prompt_ids, k=4, max_tokens=256, sample=
                  ptr(hist_arr, C.c_int32) if len(hist_arr) else None, len(hist_arr), C.byref(res))
             t_after = time.perf_counter()
             spec["cycleMs"] += (t_after - tc) * 1e3
+            spec["draftMs"] += res.ms_draft
+            spec["verifyMs"] += res.ms_total - res.ms_draft
             kk = res.kk
             drafted = list(res.drafted[:kk])
             a = res.accepted
