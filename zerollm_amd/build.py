@@ -14,23 +14,41 @@ LIB = os.path.join(HERE, "libzerollm_hip.so")
 # -ffp-contract=off: every f64/f32 step rounds where the reference's arithmetic rounds; fusions are explicit fma().
 # -packed-fp32-ops off: no v_pk_*_f32 is generated.
 FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-fno-gpu-flush-denormals-to-zero", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result", "-I" + os.path.join(ROOT, "include"),
 ]
 
 
 def build(verbose: bool = False) -> str:
+    """Compile every source to an object (in parallel), then link the shared library."""
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-    srcs = [os.path.join(HERE, "csrc", s) for s in SOURCES]
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    procs, objs = [], []
+    for s in SOURCES:
+        obj = os.path.join(objdir, os.path.splitext(s)[0] + ".o")
+        objs.append(obj)
+        cmd = [hipcc, *FLAGS, "-c", "-x", "hip", os.path.join(HERE, "csrc", s), "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append(subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True))
+    failed = False
+    for p in procs:
+        out = p.communicate()[0]
+        if p.returncode != 0:
+            sys.stderr.write(out)
+            failed = True
+    if failed:
+        raise RuntimeError("hipcc failed building libzerollm_hip.so")
     tmp = LIB + ".tmp"
-    cmd = [hipcc, *FLAGS, "-x", "hip", *srcs, "-o", tmp, "-lpthread"]
+    cmd = [hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp, "-lpthread"]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)
-        raise RuntimeError("hipcc failed building libzerollm_hip.so")
+        raise RuntimeError("linking libzerollm_hip.so failed")
     os.replace(tmp, LIB)
     return LIB
 

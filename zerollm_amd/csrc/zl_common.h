@@ -62,10 +62,56 @@ __device__ inline uint16_t f2h(float f) { return __half_as_ushort(__float2half_r
 
 __device__ inline int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// ---- cross-lane reductions over aligned groups of `width` lanes (a power of two <= 64); every lane of a group ends
+// with the group's result. Steps pair lanes like an xor butterfly (1, 2, 4, 8, 16, 32): within a quad by DPP
+// quad_perm, then DPP row_half_mirror / row_mirror (the partner lies in the other half of the 8- / 16-lane group, whose
+// lanes all hold the same partial by then, so each step adds exactly what the xor butterfly adds), then ds_swizzle
+// (xor 16) and a lane permute (xor 32). DPP moves cost no LDS round trip.
+template <int CTRL>
+__device__ inline int dpp_i32(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+
+template <int CTRL, typename T>
+__device__ inline T dpp_move(T v) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, dpp_i32<CTRL>(__builtin_bit_cast(int, v)));
+  } else {
+    static_assert(sizeof(T) == 8, "32- or 64-bit lanes");
+    const long long x = __builtin_bit_cast(long long, v);
+    const int lo = dpp_i32<CTRL>((int)x), hi = dpp_i32<CTRL>((int)(x >> 32));
+    return __builtin_bit_cast(T, (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+  }
+}
+
+template <typename T>
+__device__ inline T swizzle_xor16(T v) {
+  constexpr int pat = (0x10 << 10) | 0x1F;  // bitmask mode: and 0x1F, or 0, xor 0x10 (within 32 lanes)
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), pat));
+  } else {
+    const long long x = __builtin_bit_cast(long long, v);
+    const int lo = __builtin_amdgcn_ds_swizzle((int)x, pat), hi = __builtin_amdgcn_ds_swizzle((int)(x >> 32), pat);
+    return __builtin_bit_cast(T, (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+  }
+}
+
+template <typename T, typename Op>
+__device__ inline T group_reduce(T v, int width, Op op) {
+  if (width > 1) v = op(v, dpp_move<0xB1>(v));   // quad_perm [1,0,3,2]: xor 1
+  if (width > 2) v = op(v, dpp_move<0x4E>(v));   // quad_perm [2,3,0,1]: xor 2
+  if (width > 4) v = op(v, dpp_move<0x141>(v));  // row_half_mirror: the other quad of the 8-lane group
+  if (width > 8) v = op(v, dpp_move<0x140>(v));  // row_mirror: the other 8 lanes of the row
+  if (width > 16) v = op(v, swizzle_xor16(v));
+  if (width > 32) v = op(v, __shfl_xor(v, 32, 64));
+  return v;
+}
+
 template <typename T>
 __device__ inline T wave_sum_xor(T v, int width) {
-  for (int o = 1; o < width; o <<= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  return group_reduce(v, width, [](T a, T b) { return a + b; });
+}
+
+__device__ inline float group_fmax(float v, int width) {
+  return group_reduce(v, width, [](float a, float b) { return fmaxf(a, b); });
 }
 
 // Order-preserving key of a float (larger float -> larger key); -0 is folded onto +0 so that equal values have equal keys.

@@ -65,6 +65,7 @@ struct RopeArgs {
   double eps;
   const float *cosT, *sinT;
   int nRot, neox, nHead, nHeadKv, hd, ctx, layer, kvF16;
+  int vstride;     // positions per V cache row (V is dimension-major)
   void *kcache, *vcache;
   const Step *step;
 };
@@ -73,7 +74,11 @@ struct AttnArgs {
   const float *q;
   int ldq;
   const void *kcache, *vcache;
-  int nHead, nHeadKv, hd, ctx, layer, kvF16, pstride;
+  int nHead, nHeadKv, hd, ctx, layer, kvF16;
+  int vstride;     // positions per V cache row (V is dimension-major)
+  int hpb;         // query heads per score block (set by launch_attention)
+  float *scores;   // [token][head][sld] f32 scores
+  int sld;
   double scale;
   const Step *step;
   float *out;
@@ -83,8 +88,8 @@ struct AttnArgs {
 
 int gemv_lpr(int rows, int nslab);
 void launch_gemv(const GemvArgs &a, int epi, const float *xf, int ldx, hipStream_t st);
-void launch_attention(const AttnArgs &a, int B, int ctxMax, int hpb, hipStream_t st);
-size_t attention_lds(int hpb, int hd, int pstride);
+void launch_attention(const AttnArgs &a, int B, hipStream_t st);
+size_t attention_lds(int ctx);
 void launch_norm_quant(const float *x, int ldx, int row0, int nrows, const float *w, double eps, int n, int npad,
                        const Act &act, hipStream_t st);
 void launch_rope(const RopeArgs &a, int B, hipStream_t st);

@@ -208,14 +208,13 @@ __global__ void k_embed(const MatView m, const Step *step, float *x, int ldx) {
 // the block and of each 16-value half (src/compute/ref-kernels.js:44-62).
 __device__ inline void quant_block32(float v, int i, int8_t *xq, float *xd, int32_t *xs, int32_t *xs16) {
   float a = fabsf(v);
-  for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+  a = group_fmax(a, 32);
   double scale = (double)a / 127.0;
   double inv = scale != 0.0 ? 1.0 / scale : 0.0;
   int q = (int)round((double)v * inv);
   xq[i] = (int8_t)q;
-  int s16 = q;
-  for (int o = 1; o < 16; o <<= 1) s16 += __shfl_xor(s16, o, 64);
-  int s32 = s16 + __shfl_xor(s16, 16, 64);
+  const int s16 = wave_sum_xor(q, 16);
+  const int s32 = s16 + swizzle_xor16(s16);
   if ((i & 15) == 0) xs16[i >> 4] = s16;
   if ((i & 31) == 0) { xd[i >> 5] = (float)scale; xs[i >> 5] = s32; }
 }
@@ -476,7 +475,7 @@ __global__ __launch_bounds__(256) void k_gemv(const GemvArgs a) {
         if (t < mt) {
           #pragma unroll
           for (int r = 0; r < 2; r++)
-            for (int o = 1; o < lpr; o <<= 1) acc[r][t] += __shfl_xor(acc[r][t], o, 64);
+            acc[r][t] = wave_sum_xor(acc[r][t], lpr);
         }
       }
       if (j == 0 && valid) {
@@ -585,180 +584,210 @@ __global__ __launch_bounds__(64) void k_qk_rope_kv(const RopeArgs a) {
     for (int i = lane; i < hd; i += 64) src[i] = v[i];
     return;
   }
+  // K rows are position-major ([layer][kv head][pos][dim]); V rows are dimension-major ([layer][kv head][dim][vstride])
+  // so that the attention's weighted sum reads consecutive positions of one dimension
   const long off = (((long)a.layer * a.nHeadKv + head) * a.ctx + pos) * hd;
+  const long voff = ((long)a.layer * a.nHeadKv + head) * hd * a.vstride + pos;
   const float *vs = a.v + (long)b * a.ldkv + (long)head * hd;
   if (a.kvF16) {
-    uint16_t *kc = (uint16_t *)a.kcache + off, *vc = (uint16_t *)a.vcache + off;
-    for (int i = lane; i < hd; i += 64) { kc[i] = f2h(v[i]); vc[i] = f2h(vs[i]); }
+    uint16_t *kc = (uint16_t *)a.kcache + off, *vc = (uint16_t *)a.vcache + voff;
+    for (int i = lane; i < hd; i += 64) { kc[i] = f2h(v[i]); vc[(long)i * a.vstride] = f2h(vs[i]); }
   } else {
-    float *kc = (float *)a.kcache + off, *vc = (float *)a.vcache + off;
-    for (int i = lane; i < hd; i += 64) { kc[i] = v[i]; vc[i] = vs[i]; }
+    float *kc = (float *)a.kcache + off, *vc = (float *)a.vcache + voff;
+    for (int i = lane; i < hd; i += 64) { kc[i] = v[i]; vc[(long)i * a.vstride] = vs[i]; }
   }
 }
 
 // ================================================================================================ attention
-// Causal GQA attention for token b (position step.pos0 + b) and HPB query heads sharing one KV head, with the
-// reference's arithmetic (src/model/forward.js:213-230): scores s = sum_i q_i K_i (f64, in i order), stored f32 after
-// *1/sqrt(hd); softmax with f64 exp and sum, probabilities stored f32; out_i accumulated in f32 over positions in
-// order. The head output is quantised for the output projection in the same kernel, and also stored in f32.
-template <int HPB, int HD, bool F16KV>
-__global__ __launch_bounds__(HPB * HD) void k_attention(const AttnArgs a) {
-  extern __shared__ __align__(16) uint8_t lds[];
-  constexpr int NT = HPB * HD, NW = NT / 64;
-  constexpr int VB = F16KV ? 2 : 4;           // bytes per cached value
-  constexpr int CH = 16384 / (HD * VB);       // positions per staged V chunk (16 KB)
-  constexpr int EPL = 16 / VB;                // K values per lane per 16-byte load
-  constexpr int LP = HD / EPL;                // lanes per position in the score dots
-  constexpr int PPI = NT / LP;                // positions per score iteration
-  const int b = blockIdx.x, hg = blockIdx.y, tid = threadIdx.x;
+// Causal GQA attention with the reference's arithmetic (src/model/forward.js:213-230), in two launches:
+//   k_attn_scores  s_t = f32(sum_i q_i K_t,i (f64, exact products) * 1/sqrt(hd)) for every position t <= pos, one
+//                  block per (64-position chunk, KV head, token): all of K streams in parallel.
+//   k_attn_av      softmax over the scores (e = exp(s - max) in f64, stored f32; p = f32(e * (1/sum e))), then
+//                  out_i = sum_t p_t V_t,i accumulated in f32 in position order, one block per (64-dim slice, query
+//                  head, token); the head output is also quantised for the output projection.
+// Scores live in a [token][head][ctx] f32 buffer between the two.
+
+// Query heads handled by one score block: the largest divisor of the GQA group that is at most 8.
+inline int attn_heads_per_block(int group) {
+  for (int c = 8; c > 1; c--)
+    if (group % c == 0) return c;
+  return 1;
+}
+
+template <int HD, bool F16KV>
+__global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
+  constexpr int VB = F16KV ? 2 : 4;      // bytes per cached value
+  constexpr int EPL = 16 / VB;           // K values per lane per 16-byte load
+  constexpr int LP = HD / EPL;           // lanes per position
+  constexpr int PPI = 256 / LP;          // positions per load round
+  constexpr int P = 64;                  // positions per chunk
+  constexpr int R = P / PPI;             // load rounds per chunk
+  static_assert(R >= 1 && P % PPI == 0, "chunk geometry");
+  __shared__ float qs[8 * HD];
+  const int b = blockIdx.z, tid = threadIdx.x;
   const Step *st = a.step;
   if (b >= st->B) return;
   const int npos = st->pos0 + b + 1;
-  const int h0 = hg * HPB;
-  const int kvh = h0 / (a.nHead / a.nHeadKv);
-  const int ps = a.pstride;
-  float *qs = (float *)lds;                                   // [HPB][HD]
-  float *p = qs + HPB * HD;                                   // [HPB][ps]
-  uint8_t *vbuf = (uint8_t *)(p + HPB * ps);                  // [2][CH][HD] cached values
-  __shared__ double red[HPB * NW];
-  __shared__ float redf[HPB * NW];
-  for (int i = tid; i < HPB * HD; i += NT) qs[i] = a.q[(long)b * a.ldq + (long)h0 * HD + i];
-  __syncthreads();
+  if (blockIdx.x * P >= npos) return;
+  const int group = a.nHead / a.nHeadKv, hg = a.hpb;
+  const int h0 = blockIdx.y * hg;        // first query head of this block
+  const int kvh = h0 / group;
   const long kvoff = ((long)a.layer * a.nHeadKv + kvh) * a.ctx * HD;
   const uint8_t *kbase = (const uint8_t *)a.kcache + kvoff * VB;
-  const uint8_t *vbase = (const uint8_t *)a.vcache + kvoff * VB;
-  // ---- scores: LP lanes per position, each an exact-product f64 partial dot over EPL elements, then a butterfly
-  const int part = tid % LP;
-  float lmax[HPB];
-  #pragma unroll
-  for (int h = 0; h < HPB; h++) lmax[h] = -INFINITY;
-  for (int t0 = 0; t0 < npos; t0 += PPI) {
-    const int t = t0 + tid / LP;
-    double s[HPB];
+  float *srow = a.scores + ((long)b * a.nHead + h0) * a.sld;
+  const int part = tid % LP, sub = tid / LP;
+  uint4 u[R];
+  auto fetch = [&](int c0) {
     #pragma unroll
-    for (int h = 0; h < HPB; h++) s[h] = 0.0;
-    if (t < npos) {
-      uint4 u = *(const uint4 *)(kbase + ((long)t * HD + part * EPL) * VB);
-      uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+    for (int r = 0; r < R; r++) {
+      const int t = c0 + r * PPI + sub;
+      u[r] = t < npos ? *(const uint4 *)(kbase + ((long)t * HD + part * EPL) * VB) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  fetch(blockIdx.x * P);  // the first chunk's keys are in flight while q is staged
+  for (int i = tid; i < hg * HD; i += 256) qs[i] = a.q[(long)b * a.ldq + (long)h0 * HD + i];
+  __syncthreads();
+  for (int c0 = blockIdx.x * P; c0 < npos; c0 += gridDim.x * P) {
+    if (c0 != blockIdx.x * P) fetch(c0);
+    #pragma unroll
+    for (int r = 0; r < R; r++) {
+      const int t = c0 + r * PPI + sub;
+      const uint32_t w4[4] = {u[r].x, u[r].y, u[r].z, u[r].w};
+      double kv[EPL];
       #pragma unroll
-      for (int e = 0; e < EPL; e++) {
-        double kv = F16KV ? (double)h2f((uint16_t)((w4[e >> 1] >> (16 * (e & 1))) & 0xffff)) : (double)__uint_as_float(w4[e]);
+      for (int e = 0; e < EPL; e++)
+        kv[e] = F16KV ? (double)h2f((uint16_t)((w4[e >> 1] >> (16 * (e & 1))) & 0xffff)) : (double)__uint_as_float(w4[e]);
+      for (int h = 0; h < hg; h++) {
+        const float *qh = qs + h * HD + part * EPL;
+        double s = 0.0;
         #pragma unroll
-        for (int h = 0; h < HPB; h++) s[h] = fma((double)qs[h * HD + part * EPL + e], kv, s[h]);
-      }
-    }
-    #pragma unroll
-    for (int h = 0; h < HPB; h++)
-      for (int o = 1; o < LP; o <<= 1) s[h] += __shfl_xor(s[h], o, 64);
-    if (part == 0 && t < npos) {
-      #pragma unroll
-      for (int h = 0; h < HPB; h++) {
-        float v = (float)(s[h] * a.scale);
-        p[h * ps + t] = v;
-        lmax[h] = fmaxf(lmax[h], v);
+        for (int e = 0; e < EPL; e++) s = fma((double)qh[e], kv[e], s);
+        s = wave_sum_xor(s, LP);
+        if (part == (h % LP) && t < npos) srow[(long)h * a.sld + t] = (float)(s * a.scale);
       }
     }
   }
-  #pragma unroll
-  for (int h = 0; h < HPB; h++) {
-    float m = lmax[h];
-    for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    if ((tid & 63) == 0) redf[h * NW + (tid >> 6)] = m;
-  }
-  __syncthreads();
-  double mx[HPB], sum[HPB];
-  #pragma unroll
-  for (int h = 0; h < HPB; h++) {
-    float m = redf[h * NW];
-    for (int w = 1; w < NW; w++) m = fmaxf(m, redf[h * NW + w]);
-    mx[h] = (double)m;
-    sum[h] = 0.0;
-  }
-  // ---- softmax (src/compute/ref-kernels.js:313-320): e = exp(s - max) stored f32, sum of the unrounded e, p = e * (1/sum)
-  for (int t = tid; t < npos; t += NT) {
-    #pragma unroll
-    for (int h = 0; h < HPB; h++) {
-      double e = exp((double)p[h * ps + t] - mx[h]);
-      p[h * ps + t] = (float)e;
-      sum[h] += e;
-    }
-  }
-  #pragma unroll
-  for (int h = 0; h < HPB; h++) {
-    double sm = wave_sum_xor(sum[h], 64);
-    if ((tid & 63) == 0) red[h * NW + (tid >> 6)] = sm;
-  }
-  __syncthreads();
-  double inv[HPB];
-  #pragma unroll
-  for (int h = 0; h < HPB; h++) {
-    double sm = red[h * NW];
-    for (int w = 1; w < NW; w++) sm += red[h * NW + w];
-    inv[h] = 1.0 / sm;
-  }
-  for (int t = tid; t < npos; t += NT) {
-    #pragma unroll
-    for (int h = 0; h < HPB; h++) p[h * ps + t] = (float)((double)p[h * ps + t] * inv[h]);
-  }
-  // ---- weighted sum of V: thread -> (head tid / HD, dim tid % HD), f32 accumulation in position order. V is staged
-  // through LDS in chunks of CH positions (double buffered: the next chunk's loads are in flight during the chain).
-  constexpr int CB = CH * HD * VB;                            // chunk bytes
-  constexpr int LPT = (CB / 16 + NT - 1) / NT;                // 16-byte loads per thread per chunk
-  const int h = tid / HD, i = tid % HD;
-  const float *ph = p + h * ps;
-  const int nch = (npos + CH - 1) / CH;
+}
+
+// One block per (32-dim slice, query head, token). The slice's V rows (dimension-major in the cache) are staged
+// through LDS in chunks of 256 (f16) or 128 (f32) positions, double buffered, the first chunk during the softmax. The
+// chain runs on lanes 0-31 of wave 0, one output dimension each, reading 16 bytes of consecutive positions at a time.
+constexpr int AV_DIMS = 32;       // output dimensions per block
+constexpr int AV_ROW = 512;       // bytes of one dimension's positions per chunk
+constexpr int AV_PITCH = AV_ROW + 16;   // LDS row pitch (the pad spreads the chain's rows over the banks)
+constexpr int AV_CHUNK = AV_DIMS * AV_PITCH;
+constexpr int AV_UNIT = 32;       // positions per unrolled step of the weighted sum
+
+template <bool F16KV>
+__global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int VB = F16KV ? 2 : 4;
+  constexpr int CT = AV_ROW / VB;        // positions per chunk
+  constexpr int EPP = 16 / VB;           // positions per 16-byte piece
+  constexpr int PPR = AV_ROW / 16;       // pieces per row
+  constexpr int LPT = AV_DIMS * PPR / 256;   // 16-byte loads per thread per chunk
+  const int slice = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const Step *st = a.step;
+  if (b >= st->B) return;
+  const int npos = st->pos0 + b + 1;
+  const int hd = a.hd, kvh = h / (a.nHead / a.nHeadKv);
+  float *p = (float *)lds;                                // [ctx rounded up to AV_UNIT] probabilities
+  uint8_t *vbuf = lds + (size_t)((a.ctx + AV_UNIT - 1) / AV_UNIT * AV_UNIT) * 4;  // [2][AV_DIMS][AV_PITCH] staged V rows
+  __shared__ double redd[4];
+  __shared__ float redf[4];
+  const uint8_t *vbase = (const uint8_t *)a.vcache + (((long)a.layer * a.nHeadKv + kvh) * hd + (long)slice * AV_DIMS) * a.vstride * VB;
+  const int nch = (npos + CT - 1) / CT;
   uint4 pre[LPT];
   auto fetch = [&](int c) {
-    const long base = (long)c * CH * HD * VB;
-    const long lim = (long)npos * HD * VB;                    // rows past the last position are not read
     #pragma unroll
     for (int k = 0; k < LPT; k++) {
-      const int off = (k * NT + tid) * 16;
-      pre[k] = (off < CB && base + off < lim) ? *(const uint4 *)(vbase + base + off) : make_uint4(0, 0, 0, 0);
+      const int idx = k * 256 + tid, dim = idx / PPR, t = c * CT + (idx % PPR) * EPP;
+      pre[k] = t < npos ? *(const uint4 *)(vbase + ((long)dim * a.vstride + t) * VB) : make_uint4(0, 0, 0, 0);
     }
   };
   auto store = [&](int buf) {
     #pragma unroll
     for (int k = 0; k < LPT; k++) {
-      const int off = (k * NT + tid) * 16;
-      if (off < CB) *(uint4 *)(vbuf + buf * CB + off) = pre[k];
+      const int idx = k * 256 + tid;
+      *(uint4 *)(vbuf + buf * AV_CHUNK + (idx / PPR) * AV_PITCH + (idx % PPR) * 16) = pre[k];
     }
   };
-  fetch(0);
+  fetch(0);  // the first V chunk is in flight during the softmax
+  // ---- softmax (src/compute/ref-kernels.js:313-320)
+  const float *srow = a.scores + ((long)b * a.nHead + h) * a.sld;
+  float mx = -INFINITY;
+  for (int t0 = 0; t0 < npos; t0 += 1024) {
+    float v[4];
+    #pragma unroll
+    for (int k = 0; k < 4; k++) { const int t = t0 + k * 256 + tid; v[k] = t < npos ? srow[t] : -INFINITY; }
+    #pragma unroll
+    for (int k = 0; k < 4; k++) { const int t = t0 + k * 256 + tid; if (t < npos) p[t] = v[k]; mx = fmaxf(mx, v[k]); }
+  }
+  mx = group_fmax(mx, 64);
+  if (lane == 0) redf[wave] = mx;
   __syncthreads();
+  const double m = (double)fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
+  double sum = 0.0;
+  for (int t = tid; t < npos; t += 256) {
+    const double e = exp((double)p[t] - m);
+    p[t] = (float)e;
+    sum += e;
+  }
+  sum = wave_sum_xor(sum, 64);
+  if (lane == 0) redd[wave] = sum;
+  __syncthreads();
+  const double inv = 1.0 / ((redd[0] + redd[1]) + (redd[2] + redd[3]));
+  for (int t = tid; t < npos; t += 256) p[t] = (float)((double)p[t] * inv);
+  for (int t = npos + tid; t < (npos + AV_UNIT - 1) / AV_UNIT * AV_UNIT; t += 256) p[t] = 0.f;
   store(0);
   __syncthreads();
+  // ---- weighted sum of V: f32 fma chain in position order, one output dimension per lane (lanes 0-31 of wave 0)
+  const bool chainLane = wave == 0 && lane < AV_DIMS;
   float o = 0.f;
   for (int c = 0; c < nch; c++) {
     if (c + 1 < nch) fetch(c + 1);
-    const int t0 = c * CH, cnt = min(CH, npos - t0);
-    const uint8_t *vb = vbuf + (c & 1) * CB;
-    int tt = 0;
-    for (; tt + 4 <= cnt; tt += 4) {
-      float4 pp = *(const float4 *)(ph + t0 + tt);
-      float v0, v1, v2, v3;
-      if (F16KV) {
-        v0 = h2f(((const uint16_t *)vb)[(tt + 0) * HD + i]); v1 = h2f(((const uint16_t *)vb)[(tt + 1) * HD + i]);
-        v2 = h2f(((const uint16_t *)vb)[(tt + 2) * HD + i]); v3 = h2f(((const uint16_t *)vb)[(tt + 3) * HD + i]);
-      } else {
-        v0 = ((const float *)vb)[(tt + 0) * HD + i]; v1 = ((const float *)vb)[(tt + 1) * HD + i];
-        v2 = ((const float *)vb)[(tt + 2) * HD + i]; v3 = ((const float *)vb)[(tt + 3) * HD + i];
+    if (chainLane) {
+      // units of UNIT positions: all of a unit's LDS reads are issued first, then its fma steps run back to back
+      // (each step waits ~9 cycles on the previous one, so the reads of a unit cost one LDS latency per unit).
+      // p is zero past the last position, so a unit may run past `cnt`: fmaf(0, v, o) == o for the finite cached
+      // values read there.
+      const int t0 = c * CT, cnt = min(CT, npos - t0);
+      const uint8_t *row = vbuf + (c & 1) * AV_CHUNK + lane * AV_PITCH;
+      const float *pc = p + t0;
+      for (int u = 0; u < cnt; u += AV_UNIT) {
+        float4 pv[AV_UNIT / 4];
+        uint4 vv[AV_UNIT * VB / 16];
+        #pragma unroll
+        for (int k = 0; k < AV_UNIT / 4; k++) pv[k] = *(const float4 *)(pc + u + 4 * k);
+        #pragma unroll
+        for (int k = 0; k < AV_UNIT * VB / 16; k++) vv[k] = *(const uint4 *)(row + (u + k * EPP) * VB);
+        #pragma unroll
+        for (int k = 0; k < AV_UNIT / 4; k++) {
+          float v0, v1, v2, v3;
+          if (F16KV) {
+            const uint4 &w = vv[k >> 1];
+            const uint32_t lo = (k & 1) ? w.z : w.x, hi = (k & 1) ? w.w : w.y;
+            v0 = h2f((uint16_t)(lo & 0xffff)); v1 = h2f((uint16_t)(lo >> 16));
+            v2 = h2f((uint16_t)(hi & 0xffff)); v3 = h2f((uint16_t)(hi >> 16));
+          } else {
+            const uint4 &w = vv[k];
+            v0 = __uint_as_float(w.x); v1 = __uint_as_float(w.y); v2 = __uint_as_float(w.z); v3 = __uint_as_float(w.w);
+          }
+          o = fmaf(pv[k].x, v0, o); o = fmaf(pv[k].y, v1, o); o = fmaf(pv[k].z, v2, o); o = fmaf(pv[k].w, v3, o);
+        }
       }
-      o = fmaf(pp.x, v0, o); o = fmaf(pp.y, v1, o); o = fmaf(pp.z, v2, o); o = fmaf(pp.w, v3, o);
-    }
-    for (; tt < cnt; tt++) {
-      float v = F16KV ? h2f(((const uint16_t *)vb)[tt * HD + i]) : ((const float *)vb)[tt * HD + i];
-      o = fmaf(ph[t0 + tt], v, o);
     }
     __syncthreads();
     if (c + 1 < nch) store((c + 1) & 1);
     __syncthreads();
   }
-  const int col = (h0 + h) * HD + i;
-  if (a.out) a.out[(long)b * a.ldo + col] = o;
-  Act act = a.act;
-  quant_block32(o, col, act.q + (long)b * act.ld, act.d + (long)b * (act.ld >> 5), act.s + (long)b * (act.ld >> 5),
-                act.s16 + (long)b * (act.ld >> 4));
+  if (chainLane) {
+    const int col = h * hd + slice * AV_DIMS + lane;
+    if (a.out) a.out[(long)b * a.ldo + col] = o;
+    Act act = a.act;
+    quant_block32(o, col, act.q + (long)b * act.ld, act.d + (long)b * (act.ld >> 5), act.s + (long)b * (act.ld >> 5),
+                  act.s16 + (long)b * (act.ld >> 4));
+  }
 }
 
 // ================================================================================================ synthetic weights
@@ -856,37 +885,47 @@ void launch_gemv(const GemvArgs &a0, int epi, const float *xf, int ldx, hipStrea
   ZL_HIP(hipGetLastError());
 }
 
-template <int HPB, int HD>
-static void launch_attn_hd(const AttnArgs &a, dim3 grid, size_t lds, hipStream_t st) {
-  static size_t attrSet[2] = {64 * 1024, 64 * 1024};  // dynamic LDS above 64 KB must be requested per kernel
-  if (lds > attrSet[a.kvF16]) {
-    if (a.kvF16) ZL_HIP(hipFuncSetAttribute((const void *)k_attention<HPB, HD, true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    else ZL_HIP(hipFuncSetAttribute((const void *)k_attention<HPB, HD, false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    attrSet[a.kvF16] = lds;
-  }
-  if (a.kvF16) hipLaunchKernelGGL((k_attention<HPB, HD, true>), grid, dim3(HPB * HD), lds, st, a);
-  else hipLaunchKernelGGL((k_attention<HPB, HD, false>), grid, dim3(HPB * HD), lds, st, a);
+// Dynamic LDS of one k_attn_av block: the probabilities of ctx positions and two staged V chunks.
+size_t attention_lds(int ctx) { return (size_t)((ctx + AV_UNIT - 1) / AV_UNIT * AV_UNIT) * 4 + 2 * AV_CHUNK; }
+constexpr size_t ATTN_LDS_MAX = 150 * 1024;
+
+template <int HD, bool F16KV>
+static void launch_scores_k(const AttnArgs &a, dim3 grid, hipStream_t st) {
+  hipLaunchKernelGGL((k_attn_scores<HD, F16KV>), grid, dim3(256), 0, st, a);
 }
 
-size_t attention_lds(int hpb, int hd, int pstride) { return (size_t)hpb * hd * 4 + (size_t)hpb * pstride * 4 + 2 * 16384; }
-constexpr size_t ATTN_LDS_MAX = 150 * 1024;  // dynamic LDS of one attention block (the kernel's static LDS is < 1 KB)
-
-void launch_attention(const AttnArgs &a, int B, int ctxMax, int hpb, hipStream_t st) {
-  (void)ctxMax;
-  const size_t lds = attention_lds(hpb, a.hd, a.pstride);
-  ZL_REQUIRE(lds <= ATTN_LDS_MAX, ZL_ERR_UNSUPPORTED, "context too long for the attention kernel");
-  dim3 grid(B, a.nHead / hpb);
-  switch (hpb * 1000 + a.hd) {
-    case 1064: launch_attn_hd<1, 64>(a, grid, lds, st); break;
-    case 1128: launch_attn_hd<1, 128>(a, grid, lds, st); break;
-    case 1256: launch_attn_hd<1, 256>(a, grid, lds, st); break;
-    case 2064: launch_attn_hd<2, 64>(a, grid, lds, st); break;
-    case 2128: launch_attn_hd<2, 128>(a, grid, lds, st); break;
-    case 2256: launch_attn_hd<2, 256>(a, grid, lds, st); break;
-    case 4064: launch_attn_hd<4, 64>(a, grid, lds, st); break;
-    case 4128: launch_attn_hd<4, 128>(a, grid, lds, st); break;
-    default: throw Error(ZL_ERR_UNSUPPORTED, "attention: unsupported heads-per-block / head_dim");
+template <bool F16KV>
+static void launch_av_k(const AttnArgs &a, dim3 grid, size_t lds, hipStream_t st) {
+  static size_t attr = 64 * 1024;  // dynamic LDS above 64 KB must be requested per kernel
+  if (lds > attr) {
+    ZL_HIP(hipFuncSetAttribute((const void *)k_attn_av<F16KV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    attr = lds;
   }
+  hipLaunchKernelGGL((k_attn_av<F16KV>), grid, dim3(256), lds, st, a);
+}
+
+void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
+  AttnArgs a = a0;
+  const size_t lds = attention_lds(a.ctx);
+  ZL_REQUIRE(lds <= ATTN_LDS_MAX, ZL_ERR_UNSUPPORTED, "context too long for the attention kernel");
+  ZL_REQUIRE(a.hd == 64 || a.hd == 128 || a.hd == 256, ZL_ERR_UNSUPPORTED, "attention: head_dim must be 64, 128 or 256");
+  ZL_REQUIRE(a.sld >= a.ctx, ZL_ERR_ARG, "attention: score stride below the context");
+  const int group = a.nHead / a.nHeadKv;
+  a.hpb = attn_heads_per_block(group);
+  const int chunks = (a.ctx + 63) / 64;
+  dim3 gs(chunks < 64 ? chunks : 64, a.nHead / a.hpb, B);
+  switch (a.hd * 2 + a.kvF16) {
+    case 128: launch_scores_k<64, false>(a, gs, st); break;
+    case 129: launch_scores_k<64, true>(a, gs, st); break;
+    case 256: launch_scores_k<128, false>(a, gs, st); break;
+    case 257: launch_scores_k<128, true>(a, gs, st); break;
+    case 512: launch_scores_k<256, false>(a, gs, st); break;
+    case 513: launch_scores_k<256, true>(a, gs, st); break;
+  }
+  ZL_HIP(hipGetLastError());
+  dim3 ga(a.hd / AV_DIMS, a.nHead, B);
+  if (a.kvF16) launch_av_k<true>(a, ga, lds, st);
+  else launch_av_k<false>(a, ga, lds, st);
   ZL_HIP(hipGetLastError());
 }
 

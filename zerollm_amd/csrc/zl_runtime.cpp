@@ -88,6 +88,7 @@ struct Layer {
 struct zl_model {
   zl_config cfg{};
   int ctx = 0, kvF16 = 0, maxBatch = 16, logitsBatch = 16;
+  int vstride = 0;  // positions per V cache row
   bool closed = false;
   zl::Arena ar;
   int64_t weightBytes = 0;
@@ -97,6 +98,7 @@ struct zl_model {
   float *cosT = nullptr, *sinT = nullptr;
   void *kcache = nullptr, *vcache = nullptr;
   float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *hb = nullptr, *logits = nullptr;
+  float *scores = nullptr;  // attention scores [maxBatch][n_head][ctx]
   zl::Act act{};
   zl::Step *dstep = nullptr;
   hipStream_t st = nullptr;
@@ -189,6 +191,8 @@ static void finish_model(zl_model *m, const float *ropeFreqs) {
   ZL_REQUIRE(c.head_dim == 128 || c.head_dim == 64 || c.head_dim == 256, ZL_ERR_UNSUPPORTED,
              "head_dim " + std::to_string(c.head_dim) + " is not supported (64, 128 or 256)");
   ZL_REQUIRE(c.n_head % c.n_head_kv == 0, ZL_ERR_UNSUPPORTED, "n_head must be a multiple of n_head_kv");
+  ZL_REQUIRE(attention_lds(m->ctx) <= 150 * 1024, ZL_ERR_UNSUPPORTED,
+             "context of " + std::to_string(m->ctx) + " tokens is beyond the attention kernel's LDS limit (about 29900 tokens)");
   const int half = c.n_rot / 2;
   // RoPE tables exactly as ropeTables (src/compute/ref-kernels.js:329-342), in f64 on the host, stored f32
   std::vector<float> cs((size_t)m->ctx * half), sn((size_t)m->ctx * half);
@@ -204,11 +208,14 @@ static void finish_model(zl_model *m, const float *ropeFreqs) {
   m->sinT = (float *)m->ar.alloc(sn.size() * 4);
   ZL_HIP(hipMemcpy(m->cosT, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
   ZL_HIP(hipMemcpy(m->sinT, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
-  const size_t kvElems = (size_t)c.n_layer * c.n_head_kv * m->ctx * c.head_dim;
-  m->kcache = m->ar.alloc(kvElems * (m->kvF16 ? 2 : 4));
-  m->vcache = m->ar.alloc(kvElems * (m->kvF16 ? 2 : 4));
-  ZL_HIP(hipMemset(m->kcache, 0, kvElems * (m->kvF16 ? 2 : 4)));
-  ZL_HIP(hipMemset(m->vcache, 0, kvElems * (m->kvF16 ? 2 : 4)));
+  // K: [layer][kv head][pos][dim]; V: [layer][kv head][dim][vstride] (vstride = ctx rounded up to 16 positions)
+  m->vstride = (m->ctx + 15) / 16 * 16;
+  const size_t kElems = (size_t)c.n_layer * c.n_head_kv * m->ctx * c.head_dim;
+  const size_t vElems = (size_t)c.n_layer * c.n_head_kv * c.head_dim * m->vstride;
+  m->kcache = m->ar.alloc(kElems * (m->kvF16 ? 2 : 4));
+  m->vcache = m->ar.alloc(vElems * (m->kvF16 ? 2 : 4));
+  ZL_HIP(hipMemset(m->kcache, 0, kElems * (m->kvF16 ? 2 : 4)));
+  ZL_HIP(hipMemset(m->vcache, 0, vElems * (m->kvF16 ? 2 : 4)));
   const int B = m->maxBatch;
   m->x = (float *)m->ar.alloc((size_t)B * c.n_embd * 4);
   m->q = (float *)m->ar.alloc((size_t)B * qdim(m) * 4);
@@ -216,6 +223,7 @@ static void finish_model(zl_model *m, const float *ropeFreqs) {
   m->v = (float *)m->ar.alloc((size_t)B * kvdim(m) * 4);
   m->hb = (float *)m->ar.alloc((size_t)B * c.n_ff * 4);
   m->logits = (float *)m->ar.alloc((size_t)m->logitsBatch * c.vocab * 4);
+  m->scores = (float *)m->ar.alloc((size_t)B * c.n_head * m->ctx * 4);
   const int ld = pad64(std::max(c.n_embd, std::max(qdim(m), c.n_ff)));
   m->act.ld = ld;
   m->act.q = (int8_t *)m->ar.alloc((size_t)B * ld);
@@ -284,20 +292,15 @@ static void enqueue_forward(zl_model *m, int B, int want) {
     ra.cosT = m->cosT; ra.sinT = m->sinT;
     ra.nRot = c.n_rot; ra.neox = c.neox; ra.nHead = c.n_head; ra.nHeadKv = c.n_head_kv; ra.hd = c.head_dim;
     ra.ctx = m->ctx; ra.layer = l; ra.kvF16 = m->kvF16; ra.kcache = m->kcache; ra.vcache = m->vcache; ra.step = m->dstep;
+    ra.vstride = m->vstride;
     launch_rope(ra, B, m->st);
     AttnArgs aa;
     aa.q = m->q; aa.ldq = qd; aa.kcache = m->kcache; aa.vcache = m->vcache;
     aa.nHead = c.n_head; aa.nHeadKv = c.n_head_kv; aa.hd = c.head_dim; aa.ctx = m->ctx; aa.layer = l; aa.kvF16 = m->kvF16;
-    aa.pstride = (m->ctx + 3) / 4 * 4;
+    aa.vstride = m->vstride; aa.hpb = 1; aa.scores = m->scores; aa.sld = m->ctx;
     aa.scale = 1.0 / sqrt((double)c.head_dim);
     aa.step = m->dstep; aa.out = m->act.f; aa.ldo = m->act.ld; aa.act = m->act;
-    // heads per block: the whole GQA group when it fits (K and V are then read once per group)
-    const int group = c.n_head / c.n_head_kv;
-    int hpb = 1;
-    for (int cand : {4, 2}) {
-      if (group % cand == 0 && cand * c.head_dim <= 512 && attention_lds(cand, c.head_dim, aa.pstride) <= 150 * 1024) { hpb = cand; break; }
-    }
-    launch_attention(aa, B, m->ctx, hpb, m->st);
+    launch_attention(aa, B, m->st);
     gemv_group(m, {{&L.wo, nullptr, 0, nullptr}}, B, EPI_RESID);
     launch_norm_quant(m->x, d, 0, B, L.ffnNorm, eps, d, pad64(d), m->act, m->st);
     ZL_REQUIRE(L.wgate.type == L.wup.type, ZL_ERR_UNSUPPORTED, "ffn_gate and ffn_up must share a type");
