@@ -67,7 +67,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the speculative step runs on a single MI355X (asked for --gpus {args.gpus}); "
-              "see DESIGN.md for how the path would shard", file=sys.stderr)
+              "across GPUs it shards as independent sequences per GPU (data parallel), not by splitting a pass",
+              file=sys.stderr)
         sys.exit(2)
 
     from oracle import oracle as O
