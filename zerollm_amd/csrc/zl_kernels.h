@@ -56,6 +56,12 @@ struct GemvArgs {
   int ldr;
   float *hb;
   int ldh;
+  // Fused activation prologue: when xf is set, each block quantises rows xf[xrow0 + t] (length n, stride ldxf) itself,
+  // after RMSNorm with weights nw when nw is set, exactly as k_norm_quant would, instead of reading `act`.
+  const float *xf;
+  int ldxf, xrow0, n;
+  const float *nw;
+  double eps;
 };
 
 struct RopeArgs {
@@ -87,6 +93,7 @@ struct AttnArgs {
 };
 
 int gemv_lpr(int rows, int nslab);
+size_t gemv_lds_bytes(int fmt, int mt, int K);
 void launch_gemv(const GemvArgs &a, int epi, const float *xf, int ldx, hipStream_t st);
 void launch_attention(const AttnArgs &a, int B, hipStream_t st);
 size_t attention_lds(int ctx);

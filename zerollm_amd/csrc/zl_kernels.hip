@@ -1,5 +1,5 @@
-// Forward-pass kernels for gfx950: weight repack, dequantisation, RMSNorm + int8 activation quantisation, the k-quant
-// GEMV family (M = 1..64 tokens), per-head q/k RMSNorm + RoPE + KV append, and causal GQA attention.
+// Forward-pass kernels for gfx950: weight repack, dequantisation, RMSNorm + int8 activation quantisation, per-head q/k
+// RMSNorm + RoPE + KV append, and causal GQA attention (the GEMV family is in zl_gemv.hip).
 //
 // Numerics follow zerollm's reference path (src/model/forward.js:184-248, src/compute/ref-kernels.js): integer block
 // dots are exact; every scale combination, norm, softmax and RoPE step is done in f64 with the reference's rounding
@@ -249,300 +249,6 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x,
     if (i < n) v = w ? (float)((double)xr[i] * s * (double)w[i]) : xr[i];
     if (act.f) act.f[(long)b * act.ld + i] = v;
     quant_block32(v, i, xq, xd, xs, xs16);
-  }
-}
-
-// ================================================================================================ GEMV
-// y[t][r] = sum over the row's blocks of the reference's per-block term (src/compute/ref-kernels.js:132-277), for
-// M tokens at once. Mapping: `lpr` lanes share a row and take its 64-value slabs round robin (lane j: slabs j, j+lpr,
-// ...), each lane adds its blocks' f64 terms in slab order, then a butterfly over the lpr lanes. The per-(row, token)
-// arithmetic does not depend on M, so a batched pass gives the same bits as token-by-token passes. Int8 activations
-// of MT tokens are staged in LDS one K-window at a time (window = multiple of 64*lpr, so the slab order is kept).
-
-constexpr int GEMV_LDS_MAX = 96 * 1024;  // staged activations per block (MT tokens x K-window int8)
-constexpr int GEMV_MAX_BLOCKS = 1024;     // row-pair blocks beyond this stride over the rows
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-// weights are read once per pass: non-temporal loads keep them from displacing activations in the caches
-__device__ inline u32x4 ldnt4(const void *p) { return __builtin_nontemporal_load((const u32x4 *)p); }
-__device__ inline u32x2 ldnt2(const void *p) { return __builtin_nontemporal_load((const u32x2 *)p); }
-
-// Raw planes of one slab as loaded (unpacked only when used, so the next slab's loads stay in flight meanwhile).
-struct SlabRaw {
-  uint32_t L[16];  // Q8_0: 16 words of int8; others: 8 words of nibbles
-  uint32_t H[4];   // Q5_0/Q5_K: 2 words of 5th bits; Q6_K: 4 words of top-2 bits
-  uint32_t scw;    // scale codes (K-quants)
-  uint32_t dw;     // f16 scales: (d0 | d1 << 16) for Q8_0/Q4_0/Q5_0, (d | dmin << 16) for Q4_K/Q5_K, d for Q6_K
-};
-
-template <int FMT>
-__device__ inline void load_raw(const MatView &m, long idx, int r, int s, SlabRaw &o) {
-  if (FMT == T_Q8_0) {
-    const uint8_t *p = m.qs + idx * 64;
-    #pragma unroll
-    for (int i = 0; i < 4; i++) { u32x4 v = ldnt4(p + 16 * i); o.L[4 * i] = v.x; o.L[4 * i + 1] = v.y; o.L[4 * i + 2] = v.z; o.L[4 * i + 3] = v.w; }
-    o.dw = __builtin_nontemporal_load((const uint32_t *)(m.dd + idx * 2));
-    return;
-  }
-  const uint8_t *p = m.qs + idx * 32;
-  u32x4 a = ldnt4(p), b = ldnt4(p + 16);
-  o.L[0] = a.x; o.L[1] = a.y; o.L[2] = a.z; o.L[3] = a.w; o.L[4] = b.x; o.L[5] = b.y; o.L[6] = b.z; o.L[7] = b.w;
-  if (FMT == T_Q5_0 || FMT == T_Q5_K) { u32x2 h = ldnt2(m.qx + idx * 8); o.H[0] = h.x; o.H[1] = h.y; }
-  if (FMT == T_Q6_K) { u32x4 h = ldnt4(m.qx + idx * 16); o.H[0] = h.x; o.H[1] = h.y; o.H[2] = h.z; o.H[3] = h.w; }
-  if (FMT == T_Q4_0 || FMT == T_Q5_0) o.dw = __builtin_nontemporal_load((const uint32_t *)(m.dd + idx * 2));
-  if (FMT == T_Q4_K || FMT == T_Q5_K) {
-    o.scw = __builtin_nontemporal_load((const uint32_t *)(m.sc + idx * 4));
-    o.dw = __builtin_nontemporal_load((const uint32_t *)(m.dd + ((long)r * (m.nslab >> 2) + (s >> 2)) * 2));
-  }
-  if (FMT == T_Q6_K) {
-    o.scw = __builtin_nontemporal_load((const uint32_t *)(m.sc + idx * 4));
-    o.dw = __builtin_nontemporal_load(m.dd + (long)r * (m.nslab >> 2) + (s >> 2));
-  }
-}
-
-// 64 values of the slab as int8 lanes (natural value order), unsigned codes for the offset formats.
-template <int FMT>
-__device__ inline void unpack(const SlabRaw &o, uint32_t *w) {
-  if (FMT == T_Q8_0) {
-    #pragma unroll
-    for (int i = 0; i < 16; i++) w[i] = o.L[i];
-    return;
-  }
-  if (FMT == T_Q6_K) {
-    #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      w[i] = (o.L[i] & 0x0F0F0F0Fu) | ((o.H[i] & 0x03030303u) << 4);
-      w[4 + i] = (o.L[4 + i] & 0x0F0F0F0Fu) | ((o.H[i] & 0x0C0C0C0Cu) << 2);
-      w[8 + i] = ((o.L[i] >> 4) & 0x0F0F0F0Fu) | (o.H[i] & 0x30303030u);
-      w[12 + i] = ((o.L[4 + i] >> 4) & 0x0F0F0F0Fu) | ((o.H[i] & 0xC0C0C0C0u) >> 2);
-    }
-    return;
-  }
-  #pragma unroll
-  for (int i = 0; i < 8; i++) { w[i] = o.L[i] & 0x0F0F0F0Fu; w[8 + i] = (o.L[i] >> 4) & 0x0F0F0F0Fu; }
-  if (FMT == T_Q5_0 || FMT == T_Q5_K) {
-    #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      w[i] |= (((o.H[0] >> (4 * i)) & 15u) * 0x00204081u & 0x01010101u) << 4;
-      w[8 + i] |= (((o.H[1] >> (4 * i)) & 15u) * 0x00204081u & 0x01010101u) << 4;
-    }
-  }
-}
-
-// acc += this slab's terms for one token, in the reference's order and rounding (src/compute/ref-kernels.js:132-277).
-template <int FMT>
-__device__ inline double slab_terms(const uint32_t *w, const SlabRaw &o, const uint32_t *X, const float *xd,
-                                    const int32_t *xs, const int32_t *xs16, double acc) {
-  const float d0 = h2f(o.dw & 0xffff), d1 = h2f(o.dw >> 16);
-  if (FMT == T_Q6_K) {
-    int g[4];
-    #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      int a = 0;
-      #pragma unroll
-      for (int i = 0; i < 4; i++) a = sdot4((int)w[4 * k + i], (int)X[4 * k + i], a);
-      g[k] = a - 32 * xs16[k];
-    }
-    const double d = (double)d0;
-    #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      double sc = (double)(int8_t)((o.scw >> (8 * k)) & 0xff);
-      acc = acc + (double)xd[k >> 1] * d * sc * (double)g[k];  // ((xd*d)*scale)*gsum
-    }
-    return acc;
-  }
-  int lo = 0, hi = 0;
-  #pragma unroll
-  for (int i = 0; i < 8; i++) lo = sdot4((int)w[i], (int)X[i], lo);
-  #pragma unroll
-  for (int i = 8; i < 16; i++) hi = sdot4((int)w[i], (int)X[i], hi);
-  if (FMT == T_Q8_0) {
-    acc = acc + (double)lo * (double)d0 * (double)xd[0];
-    acc = acc + (double)hi * (double)d1 * (double)xd[1];
-    return acc;
-  }
-  if (FMT == T_Q4_0 || FMT == T_Q5_0) {
-    const int off = FMT == T_Q4_0 ? 8 : 16;
-    acc = acc + (double)(lo - off * xs[0]) * (double)d0 * (double)xd[0];
-    acc = acc + (double)(hi - off * xs[1]) * (double)d1 * (double)xd[1];
-    return acc;
-  }
-  // Q4_K / Q5_K: xd * (d*sc*sum(q*xq) - dmin*mn*sum(xq))
-  const double d = (double)d0, dm = (double)d1;
-  const double sc0 = (double)(o.scw & 0xff), sc1 = (double)((o.scw >> 8) & 0xff);
-  const double mn0 = (double)((o.scw >> 16) & 0xff), mn1 = (double)(o.scw >> 24);
-  acc = acc + (double)xd[0] * (d * sc0 * (double)lo - dm * mn0 * (double)xs[0]);
-  acc = acc + (double)xd[1] * (d * sc1 * (double)hi - dm * mn1 * (double)xs[1]);
-  return acc;
-}
-
-// y[t][r] = sum over the row's blocks of the reference's per-block term, for M tokens at once.
-// Mapping: `lpr` lanes share a pair of rows (a gate/up pair for SWIGLU) and take the row's 64-value slabs round robin
-// (lane j: slabs j, j+lpr, ...); each lane adds its blocks' f64 terms in slab order, then a butterfly over the lpr
-// lanes. lpr is fixed per matrix, so the per-(row, token) arithmetic does not depend on M: a batched pass gives the
-// same bits as token-by-token passes. The int8 activations of MT tokens are staged in LDS (one K-window when they fit,
-// else windows that are multiples of 64*lpr, which keeps the slab order). Blocks stride over row pairs; the next
-// slab's planes are loaded while the current one is computed.
-template <int FMT, int MT, int EPI>
-__global__ __launch_bounds__(256) void k_gemv(const GemvArgs a) {
-  extern __shared__ __align__(16) uint8_t lds[];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int lpr = a.lpr, slots = 64 / lpr, slot = lane / lpr, j = lane % lpr;
-  const int nunits = EPI == EPI_SWIGLU ? a.rows_total : (a.rows_total + 1) / 2;
-  const int upb = 4 * slots;  // units per block per iteration
-  const int nslab = a.nslab, K = nslab * 64;
-  const bool windowed = a.wk < K;
-  for (int t0 = 0; t0 < a.M; t0 += MT) {
-    const int mt = min(MT, a.M - t0);
-    auto stage = [&](int k0, int kw) {
-      __syncthreads();
-      const int pieces = kw >> 4;
-      for (int p = threadIdx.x; p < mt * pieces; p += 256) {
-        int t = p / pieces, c = p % pieces;
-        *(uint4 *)(lds + (long)t * kw + 16 * c) = *(const uint4 *)(a.act.q + (long)(t0 + t) * a.act.ld + k0 + 16 * c);
-      }
-      __syncthreads();
-    };
-    if (!windowed) stage(0, K);
-    for (int ub = blockIdx.x * upb; ub < nunits; ub += gridDim.x * upb) {
-      const int unit = ub + wave * slots + slot;
-      const bool valid = unit < nunits;
-      const int u = valid ? unit : nunits - 1;
-      int segi[2], lrow[2];
-      MatView mv[2];
-      #pragma unroll
-      for (int r = 0; r < 2; r++) {
-        int si = 0, base = 0, g;
-        if (EPI == EPI_SWIGLU) { si = r; g = u; }
-        else {
-          g = min(2 * u + r, a.rows_total - 1);
-          while (si + 1 < a.nseg && g >= base + a.seg[si].rows) { base += a.seg[si].rows; si++; }
-          g -= base;
-        }
-        segi[r] = si; lrow[r] = g;
-        mv[r] = a.seg[si].m;
-      }
-      double acc[2][MT];
-      #pragma unroll
-      for (int r = 0; r < 2; r++)
-        #pragma unroll
-        for (int t = 0; t < MT; t++) acc[r][t] = 0.0;
-      for (int k0 = 0; k0 < K; k0 += a.wk) {
-        const int kw = min(a.wk, K - k0);
-        if (windowed) stage(k0, kw);
-        const int send = (k0 + kw) >> 6;
-        int s = (k0 >> 6) + j;
-        SlabRaw cur[2], nxt[2];
-        if (s < send) {
-          #pragma unroll
-          for (int r = 0; r < 2; r++) load_raw<FMT>(mv[r], (long)lrow[r] * nslab + s, lrow[r], s, cur[r]);
-        }
-        while (s < send) {
-          const int sn = s + lpr;
-          if (sn < send) {
-            #pragma unroll
-            for (int r = 0; r < 2; r++) load_raw<FMT>(mv[r], (long)lrow[r] * nslab + sn, lrow[r], sn, nxt[r]);
-          }
-          uint32_t w[2][16];
-          #pragma unroll
-          for (int r = 0; r < 2; r++) unpack<FMT>(cur[r], w[r]);
-          const int ls = (s << 6) - k0;
-          const int lw = windowed ? kw : K;
-          #pragma unroll
-          for (int t = 0; t < MT; t++) {
-            if (t < mt) {
-              uint32_t X[16];
-              const uint4 *xp = (const uint4 *)(lds + (long)t * lw + ls);
-              #pragma unroll
-              for (int i = 0; i < 4; i++) { uint4 v = xp[i]; X[4 * i] = v.x; X[4 * i + 1] = v.y; X[4 * i + 2] = v.z; X[4 * i + 3] = v.w; }
-              const long tb = (long)(t0 + t);
-              const float *xd = a.act.d + tb * (a.act.ld >> 5) + 2 * s;
-              const int32_t *xs = a.act.s + tb * (a.act.ld >> 5) + 2 * s;
-              const int32_t *xs16 = a.act.s16 + tb * (a.act.ld >> 4) + 4 * s;
-              #pragma unroll
-              for (int r = 0; r < 2; r++) acc[r][t] = slab_terms<FMT>(w[r], cur[r], X, xd, xs, xs16, acc[r][t]);
-            }
-          }
-          #pragma unroll
-          for (int r = 0; r < 2; r++) cur[r] = nxt[r];
-          s = sn;
-        }
-      }
-      // butterfly over the lpr lanes of this row pair (live tokens only)
-      #pragma unroll
-      for (int t = 0; t < MT; t++) {
-        if (t < mt) {
-          #pragma unroll
-          for (int r = 0; r < 2; r++)
-            acc[r][t] = wave_sum_xor(acc[r][t], lpr);
-        }
-      }
-      if (j == 0 && valid) {
-        #pragma unroll
-        for (int t = 0; t < MT; t++) {
-          if (t >= mt) continue;
-          const long tb = t0 + t;
-          if (EPI == EPI_SWIGLU) {
-            double g = (double)(float)acc[0][t], uu = (double)(float)acc[1][t];
-            double silu = g / (1.0 + exp(-g));  // src/compute/ref-kernels.js:322
-            a.hb[tb * a.ldh + unit] = (float)(silu * uu);
-          } else {
-            #pragma unroll
-            for (int r = 0; r < 2; r++) {
-              if (2 * unit + r >= a.rows_total) continue;
-              const GemvSeg &sg = a.seg[segi[r]];
-              float y = (float)acc[r][t];
-              if (EPI == EPI_RESID) {
-                float *xp = a.resid + tb * a.ldr + lrow[r];
-                *xp = (float)((double)*xp + (double)y);
-              } else {
-                if (sg.bias) y = (float)((double)y + (double)sg.bias[lrow[r]]);
-                sg.out[tb * sg.ldo + lrow[r]] = y;
-              }
-            }
-          }
-        }
-      }
-    }
-  }
-}
-
-// Float weights (F32/F16/BF16) use the f32 activation (src/compute/ref-kernels.js:278-299): one wave per row,
-// sequential f64 sum per lane over a strided subset, then a butterfly.
-template <int EPI>
-__global__ __launch_bounds__(256) void k_gemv_float(const GemvArgs a, const float *__restrict__ xf, int ldx) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int row = blockIdx.x * 4 + wave;
-  const bool swig = EPI == EPI_SWIGLU;
-  if (row >= a.rows_total) return;
-  for (int t = 0; t < a.M; t++) {
-    double accs[2] = {0.0, 0.0};
-    for (int r = 0; r < (swig ? 2 : 1); r++) {
-      int g = swig ? row : row, si = swig ? r : 0, base = 0;
-      if (!swig) while (si + 1 < a.nseg && g >= base + a.seg[si].rows) { base += a.seg[si].rows; si++; }
-      const MatView &m = a.seg[si].m;
-      int lr = g - base;
-      double acc = 0;
-      for (int c = lane; c < m.cols; c += 64) {
-        long e = (long)lr * m.cols + c;
-        float wv = m.type == T_F32 ? ((const float *)m.qs)[e] : m.type == T_F16 ? h2f(((const uint16_t *)m.qs)[e])
-                                                                                : __uint_as_float((uint32_t)((const uint16_t *)m.qs)[e] << 16);
-        acc = acc + (double)wv * (double)xf[(long)t * ldx + c];
-      }
-      acc = wave_sum_xor(acc, 64);
-      accs[r] = acc;
-      if (!swig && lane == 0) {
-        const GemvSeg &sg = a.seg[si];
-        float y = (float)acc;
-        if (EPI == EPI_RESID) { float *xp = a.resid + (long)t * a.ldr + lr; *xp = (float)((double)*xp + (double)y); }
-        else { if (sg.bias) y = (float)((double)y + (double)sg.bias[lr]); sg.out[(long)t * sg.ldo + lr] = y; }
-      }
-    }
-    if (swig && lane == 0) {
-      double g = (double)(float)accs[0], u = (double)(float)accs[1];
-      a.hb[(long)t * a.ldh + row] = (float)(g / (1.0 + exp(-g)) * u);
-    }
   }
 }
 
@@ -808,83 +514,6 @@ __global__ void k_fill_f32(float *p, long n, float v) {
 }
 
 // ================================================================================================ launch helpers
-template <int FMT, int MT, int EPI>
-static void launch_gemv_k(const GemvArgs &a, int blocks, size_t ldsBytes, hipStream_t st) {
-  static bool attr = false;
-  if (!attr) {
-    ZL_HIP(hipFuncSetAttribute((const void *)k_gemv<FMT, MT, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize, GEMV_LDS_MAX));
-    attr = true;
-  }
-  hipLaunchKernelGGL((k_gemv<FMT, MT, EPI>), dim3(blocks), dim3(256), ldsBytes, st, a);
-}
-
-template <int FMT, int MT>
-static void launch_gemv_fmt(const GemvArgs &a, int epi, int blocks, size_t ldsBytes, hipStream_t st) {
-  if (epi == EPI_STORE) launch_gemv_k<FMT, MT, EPI_STORE>(a, blocks, ldsBytes, st);
-  else if (epi == EPI_RESID) launch_gemv_k<FMT, MT, EPI_RESID>(a, blocks, ldsBytes, st);
-  else launch_gemv_k<FMT, MT, EPI_SWIGLU>(a, blocks, ldsBytes, st);
-}
-
-template <int MT>
-static void launch_gemv_mt(int fmt, const GemvArgs &a, int epi, int blocks, size_t ldsBytes, hipStream_t st) {
-  switch (fmt) {
-    case T_Q8_0: launch_gemv_fmt<T_Q8_0, MT>(a, epi, blocks, ldsBytes, st); break;
-    case T_Q4_0: launch_gemv_fmt<T_Q4_0, MT>(a, epi, blocks, ldsBytes, st); break;
-    case T_Q5_0: launch_gemv_fmt<T_Q5_0, MT>(a, epi, blocks, ldsBytes, st); break;
-    case T_Q4_K: launch_gemv_fmt<T_Q4_K, MT>(a, epi, blocks, ldsBytes, st); break;
-    case T_Q5_K: launch_gemv_fmt<T_Q5_K, MT>(a, epi, blocks, ldsBytes, st); break;
-    case T_Q6_K: launch_gemv_fmt<T_Q6_K, MT>(a, epi, blocks, ldsBytes, st); break;
-    default: throw Error(ZL_ERR_UNSUPPORTED, "gemv: unsupported weight type");
-  }
-}
-
-// Lanes per row pair: enough lanes in total to keep the GPU's memory pipes full (about 2^19 lanes), at most 64, at
-// least 8, never more than the row's slabs. Depends only on the matrix shape (rows of the launch, columns).
-int gemv_lpr(int rows, int nslab) {
-  int want = 8;
-  while (want < 64 && (long)want * rows < (1L << 19)) want <<= 1;
-  int cap = 8;
-  while (cap * 2 <= nslab && cap < 64) cap <<= 1;
-  return want < cap ? want : cap;
-}
-
-void launch_gemv(const GemvArgs &a0, int epi, const float *xf, int ldx, hipStream_t st) {
-  GemvArgs a = a0;
-  const int fmt = a.seg[0].m.type;
-  for (int i = 1; i < a.nseg; i++) ZL_REQUIRE(a.seg[i].m.type == fmt && a.seg[i].m.nslab == a.nslab, ZL_ERR_ARG, "gemv: segments differ in type or width");
-  if (!is_quant(fmt)) {
-    int rows = a.rows_total;
-    int blocks = (rows + 3) / 4;
-    if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemv_float<EPI_STORE>), dim3(blocks), dim3(256), 0, st, a, xf, ldx);
-    else if (epi == EPI_RESID) hipLaunchKernelGGL((k_gemv_float<EPI_RESID>), dim3(blocks), dim3(256), 0, st, a, xf, ldx);
-    else hipLaunchKernelGGL((k_gemv_float<EPI_SWIGLU>), dim3(blocks), dim3(256), 0, st, a, xf, ldx);
-    ZL_HIP(hipGetLastError());
-    return;
-  }
-  const int lpr = a.lpr;
-  const int slots = 64 / lpr;
-  const int units = epi == EPI_SWIGLU ? a.rows_total : (a.rows_total + 1) / 2;
-  const int MT = a.M <= 1 ? 1 : a.M <= 2 ? 2 : a.M <= 4 ? 4 : a.M <= 8 ? 8 : 16;
-  // K window: all of K when MT rows of it fit the LDS budget, else the largest multiple of 64*lpr that does
-  const int K = a.nslab * 64;
-  const int step = 64 * lpr;
-  int wk = (GEMV_LDS_MAX / MT) / step * step;
-  if (wk < step) wk = step;
-  if (wk > K) wk = K;
-  a.wk = wk;
-  const size_t ldsBytes = (size_t)MT * wk;
-  int blocks = (units + 4 * slots - 1) / (4 * slots);
-  if (wk == K && blocks > GEMV_MAX_BLOCKS) blocks = GEMV_MAX_BLOCKS;
-  switch (MT) {
-    case 1: launch_gemv_mt<1>(fmt, a, epi, blocks, ldsBytes, st); break;
-    case 2: launch_gemv_mt<2>(fmt, a, epi, blocks, ldsBytes, st); break;
-    case 4: launch_gemv_mt<4>(fmt, a, epi, blocks, ldsBytes, st); break;
-    case 8: launch_gemv_mt<8>(fmt, a, epi, blocks, ldsBytes, st); break;
-    default: launch_gemv_mt<16>(fmt, a, epi, blocks, ldsBytes, st); break;
-  }
-  ZL_HIP(hipGetLastError());
-}
-
 // Dynamic LDS of one k_attn_av block: the probabilities of ctx positions and two staged V chunks.
 size_t attention_lds(int ctx) { return (size_t)((ctx + AV_UNIT - 1) / AV_UNIT * AV_UNIT) * 4 + 2 * AV_CHUNK; }
 constexpr size_t ATTN_LDS_MAX = 150 * 1024;

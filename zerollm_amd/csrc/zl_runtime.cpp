@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <chrono>
+#include <functional>
 #include <map>
 #include <memory>
 #include <thread>
@@ -53,8 +54,8 @@ struct Arena {
   }
 };
 
-// Allocate the planes of a rows x cols matrix of `type` and repack raw ggml rows (device pointer) into them.
-static DevMat make_mat(Arena &ar, int type, int rows, int cols, const uint8_t *draw, hipStream_t st) {
+// Planes of a rows x cols matrix of `type` (not yet filled).
+static DevMat alloc_planes(Arena &ar, int type, int rows, int cols) {
   DevMat m;
   m.type = type; m.rows = rows; m.cols = cols;
   m.nslab = (cols + 63) / 64;
@@ -64,17 +65,74 @@ static DevMat make_mat(Arena &ar, int type, int rows, int cols, const uint8_t *d
     ZL_REQUIRE(type == T_F32 || type == T_F16 || type == T_BF16, ZL_ERR_UNSUPPORTED,
                "reference kernels: unsupported tensor type " + std::to_string(type) + " (supported: F32, F16, BF16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)");
     m.qs = (uint8_t *)ar.alloc((size_t)rb * rows);
-    ZL_HIP(hipMemcpyAsync(m.qs, draw, (size_t)rb * rows, hipMemcpyDeviceToDevice, st));
     return m;
   }
   const long ns = (long)rows * m.nslab;
+  ZL_REQUIRE(ns < (1L << 31) / 64, ZL_ERR_UNSUPPORTED, "matrix too large");
   m.qs = (uint8_t *)ar.alloc(ns * qs_bytes(type));
   if (qx_bytes(type)) m.qx = (uint8_t *)ar.alloc(ns * qx_bytes(type));
   if (sc_bytes(type)) m.sc = (uint8_t *)ar.alloc(ns * sc_bytes(type));
   long nd = (type == T_Q4_K || type == T_Q5_K) ? (long)rows * (m.nslab / 4) * 2 : type == T_Q6_K ? (long)rows * (m.nslab / 4) : ns * 2;
   m.dd = (uint16_t *)ar.alloc(nd * 2);
-  launch_repack(type, draw, rb, rows, cols, m.nslab, m, st);
   return m;
+}
+
+// Rows [row0, row0 + n) of m as a matrix of its own: every plane is row-major, so the view is an offset into each.
+static DevMat row_view(const DevMat &m, int row0, int n) {
+  DevMat v = m;
+  v.rows = n;
+  if (!is_quant(m.type)) {
+    v.qs = m.qs + (size_t)ggml_row_bytes(m.type, m.cols) * row0;
+    return v;
+  }
+  const long ns = (long)row0 * m.nslab;
+  v.qs = m.qs + ns * qs_bytes(m.type);
+  if (m.qx) v.qx = m.qx + ns * qx_bytes(m.type);
+  if (m.sc) v.sc = m.sc + ns * sc_bytes(m.type);
+  v.dd = m.dd + ((m.type == T_Q4_K || m.type == T_Q5_K) ? (long)row0 * (m.nslab / 4) * 2 : m.type == T_Q6_K ? (long)row0 * (m.nslab / 4) : ns * 2);
+  return v;
+}
+
+// Fill the planes of m (or of a row view of a larger matrix) from raw ggml rows (device pointer).
+static void fill_planes(const DevMat &m, const uint8_t *draw, hipStream_t st) {
+  const int64_t rb = ggml_row_bytes(m.type, m.cols);
+  if (!is_quant(m.type)) {
+    ZL_HIP(hipMemcpyAsync(m.qs, draw, (size_t)rb * m.rows, hipMemcpyDeviceToDevice, st));
+    return;
+  }
+  DevMat mm = m;
+  launch_repack(m.type, draw, rb, m.rows, m.cols, m.nslab, mm, st);
+}
+
+// Allocate the planes of a rows x cols matrix of `type` and repack raw ggml rows (device pointer) into them.
+static DevMat make_mat(Arena &ar, int type, int rows, int cols, const uint8_t *draw, hipStream_t st) {
+  DevMat m = alloc_planes(ar, type, rows, cols);
+  fill_planes(m, draw, st);
+  return m;
+}
+
+// Matrices that one GEMV launch reads together (q, k, v): consecutive ones of the same type share one allocation, so
+// the launch addresses their rows from one base. stage(i) puts tensor i's raw rows at `draw` and returns its type.
+static std::vector<DevMat> make_group(Arena &ar, const std::vector<int> &types, const std::vector<int> &rows, int cols,
+                                      const std::function<void(size_t)> &stage, const uint8_t *draw, hipStream_t st) {
+  std::vector<DevMat> out(rows.size());
+  size_t i = 0;
+  while (i < rows.size()) {
+    size_t j = i + 1;
+    int total = rows[i];
+    while (j < rows.size() && types[j] == types[i]) total += rows[j++];
+    DevMat all = alloc_planes(ar, types[i], total, cols);
+    int r0 = 0;
+    for (size_t k = i; k < j; k++) {
+      stage(k);
+      out[k] = row_view(all, r0, rows[k]);
+      fill_planes(out[k], draw, st);
+      ZL_HIP(hipStreamSynchronize(st));
+      r0 += rows[k];
+    }
+    i = j;
+  }
+  return out;
 }
 
 // ---------------------------------------------------------------------------------------------- model
@@ -244,7 +302,23 @@ static void finish_model(zl_model *m, const float *ropeFreqs) {
 // ---------------------------------------------------------------------------------------------- forward pass
 struct SegSpec { const DevMat *m; float *out; int ldo; const float *bias; };
 
-static void gemv_group(zl_model *m, const std::vector<SegSpec> &segs, int B, int epi) {
+// Where a GEMV's quantised activation comes from: rows x[row0 .. row0+B) (length n, stride ldx), RMSNorm'd with nw
+// first when nw is set.
+struct Prologue { const float *x; int ldx, row0; const float *nw; int n; };
+
+// Rows of at most this many values in total are quantised inside each GEMV block (the block's redundant work is then
+// cheaper than a separate launch); longer ones by one k_norm_quant launch into m->act.
+constexpr long FUSE_MAX_VALUES = 4096;
+
+static bool fuse_prologue(const std::vector<std::vector<SegSpec>> &groups, int B, int n) {
+  if ((long)B * pad64(n) > FUSE_MAX_VALUES) return false;
+  for (auto &g : groups)
+    for (auto &sg : g)
+      if (!is_quant(sg.m->type)) return false;  // float weights read the f32 activation that k_norm_quant writes
+  return true;
+}
+
+static void gemv_group(zl_model *m, const std::vector<SegSpec> &segs, int B, int epi, const Prologue *pro) {
   GemvArgs a;
   memset(&a, 0, sizeof(a));
   a.nseg = (int)segs.size();
@@ -265,7 +339,19 @@ static void gemv_group(zl_model *m, const std::vector<SegSpec> &segs, int B, int
   a.ldr = m->cfg.n_embd;
   a.hb = m->hb;
   a.ldh = m->cfg.n_ff;
+  if (pro) {
+    a.xf = pro->x; a.ldxf = pro->ldx; a.xrow0 = pro->row0; a.n = pro->n; a.nw = pro->nw; a.eps = (double)m->cfg.rms_eps;
+  }
   launch_gemv(a, epi, m->act.f, m->act.ld, m->st);
+}
+
+// GEMV launches that all read the quantised activation of the same rows: the rows are quantised (after RMSNorm when
+// p.nw is set) either inside every launch or once by k_norm_quant, as fuse_prologue decides.
+static void gemv_launches(zl_model *m, const std::vector<std::vector<SegSpec>> &groups, const std::vector<int> &epis, int B,
+                          const Prologue &p) {
+  const bool fused = fuse_prologue(groups, B, p.n);
+  if (!fused) launch_norm_quant(p.x, p.ldx, p.row0, B, p.nw, (double)m->cfg.rms_eps, p.n, pad64(p.n), m->act, m->st);
+  for (size_t i = 0; i < groups.size(); i++) gemv_group(m, groups[i], B, epis[i], fused ? &p : nullptr);
 }
 
 // Enqueue one forward pass of B tokens (tokens and positions from m->dstep). want: 0 none, 1 last, 2 all.
@@ -276,16 +362,17 @@ static void enqueue_forward(zl_model *m, int B, int want) {
   launch_embed(view(m->tokEmbd), m->dstep, B, m->x, d, m->st);
   for (int l = 0; l < c.n_layer; l++) {
     Layer &L = m->layers[l];
-    launch_norm_quant(m->x, d, 0, B, L.attnNorm, eps, d, pad64(d), m->act, m->st);
     // q, k, v: consecutive matrices of one type share a launch
     SegSpec qkv[3] = {{&L.wq, m->q, qd, L.bq}, {&L.wk, m->k, kvd, L.bk}, {&L.wv, m->v, kvd, L.bv}};
+    std::vector<std::vector<SegSpec>> groups;
     int i0 = 0;
     while (i0 < 3) {
       int i1 = i0 + 1;
       while (i1 < 3 && qkv[i1].m->type == qkv[i0].m->type) i1++;
-      gemv_group(m, std::vector<SegSpec>(qkv + i0, qkv + i1), B, EPI_STORE);
+      groups.emplace_back(qkv + i0, qkv + i1);
       i0 = i1;
     }
+    gemv_launches(m, groups, std::vector<int>(groups.size(), EPI_STORE), B, Prologue{m->x, d, 0, L.attnNorm, d});
     RopeArgs ra;
     ra.q = m->q; ra.k = m->k; ra.v = m->v; ra.ldq = qd; ra.ldkv = kvd;
     ra.qNorm = L.qNorm; ra.kNorm = L.kNorm; ra.eps = eps;
@@ -301,19 +388,16 @@ static void enqueue_forward(zl_model *m, int B, int want) {
     aa.scale = 1.0 / sqrt((double)c.head_dim);
     aa.step = m->dstep; aa.out = m->act.f; aa.ldo = m->act.ld; aa.act = m->act;
     launch_attention(aa, B, m->st);
-    gemv_group(m, {{&L.wo, nullptr, 0, nullptr}}, B, EPI_RESID);
-    launch_norm_quant(m->x, d, 0, B, L.ffnNorm, eps, d, pad64(d), m->act, m->st);
+    gemv_group(m, {{&L.wo, nullptr, 0, nullptr}}, B, EPI_RESID, nullptr);
     ZL_REQUIRE(L.wgate.type == L.wup.type, ZL_ERR_UNSUPPORTED, "ffn_gate and ffn_up must share a type");
-    gemv_group(m, {{&L.wgate, nullptr, 0, nullptr}, {&L.wup, nullptr, 0, nullptr}}, B, EPI_SWIGLU);
-    launch_norm_quant(m->hb, ff, 0, B, nullptr, eps, ff, pad64(ff), m->act, m->st);
-    gemv_group(m, {{&L.wdown, nullptr, 0, nullptr}}, B, EPI_RESID);
+    gemv_launches(m, {{{&L.wgate, nullptr, 0, nullptr}, {&L.wup, nullptr, 0, nullptr}}}, {EPI_SWIGLU}, B,
+                  Prologue{m->x, d, 0, L.ffnNorm, d});
+    gemv_launches(m, {{{&L.wdown, nullptr, 0, nullptr}}}, {EPI_RESID}, B, Prologue{m->hb, ff, 0, nullptr, ff});
   }
   if (want == 2) {
-    launch_norm_quant(m->x, d, 0, B, m->outputNorm, eps, d, pad64(d), m->act, m->st);
-    gemv_group(m, {{&m->output, m->logits, c.vocab, nullptr}}, B, EPI_STORE);
+    gemv_launches(m, {{{&m->output, m->logits, c.vocab, nullptr}}}, {EPI_STORE}, B, Prologue{m->x, d, 0, m->outputNorm, d});
   } else if (want == 1) {
-    launch_norm_quant(m->x, d, B - 1, 1, m->outputNorm, eps, d, pad64(d), m->act, m->st);
-    gemv_group(m, {{&m->output, m->logits, c.vocab, nullptr}}, 1, EPI_STORE);
+    gemv_launches(m, {{{&m->output, m->logits, c.vocab, nullptr}}}, {EPI_STORE}, 1, Prologue{m->x, d, B - 1, m->outputNorm, d});
   }
 }
 
@@ -390,13 +474,13 @@ static void probe_gemv(zl_model *m, int which, int M, int iters, float *ms, int6
   ZL_HIP(hipMalloc(&xsave, xb));
   struct F { float *p; ~F() { hipFree(p); } } fr{xsave};
   ZL_HIP(hipMemcpyAsync(xsave, m->x, xb, hipMemcpyDeviceToDevice, m->st));
-  for (int l = 0; l < std::min(c.n_layer, iters); l++) gemv_group(m, segs_of(which == 4 ? 0 : l), M, epi);  // warm-up
+  for (int l = 0; l < std::min(c.n_layer, iters); l++) gemv_group(m, segs_of(which == 4 ? 0 : l), M, epi, nullptr);  // warm-up
   hipEvent_t a, e;
   ZL_HIP(hipEventCreate(&a));
   ZL_HIP(hipEventCreate(&e));
   struct E { hipEvent_t a, b; ~E() { hipEventDestroy(a); hipEventDestroy(b); } } ev{a, e};
   ZL_HIP(hipEventRecord(a, m->st));
-  for (int i = 0; i < iters; i++) gemv_group(m, segs_of(which == 4 ? 0 : i % c.n_layer), M, epi);
+  for (int i = 0; i < iters; i++) gemv_group(m, segs_of(which == 4 ? 0 : i % c.n_layer), M, epi, nullptr);
   ZL_HIP(hipEventRecord(e, m->st));
   ZL_HIP(hipEventSynchronize(e));
   float t = 0;
@@ -555,9 +639,18 @@ static zl_model *load_gguf(const char *path, const zl_model_opts *o) {
     const std::string p = "blk." + std::to_string(l) + ".";
     Layer L;
     L.attnNorm = V(p + "attn_norm.weight", c.n_embd);
-    L.wq = W(p + "attn_q.weight", qd, c.n_embd);
-    L.wk = W(p + "attn_k.weight", kvd, c.n_embd);
-    L.wv = W(p + "attn_v.weight", kvd, c.n_embd);
+    {
+      const std::string nm[3] = {p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"};
+      const std::vector<int> rows{qd, kvd, kvd};
+      std::vector<int> types;
+      for (int i = 0; i < 3; i++) {
+        const GGUFTensor &t = req(nm[i]);
+        ZL_REQUIRE(t.dims.size() >= 2 && (int)t.dims[0] == c.n_embd && (int)t.dims[1] == rows[i], ZL_ERR_FORMAT, "tensor " + nm[i] + " has unexpected shape");
+        types.push_back(t.type);
+      }
+      auto g3 = make_group(m->ar, types, rows, c.n_embd, [&](size_t i) { read_dev(req(nm[i])); }, dstage, m->st);
+      L.wq = g3[0]; L.wk = g3[1]; L.wv = g3[2];
+    }
     L.wo = W(p + "attn_output.weight", c.n_embd, qd);
     L.bq = Vopt(p + "attn_q.bias", qd); L.bk = Vopt(p + "attn_k.bias", kvd); L.bv = Vopt(p + "attn_v.bias", kvd);
     L.qNorm = Vopt(p + "attn_q_norm.weight", c.head_dim); L.kNorm = Vopt(p + "attn_k_norm.weight", c.head_dim);
@@ -623,9 +716,18 @@ static zl_model *build_synth(const zl_config *cfg, const zl_synth_tensor *ts, in
     const std::string p = "blk." + std::to_string(l) + ".";
     Layer L;
     L.attnNorm = V(p + "attn_norm.weight", c.n_embd);
-    L.wq = W(p + "attn_q.weight", qd, c.n_embd);
-    L.wk = W(p + "attn_k.weight", kvd, c.n_embd);
-    L.wv = W(p + "attn_v.weight", kvd, c.n_embd);
+    {
+      const std::string nm[3] = {p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"};
+      const std::vector<int> rows{qd, kvd, kvd};
+      std::vector<int> types;
+      for (int i = 0; i < 3; i++) {
+        const zl_synth_tensor &t = req(nm[i]);
+        ZL_REQUIRE(t.rows == rows[i] && t.cols == c.n_embd && !t.fill, ZL_ERR_ARG, "synthetic tensor " + nm[i] + " has unexpected shape");
+        types.push_back(t.type);
+      }
+      auto g3 = make_group(m->ar, types, rows, c.n_embd, [&](size_t i) { synth_to_device(req(nm[i]), dstage, m->st); }, dstage, m->st);
+      L.wq = g3[0]; L.wk = g3[1]; L.wv = g3[2];
+    }
     L.wo = W(p + "attn_output.weight", c.n_embd, qd);
     L.bq = Vopt(p + "attn_q.bias", qd); L.bk = Vopt(p + "attn_k.bias", kvd); L.bv = Vopt(p + "attn_v.bias", kvd);
     L.qNorm = Vopt(p + "attn_q_norm.weight", c.head_dim); L.kNorm = Vopt(p + "attn_k_norm.weight", c.head_dim);
