@@ -22,10 +22,11 @@ constexpr size_t GV_LDS_MAX = 150 * 1024;
 
 
 // ---------------------------------------------------------------------------------------------- staged activations
-// LDS layout for a tile of MT tokens over K values (nsb = K/32 blocks):
-//   X    int8 [MT][K]
-//   REC  16 B [MT][nsb]: f64 scale d, then  f64 block sum (Q4_K/Q5_K) | int32 sum (Q4_0/Q5_0) | two int32 16-value sums
-//        (Q6_K) | nothing (Q8_0)
+// LDS layout for a tile of MT tokens over K values (nslab = K/64 slabs, values 64s + 32h + 16p + e):
+//   X    [MT][h 2][p 2][nslab] x 16 B int8: lanes that take consecutive slabs read consecutive 16-byte pieces, so the
+//        reads of a wave hit distinct banks
+//   REC  [MT][h 2][nslab] x 16 B: per 32-value block, f64 scale d, then f64 block sum (Q4_K/Q5_K) | int32 sum
+//        (Q4_0/Q5_0) | two int32 16-value sums (Q6_K) | nothing (Q8_0)
 struct ActRec {
   double d;
   union {
@@ -35,6 +36,10 @@ struct ActRec {
 };
 __host__ __device__ inline size_t act_rec_off(int mt, int K) { return (size_t)mt * K; }
 size_t gemv_lds_bytes(int fmt, int mt, int K) { (void)fmt; return act_rec_off(mt, K) + (size_t)mt * (K / 32) * 16; }
+
+// X piece (16 values) number i of token t's row, and the record of its 32-value block b, in the layout above
+__device__ inline int x_piece(int t, int i, int nslab) { return ((t * 2 + ((i >> 1) & 1)) * 2 + (i & 1)) * nslab + (i >> 2); }
+__device__ inline int rec_index(int t, int b, int nslab) { return (t * 2 + (b & 1)) * nslab + (b >> 1); }
 
 template <int FMT>
 __device__ inline void put_rec(uint8_t *lds, int mt, int K, int b, double d, int s32, int s16a, int s16b) {
@@ -73,8 +78,8 @@ __device__ inline void stage_act(const Act &act, int t0, int mt, int MTL, int K,
     #pragma unroll
     for (int k = 0; k < 2; k++) {
       const int i = base + k * GV_THREADS + tid;
-      if (i < np) *(uint4 *)(lds + (size_t)(i / pq) * K + (i % pq) * 16) = v[k];
-      if (i < ns) put_rec<FMT>(lds, MTL, K, (i / nsb) * nsb + i % nsb, (double)d[k], sv[k], sa[k], sb[k]);
+      if (i < np) *(uint4 *)(lds + (size_t)x_piece(i / pq, i % pq, K >> 6) * 16) = v[k];
+      if (i < ns) put_rec<FMT>(lds, MTL, K, rec_index(i / nsb, i % nsb, K >> 6), (double)d[k], sv[k], sa[k], sb[k]);
     }
   }
 }
@@ -125,8 +130,8 @@ __device__ inline void stage_f32(const GemvArgs &a, int t0, int mt, int K, uint8
     const int s16b = __shfl_down(s16, 16, 32);  // the block's second 16-value sum, at its first lane
     const int s32 = s16 + swizzle_xor16(s16);
     if (live) {
-      lds[(size_t)t * K + i] = (uint8_t)(int8_t)q;
-      if ((i & 31) == 0) put_rec<FMT>(lds, MT, K, t * (K >> 5) + (i >> 5), (double)(float)scale, s32, s16, s16b);
+      lds[(size_t)x_piece(t, i >> 4, K >> 6) * 16 + (i & 15)] = (uint8_t)(int8_t)q;
+      if ((i & 31) == 0) put_rec<FMT>(lds, MT, K, rec_index(t, i >> 5, K >> 6), (double)(float)scale, s32, s16, s16b);
     }
   }
 }
@@ -298,94 +303,110 @@ __global__ __launch_bounds__(GV_THREADS) void k_gemv(const GemvArgs a) {
   const uint8_t *X = lds;
   const ActRec *REC = (const ActRec *)(lds + act_rec_off(MT, K));
 
-  for (int t0 = 0; t0 < a.M; t0 += MT) {
-    const int mt = min(MT, a.M - t0);
-    int ub = blockIdx.x * upb;
-    int g0 = unit_row(ub, 0), g1 = unit_row(ub, 1);
-    Slab<FMT> c0, c1, n0, n1;
-    load_slab<FMT>(P0, g0 * nslab + j, c0);  // lpr <= nslab, so slab j exists
-    load_slab<FMT>(P1, g1 * nslab + j, c1);
-    if (t0 > 0) __syncthreads();  // the previous tile's LDS reads are done
+  // The lane's work is a flat sequence of items (unit step, slab): spl = nslab / lpr slabs of each of the block's
+  // unit steps. Loads run two items ahead, across unit boundaries; a unit's butterfly and epilogue follow its last item.
+  const int spl = (nslab + lpr - 1) / lpr;  // the last round may leave lanes without a slab (they add nothing)
+  const int stride = gridDim.x * upb, ub0 = blockIdx.x * upb;
+  const int total = (nunits - ub0 + stride - 1) / stride * spl;
+  auto load_item = [&](int step, int m, Slab<FMT> &o0, Slab<FMT> &o1) {
+    const int ub = ub0 + step * stride, s = min(j + m * lpr, nslab - 1);
+    load_slab<FMT>(P0, unit_row(ub, 0) * nslab + s, o0);
+    load_slab<FMT>(P1, unit_row(ub, 1) * nslab + s, o1);
+  };
+  {
+    const int t0 = 0, mt = a.M;  // one tile of M <= MT tokens per launch (the host launches one per tile)
+    Slab<FMT> c0, c1, n0, n1, q0, q1;
+    // items 0 and 1 are in flight during the staging
+    load_item(0, 0, c0, c1);
+    if (total > 1) load_item(spl > 1 ? 0 : 1, spl > 1 ? 1 : 0, n0, n1);
     if (a.xf) stage_f32<FMT, MT>(a, t0, mt, K, lds);
     else stage_act<FMT>(a.act, t0, mt, MT, K, lds);
     __syncthreads();
-    for (; ub < nunits; ub += gridDim.x * upb) {
-      const int nub = ub + gridDim.x * upb;
-      const bool more = nub < nunits;
-      const int ng0 = more ? unit_row(nub, 0) : g0, ng1 = more ? unit_row(nub, 1) : g1;
-      double acc0[MT], acc1[MT];
-      #pragma unroll
-      for (int t = 0; t < MT; t++) { acc0[t] = 0.0; acc1[t] = 0.0; }
-      for (int s = j; s < nslab; s += lpr) {
-        // next slab of this unit, else this lane's first slab of the next unit
-        const int sn = s + lpr;
-        if (sn < nslab) { load_slab<FMT>(P0, g0 * nslab + sn, n0); load_slab<FMT>(P1, g1 * nslab + sn, n1); }
-        else if (more) { load_slab<FMT>(P0, ng0 * nslab + j, n0); load_slab<FMT>(P1, ng1 * nslab + j, n1); }
-        #pragma unroll
-        for (int h = 0; h < 2; h++) {
-          uint32_t w0[8], w1[8];
-          double fa0, fb0, fa1, fb1;
-          unpack_half<FMT>(c0, h, w0); half_scale<FMT>(c0, h, fa0, fb0);
-          unpack_half<FMT>(c1, h, w1); half_scale<FMT>(c1, h, fa1, fb1);
-          const int b = 2 * s + h;  // 32-value block index in the row
-          #pragma unroll
-          for (int t = 0; t < MT; t++) {
-            const int tt = min(t, mt - 1);  // a short tile repeats its last token; those results are not stored
-            uint32_t Xv[8];
-            const uint4 *xp = (const uint4 *)(X + (size_t)tt * K + b * 32);
-            const uint4 v0 = xp[0], v1 = xp[1];
-            Xv[0] = v0.x; Xv[1] = v0.y; Xv[2] = v0.z; Xv[3] = v0.w; Xv[4] = v1.x; Xv[5] = v1.y; Xv[6] = v1.z; Xv[7] = v1.w;
-            const ActRec r = REC[tt * nsb + b];
-            acc0[t] = block_term<FMT>(w0, fa0, fb0, Xv, r, acc0[t]);
-            acc1[t] = block_term<FMT>(w1, fa1, fb1, Xv, r, acc1[t]);
-          }
-        }
-        c0 = n0;
-        c1 = n1;
+    double acc0[MT], acc1[MT];
+    #pragma unroll
+    for (int t = 0; t < MT; t++) { acc0[t] = 0.0; acc1[t] = 0.0; }
+    int step = 0, m = 0;    // current item
+    int step2 = 0, m2 = 2;  // item k + 2
+    while (m2 >= spl) { m2 -= spl; step2++; }
+    for (int k = 0; k < total; k++) {
+      if (k + 2 < total) {
+        load_item(step2, m2, q0, q1);
+        if (++m2 == spl) { m2 = 0; step2++; }
       }
+      const int s = j + m * lpr;
+      const bool live = s < nslab;
       #pragma unroll
-      for (int t = 0; t < MT; t++) { acc0[t] = wave_sum_xor(acc0[t], lpr); acc1[t] = wave_sum_xor(acc1[t], lpr); }
-      const int unit = ub + wave * slots + slot;
-      if (j == 0 && unit < nunits) {
+      for (int h = 0; h < 2; h++) {
+        if (!live) break;
+        uint32_t w0[8], w1[8];
+        double fa0, fb0, fa1, fb1;
+        unpack_half<FMT>(c0, h, w0); half_scale<FMT>(c0, h, fa0, fb0);
+        unpack_half<FMT>(c1, h, w1); half_scale<FMT>(c1, h, fa1, fb1);
         #pragma unroll
         for (int t = 0; t < MT; t++) {
-          if (t >= mt) continue;
-          const long tb = t0 + t;
-          if (EPI == EPI_SWIGLU) {
+          const int tt = min(t, mt - 1);  // a short tile repeats its last token; those results are not stored
+          uint32_t Xv[8];
+          const uint4 *xp = (const uint4 *)X + ((tt * 2 + h) * 2) * nslab + s;
+          const uint4 v0 = xp[0], v1 = xp[nslab];
+          Xv[0] = v0.x; Xv[1] = v0.y; Xv[2] = v0.z; Xv[3] = v0.w; Xv[4] = v1.x; Xv[5] = v1.y; Xv[6] = v1.z; Xv[7] = v1.w;
+          const ActRec r = REC[(tt * 2 + h) * nslab + s];
+          acc0[t] = block_term<FMT>(w0, fa0, fb0, Xv, r, acc0[t]);
+          acc1[t] = block_term<FMT>(w1, fa1, fb1, Xv, r, acc1[t]);
+        }
+      }
+      c0 = n0; c1 = n1;
+      n0 = q0; n1 = q1;
+      if (++m < spl) continue;
+      // ---- last slab of this unit step: combine the lpr lanes and store
+      #pragma unroll
+      for (int t = 0; t < MT; t++) { acc0[t] = wave_sum_xor(acc0[t], lpr); acc1[t] = wave_sum_xor(acc1[t], lpr); }
+      const int unit = ub0 + step * stride + wave * slots + slot;
+      if (j == 0 && unit < nunits) {
+        if (EPI == EPI_SWIGLU) {
+          float *hb = a.hb + (long)t0 * a.ldh + unit;
+          #pragma unroll
+          for (int t = 0; t < MT; t++) {
             const double g = (double)(float)acc0[t], uu = (double)(float)acc1[t];
             const double silu = g / (1.0 + exp(-g));  // src/compute/ref-kernels.js:322
-            a.hb[tb * a.ldh + unit] = (float)(silu * uu);
-          } else {
+            if (t < mt) hb[(long)t * a.ldh] = (float)(silu * uu);
+          }
+        } else {
+          #pragma unroll
+          for (int r = 0; r < 2; r++) {
+            int g = 2 * unit + r;
+            if (g >= a.rows_total) break;
+            float *out;
+            const float *bias = nullptr;
+            long ldo;
+            if (EPI == EPI_RESID) {
+              out = a.resid + (long)t0 * a.ldr + g;
+              ldo = a.ldr;
+            } else {
+              // segment of the row, selected field by field (no dynamic indexing into the argument block)
+              int si = 0;
+              if (a.nseg > 1 && g >= a.seg[0].rows) { g -= a.seg[0].rows; si = 1; }
+              if (si == 1 && a.nseg > 2 && g >= a.seg[1].rows) { g -= a.seg[1].rows; si = 2; }
+              out = si == 0 ? a.seg[0].out : si == 1 ? a.seg[1].out : a.seg[2].out;
+              bias = si == 0 ? a.seg[0].bias : si == 1 ? a.seg[1].bias : a.seg[2].bias;
+              ldo = si == 0 ? a.seg[0].ldo : si == 1 ? a.seg[1].ldo : a.seg[2].ldo;
+              out += (long)t0 * ldo + g;
+            }
+            const double bv = bias ? (double)bias[g] : 0.0;
             #pragma unroll
-            for (int r = 0; r < 2; r++) {
-              int g = 2 * unit + r;
-              if (g >= a.rows_total) continue;
-              float y = (float)(r ? acc1[t] : acc0[t]);
-              if (EPI == EPI_RESID) {
-                float *xp = a.resid + tb * a.ldr + g;
-                *xp = (float)((double)*xp + (double)y);
-              } else {
-                // segment of the row, selected field by field (no dynamic indexing into the argument block)
-                float *out = a.seg[0].out;
-                const float *bias = a.seg[0].bias;
-                int ldo = a.seg[0].ldo;
-                if (a.nseg > 1 && g >= a.seg[0].rows) {
-                  g -= a.seg[0].rows;
-                  out = a.seg[1].out; bias = a.seg[1].bias; ldo = a.seg[1].ldo;
-                  if (a.nseg > 2 && g >= a.seg[1].rows) {
-                    g -= a.seg[1].rows;
-                    out = a.seg[2].out; bias = a.seg[2].bias; ldo = a.seg[2].ldo;
-                  }
-                }
-                if (bias) y = (float)((double)y + (double)bias[g]);
-                out[tb * ldo + g] = y;
-              }
+            for (int t = 0; t < MT; t++) {
+              if (t >= mt) break;
+              const float y = (float)(r ? acc1[t] : acc0[t]);
+              float *o = out + (long)t * ldo;
+              if (EPI == EPI_RESID) *o = (float)((double)*o + (double)y);
+              else *o = bias ? (float)((double)y + bv) : y;
             }
           }
         }
       }
-      g0 = ng0;
-      g1 = ng1;
+      #pragma unroll
+      for (int t = 0; t < MT; t++) { acc0[t] = 0.0; acc1[t] = 0.0; }
+      m = 0;
+      step++;
     }
   }
 }
@@ -473,13 +494,13 @@ static void launch_gemv_mt(int fmt, const GemvArgs &a, int epi, int blocks, size
 }
 
 // Lanes per row pair: enough lanes in total to keep the GPU's memory pipes full (about 2^19 lanes), at most 64, at
-// least 8 where the row has that many slabs, never more than the row's slabs (a power of two). Depends only on the
+// least 8 where the row has that many slabs, a power of two not above the row's slab count. Depends only on the
 // matrix shape (rows of the launch, columns).
 int gemv_lpr(int rows, int nslab) {
   int want = 8;
   while (want < 64 && (long)want * rows < (1L << 19)) want <<= 1;
-  int cap = 1;
-  while (cap * 2 <= nslab && cap < 64) cap <<= 1;
+  int cap = 1;  // the largest power of two not above nslab, at most 64
+  while (cap < 64 && cap * 2 <= nslab) cap <<= 1;
   return want < cap ? want : cap;
 }
 
@@ -527,16 +548,32 @@ void launch_gemv(const GemvArgs &a0, int epi, const float *xf, int ldx, hipStrea
   const int upb = GV_WAVES * slots;
   int blocks = (units + upb - 1) / upb;
   a.wk = K;
-  switch (MT) {
-    case 1: launch_gemv_mt<1>(fmt, a, epi, blocks, lds, st); break;
-    case 2: launch_gemv_mt<2>(fmt, a, epi, blocks, lds, st); break;
-    case 3: launch_gemv_mt<3>(fmt, a, epi, blocks, lds, st); break;
-    case 4: launch_gemv_mt<4>(fmt, a, epi, blocks, lds, st); break;
-    case 5: launch_gemv_mt<5>(fmt, a, epi, blocks, lds, st); break;
-    case 6: launch_gemv_mt<6>(fmt, a, epi, blocks, lds, st); break;
-    default: launch_gemv_mt<8>(fmt, a, epi, blocks, lds, st); break;
+  // one launch per tile of MT tokens: the tile's rows of every input and output are addressed from offset pointers
+  const int M = a0.M;
+  for (int t0 = 0; t0 < M; t0 += MT) {
+    GemvArgs b = a;
+    b.M = std::min(MT, M - t0);
+    if (t0) {
+      b.act.q += (long)t0 * a.act.ld;
+      b.act.d += (long)t0 * (a.act.ld >> 5);
+      b.act.s += (long)t0 * (a.act.ld >> 5);
+      b.act.s16 += (long)t0 * (a.act.ld >> 4);
+      b.xrow0 += t0;
+      for (int i = 0; i < b.nseg; i++) if (b.seg[i].out) b.seg[i].out += (long)t0 * b.seg[i].ldo;
+      if (b.resid) b.resid += (long)t0 * b.ldr;
+      if (b.hb) b.hb += (long)t0 * b.ldh;
+    }
+    switch (MT) {
+      case 1: launch_gemv_mt<1>(fmt, b, epi, blocks, lds, st); break;
+      case 2: launch_gemv_mt<2>(fmt, b, epi, blocks, lds, st); break;
+      case 3: launch_gemv_mt<3>(fmt, b, epi, blocks, lds, st); break;
+      case 4: launch_gemv_mt<4>(fmt, b, epi, blocks, lds, st); break;
+      case 5: launch_gemv_mt<5>(fmt, b, epi, blocks, lds, st); break;
+      case 6: launch_gemv_mt<6>(fmt, b, epi, blocks, lds, st); break;
+      default: launch_gemv_mt<8>(fmt, b, epi, blocks, lds, st); break;
+    }
+    ZL_HIP(hipGetLastError());
   }
-  ZL_HIP(hipGetLastError());
 }
 
 }  // namespace zl
