@@ -64,21 +64,16 @@ struct GemvArgs {
   double eps;
 };
 
-struct RopeArgs {
-  float *q, *k, *v;
-  int ldq, ldkv;
-  const float *qNorm, *kNorm;
-  double eps;
-  const float *cosT, *sinT;
-  int nRot, neox, nHead, nHeadKv, hd, ctx, layer, kvF16;
-  int vstride;     // positions per V cache row (V is dimension-major)
-  void *kcache, *vcache;
-  const Step *step;
-};
 
 struct AttnArgs {
   const float *q;
   int ldq;
+  const float *k, *v;        // the pass's key / value projections [B][ldkv] (normed, rotated and cached here)
+  int ldkv;
+  const float *qNorm, *kNorm;
+  double eps;
+  const float *cosT, *sinT;
+  int nRot, neox;
   const void *kcache, *vcache;
   int nHead, nHeadKv, hd, ctx, layer, kvF16;
   int vstride;     // positions per V cache row (V is dimension-major)
@@ -99,7 +94,6 @@ void launch_attention(const AttnArgs &a, int B, hipStream_t st);
 size_t attention_lds(int ctx);
 void launch_norm_quant(const float *x, int ldx, int row0, int nrows, const float *w, double eps, int n, int npad,
                        const Act &act, hipStream_t st);
-void launch_rope(const RopeArgs &a, int B, hipStream_t st);
 void launch_embed(const MatView &m, const Step *step, int B, float *x, int ldx, hipStream_t st);
 void launch_dequant_rows(const MatView &m, const int *rowIds, int nrows, float *out, int ldo, hipStream_t st);
 void launch_repack(int type, const uint8_t *raw, long rawRowBytes, int rows, int cols, int nslab, DevMat &m, hipStream_t st);
@@ -135,9 +129,16 @@ struct SpecState {
   int drafted[64];
 };
 
+// Work space of the multi-block greedy argmax: per-row block keys and arrival counters (zero between launches).
+constexpr int ARGMAX_MAX_BLOCKS = 128, ARGMAX_MAX_ROWS = 65;
+struct ArgmaxWork {
+  unsigned long long *keys;  // [ARGMAX_MAX_ROWS][blocks]
+  uint32_t *count;           // [ARGMAX_MAX_ROWS], zero-initialised
+};
+
 // Row r uses history hist[0 .. histLen0 + r * histInc).
 void launch_dist_rows(const float *logits, int ldl, int nrows, int vocab, const SamplerParams &sp, const int *hist,
-                      int histLen0, int histInc, float *scratch, DevDist *out, hipStream_t st);
+                      int histLen0, int histInc, float *scratch, const ArgmaxWork &aw, DevDist *out, hipStream_t st);
 void launch_draft_draw(const DevDist *dist, SpecState *ss, int j, const int *stopIds, int nStop, Step *draftStep,
                        int advance, Step *targetStep, int *hist, int histLen0, hipStream_t st);
 void launch_accept(const DevDist *pdist, const DevDist *qdist, SpecState *ss, int greedy, hipStream_t st);

@@ -110,97 +110,57 @@ __global__ void k_repack(int type, const uint8_t *__restrict__ raw, long rawRowB
 }
 
 // ================================================================================================ dequantisation
-// One slab (64 values) of one row, with the reference's dequantisation arithmetic (src/compute/quant.js:33-202).
-__device__ void dequant_slab(const MatView m, int r, int s, float *out) {
-  long idx = (long)r * m.nslab + s;
-  const int t = m.type;
+// dequantRow (src/compute/ref-kernels.js:80-120, src/compute/quant.js:33-202) for value c of row r of the repacked
+// planes, in f64 with one rounding to f32. One element per thread: coalesced stores, no private arrays.
+__device__ inline float dequant_value(const MatView &m, int r, int c) {
+  const int t = m.type, s = c >> 6, v = c & 63, h = v >> 5, j = v & 31;
+  const long idx = (long)r * m.nslab + s;
   if (t == T_F32 || t == T_F16 || t == T_BF16) {
-    for (int i = 0; i < 64; i++) {
-      int c = 64 * s + i;
-      if (c >= m.cols) { out[i] = 0; continue; }
-      long e = (long)r * m.cols + c;
-      if (t == T_F32) out[i] = ((const float *)m.qs)[e];
-      else if (t == T_F16) out[i] = h2f(((const uint16_t *)m.qs)[e]);
-      else out[i] = __uint_as_float((uint32_t)((const uint16_t *)m.qs)[e] << 16);
-    }
-    return;
+    if (c >= m.cols) return 0.f;
+    const long e = (long)r * m.cols + c;
+    if (t == T_F32) return ((const float *)m.qs)[e];
+    if (t == T_F16) return h2f(((const uint16_t *)m.qs)[e]);
+    return __uint_as_float((uint32_t)((const uint16_t *)m.qs)[e] << 16);
   }
   if (t == T_Q8_0) {
-    const int8_t *q = (const int8_t *)(m.qs + idx * 64);
-    for (int h = 0; h < 2; h++) {
-      double d = (double)h2f(m.dd[idx * 2 + h]);
-      for (int i = 0; i < 32; i++) out[32 * h + i] = (float)(d * (double)q[32 * h + i]);
-    }
-    return;
+    const double d = (double)h2f(m.dd[idx * 2 + h]);
+    return (float)(d * (double)((const int8_t *)m.qs)[idx * 64 + v]);
   }
-  const uint8_t *q = m.qs + idx * 32;
+  const uint8_t qb = m.qs[idx * 32 + j];
+  const int nib = h == 0 ? (qb & 15) : (qb >> 4);
   if (t == T_Q4_0 || t == T_Q5_0) {
-    const uint8_t *x = m.qx + idx * 8;
-    for (int h = 0; h < 2; h++) {
-      double d = (double)h2f(m.dd[idx * 2 + h]);
-      uint32_t hb = t == T_Q5_0 ? ((uint32_t)x[4 * h] | ((uint32_t)x[4 * h + 1] << 8) | ((uint32_t)x[4 * h + 2] << 16) | ((uint32_t)x[4 * h + 3] << 24)) : 0;
-      for (int j = 0; j < 32; j++) {
-        int v = h == 0 ? (q[j] & 15) : (q[j] >> 4);
-        int val = t == T_Q4_0 ? v - 8 : (v | (((hb >> j) & 1) << 4)) - 16;
-        out[32 * h + j] = (float)(d * (double)val);
-      }
-    }
-    return;
+    const double d = (double)h2f(m.dd[idx * 2 + h]);
+    const int hb = t == T_Q5_0 ? (m.qx[idx * 8 + 4 * h + (j >> 3)] >> (j & 7)) & 1 : 0;
+    const int val = t == T_Q4_0 ? nib - 8 : (nib | (hb << 4)) - 16;
+    return (float)(d * (double)val);
   }
   if (t == T_Q4_K || t == T_Q5_K) {
-    long di = ((long)r * (m.nslab >> 2) + (s >> 2)) * 2;
-    double d = (double)h2f(m.dd[di]), dmin = (double)h2f(m.dd[di + 1]);
-    const uint8_t *S = m.sc + idx * 4;
-    const uint8_t *x = m.qx + idx * 8;
-    for (int h = 0; h < 2; h++) {
-      int sc = S[h], mn = S[2 + h];
-      uint32_t hb = t == T_Q5_K ? ((uint32_t)x[4 * h] | ((uint32_t)x[4 * h + 1] << 8) | ((uint32_t)x[4 * h + 2] << 16) | ((uint32_t)x[4 * h + 3] << 24)) : 0;
-      for (int j = 0; j < 32; j++) {
-        int v = h == 0 ? (q[j] & 15) : (q[j] >> 4);
-        if (t == T_Q5_K) v |= ((hb >> j) & 1) << 4;
-        out[32 * h + j] = (float)(d * (double)sc * (double)v - dmin * (double)mn);
-      }
-    }
-    return;
+    const long di = ((long)r * (m.nslab >> 2) + (s >> 2)) * 2;
+    const double d = (double)h2f(m.dd[di]), dmin = (double)h2f(m.dd[di + 1]);
+    const int sc = m.sc[idx * 4 + h], mn = m.sc[idx * 4 + 2 + h];
+    int q = nib;
+    if (t == T_Q5_K) q |= ((m.qx[idx * 8 + 4 * h + (j >> 3)] >> (j & 7)) & 1) << 4;
+    return (float)(d * (double)sc * (double)q - dmin * (double)mn);
   }
-  if (t == T_Q6_K) {
-    double d = (double)h2f(m.dd[(long)r * (m.nslab >> 2) + (s >> 2)]);
-    const int8_t *S = (const int8_t *)(m.sc + idx * 4);
-    const uint8_t *x = m.qx + idx * 16;
-    for (int v = 0; v < 64; v++) {
-      int lo = v < 32 ? (q[v] & 15) : (q[v - 32] >> 4);
-      int j = v & 15, i = v >> 4;
-      int hi = (x[j] >> (2 * i)) & 3;
-      int val = (lo | (hi << 4)) - 32;
-      out[v] = (float)(d * (double)S[v >> 4] * (double)val);
-    }
-    return;
-  }
+  // Q6_K
+  const double d = (double)h2f(m.dd[(long)r * (m.nslab >> 2) + (s >> 2)]);
+  const int lo = v < 32 ? (m.qs[idx * 32 + v] & 15) : (m.qs[idx * 32 + v - 32] >> 4);
+  const int hi = (m.qx[idx * 16 + (v & 15)] >> (2 * (v >> 4))) & 3;
+  const int val = (lo | (hi << 4)) - 32;
+  return (float)(d * (double)((const int8_t *)m.sc)[idx * 4 + (v >> 4)] * (double)val);
 }
 
 __global__ void k_dequant_rows(const MatView m, const int *rowIds, int nrows, float *out, int ldo) {
-  int rr = blockIdx.x;
-  if (rr >= nrows) return;
-  int r = rowIds[rr];
-  float buf[64];
-  for (int s = threadIdx.x; s < m.nslab; s += blockDim.x) {
-    dequant_slab(m, r, s, buf);
-    int n = min(64, m.cols - 64 * s);
-    for (int i = 0; i < n; i++) out[(long)rr * ldo + 64 * s + i] = buf[i];
-  }
+  const int rr = blockIdx.y, c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (rr >= nrows || c >= m.cols) return;
+  out[(long)rr * ldo + c] = dequant_value(m, rowIds[rr], c);
 }
 
 // Embedding lookup: x[b] = dequant(token_embd row step.tokens[b]) (src/model/forward.js:195).
 __global__ void k_embed(const MatView m, const Step *step, float *x, int ldx) {
-  int b = blockIdx.x;
-  if (b >= step->B) return;
-  int tok = step->tokens[b];
-  float buf[64];
-  for (int s = threadIdx.x; s < m.nslab; s += blockDim.x) {
-    dequant_slab(m, tok, s, buf);
-    int n = min(64, m.cols - 64 * s);
-    for (int i = 0; i < n; i++) x[(long)b * ldx + 64 * s + i] = buf[i];
-  }
+  const int b = blockIdx.y, c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= step->B || c >= m.cols) return;
+  x[(long)b * ldx + c] = dequant_value(m, step->tokens[b], c);
 }
 
 // ================================================================================================ activation quantisation
@@ -252,58 +212,6 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x,
   }
 }
 
-// ================================================================================================ q/k norm, RoPE, KV append
-// One wave per (token, head). Heads [0, nHead) are query heads (normed, rotated, written back), heads
-// [nHead, nHead + nHeadKv) are KV heads (k normed and rotated, k and v appended to the cache at step.pos0 + b).
-// Order as src/model/forward.js:203-211: bias (added by the GEMV), per-head RMSNorm, RoPE, store.
-__global__ __launch_bounds__(64) void k_qk_rope_kv(const RopeArgs a) {
-  __shared__ float v[512];
-  const int b = blockIdx.x, hh = blockIdx.y, lane = threadIdx.x;
-  const Step *st = a.step;
-  if (b >= st->B) return;
-  const int pos = st->pos0 + b;
-  const bool isq = hh < a.nHead;
-  const int head = isq ? hh : hh - a.nHead;
-  const int hd = a.hd;
-  float *src = isq ? a.q + (long)b * a.ldq + (long)head * hd : a.k + (long)b * a.ldkv + (long)head * hd;
-  const float *nw = isq ? a.qNorm : a.kNorm;
-  for (int i = lane; i < hd; i += 64) v[i] = src[i];
-  __syncthreads();
-  if (nw) {
-    double ss = 0;
-    for (int i = lane; i < hd; i += 64) { double x = (double)v[i]; ss += x * x; }
-    ss = wave_sum_xor(ss, 64);
-    double s = 1.0 / sqrt(ss / (double)hd + a.eps);
-    for (int i = lane; i < hd; i += 64) v[i] = (float)((double)v[i] * s * (double)nw[i]);
-    __syncthreads();
-  }
-  const int half = a.nRot / 2;
-  for (int i = lane; i < half; i += 64) {
-    int i0 = a.neox ? i : 2 * i, i1 = a.neox ? i + half : 2 * i + 1;
-    double c = (double)a.cosT[(long)pos * half + i], sn = (double)a.sinT[(long)pos * half + i];
-    double x0 = (double)v[i0], x1 = (double)v[i1];
-    v[i0] = (float)(x0 * c - x1 * sn);  // pairs are disjoint across lanes
-    v[i1] = (float)(x0 * sn + x1 * c);
-  }
-  __syncthreads();
-  if (isq) {
-    for (int i = lane; i < hd; i += 64) src[i] = v[i];
-    return;
-  }
-  // K rows are position-major ([layer][kv head][pos][dim]); V rows are dimension-major ([layer][kv head][dim][vstride])
-  // so that the attention's weighted sum reads consecutive positions of one dimension
-  const long off = (((long)a.layer * a.nHeadKv + head) * a.ctx + pos) * hd;
-  const long voff = ((long)a.layer * a.nHeadKv + head) * hd * a.vstride + pos;
-  const float *vs = a.v + (long)b * a.ldkv + (long)head * hd;
-  if (a.kvF16) {
-    uint16_t *kc = (uint16_t *)a.kcache + off, *vc = (uint16_t *)a.vcache + voff;
-    for (int i = lane; i < hd; i += 64) { kc[i] = f2h(v[i]); vc[(long)i * a.vstride] = f2h(vs[i]); }
-  } else {
-    float *kc = (float *)a.kcache + off, *vc = (float *)a.vcache + voff;
-    for (int i = lane; i < hd; i += 64) { kc[i] = v[i]; vc[(long)i * a.vstride] = vs[i]; }
-  }
-}
-
 // ================================================================================================ attention
 // Causal GQA attention with the reference's arithmetic (src/model/forward.js:213-230), in two launches:
 //   k_attn_scores  s_t = f32(sum_i q_i K_t,i (f64, exact products) * 1/sqrt(hd)) for every position t <= pos, one
@@ -320,6 +228,34 @@ inline int attn_heads_per_block(int group) {
   return 1;
 }
 
+// Per-head RMSNorm (weights nw, when set) and RoPE at position pos of one head vector v[0..HD) in LDS, by one wave,
+// with the arithmetic of src/model/forward.js:203-211 and src/compute/ref-kernels.js:305-310, 344-363 (64-lane strided
+// f64 sum of squares and butterfly; f64 rotation of each (i, i + half) or (2i, 2i + 1) pair, stored f32).
+template <int HD>
+__device__ inline void norm_rope(float *v, const float *nw, double eps, int nRot, int neox, const float *cosT,
+                                 const float *sinT, int pos, int lane) {
+  if (nw) {
+    double ss = 0;
+    for (int i = lane; i < HD; i += 64) { const double x = (double)v[i]; ss += x * x; }
+    ss = wave_sum_xor(ss, 64);
+    const double sc = 1.0 / sqrt(ss / (double)HD + eps);
+    for (int i = lane; i < HD; i += 64) v[i] = (float)((double)v[i] * sc * (double)nw[i]);
+  }
+  const int half = nRot / 2;
+  for (int i = lane; i < half; i += 64) {
+    const int i0 = neox ? i : 2 * i, i1 = neox ? i + half : 2 * i + 1;
+    const double c = (double)cosT[(long)pos * half + i], sn = (double)sinT[(long)pos * half + i];
+    const double x0 = (double)v[i0], x1 = (double)v[i1];
+    v[i0] = (float)(x0 * c - x1 * sn);  // pairs are disjoint across lanes
+    v[i1] = (float)(x0 * sn + x1 * c);
+  }
+}
+
+// Scores of one 64-position chunk of one token for hg query heads sharing a KV head. Keys of positions before the
+// pass (pos0) come from the cache; the pass's own keys (positions pos0 .. pos0 + b) are normed and rotated here from the
+// projection output, rounded as the cache stores them, and the block of token b appends its own key and value to the
+// cache (K position-major, V dimension-major), which is where the reference's pass writes them before attending
+// (src/model/forward.js:203-214). The query heads are normed and rotated here too.
 template <int HD, bool F16KV>
 __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
   constexpr int VB = F16KV ? 2 : 4;      // bytes per cached value
@@ -330,34 +266,72 @@ __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
   constexpr int R = P / PPI;             // load rounds per chunk
   static_assert(R >= 1 && P % PPI == 0, "chunk geometry");
   __shared__ float qs[8 * HD];
-  const int b = blockIdx.z, tid = threadIdx.x;
+  __shared__ float kf[8 * HD];           // rotated keys of the pass, a batch of up to 8 positions at a time (f32)
+  extern __shared__ __align__(16) uint8_t kn[];  // the chunk's new keys in cache format, from position n0: [min(P, B)][HD]
+  const int b = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const Step *st = a.step;
   if (b >= st->B) return;
-  const int npos = st->pos0 + b + 1;
+  const int pos0 = st->pos0, npos = pos0 + b + 1;
   if (blockIdx.x * P >= npos) return;
   const int group = a.nHead / a.nHeadKv, hg = a.hpb;
   const int h0 = blockIdx.y * hg;        // first query head of this block
   const int kvh = h0 / group;
+  const bool writer = h0 % group == 0;   // the first head group of a KV head appends the pass's K and V
   const long kvoff = ((long)a.layer * a.nHeadKv + kvh) * a.ctx * HD;
   const uint8_t *kbase = (const uint8_t *)a.kcache + kvoff * VB;
   float *srow = a.scores + ((long)b * a.nHead + h0) * a.sld;
   const int part = tid % LP, sub = tid / LP;
   uint4 u[R];
-  auto fetch = [&](int c0) {
+  auto fetch = [&](int c0) {  // cached keys only: positions of the pass are filled in from kn
     #pragma unroll
     for (int r = 0; r < R; r++) {
       const int t = c0 + r * PPI + sub;
-      u[r] = t < npos ? *(const uint4 *)(kbase + ((long)t * HD + part * EPL) * VB) : make_uint4(0, 0, 0, 0);
+      u[r] = t < pos0 ? *(const uint4 *)(kbase + ((long)t * HD + part * EPL) * VB) : make_uint4(0, 0, 0, 0);
     }
   };
-  fetch(blockIdx.x * P);  // the first chunk's keys are in flight while q is staged
+  fetch(blockIdx.x * P);  // the first chunk's keys are in flight while q is prepared
   for (int i = tid; i < hg * HD; i += 256) qs[i] = a.q[(long)b * a.ldq + (long)h0 * HD + i];
+  __syncthreads();
+  for (int h = wave; h < hg; h += 4) norm_rope<HD>(qs + h * HD, a.qNorm, a.eps, a.nRot, a.neox, a.cosT, a.sinT, npos - 1, lane);
   __syncthreads();
   for (int c0 = blockIdx.x * P; c0 < npos; c0 += gridDim.x * P) {
     if (c0 != blockIdx.x * P) fetch(c0);
+    // the pass's keys in this chunk: positions [n0, n1), tokens [n0 - pos0, n1 - pos0)
+    const int n0 = max(c0, pos0), n1 = min(c0 + P, npos);
+    for (int g0 = n0; g0 < n1; g0 += 8) {
+      const int g1 = min(n1, g0 + 8);
+      for (int i = tid; i < (g1 - g0) * HD; i += 256)
+        kf[i] = a.k[(long)(g0 - pos0 + i / HD) * a.ldkv + (long)kvh * HD + i % HD];
+      __syncthreads();
+      for (int p = g0 + wave; p < g1; p += 4)
+        norm_rope<HD>(kf + (p - g0) * HD, a.kNorm, a.eps, a.nRot, a.neox, a.cosT, a.sinT, p, lane);
+      __syncthreads();
+      for (int i = tid; i < (g1 - g0) * HD; i += 256) {
+        const int p = g0 + i / HD, d = i % HD;
+        const float kv = kf[i];
+        const long off = kvoff + (long)p * HD + d;
+        if (F16KV) {
+          const uint16_t hbits = f2h(kv);
+          ((uint16_t *)kn)[(p - n0) * HD + d] = hbits;
+          if (writer && p == npos - 1) {
+            ((uint16_t *)a.kcache)[off] = hbits;
+            ((uint16_t *)a.vcache)[(((long)a.layer * a.nHeadKv + kvh) * HD + d) * a.vstride + p] =
+                f2h(a.v[(long)b * a.ldkv + (long)kvh * HD + d]);
+          }
+        } else {
+          ((float *)kn)[(p - n0) * HD + d] = kv;
+          if (writer && p == npos - 1) {
+            ((float *)a.kcache)[off] = kv;
+            ((float *)a.vcache)[(((long)a.layer * a.nHeadKv + kvh) * HD + d) * a.vstride + p] = a.v[(long)b * a.ldkv + (long)kvh * HD + d];
+          }
+        }
+      }
+      __syncthreads();
+    }
     #pragma unroll
     for (int r = 0; r < R; r++) {
       const int t = c0 + r * PPI + sub;
+      if (t >= pos0 && t < npos) u[r] = *(const uint4 *)(kn + ((t - n0) * HD + part * EPL) * VB);
       const uint32_t w4[4] = {u[r].x, u[r].y, u[r].z, u[r].w};
       double kv[EPL];
       #pragma unroll
@@ -372,6 +346,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
         if (part == (h % LP) && t < npos) srow[(long)h * a.sld + t] = (float)(s * a.scale);
       }
     }
+    __syncthreads();  // kn is refilled by the next chunk
   }
 }
 
@@ -519,8 +494,9 @@ size_t attention_lds(int ctx) { return (size_t)((ctx + AV_UNIT - 1) / AV_UNIT * 
 constexpr size_t ATTN_LDS_MAX = 150 * 1024;
 
 template <int HD, bool F16KV>
-static void launch_scores_k(const AttnArgs &a, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((k_attn_scores<HD, F16KV>), grid, dim3(256), 0, st, a);
+static void launch_scores_k(const AttnArgs &a, dim3 grid, int B, hipStream_t st) {
+  const size_t kn = (size_t)std::min(64, B) * HD * (F16KV ? 2 : 4);
+  hipLaunchKernelGGL((k_attn_scores<HD, F16KV>), grid, dim3(256), kn, st, a);
 }
 
 template <bool F16KV>
@@ -544,12 +520,12 @@ void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
   const int chunks = (a.ctx + 63) / 64;
   dim3 gs(chunks < 64 ? chunks : 64, a.nHead / a.hpb, B);
   switch (a.hd * 2 + a.kvF16) {
-    case 128: launch_scores_k<64, false>(a, gs, st); break;
-    case 129: launch_scores_k<64, true>(a, gs, st); break;
-    case 256: launch_scores_k<128, false>(a, gs, st); break;
-    case 257: launch_scores_k<128, true>(a, gs, st); break;
-    case 512: launch_scores_k<256, false>(a, gs, st); break;
-    case 513: launch_scores_k<256, true>(a, gs, st); break;
+    case 128: launch_scores_k<64, false>(a, gs, B, st); break;
+    case 129: launch_scores_k<64, true>(a, gs, B, st); break;
+    case 256: launch_scores_k<128, false>(a, gs, B, st); break;
+    case 257: launch_scores_k<128, true>(a, gs, B, st); break;
+    case 512: launch_scores_k<256, false>(a, gs, B, st); break;
+    case 513: launch_scores_k<256, true>(a, gs, B, st); break;
   }
   ZL_HIP(hipGetLastError());
   dim3 ga(a.hd / AV_DIMS, a.nHead, B);
@@ -564,18 +540,14 @@ void launch_norm_quant(const float *x, int ldx, int row0, int nrows, const float
   ZL_HIP(hipGetLastError());
 }
 
-void launch_rope(const RopeArgs &a, int B, hipStream_t st) {
-  hipLaunchKernelGGL(k_qk_rope_kv, dim3(B, a.nHead + a.nHeadKv), dim3(64), 0, st, a);
-  ZL_HIP(hipGetLastError());
-}
 
 void launch_embed(const MatView &m, const Step *step, int B, float *x, int ldx, hipStream_t st) {
-  hipLaunchKernelGGL(k_embed, dim3(B), dim3(64), 0, st, m, step, x, ldx);
+  hipLaunchKernelGGL(k_embed, dim3((m.cols + 255) / 256, B), dim3(256), 0, st, m, step, x, ldx);
   ZL_HIP(hipGetLastError());
 }
 
 void launch_dequant_rows(const MatView &m, const int *rowIds, int nrows, float *out, int ldo, hipStream_t st) {
-  hipLaunchKernelGGL(k_dequant_rows, dim3(nrows), dim3(64), 0, st, m, rowIds, nrows, out, ldo);
+  hipLaunchKernelGGL(k_dequant_rows, dim3((m.cols + 255) / 256, nrows), dim3(256), 0, st, m, rowIds, nrows, out, ldo);
   ZL_HIP(hipGetLastError());
 }
 

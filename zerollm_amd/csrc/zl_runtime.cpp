@@ -179,6 +179,7 @@ struct zl_sampler {
   int *dtok = nullptr, *htok = nullptr;
   float *scratch = nullptr;
   int scratchVocab = 0;
+  zl::ArgmaxWork am{};
   hipStream_t st = nullptr;
   ~zl_sampler();
 };
@@ -373,16 +374,10 @@ static void enqueue_forward(zl_model *m, int B, int want) {
       i0 = i1;
     }
     gemv_launches(m, groups, std::vector<int>(groups.size(), EPI_STORE), B, Prologue{m->x, d, 0, L.attnNorm, d});
-    RopeArgs ra;
-    ra.q = m->q; ra.k = m->k; ra.v = m->v; ra.ldq = qd; ra.ldkv = kvd;
-    ra.qNorm = L.qNorm; ra.kNorm = L.kNorm; ra.eps = eps;
-    ra.cosT = m->cosT; ra.sinT = m->sinT;
-    ra.nRot = c.n_rot; ra.neox = c.neox; ra.nHead = c.n_head; ra.nHeadKv = c.n_head_kv; ra.hd = c.head_dim;
-    ra.ctx = m->ctx; ra.layer = l; ra.kvF16 = m->kvF16; ra.kcache = m->kcache; ra.vcache = m->vcache; ra.step = m->dstep;
-    ra.vstride = m->vstride;
-    launch_rope(ra, B, m->st);
     AttnArgs aa;
     aa.q = m->q; aa.ldq = qd; aa.kcache = m->kcache; aa.vcache = m->vcache;
+    aa.k = m->k; aa.v = m->v; aa.ldkv = kvd; aa.qNorm = L.qNorm; aa.kNorm = L.kNorm; aa.eps = eps;
+    aa.cosT = m->cosT; aa.sinT = m->sinT; aa.nRot = c.n_rot; aa.neox = c.neox;
     aa.nHead = c.n_head; aa.nHeadKv = c.n_head_kv; aa.hd = c.head_dim; aa.ctx = m->ctx; aa.layer = l; aa.kvF16 = m->kvF16;
     aa.vstride = m->vstride; aa.hpb = 1; aa.scores = m->scores; aa.sld = m->ctx;
     aa.scale = 1.0 / sqrt((double)c.head_dim);
@@ -765,6 +760,9 @@ static zl_sampler *new_sampler(const zl_sampler_opts *o) {
   s->dstop = (int *)s->ar.alloc(sizeof(int) * 64);
   s->dtok = (int *)s->ar.alloc(sizeof(int) * 4);
   ZL_HIP(hipHostMalloc((void **)&s->htok, sizeof(int) * 4));
+  s->am.keys = (unsigned long long *)s->ar.alloc(sizeof(unsigned long long) * ARGMAX_MAX_ROWS * ARGMAX_MAX_BLOCKS);
+  s->am.count = (uint32_t *)s->ar.alloc(sizeof(uint32_t) * ARGMAX_MAX_ROWS);
+  ZL_HIP(hipMemset(s->am.count, 0, sizeof(uint32_t) * ARGMAX_MAX_ROWS));
   hipLaunchKernelGGL(k_set_rng, dim3(1), dim3(64), 0, s->st, s->ss, o->seed);
   ZL_HIP(hipGetLastError());
   ZL_HIP(hipStreamSynchronize(s->st));
@@ -805,7 +803,7 @@ static void dist_of_row(zl_sampler *s, zl_model *m, int row, const int32_t *hist
   ensure_scratch(s, m->cfg.vocab);
   const int keep = upload_hist(s, m->st, hist, nh);
   launch_dist_rows(m->logits + (size_t)row * m->cfg.vocab, m->cfg.vocab, 1, m->cfg.vocab, s->sp, keep ? s->dhist : nullptr, keep, 0,
-                   s->scratch, out, m->st);
+                   s->scratch, s->am, out, m->st);
 }
 
 // ---------------------------------------------------------------------------------------------- speculative cycle
@@ -867,14 +865,14 @@ static void spec_cycle(zl_model *T, zl_model *D, zl_sampler *s, const int32_t *f
       i += c;
     }
     for (int j = 0; j < kk; j++) {
-      launch_dist_rows(D->logits, D->cfg.vocab, 1, D->cfg.vocab, s->sp, dh, keep + j, 0, s->scratch, s->qdist + j, st);
+      launch_dist_rows(D->logits, D->cfg.vocab, 1, D->cfg.vocab, s->sp, dh, keep + j, 0, s->scratch, s->am, s->qdist + j, st);
       launch_draft_draw(s->qdist + j, s->ss, j, s->dstop, nStop, D->dstep, j == 0 ? lastChunk : 1, T->dstep, s->dhist, keep, st);
       if (j < kk - 1) launch_pass(D, 1, 1);
     }
   }
   ZL_HIP(hipEventRecord(em, st));
   launch_pass(T, kk + 1, 2);
-  launch_dist_rows(T->logits, T->cfg.vocab, kk + 1, T->cfg.vocab, s->sp, dh, keep, 1, s->scratch, s->pdist, st);
+  launch_dist_rows(T->logits, T->cfg.vocab, kk + 1, T->cfg.vocab, s->sp, dh, keep, 1, s->scratch, s->am, s->pdist, st);
   launch_accept(s->pdist, s->qdist, s->ss, (s->sp.temperature <= 0.0 || s->sp.greedyArgmax) ? 1 : 0, st);
   ZL_HIP(hipEventRecord(e1, st));
   ZL_HIP(hipMemcpyAsync(s->hss, s->ss, sizeof(SpecState), hipMemcpyDeviceToHost, st));

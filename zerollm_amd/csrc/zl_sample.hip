@@ -290,8 +290,76 @@ __global__ void k_draw_one(const DevDist *dist, uint32_t *rng, int *out) {
   *rng = s;
 }
 
+// Greedy rows without penalties: first-maximum argmax of each row split over many blocks. Each block reduces its
+// chunk to one key (order-preserving value bits, then the complement of the index, so the larger key is the larger
+// value and, among equal values, the smaller index), stores it, and the last block of the row to arrive (counted with a
+// device-scope atomic that it resets for the next launch) reduces the row's keys in one pass. NaN logits are never
+// selected, as in the single-block path.
+constexpr int AM_THREADS = 512;
+constexpr int AM_CHUNK = AM_THREADS * 8;  // logits per block
+
+__global__ __launch_bounds__(AM_THREADS) void k_argmax_rows(const float *__restrict__ logits, int ldl, int vocab,
+                                                            unsigned long long *keys, uint32_t *count, DevDist *out) {
+  __shared__ unsigned long long wk[AM_THREADS / 64];
+  __shared__ uint32_t prev;
+  const int r = blockIdx.y, nb = gridDim.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float *l = logits + (long)r * ldl;
+  const int base = blockIdx.x * AM_CHUNK + tid * 8;
+  float v[8];
+  if (base + 8 <= vocab && ((((uintptr_t)(l + base)) & 15) == 0)) {
+    const float4 a = *(const float4 *)(l + base), b = *(const float4 *)(l + base + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    #pragma unroll
+    for (int k = 0; k < 8; k++) v[k] = base + k < vocab ? l[base + k] : -INFINITY;
+  }
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  #pragma unroll
+  for (int k = 0; k < 8; k++)
+    if (v[k] > bv) { bv = v[k]; bi = base + k; }
+  unsigned long long key = ((unsigned long long)fkey(bv) << 32) | (uint32_t)~(uint32_t)bi;
+  key = group_reduce(key, 64, [](unsigned long long x, unsigned long long y) { return x > y ? x : y; });
+  if (lane == 0) wk[wave] = key;
+  __syncthreads();
+  if (tid == 0) {
+    unsigned long long k = wk[0];
+    for (int w = 1; w < AM_THREADS / 64; w++) k = wk[w] > k ? wk[w] : k;
+    keys[(long)r * nb + blockIdx.x] = k;
+    __threadfence();
+    prev = atomicAdd(&count[r], 1u);
+  }
+  __syncthreads();
+  if (prev != (uint32_t)(nb - 1)) return;
+  // last block of the row: every other block's key is visible after its fence and atomic
+  __threadfence();
+  if (tid < 64) {
+    unsigned long long k = 0;
+    for (int b = tid; b < nb; b += 64) {
+      const unsigned long long kb = __atomic_load_n(&keys[(long)r * nb + b], __ATOMIC_RELAXED);
+      k = kb > k ? kb : k;
+    }
+    k = group_reduce(k, 64, [](unsigned long long x, unsigned long long y) { return x > y ? x : y; });
+    if (tid == 0) {
+      int id = (int)~(uint32_t)(k & 0xffffffffu);
+      if (id == 0x7fffffff || id < 0 || id >= vocab) id = 0;  // no finite maximum: the reference's argmax returns 0
+      DevDist *D = out + r;
+      D->n = 1; D->greedy = 1; D->total = 1.0; D->ids[0] = id; D->probs[0] = 1.0;
+      count[r] = 0;
+    }
+  }
+}
+
 void launch_dist_rows(const float *logits, int ldl, int nrows, int vocab, const SamplerParams &sp, const int *hist,
-                      int histLen0, int histInc, float *scratch, DevDist *out, hipStream_t st) {
+                      int histLen0, int histInc, float *scratch, const ArgmaxWork &aw, DevDist *out, hipStream_t st) {
+  const bool greedy = sp.temperature <= 0.0 || sp.greedyArgmax;
+  const int nb = (vocab + AM_CHUNK - 1) / AM_CHUNK;
+  if (greedy && !(sp.penalized && hist && histLen0 + (nrows - 1) * histInc > 0) && nb <= ARGMAX_MAX_BLOCKS &&
+      nrows <= ARGMAX_MAX_ROWS) {
+    hipLaunchKernelGGL(k_argmax_rows, dim3(nb, nrows), dim3(AM_THREADS), 0, st, logits, ldl, vocab, aw.keys, aw.count, out);
+    ZL_HIP(hipGetLastError());
+    return;
+  }
   hipLaunchKernelGGL(k_dist_rows, dim3(nrows), dim3(DT), 0, st, logits, ldl, vocab, sp, hist, histLen0, histInc, scratch, out);
   ZL_HIP(hipGetLastError());
 }
