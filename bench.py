@@ -64,6 +64,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--gen", type=int, default=GEN, help="tokens generated per step (profiling runs use fewer)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the speculative step runs on a single MI355X (asked for --gpus {args.gpus}); "
@@ -89,17 +90,17 @@ def main():
 
     t1 = time.perf_counter()
     st = {}
-    first = list(generate_speculative(target, draft, prompt, k=K, max_tokens=GEN, stats=st))
+    first = list(generate_speculative(target, draft, prompt, k=K, max_tokens=args.gen, stats=st))
     log(f"first call (prefill {PROMPT} tokens + graph capture + {len(first)} tokens) {time.perf_counter() - t1:.1f}s")
     for w in range(args.warmup):
-        out = list(generate_speculative(target, draft, prompt, k=K, max_tokens=GEN, stats=st))
+        out = list(generate_speculative(target, draft, prompt, k=K, max_tokens=args.gen, stats=st))
         assert out == first, "greedy output must be deterministic"
         log(f"warmup {w}: {st['speculative']['cycles']} cycles, accept {st['speculative']['acceptRate']:.3f}")
     times, cycles, acc, drafted, dms, vms = [], 0, 0, 0, 0.0, 0.0
     for s in range(args.steps):
         st = {}
         ts = time.perf_counter()
-        out = list(generate_speculative(target, draft, prompt, k=K, max_tokens=GEN, stats=st))
+        out = list(generate_speculative(target, draft, prompt, k=K, max_tokens=args.gen, stats=st))
         times.append(time.perf_counter() - ts)
         assert out == first
         cycles += st["speculative"]["cycles"]
@@ -107,9 +108,9 @@ def main():
         drafted += st["speculative"]["drafted"]
         dms += st["speculative"]["draftMs"]
         vms += st["speculative"]["verifyMs"]
-        log(f"step {s}: {GEN / times[-1]:.1f} tok/s, {st['speculative']['cycles']} cycles")
+        log(f"step {s}: {args.gen / times[-1]:.1f} tok/s, {st['speculative']['cycles']} cycles")
     total = sum(times)
-    tok_s = GEN * args.steps / total
+    tok_s = args.gen * args.steps / total
     # the dominant kernel of the verify pass: ffn_gate+ffn_up GEMV with SwiGLU epilogue at M = k+1, timed with HIP
     # events on the target's stream over back-to-back launches through all 36 layers' weights (2 GB: cache-cold)
     iters = 4 * t_spec.n_layer
@@ -127,8 +128,8 @@ def main():
         "config": {"workload": "speculative decode, Qwen3-8B-shaped Q4_K_M target (36L d4096 32/8 heads FFN 12288 "
                                "V151936) + Qwen3-0.6B-shaped Q8_0 draft (28L d1024 16/8 heads FFN 3072), k=4, prompt 512, "
                                "256 greedy tokens per step, f16 KV",
-                   "k": K, "prompt": PROMPT, "generate": GEN, "accept_rate": round(acc / max(1, drafted), 4),
-                   "tokens_per_cycle": round(GEN * args.steps / cycles, 3), "cycle_ms": round(cycle_ms, 3),
+                   "k": K, "prompt": PROMPT, "generate": args.gen, "accept_rate": round(acc / max(1, drafted), 4),
+                   "tokens_per_cycle": round(args.gen * args.steps / cycles, 3), "cycle_ms": round(cycle_ms, 3),
                    "draft_ms_per_cycle": round(dms / cycles, 3), "verify_accept_ms_per_cycle": round(vms / cycles, 3),
                    "weight_bytes_per_cycle": bytes_cycle,
                    "cycle_weight_bw_frac": round(bytes_cycle / (cycle_ms * 1e-3) / HBM_PEAK, 4)},

@@ -32,29 +32,54 @@ struct Error : std::runtime_error {
   } while (0)
 
 // ---------------------------------------------------------------------------------------------- repacked weights
-// Every quantised matrix is stored as row-major planes of 64-value "slabs" (cols padded to a multiple of 64 with zero
-// blocks), so that one lane's unit of work is contiguous, 16-byte aligned and the same size for every format:
-//   qs  packed low bits, QB bytes per slab:
-//        Q8_0 64 (int8), Q4_0/Q5_0/Q4_K/Q5_K 32 (byte j: low nibble = value j, high nibble = value j+32),
-//        Q6_K 32 (same nibble layout, the low 4 of 6 bits)
-//   qx  extra high bits per slab: Q5_0/Q5_K 8 bytes (bit j of word w = 5th bit of value 32w+j),
-//        Q6_K 16 bytes (byte j: bits 2i..2i+1 = top 2 bits of value j + 16i)
-//   sc  4 bytes per slab: Q4_K/Q5_K scale codes of the two 32-value sub-blocks, then their min codes;
-//        Q6_K the four int8 16-value group scales
-//   dd  f16 scales: Q8_0/Q4_0/Q5_0 two per slab (one per 32-block); Q4_K/Q5_K (d, dmin) per 256-value super-block;
-//        Q6_K d per super-block
-// F32/F16/BF16 matrices keep their row-major values in qs.
+// Every quantised matrix is stored as planes of 64-value "slabs" (cols padded to a multiple of 64 with zero blocks),
+// rows grouped in tiles of 64 (rows padded to a multiple of 64 with zeros). Within a tile the planes are slab-major:
+// element (row r, slab s) has tile-slab index ts = (r / 64) * nslab + s and lane l = r % 64, and the 64 rows of one
+// tile-slab are contiguous, so a wave whose lane l works on row 64T + l reads one contiguous piece per plane per slab.
+//   qs  packed low bits, QB bytes per (row, slab), stored as QB/16 parts of 16 bytes: part p of (r, s) at
+//       ((ts * QB/16 + p) * 64 + l) * 16 (each 16-byte load of a wave covers 1 KB without gaps).
+//       Q8_0 QB 64 (int8), Q4_0/Q5_0/Q4_K/Q5_K 32 (byte j: low nibble = value j, high nibble = value j+32),
+//       Q6_K 32 (same nibble layout, the low 4 of 6 bits)
+//   qx  extra high bits at (ts * 64 + l) * QX: Q5_0/Q5_K QX 8 (bit j of word w = 5th bit of value 32w+j),
+//       Q6_K QX 16 (byte j: bits 2i..2i+1 = top 2 bits of value j + 16i)
+//   sc  4 bytes at (ts * 64 + l) * 4: Q4_K/Q5_K scale codes of the two 32-value sub-blocks, then their min codes;
+//       Q6_K the four int8 16-value group scales
+//   dd  f16 scales: Q8_0/Q4_0/Q5_0 two per (row, slab) at u16 index (ts * 64 + l) * 2 + h (h = 32-value block);
+//       Q4_K/Q5_K (d, dmin) per 256-value super-block at u16 index ((r/64 * nsb + s/4) * 64 + l) * 2 + {0, 1};
+//       Q6_K d per super-block at u16 index (r/64 * nsb + s/4) * 64 + l  (nsb = nslab / 4)
+// A view of rows [64i, 64i + n) is an offset into every plane. F32/F16/BF16 matrices keep row-major values in qs.
 struct DevMat {
   int type = -1, rows = 0, cols = 0, nslab = 0;
   uint8_t *qs = nullptr, *qx = nullptr, *sc = nullptr;
   uint16_t *dd = nullptr;
 };
 
-inline int qs_bytes(int t) { return t == T_Q8_0 ? 64 : 32; }
-inline int qx_bytes(int t) { return (t == T_Q5_0 || t == T_Q5_K) ? 8 : t == T_Q6_K ? 16 : 0; }
-inline int sc_bytes(int t) { return (t == T_Q4_K || t == T_Q5_K || t == T_Q6_K) ? 4 : 0; }
-inline bool is_quant(int t) { return t == T_Q8_0 || t == T_Q4_0 || t == T_Q5_0 || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
-inline bool is_kquant(int t) { return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
+__host__ __device__ inline int qs_bytes(int t) { return t == T_Q8_0 ? 64 : 32; }
+__host__ __device__ inline int qx_bytes(int t) { return (t == T_Q5_0 || t == T_Q5_K) ? 8 : t == T_Q6_K ? 16 : 0; }
+__host__ __device__ inline int sc_bytes(int t) { return (t == T_Q4_K || t == T_Q5_K || t == T_Q6_K) ? 4 : 0; }
+__host__ __device__ inline bool is_quant(int t) { return t == T_Q8_0 || t == T_Q4_0 || t == T_Q5_0 || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
+__host__ __device__ inline bool is_kquant(int t) { return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
+__host__ __device__ inline int tiles_of(int rows) { return (rows + 63) / 64; }
+// u16 entries of the dd plane per 64-row tile
+__host__ __device__ inline long dd_per_tile(int t, int nslab) {
+  return (t == T_Q4_K || t == T_Q5_K) ? (long)(nslab / 4) * 128 : t == T_Q6_K ? (long)(nslab / 4) * 64 : (long)nslab * 128;
+}
+
+// Byte / u16 offsets of element (r, s) in the tiled planes (device side; the host uses the same formulas).
+__host__ __device__ inline long tile_slab(int r, int s, int nslab) { return (long)(r >> 6) * nslab + s; }
+__host__ __device__ inline long qs_off(int t, int r, int s, int nslab, int j) {  // byte j of the (r, s) slab's qs
+  const int qp = t == T_Q8_0 ? 4 : 2;
+  return ((tile_slab(r, s, nslab) * qp + (j >> 4)) * 64 + (r & 63)) * 16 + (j & 15);
+}
+__host__ __device__ inline long qx_off(int t, int r, int s, int nslab, int j) {
+  return (tile_slab(r, s, nslab) * 64 + (r & 63)) * ((t == T_Q6_K) ? 16 : 8) + j;
+}
+__host__ __device__ inline long sc_off(int r, int s, int nslab, int j) { return (tile_slab(r, s, nslab) * 64 + (r & 63)) * 4 + j; }
+__host__ __device__ inline long dd_off(int t, int r, int s, int nslab, int k) {  // k: 32-block half (per-slab types) or d/dmin
+  if (t == T_Q4_K || t == T_Q5_K) return (((long)(r >> 6) * (nslab >> 2) + (s >> 2)) * 64 + (r & 63)) * 2 + k;
+  if (t == T_Q6_K) return ((long)(r >> 6) * (nslab >> 2) + (s >> 2)) * 64 + (r & 63);
+  return (tile_slab(r, s, nslab) * 64 + (r & 63)) * 2 + k;
+}
 
 // ---------------------------------------------------------------------------------------------- device helpers
 __device__ inline float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }

@@ -1,0 +1,437 @@
+// Quantised GEMV for M = 1..9 tokens on gfx950 (included by the per-format zl_gemv_*.hip files):
+// y[t][r] = sum over the row's 32-value blocks of the reference's block term (src/compute/ref-kernels.js:127-277):
+// exact int8 block dots (v_dot4_i32_i8), f64 scale combination.
+//
+// Mapping. A wave owns one 64-row tile, one row per lane, and walks slabs (64 values) of the K range its workgroup
+// holds: wave w of the workgroup takes slabs s0 + w, s0 + w + 4, ... The weights' 16-byte planes are contiguous per
+// tile-slab, so each vector load of the wave reads 1 KB without gaps. Every lane of the wave needs the same activation
+// values: the workgroup stages its slab range of the M tokens' int8 values and block records in LDS once (those loads
+// are issued before the weight loads, so they are not queued behind them), and the loop reads them as broadcast LDS
+// loads, which complete in order and pipeline. No cross-lane reduction in the loop. The four waves' f64 sums meet in
+// LDS (added in wave order); with ks > 1 K parts per tile the parts' sums go through `part` and the last part to
+// arrive adds them in part order. Every summation order depends only on the matrix shape, never on M, so a batched
+// pass gives the same bits as token-by-token passes. Raw slabs are loaded DEPTH slabs ahead of the one computed.
+#pragma once
+#include "zl_kernels.h"
+
+namespace zl {
+
+constexpr int GT_NMAX = 16;          // slabs per wave at most (the slab loop is unrolled that far)
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+constexpr int GT_KR_MAX = 96;        // slabs per K part at most (staged activations: M x 96 x 96 bytes of LDS)
+constexpr int GT_REC = 96;           // LDS bytes per (token, slab): 64 int8 values, then the two blocks' records
+
+template <int FMT>
+struct Fmt {
+  static constexpr int QW = FMT == T_Q8_0 ? 16 : 8;                                          // qs words per (row, slab)
+  static constexpr int HW = FMT == T_Q6_K ? 4 : (FMT == T_Q5_0 || FMT == T_Q5_K) ? 2 : 0;    // qx words
+  static constexpr bool SC = FMT == T_Q4_K || FMT == T_Q5_K || FMT == T_Q6_K;                // scale-code plane
+};
+
+// One (row, slab) as loaded.
+template <int FMT>
+struct Raw {
+  uint32_t q[Fmt<FMT>::QW];
+  uint32_t h[Fmt<FMT>::HW > 0 ? Fmt<FMT>::HW : 1];
+  uint32_t sc, dw;
+};
+
+// Buffer resources of one matrix's planes: loads take the lane's byte offset (VGPR, loop invariant) and the
+// tile-slab's (SGPR).
+struct Rsrc {
+  __amdgpu_buffer_rsrc_t qs, qx, sc, dd;
+};
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, (int)bytes, 0x00020000);
+}
+
+// Load tile-slab ts (super-block index sbi = tile * nslab / 4 + slab / 4 for the K-quants' dd plane). With valid
+// false the lane offsets are moved past every plane (planes are below 1 GB): the buffer range check then returns zeros
+// without a memory access, so a pipeline can issue its loads unconditionally.
+template <int FMT>
+__device__ inline void raw_load(const Rsrc &R, int ts, int sbi, int lane, bool valid, Raw<FMT> &o) {
+  constexpr int QP = Fmt<FMT>::QW / 4;
+  const int oob = valid ? 0 : 0x40000000;
+  ts = valid ? ts : 0;
+  sbi = valid ? sbi : 0;
+  #pragma unroll
+  for (int p = 0; p < QP; p++) {
+    const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(R.qs, oob + lane * 16, (ts * QP + p) * 1024, 0));
+    o.q[4 * p] = v.x; o.q[4 * p + 1] = v.y; o.q[4 * p + 2] = v.z; o.q[4 * p + 3] = v.w;
+  }
+  if constexpr (Fmt<FMT>::HW == 2) {
+    const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(R.qx, oob + lane * 8, ts * 512, 0));
+    o.h[0] = v.x; o.h[1] = v.y;
+  }
+  if constexpr (Fmt<FMT>::HW == 4) {
+    const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(R.qx, oob + lane * 16, ts * 1024, 0));
+    o.h[0] = v.x; o.h[1] = v.y; o.h[2] = v.z; o.h[3] = v.w;
+  }
+  if constexpr (Fmt<FMT>::SC) o.sc = __builtin_amdgcn_raw_buffer_load_b32(R.sc, oob + lane * 4, ts * 256, 0);
+  if constexpr (FMT == T_Q4_K || FMT == T_Q5_K) o.dw = __builtin_amdgcn_raw_buffer_load_b32(R.dd, oob + lane * 4, sbi * 256, 0);
+  else if constexpr (FMT == T_Q6_K) o.dw = __builtin_amdgcn_raw_buffer_load_b16(R.dd, oob + lane * 2, sbi * 128, 0);
+  else o.dw = __builtin_amdgcn_raw_buffer_load_b32(R.dd, oob + lane * 4, ts * 256, 0);
+}
+
+// Token-independent data of one (row, slab): int8 lanes of the 64 values (words 0-7 block 0 = values 0-31, words
+// 8-15 block 1; unsigned codes for the offset formats) and exact f64 factors per 32-value block h:
+//   Q8_0/Q4_0/Q5_0: fa = d;  Q4_K/Q5_K: fa = d*sc, fb = dmin*mn;  Q6_K: fa, fb = d*scale of the block's 16-groups
+template <int FMT>
+struct Unp {
+  uint32_t w[16];
+  double fa[2], fb[2];
+};
+
+template <int FMT>
+__device__ inline void unpack(const Raw<FMT> &o, Unp<FMT> &u) {
+  if constexpr (FMT == T_Q8_0) {
+    #pragma unroll
+    for (int i = 0; i < 16; i++) u.w[i] = o.q[i];
+  } else if constexpr (FMT == T_Q6_K) {
+    // block 0: values 0-15 | 16-31 from the low nibbles of q[0..3] | q[4..7]; block 1 from the high nibbles; the top
+    // two bits of value j + 16k are bits 2k..2k+1 of qx byte j
+    #pragma unroll
+    for (int i = 0; i < 4; i++) {
+      u.w[i] = (o.q[i] & 0x0F0F0F0Fu) | ((o.h[i] & 0x03030303u) << 4);
+      u.w[4 + i] = (o.q[4 + i] & 0x0F0F0F0Fu) | ((o.h[i] & 0x0C0C0C0Cu) << 2);
+      u.w[8 + i] = ((o.q[i] >> 4) & 0x0F0F0F0Fu) | (o.h[i] & 0x30303030u);
+      u.w[12 + i] = ((o.q[4 + i] >> 4) & 0x0F0F0F0Fu) | ((o.h[i] & 0xC0C0C0C0u) >> 2);
+    }
+  } else {
+    #pragma unroll
+    for (int i = 0; i < 8; i++) {
+      u.w[i] = o.q[i] & 0x0F0F0F0Fu;
+      u.w[8 + i] = (o.q[i] >> 4) & 0x0F0F0F0Fu;
+    }
+    if constexpr (FMT == T_Q5_0 || FMT == T_Q5_K) {
+      // bit j of h[b] is the fifth bit of value j of block b: spread 4 bits to the 4 bytes of a word
+      #pragma unroll
+      for (int b = 0; b < 2; b++) {
+        #pragma unroll
+        for (int i = 0; i < 8; i++) u.w[8 * b + i] |= ((((o.h[b] >> (4 * i)) & 15u) * 0x00204081u) & 0x01010101u) << 4;
+      }
+    }
+  }
+  const double d0 = (double)h2f((uint16_t)(o.dw & 0xffff)), d1 = (double)h2f((uint16_t)(o.dw >> 16));
+  if constexpr (FMT == T_Q4_K || FMT == T_Q5_K) {
+    #pragma unroll
+    for (int h = 0; h < 2; h++) {
+      u.fa[h] = d0 * (double)((o.sc >> (8 * h)) & 0xff);
+      u.fb[h] = d1 * (double)((o.sc >> (16 + 8 * h)) & 0xff);
+    }
+  } else if constexpr (FMT == T_Q6_K) {
+    #pragma unroll
+    for (int h = 0; h < 2; h++) {
+      u.fa[h] = d0 * (double)(int8_t)((o.sc >> (16 * h)) & 0xff);
+      u.fb[h] = d0 * (double)(int8_t)((o.sc >> (16 * h + 8)) & 0xff);
+    }
+  } else {
+    u.fa[0] = d0; u.fa[1] = d1;
+    u.fb[0] = 0.0; u.fb[1] = 0.0;
+  }
+}
+
+__device__ inline double dbl(uint32_t lo, uint32_t hi) {
+  return __builtin_bit_cast(double, (unsigned long long)lo | ((unsigned long long)hi << 32));
+}
+
+// acc + the term of block h (values 32h..32h+31) of the slab for one token. X: the token's 32 int8 values of the
+// block (uniform); R: the block's record (uniform). In the reference's arithmetic up to where f64 rounds:
+//   Q8_0 (s*d)*xd;  Q4_0/Q5_0 ((s - 8|16 sum) * d) * xd;  Q4_K/Q5_K xd*(d*sc*s - dmin*mn*sum);
+//   Q6_K per 16-group (d*scale*(s - 32 sum)) * xd.  The products before the last one are exact; the last multiply
+//   and the accumulation are one fma.
+template <int FMT>
+__device__ inline double block_term(const Unp<FMT> &u, int h, const u32x8 &X, const u32x4 &R, double acc) {
+  const double xd = dbl(R[0], R[1]);
+  if constexpr (FMT == T_Q6_K) {
+    int g0 = -(int)R[2], g1 = -(int)R[3];
+    #pragma unroll
+    for (int i = 0; i < 4; i++) g0 = sdot4((int)u.w[8 * h + i], (int)X[i], g0);
+    #pragma unroll
+    for (int i = 4; i < 8; i++) g1 = sdot4((int)u.w[8 * h + i], (int)X[i], g1);
+    acc = fma(u.fa[h] * (double)g0, xd, acc);
+    return fma(u.fb[h] * (double)g1, xd, acc);
+  } else {
+    int lo = (FMT == T_Q4_0 || FMT == T_Q5_0) ? -(int)R[FMT == T_Q4_0 ? 2 : 3] : 0;
+    #pragma unroll
+    for (int i = 0; i < 8; i++) lo = sdot4((int)u.w[8 * h + i], (int)X[i], lo);
+    if constexpr (FMT == T_Q4_K || FMT == T_Q5_K) return fma(xd, fma(u.fa[h], (double)lo, -(u.fb[h] * dbl(R[2], R[3]))), acc);
+    else return fma((double)lo * u.fa[h], xd, acc);
+  }
+}
+
+// Record array of the format family.
+template <int FMT>
+__device__ inline const void *recs_of(const Act &a) {
+  if constexpr (FMT == T_Q6_K) return a.rb;
+  else if constexpr (FMT == T_Q4_0 || FMT == T_Q5_0) return a.rc;
+  else return a.ra;
+}
+
+template <int FMT, int MT, int EPI, int DEPTH>
+__global__ __launch_bounds__(EPI == EPI_SWIGLU ? 512 : 1024) void k_gemv_tiles(const GemvArgs a) {
+  constexpr int NR = EPI == EPI_SWIGLU ? 2 : 1;
+  constexpr int WMAX = EPI == EPI_SWIGLU ? 8 : 16;  // waves per workgroup at most
+  __shared__ double red[WMAX / 2][NR * MT][64];
+  extern __shared__ __align__(16) uint8_t xl[];  // per token: [nsl][64] int8 values, then [nsl][32] records
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = a.nwave;  // waves of the workgroup (1, 2, 4, 8 or 16)
+  const int ks = a.ks, kp = blockIdx.x, tile = blockIdx.y;  // grid: (K parts, tiles)
+  // segment of the tile, selected field by field (no dynamic indexing into the argument block)
+  const int si = __builtin_amdgcn_readfirstlane(
+      EPI == EPI_SWIGLU ? 0 : (a.nseg > 2 && tile >= a.seg[2].tile0) ? 2 : (a.nseg > 1 && tile >= a.seg[1].tile0) ? 1 : 0);
+#define ZL_SEG(f) (si == 0 ? a.seg[0].f : si == 1 ? a.seg[1].f : a.seg[2].f)
+  const int lt = tile - ZL_SEG(tile0), rows = ZL_SEG(rows);
+  const int nslab = a.nslab, nsb = nslab >> 2;
+  const Rsrc R0 = {make_rsrc(ZL_SEG(m.qs), ZL_SEG(nqs)), make_rsrc(ZL_SEG(m.qx), ZL_SEG(nqx)), make_rsrc(ZL_SEG(m.sc), ZL_SEG(nsc)),
+                   make_rsrc(ZL_SEG(m.dd), ZL_SEG(ndd))};
+  const Rsrc R1 = NR == 2 ? Rsrc{make_rsrc(a.seg[1].m.qs, a.seg[1].nqs), make_rsrc(a.seg[1].m.qx, a.seg[1].nqx),
+                                 make_rsrc(a.seg[1].m.sc, a.seg[1].nsc), make_rsrc(a.seg[1].m.dd, a.seg[1].ndd)}
+                          : R0;
+  const int kr = a.kr, s0 = kp * kr, s1 = min(nslab, s0 + kr), nsl = s1 - s0;
+  const int n = nsl > wave ? (nsl - wave + W - 1) / W : 0;  // this wave's slabs: s0 + wave + W i, i < n <= GT_NMAX
+  const int M = a.M;
+  const uint8_t *xq = (const uint8_t *)a.act.q, *xr = (const uint8_t *)recs_of<FMT>(a.act);
+  const long ldq = a.act.ld, ldr = (long)(a.act.ld >> 5) * 16;
+
+  double acc[NR][MT];
+  #pragma unroll
+  for (int r = 0; r < NR; r++)
+    #pragma unroll
+    for (int t = 0; t < MT; t++) acc[r][t] = 0.0;
+  Raw<FMT> buf[DEPTH][NR];
+  auto load = [&](int i, Raw<FMT> *b) {
+    const int s = s0 + wave + W * i;
+    const int ts = lt * nslab + s, sbi = lt * nsb + (s >> 2);
+    raw_load<FMT>(R0, ts, sbi, lane, i < n, b[0]);
+    if (NR == 2) raw_load<FMT>(R1, ts, sbi, lane, i < n, b[NR - 1]);
+  };
+  #pragma unroll
+  for (int d = 0; d < DEPTH; d++) load(d, buf[d]);
+  if (a.xf) {
+    // ---- fused prologue: RMSNorm scale per token (groups of 4 waves, each in k_norm_quant's order), then quantise the
+    // slab range of every token into LDS in the staged layout
+    __shared__ double ssr[4][4];
+    __shared__ double scl[GEMV_MAX_MT];
+    const int groups = W >> 2 > 0 ? W >> 2 : 1, g = wave >> 2;
+    for (int t0 = 0; t0 < M; t0 += groups) {
+      const int t = t0 + g;
+      const bool act_ = a.nw && g < groups && t < M && W >= 4;
+      double sc = 1.0;
+      if (a.nw) {
+        // rms_scale256 synchronises the block: every thread takes part, idle groups with a dummy row
+        const float *xr = a.xf + (long)(a.xrow0 + (act_ ? t : 0)) * a.ldxf;
+        sc = rms_scale256(xr, a.n, a.eps, (int)threadIdx.x & 255, ssr[g & 3]);
+      }
+      if (act_ && (threadIdx.x & 255) == 0) scl[t] = sc;
+      __syncthreads();
+    }
+    const int per = nsl * 64;  // values of one token in the range (a multiple of 64: each wave holds whole blocks)
+    for (int e = threadIdx.x; e < M * per; e += W * 64) {
+      const int t = e / per, j = e - t * per, col = s0 * 64 + j;
+      float v = 0.f;
+      if (col < a.n) {
+        const float xv = a.xf[(long)(a.xrow0 + t) * a.ldxf + col];
+        v = a.nw ? (float)((double)xv * scl[t] * (double)a.nw[col]) : xv;
+      }
+      const QBlock b = quant32(v);
+      uint8_t *tb = xl + t * nsl * GT_REC;
+      tb[j] = (uint8_t)(int8_t)b.q;
+      if ((j & 31) == 0) *(uint4 *)(tb + nsl * 64 + (j >> 5) * 16) = block_record<FMT>(b);
+    }
+  } else {
+    // ---- stage the activations of the workgroup's slab range in LDS, after the first weight loads: per token its
+    // nsl * 64 int8 values, then its nsl * 32 record bytes, copied in 1 KB chunks by direct global-to-LDS loads (lane
+    // l moves bytes 16l..16l+15 of a chunk), one chunk per wave at a time
+    const int xb = nsl * 64, rb = nsl * 32, xc = (xb + 1023) >> 10, rc = (rb + 1023) >> 10, per = xc + rc;
+    for (int c = wave; c < M * per; c += W) {
+      const int t = c / per, k = c - t * per;
+      const bool isx = k < xc;
+      const int kk = isx ? k : k - xc, off = kk * 1024 + lane * 16;
+      const uint8_t *src = (isx ? xq + t * ldq + s0 * 64 : xr + t * ldr + s0 * 32) + off;
+      uint8_t *dst = xl + t * nsl * GT_REC + (isx ? 0 : xb) + kk * 1024;
+      if (off < (isx ? xb : rb))
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                         (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the staged bytes are in LDS
+  __syncthreads();
+  // fully unrolled over the most slabs a wave can hold (no loop-carried registers: each slot's reload lands in the
+  // registers it was loaded into, and the waits count exactly the loads still needed)
+  #pragma unroll
+  for (int i0 = 0; i0 < GT_NMAX; i0 += DEPTH) {
+    if (i0 >= n) break;
+    #pragma unroll
+    for (int d = 0; d < DEPTH; d++) {
+      const int i = i0 + d;
+      if (i >= GT_NMAX) break;
+      Unp<FMT> u[NR];
+      #pragma unroll
+      for (int r = 0; r < NR; r++) unpack<FMT>(buf[d][r], u[r]);
+      // the slot is reloaded only after it has been unpacked (the reload reuses its registers, no copies)
+      __builtin_amdgcn_sched_barrier(0);
+      load(i + DEPTH, buf[d]);  // past the wave's last slab: no memory access
+      if (i < n) {
+        const int sl = wave + W * i;  // slab within the workgroup's range
+        #pragma unroll
+        for (int t = 0; t < MT; t++) {
+          const int tt = MT == 1 ? 0 : min(t, M - 1);  // a short token tile repeats its last token (not stored)
+          const uint8_t *tb = xl + tt * nsl * GT_REC;
+          const uint4 *xp = (const uint4 *)(tb + sl * 64), *rp = (const uint4 *)(tb + nsl * 64 + sl * 32);
+          #pragma unroll
+          for (int h = 0; h < 2; h++) {
+            const uint4 a0 = xp[2 * h], a1 = xp[2 * h + 1], r = rp[h];
+            const u32x8 Xh = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            const u32x4 Rh = {r.x, r.y, r.z, r.w};
+            #pragma unroll
+            for (int rr = 0; rr < NR; rr++) acc[rr][t] = block_term<FMT>(u[rr], h, Xh, Rh, acc[rr][t]);
+          }
+        }
+      }
+    }
+  }
+
+  // ---- the workgroup's sum, as a fixed tree over the waves: at each step the upper half of the remaining waves parks
+  // its sums in LDS and the lower half adds them (wave w + half onto wave w)
+  for (int half = W >> 1; half >= 1; half >>= 1) {
+    if (wave >= half && wave < 2 * half) {
+      #pragma unroll
+      for (int r = 0; r < NR; r++)
+        #pragma unroll
+        for (int t = 0; t < MT; t++) red[wave - half][r * MT + t][lane] = acc[r][t];
+    }
+    __syncthreads();
+    if (wave < half) {
+      #pragma unroll
+      for (int r = 0; r < NR; r++)
+        #pragma unroll
+        for (int t = 0; t < MT; t++) acc[r][t] += red[wave][r * MT + t][lane];
+    }
+    __syncthreads();
+  }
+  if (wave > 0) return;
+
+  // ---- K parts: the last part of the tile to arrive adds all parts' sums in part order. Partial sums are written and
+  // read with device-scope (agent) atomic accesses, which are coherent across the XCDs' L2 caches without cache-wide
+  // fences; the writer waits for its stores to complete before it counts itself in.
+  if (ks > 1) {
+    constexpr int PW = NR * MT * 64;  // doubles per part
+    double *pp = a.part + ((long)tile * ks + kp) * PW;
+    #pragma unroll
+    for (int r = 0; r < NR; r++)
+      #pragma unroll
+      for (int t = 0; t < MT; t++) __hip_atomic_store(pp + (r * MT + t) * 64 + lane, acc[r][t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stores are complete
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    uint32_t old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __shfl(old, 0);
+    if (old != (uint32_t)(ks - 1)) return;
+    const double *pt = a.part + (long)tile * ks * PW;
+    constexpr int KSMAX = 8;  // the parts' loads of one sum are issued together
+    #pragma unroll
+    for (int r = 0; r < NR; r++)
+      #pragma unroll
+      for (int t = 0; t < MT; t++) {
+        double pv[KSMAX];
+        #pragma unroll
+        for (int k = 0; k < KSMAX; k++)
+          pv[k] = __hip_atomic_load(pt + (long)min(k, ks - 1) * PW + (r * MT + t) * 64 + lane, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+        double v = pv[0];
+        #pragma unroll
+        for (int k = 1; k < KSMAX; k++)
+          if (k < ks) v += pv[k];
+        acc[r][t] = v;
+      }
+    if (lane == 0) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // ---- epilogue: lane = row of the tile
+  const int row = lt * 64 + lane;
+  const bool live = row < rows;
+  if constexpr (EPI == EPI_SWIGLU) {
+    #pragma unroll
+    for (int t = 0; t < MT; t++) {
+      if (t >= M) break;
+      const double g = (double)(float)acc[0][t], uu = (double)(float)acc[1][t];
+      const float hv = live ? (float)(g / (1.0 + exp(-g)) * uu) : 0.f;  // src/compute/ref-kernels.js:322
+      if (live) a.hb[(long)t * a.ldh + row] = hv;
+      if (a.qout.q) quant_block32(hv, row, a.qout, t);
+    }
+  } else if constexpr (EPI == EPI_RESID) {
+    if (live) {
+      #pragma unroll
+      for (int t = 0; t < MT; t++) {
+        if (t >= M) break;
+        float *o = a.resid + (long)t * a.ldr + row;
+        *o = (float)((double)*o + (double)(float)acc[0][t]);
+      }
+    }
+  } else {
+    float *out = ZL_SEG(out);
+    const float *bias = ZL_SEG(bias);
+    const int ldo = ZL_SEG(ldo);
+    if (live) {
+      const double bv = bias ? (double)bias[row] : 0.0;
+      #pragma unroll
+      for (int t = 0; t < MT; t++) {
+        if (t >= M) break;
+        const float y = (float)acc[0][t];
+        out[(long)t * ldo + row] = bias ? (float)((double)y + bv) : y;
+      }
+    }
+  }
+#undef ZL_SEG
+}
+
+template <typename K>
+inline void allow_big_lds(K kernel) {
+  static bool done = false;  // dynamic LDS beyond 64 KB must be allowed per kernel, once
+  if (!done) {
+    ZL_HIP(hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 112 * 1024));
+    done = true;
+  }
+}
+
+// Launch one chunk of at most GEMV_MAX_MT tokens: token tile MT = M (M = 7 runs as 8).
+template <int FMT, int MT>
+inline void launch_tiles_mt(const GemvArgs &a, int epi, hipStream_t st) {
+  ZL_REQUIRE(a.kr <= GT_KR_MAX && a.M <= MT && a.ks <= 8 && a.nwave >= 1 && a.nwave <= (epi == EPI_SWIGLU ? 8 : 16) &&
+                 (a.kr + a.nwave - 1) / a.nwave <= GT_NMAX && (!a.xf || (a.nwave >= 4 && a.n <= a.nslab * 64)),
+             ZL_ERR_ARG, "gemv: launch shape out of range");
+  const dim3 grid((unsigned)a.ks, (unsigned)a.ntiles), blk((unsigned)a.nwave * 64);
+  const size_t lds = (size_t)a.M * a.kr * GT_REC;  // [M][kr] records of 96 bytes
+  if (epi == EPI_STORE) {
+    allow_big_lds(k_gemv_tiles<FMT, MT, EPI_STORE, 4>);
+    hipLaunchKernelGGL((k_gemv_tiles<FMT, MT, EPI_STORE, 4>), grid, blk, lds, st, a);
+  } else if (epi == EPI_RESID) {
+    allow_big_lds(k_gemv_tiles<FMT, MT, EPI_RESID, 4>);
+    hipLaunchKernelGGL((k_gemv_tiles<FMT, MT, EPI_RESID, 4>), grid, blk, lds, st, a);
+  } else {
+    allow_big_lds(k_gemv_tiles<FMT, MT, EPI_SWIGLU, 4>);
+    hipLaunchKernelGGL((k_gemv_tiles<FMT, MT, EPI_SWIGLU, 4>), grid, blk, lds, st, a);
+  }
+}
+
+template <int FMT>
+void launch_gemv_fmt(const GemvArgs &a, int epi, hipStream_t st) {
+  switch (a.M) {
+    case 1: launch_tiles_mt<FMT, 1>(a, epi, st); break;
+    case 2: launch_tiles_mt<FMT, 2>(a, epi, st); break;
+    case 3: launch_tiles_mt<FMT, 3>(a, epi, st); break;
+    case 4: launch_tiles_mt<FMT, 4>(a, epi, st); break;
+    case 5: launch_tiles_mt<FMT, 5>(a, epi, st); break;
+    case 6: launch_tiles_mt<FMT, 6>(a, epi, st); break;
+    case 7: case 8: launch_tiles_mt<FMT, 8>(a, epi, st); break;
+    case 9: launch_tiles_mt<FMT, 9>(a, epi, st); break;
+    default: throw Error(ZL_ERR_ARG, "gemv: bad token count");
+  }
+}
+
+}  // namespace zl

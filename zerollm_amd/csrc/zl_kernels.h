@@ -22,48 +22,86 @@ struct MatView {
 };
 inline MatView view(const DevMat &m) { return MatView{m.type, m.rows, m.cols, m.nslab, m.qs, m.qx, m.sc, m.dd}; }
 
-// Quantised activations of several rows (tokens): int8 values, f32 block scales, int block sums (per 32 and per 16),
-// optionally the f32 values. ld = padded row length (multiple of 64).
+// Quantised activations of several rows (tokens): int8 values, f32 block scales and int block sums (per 32 values),
+// optionally the f32 values, and per 32-value block one 16-byte record per weight-format family, which the GEMV reads
+// with scalar loads (the block scale as f64 plus the integer corrections the format's block term needs).
+// ld = padded row length (multiple of 64); block b of row t is entry t * (ld / 32) + b.
+struct RecA { double d, s; };                  // Q8_0, Q4_K, Q5_K: scale, block sum
+struct RecB { double d; int32_t s16a, s16b; };  // Q6_K: scale, 32 x the sums of the block's two 16-value halves
+struct RecC { double d; int32_t s8, s16; };     // Q4_0, Q5_0: scale, 8 x and 16 x the block sum
 struct Act {
   int8_t *q;
   float *d;
   int32_t *s;
-  int32_t *s16;
+  RecA *ra;
+  RecB *rb;
+  RecC *rc;
   float *f;
   int ld;
 };
+// The same activation from row t0 on.
+inline Act act_rows(const Act &a, int t0) {
+  Act r = a;
+  const long nb = (long)t0 * (a.ld >> 5);
+  r.q = a.q ? a.q + (long)t0 * a.ld : nullptr;
+  r.d = a.d ? a.d + nb : nullptr;
+  r.s = a.s ? a.s + nb : nullptr;
+  r.ra = a.ra ? a.ra + nb : nullptr;
+  r.rb = a.rb ? a.rb + nb : nullptr;
+  r.rc = a.rc ? a.rc + nb : nullptr;
+  r.f = a.f ? a.f + (long)t0 * a.ld : nullptr;
+  return r;
+}
 
 enum : int { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
 
 struct GemvSeg {
-  MatView m;
+  MatView m;        // tiled planes of the segment's matrix
+  uint32_t nqs, nqx, nsc, ndd;  // plane sizes in bytes (buffer-resource bounds)
   int rows;
+  int tile0;        // first tile of the segment in the launch's tile numbering
   float *out;
   int ldo;
   const float *bias;
 };
 
+// One GEMV launch over up to three matrices of one type laid end to end (q, k, v), or a gate/up pair (SWIGLU, seg[1]
+// = up, same tiles). A workgroup handles one 64-row tile and one of `ks` equal ranges of its slabs; with ks > 1 the
+// parts' f64 partial sums go to `part` and the last part to arrive (per-tile counters in `cnt`, left at zero) adds them
+// in part order and runs the epilogue.
 struct GemvArgs {
   GemvSeg seg[3];
   int nseg;
-  int rows_total;  // SWIGLU: rows of gate (== rows of up)
+  int ntiles;
   int nslab;
-  Act act;
-  int M;
-  int lpr;
-  int wk;
-  float *resid;
+  int ks;
+  int kr;           // slabs per K part: ceil(nslab / ks)
+  int nwave;        // waves per workgroup
+  int M;            // tokens (rows of the activation)
+  Act act;          // quantised activations read by the kernel
+  float *resid;     // EPI_RESID: resid[t * ldr + row] += y
   int ldr;
-  float *hb;
+  float *hb;        // EPI_SWIGLU: hb[t * ldh + row] = silu(gate) * up
   int ldh;
-  // Fused activation prologue: when xf is set, each block quantises rows xf[xrow0 + t] (length n, stride ldxf) itself,
-  // after RMSNorm with weights nw when nw is set, exactly as k_norm_quant would, instead of reading `act`.
+  Act qout;         // EPI_SWIGLU: also quantise hb into qout (when qout.q is set)
+  double *part;
+  uint32_t *cnt;
+  // Fused activation prologue: when xf is set, the workgroup quantises rows xf[xrow0 + t] (length n, stride ldxf)
+  // itself, after RMSNorm with weights nw when nw is set, exactly as k_norm_quant would, instead of reading `act`.
   const float *xf;
   int ldxf, xrow0, n;
   const float *nw;
   double eps;
 };
 
+// Split-K work space of GEMV launches (partial sums and per-tile arrival counters, counters zero between launches).
+constexpr int GEMV_MAX_MT = 9;              // tokens per launch
+constexpr int GEMV_CNT_TILES = 4096;        // counters available (tiles of launches with ks > 1)
+constexpr long GEMV_PART_DOUBLES = 8192L * 2 * GEMV_MAX_MT * 64;  // tiles x K parts <= 8192
+struct GemvWork {
+  double *part;
+  uint32_t *cnt;
+};
 
 struct AttnArgs {
   const float *q;
@@ -87,9 +125,74 @@ struct AttnArgs {
   Act act;
 };
 
-int gemv_lpr(int rows, int nslab);
-size_t gemv_lds_bytes(int fmt, int mt, int K);
+// Launch shape of a GEMV over ntiles tiles of nslab slabs: K parts per tile and waves per workgroup.
+void gemv_shape(int ntiles, int nslab, bool swiglu, int *ks, int *nw);
+// Launch a GEMV of a.M tokens (chunks of at most GEMV_MAX_MT); float weights read the f32 activation xf (stride ldx).
 void launch_gemv(const GemvArgs &a, int epi, const float *xf, int ldx, hipStream_t st);
+template <int FMT>
+void launch_gemv_fmt(const GemvArgs &a, int epi, hipStream_t st);
+
+// quantizeAct of one 32-value block (src/compute/ref-kernels.js:44-62) held by 32 consecutive lanes: d = amax/127 (f64,
+// stored f32), q = round-half-away(v * (1/d)). Every lane gets its q; the block's first lane (i & 31 == 0) also gets
+// the f32 scale, the block sum and the sums of the two 16-value halves.
+struct QBlock {
+  int q;
+  float d;
+  int s32, s16a, s16b;
+};
+__device__ inline QBlock quant32(float v) {
+  QBlock r;
+  const float am = group_fmax(fabsf(v), 32);
+  const double scale = (double)am / 127.0;
+  const double inv = scale != 0.0 ? 1.0 / scale : 0.0;
+  r.q = (int)round((double)v * inv);
+  r.d = (float)scale;
+  r.s16a = wave_sum_xor(r.q, 16);          // each 16-lane half holds its sum
+  r.s16b = __shfl_down(r.s16a, 16, 32);    // the second half's sum, at the block's first lane
+  r.s32 = r.s16a + swizzle_xor16(r.s16a);
+  return r;
+}
+
+// The records of one block (at its first lane).
+template <int FMT>
+__device__ inline uint4 block_record(const QBlock &b) {
+  const double d = (double)b.d;
+  const unsigned long long dl = __builtin_bit_cast(unsigned long long, d);
+  if (FMT == T_Q6_K) return make_uint4((uint32_t)dl, (uint32_t)(dl >> 32), (uint32_t)(32 * b.s16a), (uint32_t)(32 * b.s16b));
+  if (FMT == T_Q4_0 || FMT == T_Q5_0) return make_uint4((uint32_t)dl, (uint32_t)(dl >> 32), (uint32_t)(8 * b.s32), (uint32_t)(16 * b.s32));
+  const unsigned long long sl = __builtin_bit_cast(unsigned long long, (double)b.s32);
+  return make_uint4((uint32_t)dl, (uint32_t)(dl >> 32), (uint32_t)sl, (uint32_t)(sl >> 32));
+}
+
+// Quantise value v (element i of activation row `row`, 32 consecutive lanes per block) into Act a.
+__device__ inline void quant_block32(float v, int i, const Act &a, int row) {
+  const QBlock b = quant32(v);
+  a.q[(long)row * a.ld + i] = (int8_t)b.q;
+  if ((i & 31) == 0) {
+    const long k = (long)row * (a.ld >> 5) + (i >> 5);
+    const double d = (double)b.d;
+    a.d[k] = b.d;
+    a.s[k] = b.s32;
+    a.ra[k] = RecA{d, (double)b.s32};
+    a.rb[k] = RecB{d, 32 * b.s16a, 32 * b.s16b};
+    a.rc[k] = RecC{d, 8 * b.s32, 16 * b.s32};
+  }
+}
+
+// RMSNorm scale of one row (src/compute/ref-kernels.js:305-310): 1/sqrt(mean(x^2) + eps), the sum of squares taken by
+// 256 threads (tid < 256: strided sequential f64 sums, a 64-lane butterfly, then (w0 + w1) + (w2 + w3) through red[4]).
+// Every caller uses this order, so every kernel derives the same scale. All 256 threads return it; the caller
+// synchronises the block between the two uses of red.
+__device__ inline double rms_scale256(const float *xr, int n, double eps, int tid, double *red) {
+  double ss = 0;
+  for (int i = tid; i < n; i += 256) { const double v = (double)xr[i]; ss += v * v; }
+  ss = wave_sum_xor(ss, 64);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  ss = (red[0] + red[1]) + (red[2] + red[3]);
+  return 1.0 / sqrt(ss / (double)n + eps);
+}
+
 void launch_attention(const AttnArgs &a, int B, hipStream_t st);
 size_t attention_lds(int ctx);
 void launch_norm_quant(const float *x, int ldx, int row0, int nrows, const float *w, double eps, int n, int npad,

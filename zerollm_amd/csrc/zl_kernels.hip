@@ -21,20 +21,22 @@ __device__ inline void q6_value(const uint8_t *blk, int e, int &lo4, int &hi2) {
   hi2 = (blk[128 + 32 * h + l] >> (2 * qq)) & 3;
 }
 
+// One thread per (row, slab): reads the raw ggml blocks of the slab and writes its tiled-plane elements.
 __global__ void k_repack(int type, const uint8_t *__restrict__ raw, long rawRowBytes, int rows, int cols, int nslab,
                          uint8_t *qs, uint8_t *qx, uint8_t *sc, uint16_t *dd) {
   long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (long)rows * nslab) return;
   int r = (int)(idx / nslab), s = (int)(idx % nslab);
   const uint8_t *row = raw + (long)r * rawRowBytes;
+  uint8_t oq[64];
   if (type == T_Q8_0 || type == T_Q4_0 || type == T_Q5_0) {
     int nb = cols / 32;
     int bsz = type == T_Q8_0 ? 34 : type == T_Q4_0 ? 18 : 22;
-    uint8_t *oq = qs + idx * (type == T_Q8_0 ? 64 : 32);
+    for (int j = 0; j < 32; j++) oq[j] = 0;
     for (int half = 0; half < 2; half++) {
       int b = 2 * s + half;
       const uint8_t *blk = b < nb ? row + (long)b * bsz : nullptr;
-      dd[idx * 2 + half] = blk ? (uint16_t)(blk[0] | (blk[1] << 8)) : 0;
+      dd[dd_off(type, r, s, nslab, half)] = blk ? (uint16_t)(blk[0] | (blk[1] << 8)) : 0;
       if (type == T_Q8_0) {
         for (int i = 0; i < 32; i++) oq[32 * half + i] = blk ? blk[2 + i] : 0;
       } else {
@@ -43,16 +45,15 @@ __global__ void k_repack(int type, const uint8_t *__restrict__ raw, long rawRowB
         // nibble, from block 2s) and value j+32 (high nibble, from block 2s+1)
         for (int j = 0; j < 32; j++) {
           int v = nib ? (j < 16 ? (nib[j] & 15) : (nib[j - 16] >> 4)) : 0;
-          if (half == 0) oq[j] = (uint8_t)((oq[j] & 0xF0) | v);
-          else oq[j] = (uint8_t)((oq[j] & 0x0F) | (v << 4));
+          oq[j] = (uint8_t)(oq[j] | (half == 0 ? v : v << 4));
         }
         if (type == T_Q5_0) {
           uint32_t h = blk ? ((uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) | ((uint32_t)blk[5] << 24)) : 0u;
-          uint8_t *ox = qx + idx * 8 + 4 * half;
-          ox[0] = h & 0xff; ox[1] = (h >> 8) & 0xff; ox[2] = (h >> 16) & 0xff; ox[3] = (h >> 24) & 0xff;
+          for (int i = 0; i < 4; i++) qx[qx_off(type, r, s, nslab, 4 * half + i)] = (h >> (8 * i)) & 0xff;
         }
       }
     }
+    for (int j = 0; j < qs_bytes(type); j++) qs[qs_off(type, r, s, nslab, j)] = oq[j];
     return;
   }
   if (type == T_Q4_K || type == T_Q5_K) {
@@ -60,8 +61,7 @@ __global__ void k_repack(int type, const uint8_t *__restrict__ raw, long rawRowB
     int sb = s >> 2, c = s & 3;
     const uint8_t *blk = row + (long)sb * (five ? 176 : 144);
     const uint8_t *src = blk + (five ? 48 : 16) + 32 * c;
-    uint8_t *oq = qs + idx * 32;
-    for (int l = 0; l < 32; l++) oq[l] = src[l];
+    for (int l = 0; l < 32; l++) qs[qs_off(type, r, s, nslab, l)] = src[l];
     const uint8_t *S = blk + 4;
     int scv[8], mnv[8];
     for (int j = 0; j < 4; j++) {
@@ -69,12 +69,13 @@ __global__ void k_repack(int type, const uint8_t *__restrict__ raw, long rawRowB
       scv[j + 4] = (S[j + 8] & 0x0f) | ((S[j] >> 6) << 4);
       mnv[j + 4] = (S[j + 8] >> 4) | ((S[j + 4] >> 6) << 4);
     }
-    uint8_t *os = sc + idx * 4;
-    os[0] = (uint8_t)scv[2 * c]; os[1] = (uint8_t)scv[2 * c + 1]; os[2] = (uint8_t)mnv[2 * c]; os[3] = (uint8_t)mnv[2 * c + 1];
+    sc[sc_off(r, s, nslab, 0)] = (uint8_t)scv[2 * c];
+    sc[sc_off(r, s, nslab, 1)] = (uint8_t)scv[2 * c + 1];
+    sc[sc_off(r, s, nslab, 2)] = (uint8_t)mnv[2 * c];
+    sc[sc_off(r, s, nslab, 3)] = (uint8_t)mnv[2 * c + 1];
     if (c == 0) {
-      long di = ((long)r * (nslab >> 2) + sb) * 2;
-      dd[di] = (uint16_t)(blk[0] | (blk[1] << 8));
-      dd[di + 1] = (uint16_t)(blk[2] | (blk[3] << 8));
+      dd[dd_off(type, r, s, nslab, 0)] = (uint16_t)(blk[0] | (blk[1] << 8));
+      dd[dd_off(type, r, s, nslab, 1)] = (uint16_t)(blk[2] | (blk[3] << 8));
     }
     if (five) {
       uint32_t w0 = 0, w1 = 0;
@@ -82,29 +83,29 @@ __global__ void k_repack(int type, const uint8_t *__restrict__ raw, long rawRowB
         w0 |= (uint32_t)((blk[16 + l] >> (2 * c)) & 1) << l;
         w1 |= (uint32_t)((blk[16 + l] >> (2 * c + 1)) & 1) << l;
       }
-      uint8_t *ox = qx + idx * 8;
-      for (int i = 0; i < 4; i++) { ox[i] = (w0 >> (8 * i)) & 0xff; ox[4 + i] = (w1 >> (8 * i)) & 0xff; }
+      for (int i = 0; i < 4; i++) {
+        qx[qx_off(type, r, s, nslab, i)] = (w0 >> (8 * i)) & 0xff;
+        qx[qx_off(type, r, s, nslab, 4 + i)] = (w1 >> (8 * i)) & 0xff;
+      }
     }
     return;
   }
   if (type == T_Q6_K) {
     int sb = s >> 2, u = s & 3;
     const uint8_t *blk = row + (long)sb * 210;
-    uint8_t *oq = qs + idx * 32, *ox = qx + idx * 16;
     for (int j = 0; j < 32; j++) {
       int lo0, hi0, lo1, hi1;
       q6_value(blk, 64 * u + j, lo0, hi0);
       q6_value(blk, 64 * u + 32 + j, lo1, hi1);
-      oq[j] = (uint8_t)(lo0 | (lo1 << 4));
+      qs[qs_off(type, r, s, nslab, j)] = (uint8_t)(lo0 | (lo1 << 4));
     }
     for (int j = 0; j < 16; j++) {
       int b = 0;
       for (int i = 0; i < 4; i++) { int lo, hi; q6_value(blk, 64 * u + j + 16 * i, lo, hi); b |= hi << (2 * i); }
-      ox[j] = (uint8_t)b;
+      qx[qx_off(type, r, s, nslab, j)] = (uint8_t)b;
     }
-    uint8_t *os = sc + idx * 4;
-    for (int g = 0; g < 4; g++) os[g] = blk[192 + 4 * u + g];
-    if (u == 0) dd[(long)r * (nslab >> 2) + sb] = (uint16_t)(blk[208] | (blk[209] << 8));
+    for (int g = 0; g < 4; g++) sc[sc_off(r, s, nslab, g)] = blk[192 + 4 * u + g];
+    if (u == 0) dd[dd_off(type, r, s, nslab, 0)] = (uint16_t)(blk[208] | (blk[209] << 8));
     return;
   }
 }
@@ -114,7 +115,6 @@ __global__ void k_repack(int type, const uint8_t *__restrict__ raw, long rawRowB
 // planes, in f64 with one rounding to f32. One element per thread: coalesced stores, no private arrays.
 __device__ inline float dequant_value(const MatView &m, int r, int c) {
   const int t = m.type, s = c >> 6, v = c & 63, h = v >> 5, j = v & 31;
-  const long idx = (long)r * m.nslab + s;
   if (t == T_F32 || t == T_F16 || t == T_BF16) {
     if (c >= m.cols) return 0.f;
     const long e = (long)r * m.cols + c;
@@ -122,32 +122,32 @@ __device__ inline float dequant_value(const MatView &m, int r, int c) {
     if (t == T_F16) return h2f(((const uint16_t *)m.qs)[e]);
     return __uint_as_float((uint32_t)((const uint16_t *)m.qs)[e] << 16);
   }
+  const int ns = m.nslab;
   if (t == T_Q8_0) {
-    const double d = (double)h2f(m.dd[idx * 2 + h]);
-    return (float)(d * (double)((const int8_t *)m.qs)[idx * 64 + v]);
+    const double d = (double)h2f(m.dd[dd_off(t, r, s, ns, h)]);
+    return (float)(d * (double)(int8_t)m.qs[qs_off(t, r, s, ns, v)]);
   }
-  const uint8_t qb = m.qs[idx * 32 + j];
+  const uint8_t qb = m.qs[qs_off(t, r, s, ns, j)];
   const int nib = h == 0 ? (qb & 15) : (qb >> 4);
   if (t == T_Q4_0 || t == T_Q5_0) {
-    const double d = (double)h2f(m.dd[idx * 2 + h]);
-    const int hb = t == T_Q5_0 ? (m.qx[idx * 8 + 4 * h + (j >> 3)] >> (j & 7)) & 1 : 0;
+    const double d = (double)h2f(m.dd[dd_off(t, r, s, ns, h)]);
+    const int hb = t == T_Q5_0 ? (m.qx[qx_off(t, r, s, ns, 4 * h + (j >> 3))] >> (j & 7)) & 1 : 0;
     const int val = t == T_Q4_0 ? nib - 8 : (nib | (hb << 4)) - 16;
     return (float)(d * (double)val);
   }
   if (t == T_Q4_K || t == T_Q5_K) {
-    const long di = ((long)r * (m.nslab >> 2) + (s >> 2)) * 2;
-    const double d = (double)h2f(m.dd[di]), dmin = (double)h2f(m.dd[di + 1]);
-    const int sc = m.sc[idx * 4 + h], mn = m.sc[idx * 4 + 2 + h];
+    const double d = (double)h2f(m.dd[dd_off(t, r, s, ns, 0)]), dmin = (double)h2f(m.dd[dd_off(t, r, s, ns, 1)]);
+    const int sc = m.sc[sc_off(r, s, ns, h)], mn = m.sc[sc_off(r, s, ns, 2 + h)];
     int q = nib;
-    if (t == T_Q5_K) q |= ((m.qx[idx * 8 + 4 * h + (j >> 3)] >> (j & 7)) & 1) << 4;
+    if (t == T_Q5_K) q |= ((m.qx[qx_off(t, r, s, ns, 4 * h + (j >> 3))] >> (j & 7)) & 1) << 4;
     return (float)(d * (double)sc * (double)q - dmin * (double)mn);
   }
   // Q6_K
-  const double d = (double)h2f(m.dd[(long)r * (m.nslab >> 2) + (s >> 2)]);
-  const int lo = v < 32 ? (m.qs[idx * 32 + v] & 15) : (m.qs[idx * 32 + v - 32] >> 4);
-  const int hi = (m.qx[idx * 16 + (v & 15)] >> (2 * (v >> 4))) & 3;
+  const double d = (double)h2f(m.dd[dd_off(t, r, s, ns, 0)]);
+  const int lo = v < 32 ? (m.qs[qs_off(t, r, s, ns, v)] & 15) : (m.qs[qs_off(t, r, s, ns, v - 32)] >> 4);
+  const int hi = (m.qx[qx_off(t, r, s, ns, v & 15)] >> (2 * (v >> 4))) & 3;
   const int val = (lo | (hi << 4)) - 32;
-  return (float)(d * (double)((const int8_t *)m.sc)[idx * 4 + (v >> 4)] * (double)val);
+  return (float)(d * (double)(int8_t)m.sc[sc_off(r, s, ns, v >> 4)] * (double)val);
 }
 
 __global__ void k_dequant_rows(const MatView m, const int *rowIds, int nrows, float *out, int ldo) {
@@ -164,21 +164,6 @@ __global__ void k_embed(const MatView m, const Step *step, float *x, int ldx) {
 }
 
 // ================================================================================================ activation quantisation
-// 32 consecutive lanes own one 32-value block: d = amax/127 (f64, stored f32), q = round-half-away(x * (1/d)), sums of
-// the block and of each 16-value half (src/compute/ref-kernels.js:44-62).
-__device__ inline void quant_block32(float v, int i, int8_t *xq, float *xd, int32_t *xs, int32_t *xs16) {
-  float a = fabsf(v);
-  a = group_fmax(a, 32);
-  double scale = (double)a / 127.0;
-  double inv = scale != 0.0 ? 1.0 / scale : 0.0;
-  int q = (int)round((double)v * inv);
-  xq[i] = (int8_t)q;
-  const int s16 = wave_sum_xor(q, 16);
-  const int s32 = s16 + swizzle_xor16(s16);
-  if ((i & 15) == 0) xs16[i >> 4] = s16;
-  if ((i & 31) == 0) { xd[i >> 5] = (float)scale; xs[i >> 5] = s32; }
-}
-
 // RMSNorm (optional) + quantisation of rows x[row0 + blockIdx.y] (length n) into activation row blockIdx.y (length
 // npad >= n, zero padded). rmsnorm: s = 1/sqrt(mean(x^2) + eps), xb = x*s*w (src/compute/ref-kernels.js:305-310).
 // Block blockIdx.x quantises elements [512*blockIdx.x, +512); every block of a row computes the same sum of squares
@@ -189,26 +174,13 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x,
   __shared__ double red[4];
   const int b = blockIdx.y, tid = threadIdx.x;
   const float *xr = x + (long)(row0 + b) * ldx;
-  double s = 1.0;
-  if (w) {
-    double ss = 0;
-    for (int i = tid; i < n; i += 256) { double v = (double)xr[i]; ss += v * v; }
-    ss = wave_sum_xor(ss, 64);
-    if ((tid & 63) == 0) red[tid >> 6] = ss;
-    __syncthreads();
-    ss = (red[0] + red[1]) + (red[2] + red[3]);
-    s = 1.0 / sqrt(ss / (double)n + eps);
-  }
-  int8_t *xq = act.q + (long)b * act.ld;
-  float *xd = act.d + (long)b * (act.ld >> 5);
-  int32_t *xs = act.s + (long)b * (act.ld >> 5);
-  int32_t *xs16 = act.s16 + (long)b * (act.ld >> 4);
+  const double s = w ? rms_scale256(xr, n, eps, tid, red) : 1.0;
   const int c0 = blockIdx.x * NQ_CHUNK, c1 = min(npad, c0 + NQ_CHUNK);
   for (int i = c0 + tid; i < c1; i += 256) {
     float v = 0.f;
     if (i < n) v = w ? (float)((double)xr[i] * s * (double)w[i]) : xr[i];
     if (act.f) act.f[(long)b * act.ld + i] = v;
-    quant_block32(v, i, xq, xd, xs, xs16);
+    quant_block32(v, i, act, b);
   }
 }
 
@@ -465,9 +437,7 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
   if (chainLane) {
     const int col = h * hd + slice * AV_DIMS + lane;
     if (a.out) a.out[(long)b * a.ldo + col] = o;
-    Act act = a.act;
-    quant_block32(o, col, act.q + (long)b * act.ld, act.d + (long)b * (act.ld >> 5), act.s + (long)b * (act.ld >> 5),
-                  act.s16 + (long)b * (act.ld >> 4));
+    quant_block32(o, col, a.act, b);
   }
 }
 

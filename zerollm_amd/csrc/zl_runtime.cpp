@@ -36,6 +36,13 @@ static void ensure_init() {
 static int pad64(int n) { return (n + 63) / 64 * 64; }
 
 // ---------------------------------------------------------------------------------------------- allocations
+// Zero device memory before any stream uses it: hipMemset runs on the null stream, which does not order with the
+// library's non-blocking streams, so it is waited for here.
+static void zero_now(void *p, size_t n) {
+  ZL_HIP(hipMemset(p, 0, n));
+  ZL_HIP(hipDeviceSynchronize());
+}
+
 struct Arena {
   std::vector<void *> ptrs;
   int64_t bytes = 0;
@@ -54,7 +61,7 @@ struct Arena {
   }
 };
 
-// Planes of a rows x cols matrix of `type` (not yet filled).
+// Planes of a rows x cols matrix of `type` (not yet filled): rows are padded to whole 64-row tiles, which stay zero.
 static DevMat alloc_planes(Arena &ar, int type, int rows, int cols) {
   DevMat m;
   m.type = type; m.rows = rows; m.cols = cols;
@@ -67,17 +74,17 @@ static DevMat alloc_planes(Arena &ar, int type, int rows, int cols) {
     m.qs = (uint8_t *)ar.alloc((size_t)rb * rows);
     return m;
   }
-  const long ns = (long)rows * m.nslab;
-  ZL_REQUIRE(ns < (1L << 31) / 64, ZL_ERR_UNSUPPORTED, "matrix too large");
-  m.qs = (uint8_t *)ar.alloc(ns * qs_bytes(type));
-  if (qx_bytes(type)) m.qx = (uint8_t *)ar.alloc(ns * qx_bytes(type));
-  if (sc_bytes(type)) m.sc = (uint8_t *)ar.alloc(ns * sc_bytes(type));
-  long nd = (type == T_Q4_K || type == T_Q5_K) ? (long)rows * (m.nslab / 4) * 2 : type == T_Q6_K ? (long)rows * (m.nslab / 4) : ns * 2;
-  m.dd = (uint16_t *)ar.alloc(nd * 2);
+  const long T = tiles_of(rows), ns = T * 64 * m.nslab;
+  ZL_REQUIRE(ns * qs_bytes(type) < (1L << 32), ZL_ERR_UNSUPPORTED, "matrix too large");
+  auto zalloc = [&](size_t n) { void *p = ar.alloc(n); zero_now(p, n); return p; };
+  m.qs = (uint8_t *)zalloc(ns * qs_bytes(type));
+  if (qx_bytes(type)) m.qx = (uint8_t *)zalloc(ns * qx_bytes(type));
+  if (sc_bytes(type)) m.sc = (uint8_t *)zalloc(ns * sc_bytes(type));
+  m.dd = (uint16_t *)zalloc(T * dd_per_tile(type, m.nslab) * 2);
   return m;
 }
 
-// Rows [row0, row0 + n) of m as a matrix of its own: every plane is row-major, so the view is an offset into each.
+// Rows [row0, row0 + n) of m as a matrix of its own (row0 a multiple of 64): an offset into each plane.
 static DevMat row_view(const DevMat &m, int row0, int n) {
   DevMat v = m;
   v.rows = n;
@@ -85,11 +92,12 @@ static DevMat row_view(const DevMat &m, int row0, int n) {
     v.qs = m.qs + (size_t)ggml_row_bytes(m.type, m.cols) * row0;
     return v;
   }
+  ZL_REQUIRE(row0 % 64 == 0, ZL_ERR_ARG, "row view must start at a 64-row tile");
   const long ns = (long)row0 * m.nslab;
   v.qs = m.qs + ns * qs_bytes(m.type);
   if (m.qx) v.qx = m.qx + ns * qx_bytes(m.type);
   if (m.sc) v.sc = m.sc + ns * sc_bytes(m.type);
-  v.dd = m.dd + ((m.type == T_Q4_K || m.type == T_Q5_K) ? (long)row0 * (m.nslab / 4) * 2 : m.type == T_Q6_K ? (long)row0 * (m.nslab / 4) : ns * 2);
+  v.dd = m.dd + (long)(row0 / 64) * dd_per_tile(m.type, m.nslab);
   return v;
 }
 
@@ -111,16 +119,16 @@ static DevMat make_mat(Arena &ar, int type, int rows, int cols, const uint8_t *d
   return m;
 }
 
-// Matrices that one GEMV launch reads together (q, k, v): consecutive ones of the same type share one allocation, so
-// the launch addresses their rows from one base. stage(i) puts tensor i's raw rows at `draw` and returns its type.
+// Matrices that one GEMV launch reads together (q, k, v): consecutive ones of the same type share one allocation
+// (each padded to whole tiles). stage(i) puts tensor i's raw rows at `draw` and returns its type.
 static std::vector<DevMat> make_group(Arena &ar, const std::vector<int> &types, const std::vector<int> &rows, int cols,
                                       const std::function<void(size_t)> &stage, const uint8_t *draw, hipStream_t st) {
   std::vector<DevMat> out(rows.size());
   size_t i = 0;
   while (i < rows.size()) {
     size_t j = i + 1;
-    int total = rows[i];
-    while (j < rows.size() && types[j] == types[i]) total += rows[j++];
+    int total = tiles_of(rows[i]) * 64;
+    while (j < rows.size() && types[j] == types[i] && is_quant(types[i])) total += tiles_of(rows[j++]) * 64;
     DevMat all = alloc_planes(ar, types[i], total, cols);
     int r0 = 0;
     for (size_t k = i; k < j; k++) {
@@ -128,7 +136,7 @@ static std::vector<DevMat> make_group(Arena &ar, const std::vector<int> &types, 
       out[k] = row_view(all, r0, rows[k]);
       fill_planes(out[k], draw, st);
       ZL_HIP(hipStreamSynchronize(st));
-      r0 += rows[k];
+      r0 += tiles_of(rows[k]) * 64;
     }
     i = j;
   }
@@ -157,7 +165,9 @@ struct zl_model {
   void *kcache = nullptr, *vcache = nullptr;
   float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *hb = nullptr, *logits = nullptr;
   float *scores = nullptr;  // attention scores [maxBatch][n_head][ctx]
-  zl::Act act{};
+  zl::Act act{};    // quantised input of the q/k/v, attention-output and gate/up GEMVs
+  zl::Act act2{};   // quantised FFN hidden state (written by the gate/up GEMV, read by the down GEMV)
+  zl::GemvWork gw{};
   zl::Step *dstep = nullptr;
   hipStream_t st = nullptr;
   hipStream_t cst = nullptr;  // graphs are captured on their own stream
@@ -244,6 +254,30 @@ static int kvdim(const zl_model *m) { return m->cfg.n_head_kv * m->cfg.head_dim;
 
 static int64_t mat_bytes(const DevMat &mm) { int64_t rb = ggml_row_bytes(mm.type, mm.cols); return rb < 0 ? 0 : rb * mm.rows; }
 
+// Quantised activation rows (B rows of ld values, ld a multiple of 64), zeroed; with the f32 copy when f32 is set.
+static Act alloc_act(Arena &ar, int B, int ld, bool f32) {
+  Act a{};
+  a.ld = ld;
+  const size_t nb = (size_t)B * (ld / 32);
+  auto zalloc = [&](size_t n) { void *p = ar.alloc(n); zero_now(p, n); return p; };
+  a.q = (int8_t *)zalloc((size_t)B * ld);
+  a.d = (float *)zalloc(nb * 4);
+  a.s = (int32_t *)zalloc(nb * 4);
+  a.ra = (RecA *)zalloc(nb * sizeof(RecA));
+  a.rb = (RecB *)zalloc(nb * sizeof(RecB));
+  a.rc = (RecC *)zalloc(nb * sizeof(RecC));
+  a.f = f32 ? (float *)zalloc((size_t)B * ld * 4) : nullptr;
+  return a;
+}
+
+static GemvWork alloc_gemv_work(Arena &ar) {
+  GemvWork w;
+  w.part = (double *)ar.alloc(GEMV_PART_DOUBLES * 8);
+  w.cnt = (uint32_t *)ar.alloc(GEMV_CNT_TILES * 4);
+  zero_now(w.cnt, GEMV_CNT_TILES * 4);
+  return w;
+}
+
 // Allocate KV cache, activations, RoPE tables; compute pass bytes.
 static void finish_model(zl_model *m, const float *ropeFreqs) {
   const zl_config &c = m->cfg;
@@ -273,8 +307,8 @@ static void finish_model(zl_model *m, const float *ropeFreqs) {
   const size_t vElems = (size_t)c.n_layer * c.n_head_kv * c.head_dim * m->vstride;
   m->kcache = m->ar.alloc(kElems * (m->kvF16 ? 2 : 4));
   m->vcache = m->ar.alloc(vElems * (m->kvF16 ? 2 : 4));
-  ZL_HIP(hipMemset(m->kcache, 0, kElems * (m->kvF16 ? 2 : 4)));
-  ZL_HIP(hipMemset(m->vcache, 0, vElems * (m->kvF16 ? 2 : 4)));
+  zero_now(m->kcache, kElems * (m->kvF16 ? 2 : 4));
+  zero_now(m->vcache, vElems * (m->kvF16 ? 2 : 4));
   const int B = m->maxBatch;
   m->x = (float *)m->ar.alloc((size_t)B * c.n_embd * 4);
   m->q = (float *)m->ar.alloc((size_t)B * qdim(m) * 4);
@@ -284,15 +318,11 @@ static void finish_model(zl_model *m, const float *ropeFreqs) {
   m->logits = (float *)m->ar.alloc((size_t)m->logitsBatch * c.vocab * 4);
   m->scores = (float *)m->ar.alloc((size_t)B * c.n_head * m->ctx * 4);
   const int ld = pad64(std::max(c.n_embd, std::max(qdim(m), c.n_ff)));
-  m->act.ld = ld;
-  m->act.q = (int8_t *)m->ar.alloc((size_t)B * ld);
-  m->act.d = (float *)m->ar.alloc((size_t)B * (ld / 32) * 4);
-  m->act.s = (int32_t *)m->ar.alloc((size_t)B * (ld / 32) * 4);
-  m->act.s16 = (int32_t *)m->ar.alloc((size_t)B * (ld / 16) * 4);
-  m->act.f = (float *)m->ar.alloc((size_t)B * ld * 4);
-  ZL_HIP(hipMemset(m->act.q, 0, (size_t)B * ld));
+  m->act = alloc_act(m->ar, B, ld, true);
+  m->act2 = alloc_act(m->ar, B, pad64(c.n_ff), false);
+  m->gw = alloc_gemv_work(m->ar);
   m->dstep = (Step *)m->ar.alloc(sizeof(Step));
-  ZL_HIP(hipMemset(m->dstep, 0, sizeof(Step)));
+  zero_now(m->dstep, sizeof(Step));
   int64_t wb = 0;
   for (auto &L : m->layers) wb += mat_bytes(L.wq) + mat_bytes(L.wk) + mat_bytes(L.wv) + mat_bytes(L.wo) + mat_bytes(L.wgate) + mat_bytes(L.wup) + mat_bytes(L.wdown);
   wb += mat_bytes(m->output);
@@ -303,56 +333,98 @@ static void finish_model(zl_model *m, const float *ropeFreqs) {
 // ---------------------------------------------------------------------------------------------- forward pass
 struct SegSpec { const DevMat *m; float *out; int ldo; const float *bias; };
 
-// Where a GEMV's quantised activation comes from: rows x[row0 .. row0+B) (length n, stride ldx), RMSNorm'd with nw
-// first when nw is set.
-struct Prologue { const float *x; int ldx, row0; const float *nw; int n; };
-
-// Rows of at most this many values in total are quantised inside each GEMV block (the block's redundant work is then
-// cheaper than a separate launch); longer ones by one k_norm_quant launch into m->act.
-constexpr long FUSE_MAX_VALUES = 4096;
-
-static bool fuse_prologue(const std::vector<std::vector<SegSpec>> &groups, int B, int n) {
-  if ((long)B * pad64(n) > FUSE_MAX_VALUES) return false;
-  for (auto &g : groups)
-    for (auto &sg : g)
-      if (!is_quant(sg.m->type)) return false;  // float weights read the f32 activation that k_norm_quant writes
-  return true;
-}
-
-static void gemv_group(zl_model *m, const std::vector<SegSpec> &segs, int B, int epi, const Prologue *pro) {
+// Arguments of one GEMV launch over `segs` (laid end to end in tile order; SWIGLU: gate, up on the same tiles).
+static GemvArgs gemv_args(const std::vector<SegSpec> &segs, int B, int epi, const Act &act, const GemvWork &gw) {
   GemvArgs a;
   memset(&a, 0, sizeof(a));
+  ZL_REQUIRE(segs.size() >= 1 && segs.size() <= 3, ZL_ERR_ARG, "gemv: 1 to 3 matrices per launch");
   a.nseg = (int)segs.size();
-  a.rows_total = 0;
+  int t0 = 0;
   for (int i = 0; i < a.nseg; i++) {
-    a.seg[i].m = view(*segs[i].m);
-    a.seg[i].rows = segs[i].m->rows;
-    a.seg[i].out = segs[i].out;
-    a.seg[i].ldo = segs[i].ldo;
-    a.seg[i].bias = segs[i].bias;
-    if (epi != EPI_SWIGLU || i == 0) a.rows_total += segs[i].m->rows;
+    const DevMat &mm = *segs[i].m;
+    GemvSeg &g = a.seg[i];
+    g.m = view(mm);
+    g.rows = mm.rows;
+    g.out = segs[i].out;
+    g.ldo = segs[i].ldo;
+    g.bias = segs[i].bias;
+    if (is_quant(mm.type)) {
+      const long ts = (long)tiles_of(mm.rows) * mm.nslab;
+      g.nqs = (uint32_t)(ts * 64 * qs_bytes(mm.type));
+      g.nqx = (uint32_t)(ts * 64 * qx_bytes(mm.type));
+      g.nsc = (uint32_t)(ts * 64 * sc_bytes(mm.type));
+      g.ndd = (uint32_t)(tiles_of(mm.rows) * dd_per_tile(mm.type, mm.nslab) * 2);
+    }
+    g.tile0 = epi == EPI_SWIGLU ? 0 : t0;
+    if (epi != EPI_SWIGLU || i == 0) t0 += tiles_of(mm.rows);
   }
+  ZL_REQUIRE(epi != EPI_SWIGLU || (a.nseg == 2 && segs[1].m->rows == segs[0].m->rows), ZL_ERR_ARG, "gemv: gate and up differ");
+  a.ntiles = t0;
   a.nslab = segs[0].m->nslab;
-  a.act = m->act;
+  gemv_shape(a.ntiles, a.nslab, epi == EPI_SWIGLU, &a.ks, &a.nwave);
+  a.kr = (a.nslab + a.ks - 1) / a.ks;
   a.M = B;
-  a.lpr = gemv_lpr(epi == EPI_SWIGLU ? 2 * a.rows_total : a.rows_total, a.nslab);
+  a.act = act;
+  a.part = gw.part;
+  a.cnt = gw.cnt;
+  return a;
+}
+
+// One GEMV launch of the model's pass reading quantised activation `act` (float weights: the f32 rows xf, stride ldx).
+// RESID adds into x; SWIGLU writes hb and, with qout set, its quantisation.
+static void gemv_group(zl_model *m, const std::vector<SegSpec> &segs, int B, int epi, const Act &act, const float *xf,
+                       int ldx, const Act *qout = nullptr) {
+  GemvArgs a = gemv_args(segs, B, epi, act, m->gw);
   a.resid = m->x;
   a.ldr = m->cfg.n_embd;
   a.hb = m->hb;
   a.ldh = m->cfg.n_ff;
-  if (pro) {
-    a.xf = pro->x; a.ldxf = pro->ldx; a.xrow0 = pro->row0; a.n = pro->n; a.nw = pro->nw; a.eps = (double)m->cfg.rms_eps;
-  }
-  launch_gemv(a, epi, m->act.f, m->act.ld, m->st);
+  if (qout) a.qout = *qout;
+  launch_gemv(a, epi, xf, ldx, m->st);
 }
 
-// GEMV launches that all read the quantised activation of the same rows: the rows are quantised (after RMSNorm when
-// p.nw is set) either inside every launch or once by k_norm_quant, as fuse_prologue decides.
-static void gemv_launches(zl_model *m, const std::vector<std::vector<SegSpec>> &groups, const std::vector<int> &epis, int B,
-                          const Prologue &p) {
-  const bool fused = fuse_prologue(groups, B, p.n);
-  if (!fused) launch_norm_quant(p.x, p.ldx, p.row0, B, p.nw, (double)m->cfg.rms_eps, p.n, pad64(p.n), m->act, m->st);
-  for (size_t i = 0; i < groups.size(); i++) gemv_group(m, groups[i], B, epis[i], fused ? &p : nullptr);
+// RMSNorm (weights nw; none when null) + quantisation of rows x[row0 .. row0+B) (length n, stride ldx) into act.
+static void norm_quant(zl_model *m, const float *x, int ldx, int row0, int B, const float *nw, int n, const Act &act) {
+  launch_norm_quant(x, ldx, row0, B, nw, (double)m->cfg.rms_eps, n, pad64(n), act, m->st);
+}
+
+// A GEMV input that is f32 rows, RMSNorm'd with nw first when nw is set: x[row0 .. row0+B) (length n, stride ldx).
+struct Prologue { const float *x; int ldx, row0; const float *nw; int n; };
+
+// Rows of at most this many values in total are quantised inside each GEMV workgroup (the repeated work then costs
+// less than a launch); longer ones by one k_norm_quant launch.
+constexpr long FUSE_MAX_VALUES = 4096;
+
+// Launches of the same input rows. A launch of quantised matrices with fewer than 256 tiles (few, large workgroups)
+// quantises short rows itself; otherwise one k_norm_quant launch writes m->act first, and the f32 normed rows for
+// float weights.
+static void gemv_rows(zl_model *m, const std::vector<std::vector<SegSpec>> &groups, const std::vector<int> &epis, int B,
+                      const Prologue &p, const Act *qout = nullptr) {
+  std::vector<bool> fused(groups.size());
+  bool need = false;
+  for (size_t i = 0; i < groups.size(); i++) {
+    bool q = true;
+    int tiles = 0;
+    for (size_t k = 0; k < groups[i].size(); k++) {
+      q = q && is_quant(groups[i][k].m->type);
+      if (epis[i] != EPI_SWIGLU || k == 0) tiles += tiles_of(groups[i][k].m->rows);
+    }
+    fused[i] = q && tiles < 256 && (long)B * pad64(p.n) <= FUSE_MAX_VALUES;
+    need = need || !fused[i];
+  }
+  if (need) norm_quant(m, p.x, p.ldx, p.row0, B, p.nw, p.n, m->act);
+  for (size_t i = 0; i < groups.size(); i++) {
+    GemvArgs a = gemv_args(groups[i], B, epis[i], m->act, m->gw);
+    a.resid = m->x;
+    a.ldr = m->cfg.n_embd;
+    a.hb = m->hb;
+    a.ldh = m->cfg.n_ff;
+    if (qout && epis[i] == EPI_SWIGLU) a.qout = *qout;
+    if (fused[i]) {
+      a.xf = p.x; a.ldxf = p.ldx; a.xrow0 = p.row0; a.n = p.n; a.nw = p.nw; a.eps = (double)m->cfg.rms_eps;
+    }
+    launch_gemv(a, epis[i], m->act.f, m->act.ld, m->st);
+  }
 }
 
 // Enqueue one forward pass of B tokens (tokens and positions from m->dstep). want: 0 none, 1 last, 2 all.
@@ -369,11 +441,11 @@ static void enqueue_forward(zl_model *m, int B, int want) {
     int i0 = 0;
     while (i0 < 3) {
       int i1 = i0 + 1;
-      while (i1 < 3 && qkv[i1].m->type == qkv[i0].m->type) i1++;
+      while (i1 < 3 && qkv[i1].m->type == qkv[i0].m->type && is_quant(qkv[i0].m->type)) i1++;
       groups.emplace_back(qkv + i0, qkv + i1);
       i0 = i1;
     }
-    gemv_launches(m, groups, std::vector<int>(groups.size(), EPI_STORE), B, Prologue{m->x, d, 0, L.attnNorm, d});
+    gemv_rows(m, groups, std::vector<int>(groups.size(), EPI_STORE), B, Prologue{m->x, d, 0, L.attnNorm, d});
     AttnArgs aa;
     aa.q = m->q; aa.ldq = qd; aa.kcache = m->kcache; aa.vcache = m->vcache;
     aa.k = m->k; aa.v = m->v; aa.ldkv = kvd; aa.qNorm = L.qNorm; aa.kNorm = L.kNorm; aa.eps = eps;
@@ -383,17 +455,17 @@ static void enqueue_forward(zl_model *m, int B, int want) {
     aa.scale = 1.0 / sqrt((double)c.head_dim);
     aa.step = m->dstep; aa.out = m->act.f; aa.ldo = m->act.ld; aa.act = m->act;
     launch_attention(aa, B, m->st);
-    gemv_group(m, {{&L.wo, nullptr, 0, nullptr}}, B, EPI_RESID, nullptr);
+    gemv_group(m, {{&L.wo, nullptr, 0, nullptr}}, B, EPI_RESID, m->act, m->act.f, m->act.ld);
     ZL_REQUIRE(L.wgate.type == L.wup.type, ZL_ERR_UNSUPPORTED, "ffn_gate and ffn_up must share a type");
-    gemv_launches(m, {{{&L.wgate, nullptr, 0, nullptr}, {&L.wup, nullptr, 0, nullptr}}}, {EPI_SWIGLU}, B,
-                  Prologue{m->x, d, 0, L.ffnNorm, d});
-    gemv_launches(m, {{{&L.wdown, nullptr, 0, nullptr}}}, {EPI_RESID}, B, Prologue{m->hb, ff, 0, nullptr, ff});
+    // the gate/up launch quantises hb for a quantised down matrix itself; otherwise it is quantised here
+    const bool qdown = is_quant(L.wdown.type), fusedq = qdown && is_quant(L.wgate.type);
+    gemv_rows(m, {{{&L.wgate, nullptr, 0, nullptr}, {&L.wup, nullptr, 0, nullptr}}}, {EPI_SWIGLU}, B,
+              Prologue{m->x, d, 0, L.ffnNorm, d}, fusedq ? &m->act2 : nullptr);
+    if (qdown && !fusedq) norm_quant(m, m->hb, ff, 0, B, nullptr, ff, m->act2);
+    gemv_group(m, {{&L.wdown, nullptr, 0, nullptr}}, B, EPI_RESID, m->act2, m->hb, ff);
   }
-  if (want == 2) {
-    gemv_launches(m, {{{&m->output, m->logits, c.vocab, nullptr}}}, {EPI_STORE}, B, Prologue{m->x, d, 0, m->outputNorm, d});
-  } else if (want == 1) {
-    gemv_launches(m, {{{&m->output, m->logits, c.vocab, nullptr}}}, {EPI_STORE}, 1, Prologue{m->x, d, B - 1, m->outputNorm, d});
-  }
+  if (want == 2) gemv_rows(m, {{{&m->output, m->logits, c.vocab, nullptr}}}, {EPI_STORE}, B, Prologue{m->x, d, 0, m->outputNorm, d});
+  else if (want == 1) gemv_rows(m, {{{&m->output, m->logits, c.vocab, nullptr}}}, {EPI_STORE}, 1, Prologue{m->x, d, B - 1, m->outputNorm, d});
 }
 
 static hipGraphExec_t graph_for(zl_model *m, int B, int want) {
@@ -437,6 +509,37 @@ static void launch_pass(zl_model *m, int B, int want) {
   else enqueue_forward(m, B, want);
 }
 
+// Milliseconds per call of `enqueue` (which enqueues work on st), over `iters` calls captured into one HIP graph and
+// replayed once after a warm-up replay: launch gaps are then those of the forward pass's graphs.
+static float time_graph(hipStream_t st, int iters, const std::function<void(int)> &enqueue) {
+  hipGraph_t g = nullptr;
+  hipGraphExec_t ex = nullptr;
+  ZL_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  try {
+    for (int i = 0; i < iters; i++) enqueue(i);
+  } catch (...) {
+    hipStreamEndCapture(st, &g);
+    if (g) hipGraphDestroy(g);
+    throw;
+  }
+  ZL_HIP(hipStreamEndCapture(st, &g));
+  struct G { hipGraph_t g; hipGraphExec_t e; ~G() { if (e) hipGraphExecDestroy(e); if (g) hipGraphDestroy(g); } } gg{g, nullptr};
+  ZL_HIP(hipGraphInstantiate(&ex, g, nullptr, nullptr, 0));
+  gg.e = ex;
+  ZL_HIP(hipGraphLaunch(ex, st));  // warm-up
+  hipEvent_t a, e;
+  ZL_HIP(hipEventCreate(&a));
+  ZL_HIP(hipEventCreate(&e));
+  struct E { hipEvent_t a, b; ~E() { hipEventDestroy(a); hipEventDestroy(b); } } ev{a, e};
+  ZL_HIP(hipEventRecord(a, st));
+  ZL_HIP(hipGraphLaunch(ex, st));
+  ZL_HIP(hipEventRecord(e, st));
+  ZL_HIP(hipEventSynchronize(e));
+  float t = 0;
+  ZL_HIP(hipEventElapsedTime(&t, a, e));
+  return t / iters;
+}
+
 // Time `iters` back-to-back launches of one GEMV of the pass (which: 0 first q/k/v group, 1 wo, 2 gate+up, 3 down,
 // 4 output head) with M tokens, cycling through the layers' weights (cache-cold), between two events on the model's
 // stream. Uses the model's activation buffers as the last pass left them.
@@ -469,18 +572,21 @@ static void probe_gemv(zl_model *m, int which, int M, int iters, float *ms, int6
   ZL_HIP(hipMalloc(&xsave, xb));
   struct F { float *p; ~F() { hipFree(p); } } fr{xsave};
   ZL_HIP(hipMemcpyAsync(xsave, m->x, xb, hipMemcpyDeviceToDevice, m->st));
-  for (int l = 0; l < std::min(c.n_layer, iters); l++) gemv_group(m, segs_of(which == 4 ? 0 : l), M, epi, nullptr);  // warm-up
-  hipEvent_t a, e;
-  ZL_HIP(hipEventCreate(&a));
-  ZL_HIP(hipEventCreate(&e));
-  struct E { hipEvent_t a, b; ~E() { hipEventDestroy(a); hipEventDestroy(b); } } ev{a, e};
-  ZL_HIP(hipEventRecord(a, m->st));
-  for (int i = 0; i < iters; i++) gemv_group(m, segs_of(which == 4 ? 0 : i % c.n_layer), M, epi, nullptr);
-  ZL_HIP(hipEventRecord(e, m->st));
-  ZL_HIP(hipEventSynchronize(e));
-  float t = 0;
-  ZL_HIP(hipEventElapsedTime(&t, a, e));
-  *ms = t / iters;
+  // the launch(es) exactly as the pass issues them: q/k/v, gate/up and the output head read the residual rows (fused
+  // prologue, or a k_norm_quant launch first); wo reads the attention output, down the gate/up launch's quantised hb
+  auto launch = [&](int l) {
+    const Layer &L = m->layers[l];
+    const int d = c.n_embd;
+    if (which == 0) gemv_rows(m, {segs_of(l)}, {EPI_STORE}, M, Prologue{m->x, d, 0, L.attnNorm, d});
+    else if (which == 1) gemv_group(m, segs_of(l), M, epi, m->act, m->act.f, m->act.ld);
+    else if (which == 2)
+      gemv_rows(m, {segs_of(l)}, {EPI_SWIGLU}, M, Prologue{m->x, d, 0, L.ffnNorm, d},
+                is_quant(L.wdown.type) && is_quant(L.wgate.type) ? &m->act2 : nullptr);
+    else if (which == 3) gemv_group(m, segs_of(l), M, epi, m->act2, m->hb, c.n_ff);
+    else gemv_rows(m, {segs_of(l)}, {EPI_STORE}, M, Prologue{m->x, d, 0, m->outputNorm, d});
+  };
+  for (int l = 0; l < std::min(c.n_layer, iters); l++) launch(which == 4 ? 0 : l);  // warm-up (outside capture)
+  *ms = time_graph(m->st, iters, [&](int i) { launch(which == 4 ? 0 : i % c.n_layer); });
   ZL_HIP(hipMemcpyAsync(m->x, xsave, xb, hipMemcpyDeviceToDevice, m->st));
   ZL_HIP(hipStreamSynchronize(m->st));
 }
@@ -750,7 +856,7 @@ static zl_sampler *new_sampler(const zl_sampler_opts *o) {
   ZL_REQUIRE(p.repeatLastN >= 0 && p.repeatLastN <= 64, ZL_ERR_UNSUPPORTED, "repeat_last_n must be 0..64 on the GPU sampler");
   ZL_HIP(hipStreamCreateWithFlags(&s->st, hipStreamNonBlocking));
   s->ss = (SpecState *)s->ar.alloc(sizeof(SpecState));
-  ZL_HIP(hipMemset(s->ss, 0, sizeof(SpecState)));
+  zero_now(s->ss, sizeof(SpecState));
   ZL_HIP(hipHostMalloc((void **)&s->hss, sizeof(SpecState)));
   s->pdist = (DevDist *)s->ar.alloc(sizeof(DevDist) * 65);
   s->qdist = (DevDist *)s->ar.alloc(sizeof(DevDist) * 64);
@@ -762,7 +868,7 @@ static zl_sampler *new_sampler(const zl_sampler_opts *o) {
   ZL_HIP(hipHostMalloc((void **)&s->htok, sizeof(int) * 4));
   s->am.keys = (unsigned long long *)s->ar.alloc(sizeof(unsigned long long) * ARGMAX_MAX_ROWS * ARGMAX_MAX_BLOCKS);
   s->am.count = (uint32_t *)s->ar.alloc(sizeof(uint32_t) * ARGMAX_MAX_ROWS);
-  ZL_HIP(hipMemset(s->am.count, 0, sizeof(uint32_t) * ARGMAX_MAX_ROWS));
+  zero_now(s->am.count, sizeof(uint32_t) * ARGMAX_MAX_ROWS);
   hipLaunchKernelGGL(k_set_rng, dim3(1), dim3(64), 0, s->st, s->ss, o->seed);
   ZL_HIP(hipGetLastError());
   ZL_HIP(hipStreamSynchronize(s->st));
@@ -1202,29 +1308,22 @@ int zl_mat_dequant(zl_mat *m, int64_t row0, int64_t nrows, float *out) {
 struct ProbeAct {
   Arena ar;
   Act act{};
+  GemvWork gw{};
   float *x = nullptr;
 };
 static void probe_act(ProbeAct &pa, const float *x, int64_t K, int M, hipStream_t st) {
   const int ld = pad64((int)K);
-  pa.act.ld = ld;
-  pa.act.q = (int8_t *)pa.ar.alloc((size_t)M * ld);
-  pa.act.d = (float *)pa.ar.alloc((size_t)M * (ld / 32) * 4);
-  pa.act.s = (int32_t *)pa.ar.alloc((size_t)M * (ld / 32) * 4);
-  pa.act.s16 = (int32_t *)pa.ar.alloc((size_t)M * (ld / 16) * 4);
-  pa.act.f = (float *)pa.ar.alloc((size_t)M * ld * 4);
+  pa.act = alloc_act(pa.ar, M, ld, true);
+  pa.gw = alloc_gemv_work(pa.ar);
   pa.x = (float *)pa.ar.alloc((size_t)M * K * 4);
   if (x) ZL_HIP(hipMemcpy(pa.x, x, (size_t)M * K * 4, hipMemcpyHostToDevice));
   else launch_fill(pa.x, (long)M * K, 0.5f, st);
   launch_norm_quant(pa.x, (int)K, 0, M, nullptr, 0.0, (int)K, ld, pa.act, st);
 }
 
-static void probe_gemv(const DevMat &mm, const Act &act, int M, float *y, hipStream_t st) {
-  GemvArgs a;
-  memset(&a, 0, sizeof(a));
-  a.nseg = 1;
-  a.seg[0].m = view(mm); a.seg[0].rows = mm.rows; a.seg[0].out = y; a.seg[0].ldo = mm.rows;
-  a.rows_total = mm.rows; a.nslab = mm.nslab; a.act = act; a.M = M; a.lpr = gemv_lpr(mm.rows, mm.nslab);
-  launch_gemv(a, EPI_STORE, act.f, act.ld, st);
+static void probe_gemv(const DevMat &mm, const ProbeAct &pa, int M, float *y, hipStream_t st) {
+  GemvArgs a = gemv_args({{&mm, y, mm.rows, nullptr}}, M, EPI_STORE, pa.act, pa.gw);
+  launch_gemv(a, EPI_STORE, pa.act.f, pa.act.ld, st);
 }
 
 int zl_mat_gemv(zl_mat *m, const float *x, int M, float *y) {
@@ -1235,7 +1334,7 @@ int zl_mat_gemv(zl_mat *m, const float *x, int M, float *y) {
   struct R { ProbeAct *p; ~R() { p->ar.release(); } } rel{&pa};
   probe_act(pa, x, mm.cols, M, m->st);
   float *dy = (float *)pa.ar.alloc((size_t)M * mm.rows * 4);
-  probe_gemv(mm, pa.act, M, dy, m->st);
+  probe_gemv(mm, pa, M, dy, m->st);
   ZL_HIP(hipStreamSynchronize(m->st));
   ZL_HIP(hipMemcpy(y, dy, (size_t)M * mm.rows * 4, hipMemcpyDeviceToHost));
   ZL_API_END
@@ -1250,18 +1349,9 @@ int zl_mat_gemv_time(zl_mat *m, int M, int iters, float *ms_per_call) {
   probe_act(pa, nullptr, m0.cols, M, m->st);
   float *dy = (float *)pa.ar.alloc((size_t)M * m0.rows * 4);
   const int nc = (int)m->copies.size();
-  for (int i = 0; i < nc; i++) probe_gemv(m->copies[i], pa.act, M, dy, m->st);  // warm-up
-  hipEvent_t a, b;
-  ZL_HIP(hipEventCreate(&a));
-  ZL_HIP(hipEventCreate(&b));
-  struct E { hipEvent_t a, b; ~E() { hipEventDestroy(a); hipEventDestroy(b); } } ev{a, b};
-  ZL_HIP(hipEventRecord(a, m->st));
-  for (int i = 0; i < iters; i++) probe_gemv(m->copies[i % nc], pa.act, M, dy, m->st);
-  ZL_HIP(hipEventRecord(b, m->st));
-  ZL_HIP(hipEventSynchronize(b));
-  float ms = 0;
-  ZL_HIP(hipEventElapsedTime(&ms, a, b));
-  *ms_per_call = ms / iters;
+  for (int i = 0; i < nc; i++) probe_gemv(m->copies[i], pa, M, dy, m->st);  // warm-up (outside capture)
+  const float ms = time_graph(m->st, iters, [&](int i) { probe_gemv(m->copies[i % nc], pa, M, dy, m->st); });
+  *ms_per_call = ms;
   ZL_API_END
 }
 

@@ -50,7 +50,7 @@ def run(shapes, ms_list, min_mb=512, target_ms=40.0, seed=7):
             for m in ms_list:
                 ms = C.c_float()
                 _lib.call("zl_mat_gemv_time", h, m, max(8, copies), C.byref(ms))  # warm-up and estimate
-                iters = max(copies, int(target_ms / max(ms.value, 1e-4)))
+                iters = min(2000, max(copies, int(target_ms / max(ms.value, 1e-4))))
                 _lib.call("zl_mat_gemv_time", h, m, iters, C.byref(ms))
                 gbs = wb / (ms.value * 1e-3) / 1e9
                 r = {"shape": name, "type": {Q4_K: "Q4_K", Q6_K: "Q6_K", Q8_0: "Q8_0"}[t], "N": n, "K": k, "M": m,
