@@ -184,263 +184,6 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x,
   }
 }
 
-// ================================================================================================ attention
-// Causal GQA attention with the reference's arithmetic (src/model/forward.js:213-230), in two launches:
-//   k_attn_scores  s_t = f32(sum_i q_i K_t,i (f64, exact products) * 1/sqrt(hd)) for every position t <= pos, one
-//                  block per (64-position chunk, KV head, token): all of K streams in parallel.
-//   k_attn_av      softmax over the scores (e = exp(s - max) in f64, stored f32; p = f32(e * (1/sum e))), then
-//                  out_i = sum_t p_t V_t,i accumulated in f32 in position order, one block per (64-dim slice, query
-//                  head, token); the head output is also quantised for the output projection.
-// Scores live in a [token][head][ctx] f32 buffer between the two.
-
-// Query heads handled by one score block: the largest divisor of the GQA group that is at most 8.
-inline int attn_heads_per_block(int group) {
-  for (int c = 8; c > 1; c--)
-    if (group % c == 0) return c;
-  return 1;
-}
-
-// Per-head RMSNorm (weights nw, when set) and RoPE at position pos of one head vector v[0..HD) in LDS, by one wave,
-// with the arithmetic of src/model/forward.js:203-211 and src/compute/ref-kernels.js:305-310, 344-363 (64-lane strided
-// f64 sum of squares and butterfly; f64 rotation of each (i, i + half) or (2i, 2i + 1) pair, stored f32).
-template <int HD>
-__device__ inline void norm_rope(float *v, const float *nw, double eps, int nRot, int neox, const float *cosT,
-                                 const float *sinT, int pos, int lane) {
-  if (nw) {
-    double ss = 0;
-    for (int i = lane; i < HD; i += 64) { const double x = (double)v[i]; ss += x * x; }
-    ss = wave_sum_xor(ss, 64);
-    const double sc = 1.0 / sqrt(ss / (double)HD + eps);
-    for (int i = lane; i < HD; i += 64) v[i] = (float)((double)v[i] * sc * (double)nw[i]);
-  }
-  const int half = nRot / 2;
-  for (int i = lane; i < half; i += 64) {
-    const int i0 = neox ? i : 2 * i, i1 = neox ? i + half : 2 * i + 1;
-    const double c = (double)cosT[(long)pos * half + i], sn = (double)sinT[(long)pos * half + i];
-    const double x0 = (double)v[i0], x1 = (double)v[i1];
-    v[i0] = (float)(x0 * c - x1 * sn);  // pairs are disjoint across lanes
-    v[i1] = (float)(x0 * sn + x1 * c);
-  }
-}
-
-// Scores of one 64-position chunk of one token for hg query heads sharing a KV head. Keys of positions before the
-// pass (pos0) come from the cache; the pass's own keys (positions pos0 .. pos0 + b) are normed and rotated here from the
-// projection output, rounded as the cache stores them, and the block of token b appends its own key and value to the
-// cache (K position-major, V dimension-major), which is where the reference's pass writes them before attending
-// (src/model/forward.js:203-214). The query heads are normed and rotated here too.
-template <int HD, bool F16KV>
-__global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
-  constexpr int VB = F16KV ? 2 : 4;      // bytes per cached value
-  constexpr int EPL = 16 / VB;           // K values per lane per 16-byte load
-  constexpr int LP = HD / EPL;           // lanes per position
-  constexpr int PPI = 256 / LP;          // positions per load round
-  constexpr int P = 64;                  // positions per chunk
-  constexpr int R = P / PPI;             // load rounds per chunk
-  static_assert(R >= 1 && P % PPI == 0, "chunk geometry");
-  __shared__ float qs[8 * HD];
-  __shared__ float kf[8 * HD];           // rotated keys of the pass, a batch of up to 8 positions at a time (f32)
-  extern __shared__ __align__(16) uint8_t kn[];  // the chunk's new keys in cache format, from position n0: [min(P, B)][HD]
-  const int b = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const Step *st = a.step;
-  if (b >= st->B) return;
-  const int pos0 = st->pos0, npos = pos0 + b + 1;
-  if (blockIdx.x * P >= npos) return;
-  const int group = a.nHead / a.nHeadKv, hg = a.hpb;
-  const int h0 = blockIdx.y * hg;        // first query head of this block
-  const int kvh = h0 / group;
-  const bool writer = h0 % group == 0;   // the first head group of a KV head appends the pass's K and V
-  const long kvoff = ((long)a.layer * a.nHeadKv + kvh) * a.ctx * HD;
-  const uint8_t *kbase = (const uint8_t *)a.kcache + kvoff * VB;
-  float *srow = a.scores + ((long)b * a.nHead + h0) * a.sld;
-  const int part = tid % LP, sub = tid / LP;
-  uint4 u[R];
-  auto fetch = [&](int c0) {  // cached keys only: positions of the pass are filled in from kn
-    #pragma unroll
-    for (int r = 0; r < R; r++) {
-      const int t = c0 + r * PPI + sub;
-      u[r] = t < pos0 ? *(const uint4 *)(kbase + ((long)t * HD + part * EPL) * VB) : make_uint4(0, 0, 0, 0);
-    }
-  };
-  fetch(blockIdx.x * P);  // the first chunk's keys are in flight while q is prepared
-  for (int i = tid; i < hg * HD; i += 256) qs[i] = a.q[(long)b * a.ldq + (long)h0 * HD + i];
-  __syncthreads();
-  for (int h = wave; h < hg; h += 4) norm_rope<HD>(qs + h * HD, a.qNorm, a.eps, a.nRot, a.neox, a.cosT, a.sinT, npos - 1, lane);
-  __syncthreads();
-  for (int c0 = blockIdx.x * P; c0 < npos; c0 += gridDim.x * P) {
-    if (c0 != blockIdx.x * P) fetch(c0);
-    // the pass's keys in this chunk: positions [n0, n1), tokens [n0 - pos0, n1 - pos0)
-    const int n0 = max(c0, pos0), n1 = min(c0 + P, npos);
-    for (int g0 = n0; g0 < n1; g0 += 8) {
-      const int g1 = min(n1, g0 + 8);
-      for (int i = tid; i < (g1 - g0) * HD; i += 256)
-        kf[i] = a.k[(long)(g0 - pos0 + i / HD) * a.ldkv + (long)kvh * HD + i % HD];
-      __syncthreads();
-      for (int p = g0 + wave; p < g1; p += 4)
-        norm_rope<HD>(kf + (p - g0) * HD, a.kNorm, a.eps, a.nRot, a.neox, a.cosT, a.sinT, p, lane);
-      __syncthreads();
-      for (int i = tid; i < (g1 - g0) * HD; i += 256) {
-        const int p = g0 + i / HD, d = i % HD;
-        const float kv = kf[i];
-        const long off = kvoff + (long)p * HD + d;
-        if (F16KV) {
-          const uint16_t hbits = f2h(kv);
-          ((uint16_t *)kn)[(p - n0) * HD + d] = hbits;
-          if (writer && p == npos - 1) {
-            ((uint16_t *)a.kcache)[off] = hbits;
-            ((uint16_t *)a.vcache)[(((long)a.layer * a.nHeadKv + kvh) * HD + d) * a.vstride + p] =
-                f2h(a.v[(long)b * a.ldkv + (long)kvh * HD + d]);
-          }
-        } else {
-          ((float *)kn)[(p - n0) * HD + d] = kv;
-          if (writer && p == npos - 1) {
-            ((float *)a.kcache)[off] = kv;
-            ((float *)a.vcache)[(((long)a.layer * a.nHeadKv + kvh) * HD + d) * a.vstride + p] = a.v[(long)b * a.ldkv + (long)kvh * HD + d];
-          }
-        }
-      }
-      __syncthreads();
-    }
-    #pragma unroll
-    for (int r = 0; r < R; r++) {
-      const int t = c0 + r * PPI + sub;
-      if (t >= pos0 && t < npos) u[r] = *(const uint4 *)(kn + ((t - n0) * HD + part * EPL) * VB);
-      const uint32_t w4[4] = {u[r].x, u[r].y, u[r].z, u[r].w};
-      double kv[EPL];
-      #pragma unroll
-      for (int e = 0; e < EPL; e++)
-        kv[e] = F16KV ? (double)h2f((uint16_t)((w4[e >> 1] >> (16 * (e & 1))) & 0xffff)) : (double)__uint_as_float(w4[e]);
-      for (int h = 0; h < hg; h++) {
-        const float *qh = qs + h * HD + part * EPL;
-        double s = 0.0;
-        #pragma unroll
-        for (int e = 0; e < EPL; e++) s = fma((double)qh[e], kv[e], s);
-        s = wave_sum_xor(s, LP);
-        if (part == (h % LP) && t < npos) srow[(long)h * a.sld + t] = (float)(s * a.scale);
-      }
-    }
-    __syncthreads();  // kn is refilled by the next chunk
-  }
-}
-
-// One block per (32-dim slice, query head, token). The slice's V rows (dimension-major in the cache) are staged
-// through LDS in chunks of 256 (f16) or 128 (f32) positions, double buffered, the first chunk during the softmax. The
-// chain runs on lanes 0-31 of wave 0, one output dimension each, reading 16 bytes of consecutive positions at a time.
-constexpr int AV_DIMS = 32;       // output dimensions per block
-constexpr int AV_ROW = 512;       // bytes of one dimension's positions per chunk
-constexpr int AV_PITCH = AV_ROW + 16;   // LDS row pitch (the pad spreads the chain's rows over the banks)
-constexpr int AV_CHUNK = AV_DIMS * AV_PITCH;
-constexpr int AV_UNIT = 32;       // positions per unrolled step of the weighted sum
-
-template <bool F16KV>
-__global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
-  extern __shared__ __align__(16) uint8_t lds[];
-  constexpr int VB = F16KV ? 2 : 4;
-  constexpr int CT = AV_ROW / VB;        // positions per chunk
-  constexpr int EPP = 16 / VB;           // positions per 16-byte piece
-  constexpr int PPR = AV_ROW / 16;       // pieces per row
-  constexpr int LPT = AV_DIMS * PPR / 256;   // 16-byte loads per thread per chunk
-  const int slice = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const Step *st = a.step;
-  if (b >= st->B) return;
-  const int npos = st->pos0 + b + 1;
-  const int hd = a.hd, kvh = h / (a.nHead / a.nHeadKv);
-  float *p = (float *)lds;                                // [ctx rounded up to AV_UNIT] probabilities
-  uint8_t *vbuf = lds + (size_t)((a.ctx + AV_UNIT - 1) / AV_UNIT * AV_UNIT) * 4;  // [2][AV_DIMS][AV_PITCH] staged V rows
-  __shared__ double redd[4];
-  __shared__ float redf[4];
-  const uint8_t *vbase = (const uint8_t *)a.vcache + (((long)a.layer * a.nHeadKv + kvh) * hd + (long)slice * AV_DIMS) * a.vstride * VB;
-  const int nch = (npos + CT - 1) / CT;
-  uint4 pre[LPT];
-  auto fetch = [&](int c) {
-    #pragma unroll
-    for (int k = 0; k < LPT; k++) {
-      const int idx = k * 256 + tid, dim = idx / PPR, t = c * CT + (idx % PPR) * EPP;
-      pre[k] = t < npos ? *(const uint4 *)(vbase + ((long)dim * a.vstride + t) * VB) : make_uint4(0, 0, 0, 0);
-    }
-  };
-  auto store = [&](int buf) {
-    #pragma unroll
-    for (int k = 0; k < LPT; k++) {
-      const int idx = k * 256 + tid;
-      *(uint4 *)(vbuf + buf * AV_CHUNK + (idx / PPR) * AV_PITCH + (idx % PPR) * 16) = pre[k];
-    }
-  };
-  fetch(0);  // the first V chunk is in flight during the softmax
-  // ---- softmax (src/compute/ref-kernels.js:313-320)
-  const float *srow = a.scores + ((long)b * a.nHead + h) * a.sld;
-  float mx = -INFINITY;
-  for (int t0 = 0; t0 < npos; t0 += 1024) {
-    float v[4];
-    #pragma unroll
-    for (int k = 0; k < 4; k++) { const int t = t0 + k * 256 + tid; v[k] = t < npos ? srow[t] : -INFINITY; }
-    #pragma unroll
-    for (int k = 0; k < 4; k++) { const int t = t0 + k * 256 + tid; if (t < npos) p[t] = v[k]; mx = fmaxf(mx, v[k]); }
-  }
-  mx = group_fmax(mx, 64);
-  if (lane == 0) redf[wave] = mx;
-  __syncthreads();
-  const double m = (double)fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
-  double sum = 0.0;
-  for (int t = tid; t < npos; t += 256) {
-    const double e = exp((double)p[t] - m);
-    p[t] = (float)e;
-    sum += e;
-  }
-  sum = wave_sum_xor(sum, 64);
-  if (lane == 0) redd[wave] = sum;
-  __syncthreads();
-  const double inv = 1.0 / ((redd[0] + redd[1]) + (redd[2] + redd[3]));
-  for (int t = tid; t < npos; t += 256) p[t] = (float)((double)p[t] * inv);
-  for (int t = npos + tid; t < (npos + AV_UNIT - 1) / AV_UNIT * AV_UNIT; t += 256) p[t] = 0.f;
-  store(0);
-  __syncthreads();
-  // ---- weighted sum of V: f32 fma chain in position order, one output dimension per lane (lanes 0-31 of wave 0)
-  const bool chainLane = wave == 0 && lane < AV_DIMS;
-  float o = 0.f;
-  for (int c = 0; c < nch; c++) {
-    if (c + 1 < nch) fetch(c + 1);
-    if (chainLane) {
-      // units of UNIT positions: all of a unit's LDS reads are issued first, then its fma steps run back to back
-      // (each step waits ~9 cycles on the previous one, so the reads of a unit cost one LDS latency per unit).
-      // p is zero past the last position, so a unit may run past `cnt`: fmaf(0, v, o) == o for the finite cached
-      // values read there.
-      const int t0 = c * CT, cnt = min(CT, npos - t0);
-      const uint8_t *row = vbuf + (c & 1) * AV_CHUNK + lane * AV_PITCH;
-      const float *pc = p + t0;
-      for (int u = 0; u < cnt; u += AV_UNIT) {
-        float4 pv[AV_UNIT / 4];
-        uint4 vv[AV_UNIT * VB / 16];
-        #pragma unroll
-        for (int k = 0; k < AV_UNIT / 4; k++) pv[k] = *(const float4 *)(pc + u + 4 * k);
-        #pragma unroll
-        for (int k = 0; k < AV_UNIT * VB / 16; k++) vv[k] = *(const uint4 *)(row + (u + k * EPP) * VB);
-        #pragma unroll
-        for (int k = 0; k < AV_UNIT / 4; k++) {
-          float v0, v1, v2, v3;
-          if (F16KV) {
-            const uint4 &w = vv[k >> 1];
-            const uint32_t lo = (k & 1) ? w.z : w.x, hi = (k & 1) ? w.w : w.y;
-            v0 = h2f((uint16_t)(lo & 0xffff)); v1 = h2f((uint16_t)(lo >> 16));
-            v2 = h2f((uint16_t)(hi & 0xffff)); v3 = h2f((uint16_t)(hi >> 16));
-          } else {
-            const uint4 &w = vv[k];
-            v0 = __uint_as_float(w.x); v1 = __uint_as_float(w.y); v2 = __uint_as_float(w.z); v3 = __uint_as_float(w.w);
-          }
-          o = fmaf(pv[k].x, v0, o); o = fmaf(pv[k].y, v1, o); o = fmaf(pv[k].z, v2, o); o = fmaf(pv[k].w, v3, o);
-        }
-      }
-    }
-    __syncthreads();
-    if (c + 1 < nch) store((c + 1) & 1);
-    __syncthreads();
-  }
-  if (chainLane) {
-    const int col = h * hd + slice * AV_DIMS + lane;
-    if (a.out) a.out[(long)b * a.ldo + col] = o;
-    quant_block32(o, col, a.act, b);
-  }
-}
-
 // ================================================================================================ synthetic weights
 // Raw ggml blocks of a synthetic tensor generated in place (zerollm_amd/csrc/synth.h): one thread per block.
 __global__ void k_synth(int type, uint64_t seed, double std, uint64_t srcCols, uint64_t col0, int rows, int cols,
@@ -459,51 +202,6 @@ __global__ void k_fill_f32(float *p, long n, float v) {
 }
 
 // ================================================================================================ launch helpers
-// Dynamic LDS of one k_attn_av block: the probabilities of ctx positions and two staged V chunks.
-size_t attention_lds(int ctx) { return (size_t)((ctx + AV_UNIT - 1) / AV_UNIT * AV_UNIT) * 4 + 2 * AV_CHUNK; }
-constexpr size_t ATTN_LDS_MAX = 150 * 1024;
-
-template <int HD, bool F16KV>
-static void launch_scores_k(const AttnArgs &a, dim3 grid, int B, hipStream_t st) {
-  const size_t kn = (size_t)std::min(64, B) * HD * (F16KV ? 2 : 4);
-  hipLaunchKernelGGL((k_attn_scores<HD, F16KV>), grid, dim3(256), kn, st, a);
-}
-
-template <bool F16KV>
-static void launch_av_k(const AttnArgs &a, dim3 grid, size_t lds, hipStream_t st) {
-  static size_t attr = 64 * 1024;  // dynamic LDS above 64 KB must be requested per kernel
-  if (lds > attr) {
-    ZL_HIP(hipFuncSetAttribute((const void *)k_attn_av<F16KV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    attr = lds;
-  }
-  hipLaunchKernelGGL((k_attn_av<F16KV>), grid, dim3(256), lds, st, a);
-}
-
-void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
-  AttnArgs a = a0;
-  const size_t lds = attention_lds(a.ctx);
-  ZL_REQUIRE(lds <= ATTN_LDS_MAX, ZL_ERR_UNSUPPORTED, "context too long for the attention kernel");
-  ZL_REQUIRE(a.hd == 64 || a.hd == 128 || a.hd == 256, ZL_ERR_UNSUPPORTED, "attention: head_dim must be 64, 128 or 256");
-  ZL_REQUIRE(a.sld >= a.ctx, ZL_ERR_ARG, "attention: score stride below the context");
-  const int group = a.nHead / a.nHeadKv;
-  a.hpb = attn_heads_per_block(group);
-  const int chunks = (a.ctx + 63) / 64;
-  dim3 gs(chunks < 64 ? chunks : 64, a.nHead / a.hpb, B);
-  switch (a.hd * 2 + a.kvF16) {
-    case 128: launch_scores_k<64, false>(a, gs, B, st); break;
-    case 129: launch_scores_k<64, true>(a, gs, B, st); break;
-    case 256: launch_scores_k<128, false>(a, gs, B, st); break;
-    case 257: launch_scores_k<128, true>(a, gs, B, st); break;
-    case 512: launch_scores_k<256, false>(a, gs, B, st); break;
-    case 513: launch_scores_k<256, true>(a, gs, B, st); break;
-  }
-  ZL_HIP(hipGetLastError());
-  dim3 ga(a.hd / AV_DIMS, a.nHead, B);
-  if (a.kvF16) launch_av_k<true>(a, ga, lds, st);
-  else launch_av_k<false>(a, ga, lds, st);
-  ZL_HIP(hipGetLastError());
-}
-
 void launch_norm_quant(const float *x, int ldx, int row0, int nrows, const float *w, double eps, int n, int npad,
                        const Act &act, hipStream_t st) {
   hipLaunchKernelGGL(k_norm_quant, dim3((npad + NQ_CHUNK - 1) / NQ_CHUNK, nrows), dim3(256), 0, st, x, ldx, row0, w, eps, n, npad, act);
