@@ -56,12 +56,16 @@ typedef struct {
   int logits_batch;
 } zl_model_opts;
 
-/* ModelConfig (src/model/config.js:233-267); arch: 0 llama, 1 qwen2, 2 qwen3. */
+/* ModelConfig (src/model/config.js:233-267); arch: 0 llama, 1 qwen2, 2 qwen3, 3 qwen35. The qwen35 hybrid
+ * (src/model/config.js:126-156): layer l is a Gated DeltaNet layer unless (l + 1) % full_attn_interval == 0; DeltaNet
+ * shape ssm.conv_kernel, ssm.state_size (key head size), ssm.group_count (key heads), ssm.time_step_rank (value heads),
+ * ssm.inner_size (value heads x value head size); its attention layers project [query | gate] per head. */
 typedef struct {
   int arch;
   int n_ctx_train, n_embd, n_layer, n_ff, n_head, n_head_kv, head_dim, n_rot, vocab;
   float rms_eps, rope_base;
   int neox, qk_norm, qkv_bias, tied, has_rope_freqs;
+  int hybrid, full_attn_interval, ssm_conv_kernel, ssm_d_state, ssm_n_group, ssm_dt_rank, ssm_d_inner;
 } zl_config;
 
 typedef struct {
@@ -96,8 +100,9 @@ int zl_model_logits(const zl_model *m, int row0, int nrows, float *host_out);
 
 /* ---------------------------------------------------------------------------------------------- synthetic models */
 /* One tensor of a synthetic model: values std * N(0,1) from stream `seed` (element (r, c) is deviate
- * r * src_cols + col0 + c), quantised with this library's quantisers into ggml type `type`; or, with fill != 0,
- * a constant F32 vector (norm weights). Mirrors the reference generator's role (tools/make-tiny-gguf.js:28-149). */
+ * r * src_cols + col0 + c), quantised with this library's quantisers into ggml type `type`; with fill = 1 a
+ * constant F32 tensor of fill_value (norm weights); with fill = 2 an F32 tensor of fill_value + std * N(0,1).
+ * Mirrors the reference generators' role (tools/make-tiny-gguf.js:28-149, tools/make-synth-qwen35.js:30-60). */
 typedef struct {
   const char *name;
   int type;
@@ -177,7 +182,8 @@ int zl_quant_act(const float *x, int64_t K, int M, int8_t *q, float *d, int32_t 
 /* ---------------------------------------------------------------------------------------------- timing probe */
 /* Mean duration of `iters` back-to-back launches of one GEMV of the forward pass (which: 0 first q/k/v group, 1 wo,
  * 2 gate+up, 3 down, 4 output head) with M tokens, cycling through the layers' weights, timed with HIP events on the
- * model's stream; also the weight bytes one launch streams. Measurement aid (the reference times its kernels with
+ * model's stream; also the weight bytes one launch streams. The GEMV kernel alone is timed: where the pass quantises
+ * the input rows in a k_norm_quant launch first, that launch runs once before the timed ones. Measurement aid (the reference times its kernels with
  * tools/kbench.mjs). */
 int zl_probe_gemv(zl_model *m, int which, int M, int iters, float *ms_per_launch, int64_t *bytes_per_launch);
 

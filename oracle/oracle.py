@@ -24,7 +24,9 @@ U8P = C.POINTER(C.c_uint8)
 class orc_cfg(C.Structure):
     _fields_ = [("nEmbd", C.c_int), ("nLayer", C.c_int), ("nFF", C.c_int), ("nHead", C.c_int), ("nHeadKv", C.c_int),
                 ("headDim", C.c_int), ("nRot", C.c_int), ("vocab", C.c_int), ("neox", C.c_int), ("ctx", C.c_int),
-                ("kvF16", C.c_int), ("eps", C.c_double), ("ropeBase", C.c_double)]
+                ("kvF16", C.c_int), ("eps", C.c_double), ("ropeBase", C.c_double), ("hybrid", C.c_int),
+                ("interval", C.c_int), ("convK", C.c_int), ("dk", C.c_int), ("dv", C.c_int), ("nK", C.c_int),
+                ("nV", C.c_int)]
 
 
 class orc_rng(C.Structure):
@@ -71,6 +73,16 @@ def lib():
             "orc_model_set_global": (None, [C.c_void_p, C.c_int, C.c_long, C.c_long, U8P, C.c_int, U8P, F32P]),
             "orc_model_set_layer": (None, [C.c_void_p, C.c_int, F32P, F32P, F32P, F32P, F32P, F32P, F32P,
                                            C.POINTER(C.c_int), C.POINTER(U8P)]),
+            "orc_model_set_layer_hybrid": (None, [C.c_void_p, C.c_int, F32P, F32P, F32P, F32P, F32P, F32P, F32P, F32P,
+                                                  C.POINTER(C.c_int), C.POINTER(U8P)]),
+            "orc_model_conv_state": (F32P, [C.c_void_p, C.POINTER(C.c_long)]),
+            "orc_model_ssm_state": (F32P, [C.c_void_p, C.POINTER(C.c_long)]),
+            "orc_sigmoid": (C.c_double, [C.c_double]),
+            "orc_softplus": (C.c_double, [C.c_double]),
+            "orc_conv_step": (None, [F32P, F32P, F32P, F32P, C.c_int, C.c_int]),
+            "orc_l2norm_heads": (None, [F32P, C.c_int, C.c_int, C.c_double, C.c_double]),
+            "orc_delta_rule_head": (None, [F32P, F32P, F32P, F32P, F32P, C.c_int, C.c_int, C.c_double, C.c_double]),
+            "orc_gated_rmsnorm_head": (None, [F32P, F32P, F32P, C.c_int, C.c_double]),
             "orc_model_free": (None, [C.c_void_p]),
             "orc_model_pos": (C.c_int, [C.c_void_p]),
             "orc_model_truncate": (None, [C.c_void_p, C.c_int]),
@@ -234,18 +246,26 @@ def topk_select(logits: np.ndarray, k: int):
 
 
 # ------------------------------------------------------------------------------------------------ model
-class OracleModel:
-    """RefModel (src/model/forward.js:100-257): single-token forward, f64 math, f32 storage; kv='f16' rounds the cache
-    like the pool's js-kernel path. Weights are memory-mapped from the GGUF file (zerollm_amd.gguf reader)."""
+HYBRID_ARCHS = ("qwen35",)
 
-    def __init__(self, path_or_gguf, ctx=2048, kv="f32", threads=1):
+
+class OracleModel:
+    """RefModel (src/model/forward.js:100-257) and, for arch qwen35, Qwen35Model (src/model/forward-qwen35.js:177-342):
+    single-token forward, f64 math, f32 storage; kv='f16' rounds the cache like the pool's js-kernel path. Hybrid models
+    keep the recurrent state, its checkpoints (oracle.checkpoints) and truncate by restore + replay. Weights are
+    memory-mapped from the GGUF file (zerollm_amd.gguf reader) or come from an ArraySource."""
+
+    def __init__(self, path_or_gguf, ctx=2048, kv="f32", threads=1, max_checkpoints=None, checkpoint_every=0,
+                 boundary_ids=()):
         from zerollm_amd import gguf as G  # the GGUF container parser (file format only)
+        from .checkpoints import StateCheckpoints
 
         g = G.read_gguf(path_or_gguf) if isinstance(path_or_gguf, str) else path_or_gguf
         self.g = g
         a = g.get("general.architecture")
-        if a not in ("llama", "qwen2", "qwen3"):
+        if a not in ("llama", "qwen2", "qwen3") + HYBRID_ARCHS:
             raise ValueError(f"oracle: unsupported architecture {a}")
+        self.hybrid = a in HYBRID_ARCHS
         n_embd = g.get(f"{a}.embedding_length")
         n_head = g.get(f"{a}.attention.head_count")
         n_head_kv = g.get(f"{a}.attention.head_count_kv", n_head)
@@ -258,9 +278,18 @@ class OracleModel:
                         rmsEps=g.get(f"{a}.attention.layer_norm_rms_epsilon", 1e-5),
                         ropeBase=g.get(f"{a}.rope.freq_base", 10000.0))
         self.ctx = min(ctx, self.cfg["nCtxTrain"])
+        hyb = {}
+        if self.hybrid:
+            # qwen35 layout (src/model/config.js:126-156)
+            hyb = dict(hybrid=1, interval=g.get(f"{a}.full_attention_interval", 4), convK=g.get(f"{a}.ssm.conv_kernel"),
+                       dk=g.get(f"{a}.ssm.state_size"), nK=g.get(f"{a}.ssm.group_count"),
+                       nV=g.get(f"{a}.ssm.time_step_rank"))
+            hyb["dv"] = g.get(f"{a}.ssm.inner_size") // hyb["nV"]
+            self.cfg.update(hyb)
         c = orc_cfg(nEmbd=n_embd, nLayer=self.cfg["nLayer"], nFF=self.cfg["nFF"], nHead=n_head, nHeadKv=n_head_kv,
                     headDim=hd, nRot=self.cfg["nRot"], vocab=vocab, neox=0 if a == "llama" else 1, ctx=self.ctx,
-                    kvF16=1 if kv == "f16" else 0, eps=float(self.cfg["rmsEps"]), ropeBase=float(self.cfg["ropeBase"]))
+                    kvF16=1 if kv == "f16" else 0, eps=float(self.cfg["rmsEps"]), ropeBase=float(self.cfg["ropeBase"]),
+                    **hyb)
         self._keep = []
         rf = g.floats("rope_freqs.weight") if g.tensor("rope_freqs.weight") else None
         if rf is not None:
@@ -289,6 +318,18 @@ class OracleModel:
                                vec("output_norm.weight"))
         for l in range(self.cfg["nLayer"]):
             pre = f"blk.{l}."
+            if self.hybrid:
+                rec = (l + 1) % hyb["interval"] != 0
+                mix = ["attn_qkv", "attn_gate", "ssm_alpha", "ssm_beta", "ssm_out"] if rec else \
+                    ["attn_q", "attn_k", "attn_v", "attn_output", None]
+                names = mix + ["ffn_gate", "ffn_up", "ffn_down"]
+                types = (C.c_int * 8)(*[g.tensor(pre + n + ".weight").type if n else 0 for n in names])
+                datas = (U8P * 8)(*[raw(pre + n + ".weight") if n else None for n in names])
+                L.orc_model_set_layer_hybrid(self.h, l, vec(pre + "attn_norm.weight"), vec(pre + "post_attention_norm.weight"),
+                                             vec(pre + "attn_q_norm.weight"), vec(pre + "attn_k_norm.weight"),
+                                             vec(pre + "ssm_conv1d.weight"), vec(pre + "ssm_dt.bias"), vec(pre + "ssm_a"),
+                                             vec(pre + "ssm_norm.weight"), types, datas)
+                continue
             names = ["attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"]
             types = (C.c_int * 7)(*[g.tensor(pre + n + ".weight").type for n in names])
             datas = (U8P * 7)(*[raw(pre + n + ".weight") for n in names])
@@ -296,12 +337,37 @@ class OracleModel:
                                   vec(pre + "attn_q_norm.weight"), vec(pre + "attn_k_norm.weight"),
                                   vec(pre + "attn_q.bias"), vec(pre + "attn_k.bias"), vec(pre + "attn_v.bias"), types, datas)
         self.tokens = []
+        self.ck = StateCheckpoints(max_checkpoints, checkpoint_every, boundary_ids) if self.hybrid else None
+        self.prev_no_logits = False
 
     @property
     def pos(self):
         return lib().orc_model_pos(self.h)
 
+    # ---- hybrid models: the live recurrent state as numpy views (conv, ssm)
+    def state(self):
+        n1, n2 = C.c_long(), C.c_long()
+        cp = lib().orc_model_conv_state(self.h, C.byref(n1))
+        sp = lib().orc_model_ssm_state(self.h, C.byref(n2))
+        return np.ctypeslib.as_array(cp, shape=(n1.value,)), np.ctypeslib.as_array(sp, shape=(n2.value,))
+
+    def checkpoint(self):
+        self.ck.save(self.pos, self.state())
+
+    def mark_rollback(self):
+        """markRollback (src/compute/pool.js:269): the rollback slot, hybrid models only."""
+        if self.hybrid:
+            self.ck.mark(self.pos, self.state())
+
+    def truncate_plan(self, n):
+        return self.ck.plan(n, self.pos) if self.hybrid else (min(n, self.pos), 0)
+
     def forward(self, token: int, logits=True):
+        if self.hybrid and 0 <= token < self.vocab and self.pos < self.ctx:
+            # checkpoint policy before the token (src/model/forward-qwen35.js:312-314)
+            if self.ck.wants_before(self.pos, int(token), bool(logits), self.prev_no_logits):
+                self.checkpoint()
+            self.prev_no_logits = not logits
         rc = lib().orc_model_forward(self.h, int(token), 1 if logits else 0)
         if rc == -1:
             raise RuntimeError(f"context full ({self.ctx} tokens)")
@@ -313,10 +379,38 @@ class OracleModel:
         ptr = lib().orc_model_logits(self.h)
         return np.ctypeslib.as_array(ptr, shape=(self.vocab,)).copy()
 
-    def truncate(self, n: int):
-        if n < self.pos:
-            lib().orc_model_truncate(self.h, max(0, n))
-            del self.tokens[max(0, n):]
+    def truncate(self, n: int) -> int:
+        """Positional for KV-cache models; hybrid models restore the nearest snapshot <= n and replay the tokens in
+        between (Qwen35Model.truncate, src/model/forward-qwen35.js:286-298). Returns the tokens replayed."""
+        if n >= self.pos:
+            return 0
+        n = max(0, n)
+        if not self.hybrid:
+            lib().orc_model_truncate(self.h, n)
+            del self.tokens[n:]
+            return 0
+        frm, replay = self.ck.plan(n, self.pos)
+        tail = self.tokens[frm:n]
+        self.ck.drop_after(n)
+        self.ck.restore(self.state(), frm)
+        lib().orc_model_truncate(self.h, frm)
+        del self.tokens[frm:]
+        self.prev_no_logits = False
+        for t in tail:
+            self.forward(t, logits=False)
+        if replay > 0:
+            self.checkpoint()
+        self.prev_no_logits = False
+        return replay
+
+    def reset(self):
+        self.truncate(0)
+        if self.hybrid:
+            st = self.state()
+            st[0][:] = 0
+            st[1][:] = 0
+            self.ck.clear()
+            self.prev_no_logits = False
 
     def close(self):
         if self.h:
@@ -348,6 +442,13 @@ class ArraySource:
             f"{a}.attention.layer_norm_rms_epsilon": float(np.float32(spec.rms_eps)),
             f"{a}.rope.freq_base": float(np.float32(spec.rope_base)),
         }
+        if getattr(spec, "hybrid", False):
+            self.meta.update({
+                f"{a}.rope.dimension_count": spec.n_rot, f"{a}.full_attention_interval": spec.interval,
+                f"{a}.ssm.conv_kernel": spec.conv_k, f"{a}.ssm.state_size": spec.d_state,
+                f"{a}.ssm.group_count": spec.n_group, f"{a}.ssm.time_step_rank": spec.dt_rank,
+                f"{a}.ssm.inner_size": spec.d_inner,
+            })
         self.arrays = arrays
         self.tensors = {t.name: self._T(t.name, t.type, t.dims) for t in spec.tensors}
 

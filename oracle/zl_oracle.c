@@ -469,11 +469,18 @@ typedef struct {
   /* config (src/model/config.js:275-325) */
   int nEmbd, nLayer, nFF, nHead, nHeadKv, headDim, nRot, vocab, neox, ctx, kvF16;
   double eps, ropeBase;
+  /* qwen35 hybrid (src/model/config.js:126-156): layer l is recurrent unless (l + 1) % interval == 0; the
+   * attention layers project [query | gate] per head */
+  int hybrid, interval, convK, dk, dv, nK, nV;
 } orc_cfg;
 
 typedef struct {
   const float *attnNorm, *ffnNorm, *qNorm, *kNorm, *bq, *bk, *bv;
   orc_w wq, wk, wv, wo, wgate, wup, wdown;
+  /* Gated DeltaNet layer (src/model/forward-qwen35.js:187-207) */
+  int recurrent;
+  orc_w wqkv, wz, walpha, wbeta, wout;
+  const float *conv, *dtBias, *ssmA, *ssmNorm;
 } orc_layer;
 
 typedef struct {
@@ -487,6 +494,12 @@ typedef struct {
   int pos;
   float *x, *xb, *q, *k, *v, *att, *attOut, *proj, *gate, *up, *hb, *logits;
   int8_t *aq; float *ad; int32_t *as;
+  /* hybrid: KV cache index of each layer (-1: recurrent), recurrent index, the live recurrent state
+   * (src/model/recurrent-state.js:8-37: conv [layer][channel][kernel-1], ssm [layer][vHead][dv][dk]) and scratch */
+  int *attnIdx, *recIdx, nAttn, nRec;
+  long convSize, ssmSize;
+  float *conv, *ssm;
+  float *qkv, *z, *alpha, *beta, *core, *qfull, *agate;
 } orc_model;
 
 orc_model *orc_model_new(const orc_cfg *c, const float *ropeFreqs) {
@@ -499,7 +512,14 @@ orc_model *orc_model_new(const orc_cfg *c, const float *ropeFreqs) {
   m->sinT = (float *)malloc(sizeof(float) * (long)c->ctx * half);
   orc_rope_tables(c->nRot, c->ropeBase, c->ctx, ropeFreqs, m->cosT, m->sinT);
   long kvDim = (long)c->nHeadKv * c->headDim;
-  long kvN = (long)c->nLayer * c->ctx * kvDim;
+  m->attnIdx = (int *)calloc(c->nLayer, sizeof(int));
+  m->recIdx = (int *)calloc(c->nLayer, sizeof(int));
+  for (int l = 0; l < c->nLayer; l++) {
+    int rec = c->hybrid && (l + 1) % c->interval != 0;
+    m->attnIdx[l] = rec ? -1 : m->nAttn++;
+    m->recIdx[l] = rec ? m->nRec++ : -1;
+  }
+  long kvN = (long)m->nAttn * c->ctx * kvDim;
   if (c->kvF16) { m->kcache16 = (uint16_t *)calloc(kvN, 2); m->vcache16 = (uint16_t *)calloc(kvN, 2); }
   else { m->kcache = (float *)calloc(kvN, 4); m->vcache = (float *)calloc(kvN, 4); }
   long qDim = (long)c->nHead * c->headDim;
@@ -509,6 +529,18 @@ orc_model *orc_model_new(const orc_cfg *c, const float *ropeFreqs) {
   m->att = (float *)calloc(c->ctx, 4); m->attOut = (float *)calloc(qDim, 4); m->proj = (float *)calloc(c->nEmbd, 4);
   m->gate = (float *)calloc(c->nFF, 4); m->up = (float *)calloc(c->nFF, 4); m->hb = (float *)calloc(c->nFF, 4);
   m->logits = (float *)calloc(c->vocab, 4);
+  if (c->hybrid) {
+    long keyDim = (long)c->nK * c->dk, inner = (long)c->nV * c->dv, convDim = 2 * keyDim + inner;
+    m->convSize = (long)(c->convK - 1) * convDim;
+    m->ssmSize = (long)c->nV * c->dv * c->dk;
+    m->conv = (float *)calloc(m->nRec * m->convSize + 1, 4);
+    m->ssm = (float *)calloc(m->nRec * m->ssmSize + 1, 4);
+    m->qkv = (float *)calloc(convDim, 4); m->z = (float *)calloc(inner, 4);
+    m->alpha = (float *)calloc(c->nV, 4); m->beta = (float *)calloc(c->nV, 4); m->core = (float *)calloc(inner, 4);
+    m->qfull = (float *)calloc(2 * qDim, 4); m->agate = (float *)calloc(qDim, 4);
+    if (inner > big) big = inner;
+    if (2 * qDim > big) big = 2 * qDim;
+  }
   m->aq = (int8_t *)calloc(big, 1); m->ad = (float *)calloc(big / QK + 1, 4); m->as = (int32_t *)calloc(big / QK + 1, 4);
   return m;
 }
@@ -535,8 +567,39 @@ void orc_model_set_layer(orc_model *m, int l, const float *attnNorm, const float
   L->wdown = (orc_w){types[6], c->nEmbd, c->nFF, datas[6]};
 }
 
+/* A qwen35 layer (src/model/forward-qwen35.js:187-207). types/datas: recurrent layer [attn_qkv, attn_gate, ssm_alpha,
+ * ssm_beta, ssm_out, ffn_gate, ffn_up, ffn_down]; attention layer [attn_q, attn_k, attn_v, attn_output, -, ffn_gate,
+ * ffn_up, ffn_down]. ffnNorm is post_attention_norm (the pre-FFN norm). */
+void orc_model_set_layer_hybrid(orc_model *m, int l, const float *attnNorm, const float *ffnNorm, const float *qNorm,
+                                const float *kNorm, const float *conv, const float *dtBias, const float *ssmA,
+                                const float *ssmNorm, const int *types, const uint8_t *const *datas) {
+  orc_cfg *c = &m->c; orc_layer *L = &m->layers[l];
+  long qDim = (long)c->nHead * c->headDim, kvDim = (long)c->nHeadKv * c->headDim;
+  long keyDim = (long)c->nK * c->dk, inner = (long)c->nV * c->dv, convDim = 2 * keyDim + inner;
+  L->attnNorm = attnNorm; L->ffnNorm = ffnNorm; L->qNorm = qNorm; L->kNorm = kNorm;
+  L->recurrent = m->recIdx[l] >= 0;
+  if (L->recurrent) {
+    L->wqkv = (orc_w){types[0], convDim, c->nEmbd, datas[0]};
+    L->wz = (orc_w){types[1], inner, c->nEmbd, datas[1]};
+    L->walpha = (orc_w){types[2], c->nV, c->nEmbd, datas[2]};
+    L->wbeta = (orc_w){types[3], c->nV, c->nEmbd, datas[3]};
+    L->wout = (orc_w){types[4], c->nEmbd, inner, datas[4]};
+    L->conv = conv; L->dtBias = dtBias; L->ssmA = ssmA; L->ssmNorm = ssmNorm;
+  } else {
+    L->wq = (orc_w){types[0], 2 * qDim, c->nEmbd, datas[0]};
+    L->wk = (orc_w){types[1], kvDim, c->nEmbd, datas[1]};
+    L->wv = (orc_w){types[2], kvDim, c->nEmbd, datas[2]};
+    L->wo = (orc_w){types[3], c->nEmbd, qDim, datas[3]};
+  }
+  L->wgate = (orc_w){types[5], c->nFF, c->nEmbd, datas[5]};
+  L->wup = (orc_w){types[6], c->nFF, c->nEmbd, datas[6]};
+  L->wdown = (orc_w){types[7], c->nEmbd, c->nFF, datas[7]};
+}
+
 void orc_model_free(orc_model *m) {
   if (!m) return;
+  free(m->attnIdx); free(m->recIdx); free(m->conv); free(m->ssm); free(m->qkv); free(m->z); free(m->alpha);
+  free(m->beta); free(m->core); free(m->qfull); free(m->agate);
   free(m->layers); free(m->cosT); free(m->sinT); free(m->kcache); free(m->vcache); free(m->kcache16); free(m->vcache16);
   free(m->x); free(m->xb); free(m->q); free(m->k); free(m->v); free(m->att); free(m->attOut); free(m->proj);
   free(m->gate); free(m->up); free(m->hb); free(m->logits); free(m->aq); free(m->ad); free(m->as);
@@ -545,6 +608,9 @@ void orc_model_free(orc_model *m) {
 
 int orc_model_pos(orc_model *m) { return m->pos; }
 void orc_model_truncate(orc_model *m, int n) { if (n < m->pos) m->pos = n < 0 ? 0 : n; }
+/* The live recurrent state arrays (hybrid models): conv then ssm; sizes in floats through the out arguments. */
+float *orc_model_conv_state(orc_model *m, long *n) { *n = m->nRec * m->convSize; return m->conv; }
+float *orc_model_ssm_state(orc_model *m, long *n) { *n = m->nRec * m->ssmSize; return m->ssm; }
 const float *orc_model_logits(orc_model *m) { return m->logits; }
 
 /* matvec with a fresh Act over `in` (new Act(xb) in src/model/forward.js:201) */
@@ -553,9 +619,156 @@ static void mv(orc_model *m, const orc_w *w, const float *in, float *y) {
   orc_matvec(w->type, w->data, w->rows, w->cols, in, m->aq, m->ad, m->as, y);
 }
 
-/* RefModel.forward (src/model/forward.js:184-248); with kvF16 the K/V stores round to f16 as the pool's
- * js-kernel path does (src/compute/worker.js:304-306, 324, 332). Returns 0, or -1 when the context is full,
- * -2 for an out-of-range token. */
+/* ------------------------------------------------------------------ Gated DeltaNet (src/compute/ref-deltanet.js:11-106) */
+double orc_sigmoid(double x) { return 1.0 / (1.0 + exp(-x)); }
+
+/* log(1 + e^x), linear above 20 (src/compute/ref-deltanet.js:14) */
+double orc_softplus(double x) { return x > 20 ? x : log1p(exp(x)); }
+
+/* convStep (src/compute/ref-deltanet.js:42-55): depthwise causal conv over [state oldest .. newest, x] + SiLU,
+ * updating the window; out may alias x. */
+void orc_conv_step(float *state, const float *w, const float *x, float *out, int channels, int kernel) {
+  int m = kernel - 1;
+  for (int c = 0; c < channels; c++) {
+    long so = (long)c * m, wo = (long)c * kernel;
+    float cur = x[c];
+    double acc = 0;
+    for (int t = 0; t < m; t++) acc += (double)w[wo + t] * (double)state[so + t];
+    acc += (double)w[wo + m] * (double)cur;
+    for (int t = 0; t + 1 < m; t++) state[so + t] = state[so + t + 1];
+    if (m > 0) state[so + m - 1] = cur;
+    out[c] = (float)orc_silu(acc);
+  }
+}
+
+/* l2normHeads (src/compute/ref-deltanet.js:61-69): v *= scale / sqrt(sum v^2 + eps) per head */
+void orc_l2norm_heads(float *v, int nHeads, int dim, double eps, double scale) {
+  for (int h = 0; h < nHeads; h++) {
+    float *o = v + (long)h * dim;
+    double ss = 0;
+    for (int i = 0; i < dim; i++) ss += (double)o[i] * (double)o[i];
+    double s = scale / sqrt(ss + eps);
+    for (int i = 0; i < dim; i++) o[i] = (float)((double)o[i] * s);
+  }
+}
+
+/* deltaRuleHead (src/compute/ref-deltanet.js:86-96): S <- gExp S; d = beta (v - S^T k); S <- S + k d^T; o = S^T q.
+ * S is this head's [dv][dk] block. The decayed value feeds the sum unrounded, as the reference's local does. */
+void orc_delta_rule_head(float *S, const float *q, const float *k, const float *v, float *out, int dk, int dv,
+                         double gExp, double beta) {
+  for (int j = 0; j < dv; j++) {
+    float *r = S + (long)j * dk;
+    double sk = 0;
+    for (int i = 0; i < dk; i++) { double s = (double)r[i] * gExp; r[i] = (float)s; sk += s * (double)k[i]; }
+    double d = ((double)v[j] - sk) * beta;
+    double o = 0;
+    for (int i = 0; i < dk; i++) { double s = (double)r[i] + (double)k[i] * d; r[i] = (float)s; o += s * (double)q[i]; }
+    out[j] = (float)o;
+  }
+}
+
+/* gatedRmsNormHead (src/compute/ref-deltanet.js:102-106): o = o / sqrt(mean o^2 + eps) * w * silu(z) */
+void orc_gated_rmsnorm_head(float *o, const float *z, const float *w, int dim, double eps) {
+  double ss = 0;
+  for (int i = 0; i < dim; i++) ss += (double)o[i] * (double)o[i];
+  double s = 1.0 / sqrt(ss / dim + eps);
+  for (int i = 0; i < dim; i++) o[i] = (float)((double)o[i] * s * (double)w[i] * orc_silu((double)z[i]));
+}
+
+/* softmax attention of every query head over cache slot ai, positions 0..pos (src/model/forward.js:123-140); the
+ * weighted sum of V accumulates in f32 (Float32Array) */
+static void attend(orc_model *m, int ai, int pos, const float *q, float *attOut) {
+  orc_cfg *c = &m->c;
+  int hd = c->headDim, group = c->nHead / c->nHeadKv;
+  long kvDim = (long)c->nHeadKv * hd, lo = (long)ai * c->ctx * kvDim;
+  double scale = 1.0 / sqrt((double)hd);
+  float *att = m->att;
+  for (int h = 0; h < c->nHead; h++) {
+    int kvh = h / group, qo = h * hd;
+    for (int t = 0; t <= pos; t++) {
+      long ko = lo + t * kvDim + (long)kvh * hd;
+      double s = 0;
+      if (c->kvF16) for (int i = 0; i < hd; i++) s += (double)q[qo + i] * (double)F16_TBL[m->kcache16[ko + i]];
+      else for (int i = 0; i < hd; i++) s += (double)q[qo + i] * (double)m->kcache[ko + i];
+      att[t] = (float)(s * scale);
+    }
+    orc_softmax(att, pos + 1);
+    for (int i = 0; i < hd; i++) attOut[qo + i] = 0;
+    for (int t = 0; t <= pos; t++) {
+      double p = att[t];
+      long vo = lo + t * kvDim + (long)kvh * hd;
+      if (c->kvF16) for (int i = 0; i < hd; i++) attOut[qo + i] = (float)((double)attOut[qo + i] + p * (double)F16_TBL[m->vcache16[vo + i]]);
+      else for (int i = 0; i < hd; i++) attOut[qo + i] = (float)((double)attOut[qo + i] + p * (double)m->vcache[vo + i]);
+    }
+  }
+}
+
+/* append k, v at position pos of cache slot ai (f16 by RNE when the cache is f16) */
+static void kv_store(orc_model *m, int ai, int pos, const float *k, const float *v) {
+  orc_cfg *c = &m->c;
+  long kvDim = (long)c->nHeadKv * c->headDim, o = (long)ai * c->ctx * kvDim + (long)pos * kvDim;
+  if (c->kvF16) {
+    for (long i = 0; i < kvDim; i++) { m->kcache16[o + i] = orc_f32_to_f16(k[i]); m->vcache16[o + i] = orc_f32_to_f16(v[i]); }
+  } else {
+    memcpy(m->kcache + o, k, kvDim * 4);
+    memcpy(m->vcache + o, v, kvDim * 4);
+  }
+}
+
+/* matvec of several matrices over one Act of xb (new Act(h) shared by the projections of one input) */
+static void mv_shared(orc_model *m, const float *xb, int n, const orc_w *const *ws, float *const *ys) {
+  orc_quantize_act(xb, m->c.nEmbd, m->aq, m->ad, m->as);
+  for (int i = 0; i < n; i++) orc_matvec(ws[i]->type, ws[i]->data, ws[i]->rows, ws[i]->cols, xb, m->aq, m->ad, m->as, ys[i]);
+}
+
+/* ssmLayerStep (src/model/forward-qwen35.js:45-61): Gated DeltaNet layer of one token; value head hv reads key head
+ * hv % nK (keyHeadOfValueHead, src/compute/ref-deltanet.js:27-29) */
+static void ssm_layer(orc_model *m, orc_layer *L, int ri, const float *xb, float *out) {
+  orc_cfg *c = &m->c;
+  int dk = c->dk, dv = c->dv, nK = c->nK, nV = c->nV;
+  long keyDim = (long)nK * dk, convDim = 2 * keyDim + (long)nV * dv;
+  const orc_w *ws[4] = {&L->wqkv, &L->wz, &L->wbeta, &L->walpha};
+  float *ys[4] = {m->qkv, m->z, m->beta, m->alpha};
+  mv_shared(m, xb, 4, ws, ys);
+  orc_conv_step(m->conv + ri * m->convSize, L->conv, m->qkv, m->qkv, (int)convDim, c->convK);
+  orc_l2norm_heads(m->qkv, nK, dk, c->eps, 1.0 / sqrt((double)dk));
+  orc_l2norm_heads(m->qkv + keyDim, nK, dk, c->eps, 1.0);
+  float *S = m->ssm + ri * m->ssmSize;
+  for (int hv = 0; hv < nV; hv++) {
+    int kh = hv % nK;
+    double beta = orc_sigmoid((double)m->beta[hv]);
+    double g = orc_softplus((double)m->alpha[hv] + (double)L->dtBias[hv]) * (double)L->ssmA[hv];
+    orc_delta_rule_head(S + (long)hv * dv * dk, m->qkv + (long)kh * dk, m->qkv + keyDim + (long)kh * dk,
+                        m->qkv + 2 * keyDim + (long)hv * dv, m->core + (long)hv * dv, dk, dv, exp(g), beta);
+    orc_gated_rmsnorm_head(m->core + (long)hv * dv, m->z + (long)hv * dv, L->ssmNorm, dv, c->eps);
+  }
+  mv(m, &L->wout, m->core, out);
+}
+
+/* attnLayerStep (src/model/forward-qwen35.js:73-105): gated attention; attn_q rows per head are [query | gate] */
+static void gated_attn_layer(orc_model *m, orc_layer *L, int ai, int pos, const float *xb, float *out) {
+  orc_cfg *c = &m->c;
+  int D = c->headDim, nHead = c->nHead;
+  long qDim = (long)nHead * D;
+  const orc_w *ws[3] = {&L->wq, &L->wk, &L->wv};
+  float *ys[3] = {m->qfull, m->k, m->v};
+  mv_shared(m, xb, 3, ws, ys);
+  for (int h = 0; h < nHead; h++) {
+    for (int i = 0; i < D; i++) { m->q[h * D + i] = m->qfull[(long)h * 2 * D + i]; m->agate[h * D + i] = m->qfull[(long)h * 2 * D + D + i]; }
+    orc_rmsnorm(m->q + h * D, m->q + h * D, L->qNorm, c->eps, D);
+  }
+  for (int h = 0; h < c->nHeadKv; h++) orc_rmsnorm(m->k + h * D, m->k + h * D, L->kNorm, c->eps, D);
+  orc_apply_rope(m->q, nHead, D, c->nRot, 1, m->cosT, m->sinT, pos);
+  orc_apply_rope(m->k, c->nHeadKv, D, c->nRot, 1, m->cosT, m->sinT, pos);
+  kv_store(m, ai, pos, m->k, m->v);
+  attend(m, ai, pos, m->q, m->attOut);
+  for (long i = 0; i < qDim; i++) m->attOut[i] = (float)((double)m->attOut[i] * orc_sigmoid((double)m->agate[i]));
+  mv(m, &L->wo, m->attOut, out);
+}
+
+/* RefModel.forward (src/model/forward.js:184-248) and Qwen35Model.forward (src/model/forward-qwen35.js:305-341);
+ * with kvF16 the K/V stores round to f16 as the pool's js-kernel path does (src/compute/worker.js:304-306, 324, 332).
+ * Returns 0, or -1 when the context is full, -2 for an out-of-range token. */
 int orc_model_forward(orc_model *m, int token, int wantLogits) {
   orc_cfg *c = &m->c;
   int pos = m->pos;
@@ -563,54 +776,31 @@ int orc_model_forward(orc_model *m, int token, int wantLogits) {
   if (token < 0 || token >= c->vocab) return -2;
   int nEmbd = c->nEmbd, nHead = c->nHead, nHeadKv = c->nHeadKv, hd = c->headDim;
   long kvDim = (long)nHeadKv * hd;
-  int group = nHead / nHeadKv;
-  double scale = 1.0 / sqrt((double)hd);
-  float *x = m->x, *xb = m->xb, *q = m->q, *k = m->k, *v = m->v, *att = m->att, *attOut = m->attOut, *proj = m->proj;
+  float *x = m->x, *xb = m->xb, *q = m->q, *k = m->k, *v = m->v, *proj = m->proj;
 
   orc_dequant_row(m->tokEmbd.type, m->tokEmbd.data, nEmbd, token, x);
   for (int l = 0; l < c->nLayer; l++) {
     orc_layer *L = &m->layers[l];
     orc_rmsnorm(xb, x, L->attnNorm, c->eps, nEmbd);
-    /* one Act shared by q, k, v (src/model/forward.js:201-202) */
-    orc_quantize_act(xb, nEmbd, m->aq, m->ad, m->as);
-    orc_matvec(L->wq.type, L->wq.data, L->wq.rows, L->wq.cols, xb, m->aq, m->ad, m->as, q);
-    orc_matvec(L->wk.type, L->wk.data, L->wk.rows, L->wk.cols, xb, m->aq, m->ad, m->as, k);
-    orc_matvec(L->wv.type, L->wv.data, L->wv.rows, L->wv.cols, xb, m->aq, m->ad, m->as, v);
-    if (L->bq) for (long i = 0; i < (long)nHead * hd; i++) q[i] = (float)((double)q[i] + (double)L->bq[i]);
-    if (L->bk) for (long i = 0; i < kvDim; i++) k[i] = (float)((double)k[i] + (double)L->bk[i]);
-    if (L->bv) for (long i = 0; i < kvDim; i++) v[i] = (float)((double)v[i] + (double)L->bv[i]);
-    if (L->qNorm) for (int h = 0; h < nHead; h++) orc_rmsnorm(q + h * hd, q + h * hd, L->qNorm, c->eps, hd);
-    if (L->kNorm) for (int h = 0; h < nHeadKv; h++) orc_rmsnorm(k + h * hd, k + h * hd, L->kNorm, c->eps, hd);
-    orc_apply_rope(q, nHead, hd, c->nRot, c->neox, m->cosT, m->sinT, pos);
-    orc_apply_rope(k, nHeadKv, hd, c->nRot, c->neox, m->cosT, m->sinT, pos);
-    long lo = (long)l * c->ctx * kvDim;
-    if (c->kvF16) {
-      for (long i = 0; i < kvDim; i++) { m->kcache16[lo + pos * kvDim + i] = orc_f32_to_f16(k[i]); m->vcache16[lo + pos * kvDim + i] = orc_f32_to_f16(v[i]); }
+    if (c->hybrid) {
+      if (L->recurrent) ssm_layer(m, L, m->recIdx[l], xb, proj);
+      else gated_attn_layer(m, L, m->attnIdx[l], pos, xb, proj);
     } else {
-      memcpy(m->kcache + lo + pos * kvDim, k, kvDim * 4);
-      memcpy(m->vcache + lo + pos * kvDim, v, kvDim * 4);
+      /* one Act shared by q, k, v (src/model/forward.js:201-202) */
+      const orc_w *ws[3] = {&L->wq, &L->wk, &L->wv};
+      float *ys[3] = {q, k, v};
+      mv_shared(m, xb, 3, ws, ys);
+      if (L->bq) for (long i = 0; i < (long)nHead * hd; i++) q[i] = (float)((double)q[i] + (double)L->bq[i]);
+      if (L->bk) for (long i = 0; i < kvDim; i++) k[i] = (float)((double)k[i] + (double)L->bk[i]);
+      if (L->bv) for (long i = 0; i < kvDim; i++) v[i] = (float)((double)v[i] + (double)L->bv[i]);
+      if (L->qNorm) for (int h = 0; h < nHead; h++) orc_rmsnorm(q + h * hd, q + h * hd, L->qNorm, c->eps, hd);
+      if (L->kNorm) for (int h = 0; h < nHeadKv; h++) orc_rmsnorm(k + h * hd, k + h * hd, L->kNorm, c->eps, hd);
+      orc_apply_rope(q, nHead, hd, c->nRot, c->neox, m->cosT, m->sinT, pos);
+      orc_apply_rope(k, nHeadKv, hd, c->nRot, c->neox, m->cosT, m->sinT, pos);
+      kv_store(m, m->attnIdx[l], pos, k, v);
+      attend(m, m->attnIdx[l], pos, q, m->attOut);
+      mv(m, &L->wo, m->attOut, proj);
     }
-    for (int h = 0; h < nHead; h++) {
-      int kvh = h / group;
-      int qo = h * hd;
-      for (int t = 0; t <= pos; t++) {
-        long ko = lo + t * kvDim + (long)kvh * hd;
-        double s = 0;
-        if (c->kvF16) for (int i = 0; i < hd; i++) s += (double)q[qo + i] * (double)F16_TBL[m->kcache16[ko + i]];
-        else for (int i = 0; i < hd; i++) s += (double)q[qo + i] * (double)m->kcache[ko + i];
-        att[t] = (float)(s * scale);
-      }
-      orc_softmax(att, pos + 1);
-      int oo = h * hd;
-      for (int i = 0; i < hd; i++) attOut[oo + i] = 0;
-      for (int t = 0; t <= pos; t++) {
-        double p = att[t];
-        long vo = lo + t * kvDim + (long)kvh * hd;
-        if (c->kvF16) for (int i = 0; i < hd; i++) attOut[oo + i] = (float)((double)attOut[oo + i] + p * (double)F16_TBL[m->vcache16[vo + i]]);
-        else for (int i = 0; i < hd; i++) attOut[oo + i] = (float)((double)attOut[oo + i] + p * (double)m->vcache[vo + i]);
-      }
-    }
-    mv(m, &L->wo, attOut, proj);
     for (int i = 0; i < nEmbd; i++) x[i] = (float)((double)x[i] + (double)proj[i]);
 
     orc_rmsnorm(xb, x, L->ffnNorm, c->eps, nEmbd);

@@ -33,7 +33,9 @@ class zl_config(C.Structure):
     _fields_ = [("arch", C.c_int), ("n_ctx_train", C.c_int), ("n_embd", C.c_int), ("n_layer", C.c_int), ("n_ff", C.c_int),
                 ("n_head", C.c_int), ("n_head_kv", C.c_int), ("head_dim", C.c_int), ("n_rot", C.c_int), ("vocab", C.c_int),
                 ("rms_eps", C.c_float), ("rope_base", C.c_float), ("neox", C.c_int), ("qk_norm", C.c_int),
-                ("qkv_bias", C.c_int), ("tied", C.c_int), ("has_rope_freqs", C.c_int)]
+                ("qkv_bias", C.c_int), ("tied", C.c_int), ("has_rope_freqs", C.c_int), ("hybrid", C.c_int),
+                ("full_attn_interval", C.c_int), ("ssm_conv_kernel", C.c_int), ("ssm_d_state", C.c_int),
+                ("ssm_n_group", C.c_int), ("ssm_dt_rank", C.c_int), ("ssm_d_inner", C.c_int)]
 
 
 class zl_model_info(C.Structure):

@@ -398,8 +398,9 @@ constexpr long FUSE_MAX_VALUES = 4096;
 // Launches of the same input rows. A launch of quantised matrices with fewer than 256 tiles (few, large workgroups)
 // quantises short rows itself; otherwise one k_norm_quant launch writes m->act first, and the f32 normed rows for
 // float weights.
+// With norm unset the k_norm_quant launch is left out (m->act already holds these rows: GEMV timing probes).
 static void gemv_rows(zl_model *m, const std::vector<std::vector<SegSpec>> &groups, const std::vector<int> &epis, int B,
-                      const Prologue &p, const Act *qout = nullptr) {
+                      const Prologue &p, const Act *qout = nullptr, bool norm = true) {
   std::vector<bool> fused(groups.size());
   bool need = false;
   for (size_t i = 0; i < groups.size(); i++) {
@@ -412,7 +413,7 @@ static void gemv_rows(zl_model *m, const std::vector<std::vector<SegSpec>> &grou
     fused[i] = q && tiles < 256 && (long)B * pad64(p.n) <= FUSE_MAX_VALUES;
     need = need || !fused[i];
   }
-  if (need) norm_quant(m, p.x, p.ldx, p.row0, B, p.nw, p.n, m->act);
+  if (need && norm) norm_quant(m, p.x, p.ldx, p.row0, B, p.nw, p.n, m->act);
   for (size_t i = 0; i < groups.size(); i++) {
     GemvArgs a = gemv_args(groups[i], B, epis[i], m->act, m->gw);
     a.resid = m->x;
@@ -572,21 +573,22 @@ static void probe_gemv(zl_model *m, int which, int M, int iters, float *ms, int6
   ZL_HIP(hipMalloc(&xsave, xb));
   struct F { float *p; ~F() { hipFree(p); } } fr{xsave};
   ZL_HIP(hipMemcpyAsync(xsave, m->x, xb, hipMemcpyDeviceToDevice, m->st));
-  // the launch(es) exactly as the pass issues them: q/k/v, gate/up and the output head read the residual rows (fused
-  // prologue, or a k_norm_quant launch first); wo reads the attention output, down the gate/up launch's quantised hb
-  auto launch = [&](int l) {
+  // the GEMV launch exactly as the pass issues it: q/k/v, gate/up and the output head read the residual rows (a fused
+  // prologue inside the GEMV, or quantised rows that a k_norm_quant launch wrote first: the warm-up launches write
+  // them, the timed launches are the GEMV alone); wo reads the attention output, down the gate/up launch's quantised hb
+  auto launch = [&](int l, bool norm) {
     const Layer &L = m->layers[l];
     const int d = c.n_embd;
-    if (which == 0) gemv_rows(m, {segs_of(l)}, {EPI_STORE}, M, Prologue{m->x, d, 0, L.attnNorm, d});
+    if (which == 0) gemv_rows(m, {segs_of(l)}, {EPI_STORE}, M, Prologue{m->x, d, 0, L.attnNorm, d}, nullptr, norm);
     else if (which == 1) gemv_group(m, segs_of(l), M, epi, m->act, m->act.f, m->act.ld);
     else if (which == 2)
       gemv_rows(m, {segs_of(l)}, {EPI_SWIGLU}, M, Prologue{m->x, d, 0, L.ffnNorm, d},
-                is_quant(L.wdown.type) && is_quant(L.wgate.type) ? &m->act2 : nullptr);
+                is_quant(L.wdown.type) && is_quant(L.wgate.type) ? &m->act2 : nullptr, norm);
     else if (which == 3) gemv_group(m, segs_of(l), M, epi, m->act2, m->hb, c.n_ff);
-    else gemv_rows(m, {segs_of(l)}, {EPI_STORE}, M, Prologue{m->x, d, 0, m->outputNorm, d});
+    else gemv_rows(m, {segs_of(l)}, {EPI_STORE}, M, Prologue{m->x, d, 0, m->outputNorm, d}, nullptr, norm);
   };
-  for (int l = 0; l < std::min(c.n_layer, iters); l++) launch(which == 4 ? 0 : l);  // warm-up (outside capture)
-  *ms = time_graph(m->st, iters, [&](int i) { launch(which == 4 ? 0 : i % c.n_layer); });
+  for (int l = 0; l < std::min(c.n_layer, iters); l++) launch(which == 4 ? 0 : l, true);  // warm-up (outside capture)
+  *ms = time_graph(m->st, iters, [&](int i) { launch(which == 4 ? 0 : i % c.n_layer, false); });
   ZL_HIP(hipMemcpyAsync(m->x, xsave, xb, hipMemcpyDeviceToDevice, m->st));
   ZL_HIP(hipStreamSynchronize(m->st));
 }
@@ -1142,10 +1144,11 @@ int zl_model_tokens(const zl_model *m, int32_t *out, int cap) {
 int zl_synth_tensor_bytes(const zl_synth_tensor *t, int use_device, void *host_out) {
   ZL_API_BEGIN
   ZL_REQUIRE(t && host_out, ZL_ERR_ARG, "null argument");
-  if (t->fill) {
+  if (t->fill == 1) {
     for (int64_t i = 0; i < t->rows * t->cols; i++) ((float *)host_out)[i] = t->fill_value;
     return ZL_OK;
   }
+  ZL_REQUIRE(t->fill == 0 || (t->fill == 2 && t->type == T_F32), ZL_ERR_ARG, "fill 2 (offset normal values) needs type F32");
   const int bv = zl_synth::block_values(t->type), bb = zl_synth::block_bytes(t->type);
   ZL_REQUIRE(bv > 0 && t->cols % bv == 0, ZL_ERR_UNSUPPORTED, "unsupported synthetic tensor type/shape");
   const int64_t nbr = t->cols / bv;
@@ -1172,6 +1175,8 @@ int zl_synth_tensor_bytes(const zl_synth_tensor *t, int use_device, void *host_o
     }
     for (auto &x : th) x.join();
   }
+  if (t->fill == 2)
+    for (int64_t i = 0; i < t->rows * t->cols; i++) ((float *)host_out)[i] = (float)((double)t->fill_value + (double)((float *)host_out)[i]);
   ZL_API_END
 }
 

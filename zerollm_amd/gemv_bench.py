@@ -7,6 +7,7 @@ cycle through them, timed with HIP events on the library's stream. Reports weigh
 the fraction of the 8 TB/s HBM peak. Activations are device-resident.
 
     python -m zerollm_amd.gemv_bench [--m 1,2,5,9,17] [--shapes all|name,...] [--min-mb 512] [--json out.json]
+                                     [--iters N] [--copy-mb MB]
 """
 from __future__ import annotations
 
@@ -38,7 +39,20 @@ def weight_bytes(t, rows, cols):
     return rows * row_size(t, cols)
 
 
-def run(shapes, ms_list, min_mb=512, target_ms=40.0, seed=7):
+def copy_calibration(mb):
+    """One plain device-to-device copy of `mb` MiB (torch's elementwise copy kernel): a kernel of known traffic, read
+    `mb` MiB and write `mb` MiB, against which FETCH_SIZE / WRITE_SIZE counter readings are scaled."""
+    import torch
+    n = mb << 20
+    a = torch.ones(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    print(f"copy calibration: {n} B read, {n} B written", flush=True)
+
+
+def run(shapes, ms_list, min_mb=512, target_ms=40.0, seed=7, iters=None):
     _lib.call("zl_init", 0)
     results = []
     for name, t, n, k in shapes:
@@ -49,12 +63,15 @@ def run(shapes, ms_list, min_mb=512, target_ms=40.0, seed=7):
         try:
             for m in ms_list:
                 ms = C.c_float()
-                _lib.call("zl_mat_gemv_time", h, m, max(8, copies), C.byref(ms))  # warm-up and estimate
-                iters = min(2000, max(copies, int(target_ms / max(ms.value, 1e-4))))
-                _lib.call("zl_mat_gemv_time", h, m, iters, C.byref(ms))
+                if iters is None:
+                    _lib.call("zl_mat_gemv_time", h, m, max(8, copies), C.byref(ms))  # warm-up and estimate
+                    n_it = min(2000, max(copies, int(target_ms / max(ms.value, 1e-4))))
+                else:
+                    n_it = iters
+                _lib.call("zl_mat_gemv_time", h, m, n_it, C.byref(ms))
                 gbs = wb / (ms.value * 1e-3) / 1e9
                 r = {"shape": name, "type": {Q4_K: "Q4_K", Q6_K: "Q6_K", Q8_0: "Q8_0"}[t], "N": n, "K": k, "M": m,
-                     "weight_bytes": wb, "copies": copies, "iters": iters, "us": round(ms.value * 1e3, 2),
+                     "weight_bytes": wb, "copies": copies, "iters": n_it, "us": round(ms.value * 1e3, 2),
                      "GBps": round(gbs, 1), "frac_hbm": round(gbs * 1e9 / HBM_PEAK, 4)}
                 results.append(r)
                 print(f"{name:30s} M={m:2d}  {r['us']:9.2f} us  {gbs:8.1f} GB/s  {100 * r['frac_hbm']:5.1f}% of HBM peak",
@@ -70,10 +87,16 @@ def main(argv=None):
     ap.add_argument("--shapes", default="all")
     ap.add_argument("--min-mb", type=int, default=512)
     ap.add_argument("--json", default=None)
+    ap.add_argument("--iters", type=int, default=None,
+                    help="timed launches per shape and M (default: about 40 ms worth); every call first launches each "
+                         "copy once eagerly, cache-cold, which is what counter runs read")
+    ap.add_argument("--copy-mb", type=int, default=0, help="first run a plain copy of this many MiB (counter scaling)")
     a = ap.parse_args(argv)
+    if a.copy_mb:
+        copy_calibration(a.copy_mb)
     ms_list = [int(x) for x in a.m.split(",")]
     shapes = SHAPES if a.shapes == "all" else [s for s in SHAPES if s[0] in a.shapes.split(",")]
-    res = run(shapes, ms_list, a.min_mb)
+    res = run(shapes, ms_list, a.min_mb, iters=a.iters)
     if a.json:
         with open(a.json, "w") as f:
             json.dump(res, f, indent=1)
