@@ -48,12 +48,19 @@ int zl_device_query(zl_device_info *out);
 typedef struct zl_model zl_model;
 
 /* PoolModel.create options (src/compute/pool.js:27-31): ctx (0 = 2048, capped at the trained context), kv precision,
- * maxBatch (default 16, cap 64, src/compute/layout.js:23), logitsBatch (default min(maxBatch, 16), layout.js:48). */
+ * maxBatch (default 16, cap 64, src/compute/layout.js:23), logitsBatch (default min(maxBatch, 16), layout.js:48).
+ * Hybrid (qwen35) models only, the checkpoint policy (src/model/state-checkpoints.js:18-35): max_checkpoints (0: the
+ * default 6, negative: none), checkpoint_every (0: off) and the boundary token ids that get a snapshot before them
+ * (<|im_start|>). */
 typedef struct {
   int ctx;
   int kv_f16;
   int max_batch;
   int logits_batch;
+  int max_checkpoints;
+  int checkpoint_every;
+  const int32_t *boundary_ids;
+  int n_boundary;
 } zl_model_opts;
 
 /* ModelConfig (src/model/config.js:233-267); arch: 0 llama, 1 qwen2, 2 qwen3, 3 qwen35. The qwen35 hybrid
@@ -72,6 +79,7 @@ typedef struct {
   int ctx, max_batch, logits_batch, kv_f16;
   int64_t weight_bytes;      /* quantised matrix bytes streamed by one pass (all layers + output head) */
   int64_t device_bytes;      /* HBM held by the model */
+  int64_t state_bytes;       /* recurrent state of a hybrid model (each snapshot holds as much); 0 otherwise */
 } zl_model_info;
 
 /* Load a GGUF model into HBM (RefModel/PoolModel construction: src/model/forward.js:105-153,
@@ -86,10 +94,19 @@ int zl_model_free(zl_model *m);
  * logits_mode 0 = none, 1 = last token, 2 = every token (row b = distribution after tokens[b]). When host_logits is
  * not NULL the logits are copied there (vocab or n*vocab floats); they also stay on the device for zl_sample. */
 int zl_forward(zl_model *m, const int32_t *tokens, int n, int logits_mode, float *host_logits);
-/* PoolModel.truncate (src/compute/pool.js:278-294): positional KV, so bookkeeping only. */
-int zl_truncate(zl_model *m, int n);
-/* PoolModel.markRollback (src/compute/pool.js:269): no-op for KV-cache models. */
+/* PoolModel.truncate (src/compute/pool.js:278-294): positional KV is bookkeeping only; a hybrid model restores the
+ * nearest recurrent-state snapshot at or before n and replays the tokens in between (*replayed, may be NULL). */
+int zl_truncate(zl_model *m, int n, int *replayed);
+/* PoolModel.truncatePlan (src/compute/pool.js:262): the snapshot position truncate(n) restores and the replay count. */
+int zl_truncate_plan(const zl_model *m, int n, int *from, int *replay);
+/* PoolModel.markRollback (src/compute/pool.js:269): the rollback snapshot of a hybrid model; no-op for KV-cache models. */
 int zl_mark_rollback(zl_model *m);
+/* PoolModel.checkpointPositions (src/compute/pool.js:259): the count; copies up to cap positions (ascending). */
+int zl_model_checkpoints(const zl_model *m, int32_t *pos, int cap);
+/* PoolModel.getRecurrentState (src/compute/pool.js:265) in the reference's layout (src/model/recurrent-state.js:8-37):
+ * conv [recurrent layer][channel][conv_kernel-1], ssm [recurrent layer][value head][value dim][key dim]; either may be
+ * NULL. */
+int zl_model_recurrent_state(zl_model *m, float *conv, float *ssm);
 /* PoolModel.reset (src/compute/pool.js:296-299). */
 int zl_reset(zl_model *m);
 /* PoolModel.pos / tokens (src/compute/pool.js:40, 57). zl_model_tokens returns the count, copies up to cap ids. */

@@ -1,0 +1,179 @@
+"""GPU parity of the qwen35 hybrid (Gated DeltaNet + gated attention) path on tiny models: logits and recurrent state
+against the oracle (zerollm's Qwen35Model restated), batched = sequential, the checkpoint policy, truncate (snapshot
+restore + replay) to every position = a fresh run, and hybrid speculative decoding = plain greedy decoding
+(test/qwen35.test.js:158-244, test/qwen35-pool.test.js:209-351)."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from zerollm_amd import synth
+from zerollm_amd.generate import generate
+from zerollm_amd.speculative import generate_speculative
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+IM = 1  # boundary token of these tests (a chat-turn start)
+
+
+def prompt(n, seed=1, vocab=2048):
+    r = O.Rng(seed)
+    return [int(r() * vocab) for _ in range(n)]
+
+
+_arrays = {}
+
+
+def arrays_of(spec):
+    if spec.name + str(spec.tensors[0].seed) not in _arrays:
+        _arrays[spec.name + str(spec.tensors[0].seed)] = {t.name: synth.tensor_bytes(t) for t in spec.tensors}
+    return _arrays[spec.name + str(spec.tensors[0].seed)]
+
+
+def oracle(spec, ctx=128, kv="f32", **kw):
+    return O.OracleModel(O.ArraySource(spec, arrays_of(spec)), ctx=ctx, kv=kv, **kw)
+
+
+def check_close(got, want, what):
+    d = np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64))
+    assert d.max() <= MAX_ABS and d.mean() <= MEAN_ABS, (what, d.max(), d.mean())
+    return d
+
+
+@pytest.mark.parametrize("quant,kv", [("q8_0", "f32"), ("q4_k_m", "f16"), ("f32", "f32")])
+def test_logits_and_state_match_oracle(gpu, quant, kv):
+    spec = synth.tiny_qwen35(seed=21, quant=quant)
+    toks = prompt(24, seed=5)
+    ref = oracle(spec, kv=kv)
+    want = np.stack([ref.forward(t) for t in toks])
+    print(f"case qwen35 {quant} kv={kv}", flush=True)
+    m = synth.build_on_device(spec, ctx=128, kv=kv)
+    got = np.stack([m.forward(t).copy() for t in toks])
+    d = check_close(got, want, quant)
+    print(f"{quant} kv={kv}: max-abs {d.max():.3g}, mean-abs {d.mean():.3g}, bit-exact {np.mean(got == want):.4f}")
+    assert (got.argmax(1) == want.argmax(1)).all()
+    conv, ssm = m.recurrent_state()
+    rconv, rssm = ref.state()
+    np.testing.assert_allclose(conv, rconv, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(ssm, rssm, rtol=1e-4, atol=1e-5)
+    m.close()
+    ref.close()
+
+
+def test_verify_width_batch_over_prefix_equals_sequential_and_oracle(gpu):
+    """A 5-token verify pass (logits for every row) after a prefix: the rows equal five single-token passes bit for bit,
+    and the oracle within the contract."""
+    spec = synth.tiny_qwen35(seed=22, quant="q4_k_m")
+    pre, ver = prompt(40, seed=6), prompt(5, seed=7)
+    a = synth.build_on_device(spec, ctx=128, kv="f16")
+    for i in range(0, len(pre), 16):
+        a.forward_batch(pre[i:i + 16], logits="none")
+    rows = a.forward_batch(ver, logits="all").copy()
+    b = synth.build_on_device(spec, ctx=128, kv="f16")
+    for t in pre:
+        b.forward(t, logits=False)
+    seq = np.stack([b.forward(t).copy() for t in ver])
+    assert (rows.view(np.uint32) == seq.view(np.uint32)).all()
+    sa, sb = a.recurrent_state(), b.recurrent_state()
+    assert (sa[0] == sb[0]).all() and (sa[1] == sb[1]).all()
+    ref = oracle(spec, kv="f16")
+    for t in pre:
+        ref.forward(t, logits=False)
+    want = np.stack([ref.forward(t) for t in ver])
+    check_close(rows, want, "verify rows")
+    a.close()
+    b.close()
+
+
+def test_checkpoint_policy_matches_oracle(gpu):
+    spec = synth.tiny_qwen35(seed=2)
+    seq = [IM, 4, 5, IM, 6, 7, 8]
+    for max_batch in (16, 2):
+        m = synth.build_on_device(spec, ctx=64, max_batch=max_batch, boundary_ids=[IM])
+        # how generate() feeds a prompt: logits only for the last token, in chunks of max_batch
+        for i in range(0, len(seq), max_batch):
+            chunk = seq[i:i + max_batch]
+            m.forward_batch(chunk, logits="last" if i + max_batch >= len(seq) else "none")
+        assert m.checkpoint_positions == [3, 6]
+        assert m.truncate_plan(5) == (3, 2) and m.truncate_plan(6) == (6, 0) and m.truncate_plan(2) == (0, 2)
+        assert m.truncate(5) == 2
+        assert m.checkpoint_positions == [3, 5]
+        m.reset()
+        assert m.checkpoint_positions == [] and m.pos == 0
+        m.close()
+    small = synth.build_on_device(spec, ctx=64, max_checkpoints=2, boundary_ids=[IM])
+    small.forward_batch([IM, 4, IM, 5, IM, 6, 7], logits="last")
+    assert small.checkpoint_positions == [4, 6]
+    small.close()
+
+
+def test_truncate_to_every_position_equals_fresh_run(gpu):
+    spec = synth.tiny_qwen35(seed=9)
+    seq = [IM, 70, 5, 200, IM, 9, 255, 1, 17, 3, 33]
+    fresh = synth.build_on_device(spec, ctx=64)
+    want = [fresh.forward(t).copy() for t in seq]
+    fresh.close()
+    for opts in ({}, {"max_checkpoints": 0}, {"max_checkpoints": 1}, {"checkpoint_every": 3, "max_checkpoints": 2}):
+        print(f"case truncate {opts}", flush=True)
+        m = synth.build_on_device(spec, ctx=64, boundary_ids=[IM], **opts)
+        for t in seq:
+            m.forward(t)
+        for cut in range(len(seq), -1, -1):
+            frm, replay = m.truncate_plan(cut)
+            got = m.truncate(cut)
+            assert got == (0 if cut == len(seq) else replay)
+            assert m.pos == cut and m.tokens == seq[:cut]
+            for i in range(cut, len(seq)):
+                assert (m.forward(seq[i]).view(np.uint32) == want[i].view(np.uint32)).all(), (opts, cut, i)
+        m.close()
+
+
+def test_rollback_slot_makes_partial_acceptance_a_short_replay(gpu):
+    """markRollback before a verify pass, then truncate into it: the replay covers only the accepted tokens, and the
+    result equals a fresh run."""
+    spec = synth.tiny_qwen35(seed=13, quant="q4_k_m")
+    pre, ver = prompt(12, seed=8), prompt(5, seed=9)
+    m = synth.build_on_device(spec, ctx=64, kv="f16")
+    m.forward_batch(pre, logits="last")
+    m.mark_rollback()
+    m.forward_batch(ver, logits="all")
+    assert m.truncate_plan(len(pre) + 2) == (len(pre), 2)
+    assert m.truncate(len(pre) + 2) == 2
+    nxt = m.forward(77).copy()
+    f = synth.build_on_device(spec, ctx=64, kv="f16")
+    f.forward_batch(pre + ver[:2], logits="none")
+    assert (f.forward(77).view(np.uint32) == nxt.view(np.uint32)).all()
+    conv, ssm = m.recurrent_state()
+    fc, fs = f.recurrent_state()
+    assert (conv == fc).all() and (ssm == fs).all()
+    m.close()
+    f.close()
+
+
+def test_hybrid_speculative_greedy_equals_plain_greedy(gpu):
+    """test/qwen35-pool.test.js:323-349: hybrid target and hybrid draft, rollback by snapshot + replay."""
+    tspec = synth.tiny_qwen35(seed=51)
+    dspec = synth.tiny_qwen35(seed=52, n_layer=2, interval=2)
+    p = [3, 70, 5, 200, 12, 9]
+    plain = synth.build_on_device(tspec, ctx=96)
+    want = list(generate(plain, p, max_tokens=24))
+    T = synth.build_on_device(tspec, ctx=96, max_batch=8)
+    D = synth.build_on_device(dspec, ctx=96)
+    for k in (1, 3, 5):
+        print(f"case hybrid speculative k={k}", flush=True)
+        st = {}
+        got = list(generate_speculative(T, D, p, k=k, max_tokens=24, stats=st))
+        assert got == want, k
+        assert st["speculative"]["cycles"] > 0
+    p2 = p + want[:5] + [77]
+    plain.truncate(0)
+    want2 = list(generate(plain, p2, max_tokens=12))
+    got2 = list(generate_speculative(T, D, p2, k=3, max_tokens=12))
+    assert got2 == want2
+    # a draft equal to the target is always accepted
+    D2 = synth.build_on_device(tspec, ctx=96)
+    st = {}
+    got3 = list(generate_speculative(T, D2, p, k=4, max_tokens=16, stats=st))
+    assert got3 == want[:16] and st["speculative"]["acceptRate"] == 1.0
+    for x in (plain, T, D, D2):
+        x.close()

@@ -26,7 +26,9 @@ class zl_device_info(C.Structure):
 
 
 class zl_model_opts(C.Structure):
-    _fields_ = [("ctx", C.c_int), ("kv_f16", C.c_int), ("max_batch", C.c_int), ("logits_batch", C.c_int)]
+    _fields_ = [("ctx", C.c_int), ("kv_f16", C.c_int), ("max_batch", C.c_int), ("logits_batch", C.c_int),
+                ("max_checkpoints", C.c_int), ("checkpoint_every", C.c_int), ("boundary_ids", C.POINTER(C.c_int32)),
+                ("n_boundary", C.c_int)]
 
 
 class zl_config(C.Structure):
@@ -40,7 +42,7 @@ class zl_config(C.Structure):
 
 class zl_model_info(C.Structure):
     _fields_ = [("ctx", C.c_int), ("max_batch", C.c_int), ("logits_batch", C.c_int), ("kv_f16", C.c_int),
-                ("weight_bytes", C.c_int64), ("device_bytes", C.c_int64)]
+                ("weight_bytes", C.c_int64), ("device_bytes", C.c_int64), ("state_bytes", C.c_int64)]
 
 
 class zl_synth_tensor(C.Structure):
@@ -74,8 +76,11 @@ SIGNATURES = [
     ("zl_model_info_get", C.c_int, [P, C.POINTER(zl_model_info)]),
     ("zl_model_free", C.c_int, [P]),
     ("zl_forward", C.c_int, [P, I32P, C.c_int, C.c_int, F32P]),
-    ("zl_truncate", C.c_int, [P, C.c_int]),
+    ("zl_truncate", C.c_int, [P, C.c_int, C.POINTER(C.c_int)]),
+    ("zl_truncate_plan", C.c_int, [P, C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     ("zl_mark_rollback", C.c_int, [P]),
+    ("zl_model_checkpoints", C.c_int, [P, I32P, C.c_int]),
+    ("zl_model_recurrent_state", C.c_int, [P, F32P, F32P]),
     ("zl_reset", C.c_int, [P]),
     ("zl_model_pos", C.c_int, [P]),
     ("zl_model_tokens", C.c_int, [P, I32P, C.c_int]),

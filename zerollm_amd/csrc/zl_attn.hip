@@ -1,4 +1,5 @@
-// Causal GQA attention with the reference's arithmetic (src/model/forward.js:115-140), in two launches per layer:
+// Causal GQA attention with the reference's arithmetic (src/model/forward.js:115-140; the gated form of
+// src/model/forward-qwen35.js:73-105 when a.gate is set), in two launches per layer:
 //   k_attn_scores  s_t = f32(sum_i q_i K_t,i (f64, exact products) * 1/sqrt(hd)) for every position t <= pos, one
 //                  block per (64-position chunk, KV head, token): all of K streams in parallel.
 //   k_attn_av      softmax over the scores (e = exp(s - max) in f64, stored f32; p = f32(e * (1/sum e))), then
@@ -79,7 +80,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
     }
   };
   fetch(blockIdx.x * P);  // the first chunk's keys are in flight while q is prepared
-  for (int i = tid; i < hg * HD; i += 256) qs[i] = a.q[(long)b * a.ldq + (long)h0 * HD + i];
+  for (int i = tid; i < hg * HD; i += 256) qs[i] = a.q[(long)b * a.ldq + (long)(h0 + i / HD) * a.qhs + i % HD];
   __syncthreads();
   for (int h = wave; h < hg; h += 4) norm_rope<HD>(qs + h * HD, a.qNorm, a.eps, a.nRot, a.neox, a.cosT, a.sinT, npos - 1, lane);
   __syncthreads();
@@ -253,6 +254,10 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
   }
   if (chainLane) {
     const int col = h * hd + slice * AV_DIMS + lane;
+    if (a.gate) {  // gated attention output (src/model/forward-qwen35.js:103): o * sigmoid(gate), f64, stored f32
+      const double g = (double)a.gate[(long)b * a.ldq + (long)h * a.qhs + slice * AV_DIMS + lane];
+      o = (float)((double)o * (1.0 / (1.0 + exp(-g))));
+    }
     if (a.out) a.out[(long)b * a.ldo + col] = o;
     quant_block32(o, col, a.act, b);
   }
@@ -284,6 +289,7 @@ void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
   ZL_REQUIRE(lds <= ATTN_LDS_MAX, ZL_ERR_UNSUPPORTED, "context too long for the attention kernel");
   ZL_REQUIRE(a.hd == 64 || a.hd == 128 || a.hd == 256, ZL_ERR_UNSUPPORTED, "attention: head_dim must be 64, 128 or 256");
   ZL_REQUIRE(a.sld >= a.ctx, ZL_ERR_ARG, "attention: score stride below the context");
+  ZL_REQUIRE(a.qhs >= a.hd && a.ldq >= a.nHead * a.qhs, ZL_ERR_ARG, "attention: query head stride below the head size");
   const int group = a.nHead / a.nHeadKv;
   a.hpb = attn_heads_per_block(group);
   const int chunks = (a.ctx + 63) / 64;

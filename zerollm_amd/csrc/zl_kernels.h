@@ -123,7 +123,33 @@ struct AttnArgs {
   float *out;
   int ldo;
   Act act;
+  int qhs;              // floats from one query head to the next in q (hd; 2 hd where q rows are [query | gate])
+  const float *gate;    // output gate (q + hd for [query | gate] rows, same strides), or null
 };
+
+// One Gated DeltaNet layer over the B tokens of a pass (src/model/forward-qwen35.js:45-61). Conv window and delta-rule
+// matrices of the layer are read, advanced token by token and written back. The conv window is kept per value head:
+// [nV][3][D][K-1] with slots q and k of the head's key head and v of the head itself, so that no workgroup reads what
+// another one writes (value heads sharing a key head hold identical copies of its q/k window).
+struct DeltaArgs {
+  const float *qkv;    // conv input: attn_qkv rows [B][ldqkv] as [q: nK x D | k: nK x D | v: nV x D]
+  int ldqkv;
+  const float *z;      // attn_gate rows [B][ldz]
+  int ldz;
+  const float *alpha, *beta;  // ssm_alpha / ssm_beta rows [B][ldab]
+  int ldab;
+  const float *convW;  // ssm_conv1d [convDim][K]
+  float *conv;         // this layer's conv windows [nV][3][D][K-1]
+  float *ssm;          // this layer's delta-rule matrices [nV][D (value dim)][D (key dim)]
+  const float *dtBias, *ssmA, *normW;
+  int nK, nV, K, B;
+  double eps;
+  Act act;             // the quantised core rows (input of ssm_out), columns hv * D + j
+  float *out;          // and the f32 core rows (act.f), or null
+  int ldo;
+};
+constexpr int DELTA_MAX_B = 16;  // tokens per k_deltanet launch (longer passes run as several launches in order)
+void launch_deltanet(const DeltaArgs &a, int D, hipStream_t st);
 
 // Launch shape of a GEMV over ntiles tiles of nslab slabs: K parts per tile and waves per workgroup.
 void gemv_shape(int ntiles, int nslab, bool swiglu, int *ks, int *nw);

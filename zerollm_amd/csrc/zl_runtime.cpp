@@ -10,6 +10,7 @@
 #include <chrono>
 #include <functional>
 #include <map>
+#include <set>
 #include <memory>
 #include <thread>
 #include <vector>
@@ -147,6 +148,61 @@ static std::vector<DevMat> make_group(Arena &ar, const std::vector<int> &types, 
 struct Layer {
   DevMat wq, wk, wv, wo, wgate, wup, wdown;
   float *attnNorm = nullptr, *ffnNorm = nullptr, *qNorm = nullptr, *kNorm = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr;
+  // qwen35: a Gated DeltaNet layer (rec) or a gated attention layer; ai / ri index the KV cache / the recurrent state
+  bool rec = false;
+  int ai = -1, ri = -1;
+  DevMat wqkv, wz, walpha, wbeta, wssmout;
+  float *conv = nullptr, *dtBias = nullptr, *ssmA = nullptr, *ssmNorm = nullptr;
+};
+
+// Recurrent-state snapshots of a hybrid model in HBM (StateCheckpoints, src/model/state-checkpoints.js:18-85): at most
+// `max` positional checkpoints (smallest position evicted) plus one rollback slot; buffers are reused.
+struct Snap {
+  int pos = -1;
+  float *buf = nullptr;
+};
+struct Checkpoints {
+  int max = 6, every = 0;
+  std::set<int> boundary;
+  std::vector<Snap> list;  // ascending pos
+  Snap rollback;           // pos -1: empty
+  std::vector<float *> spare;
+  // wantsBefore (src/model/state-checkpoints.js:37-39)
+  bool wants_before(int pos, int token, bool wantLogits, bool prevNoLogits) const {
+    return pos > 0 && ((wantLogits && prevNoLogits) || boundary.count(token) || (every > 0 && pos % every == 0));
+  }
+  bool has(int pos) const {
+    for (auto &c : list) if (c.pos == pos) return true;
+    return false;
+  }
+  // plan (:61-67): the snapshot restored (0 = zeros) and the tokens replayed when n < pos
+  void plan(int n, int pos, int *from, int *replay) const {
+    if (n >= pos) { *from = pos; *replay = 0; return; }
+    int f = 0;
+    for (auto &c : list) if (c.pos <= n && c.pos > f) f = c.pos;
+    if (rollback.pos >= 0 && rollback.pos <= n && rollback.pos > f) f = rollback.pos;
+    *from = f;
+    *replay = n - f;
+  }
+  // dropAfter (:70-73)
+  void drop_after(int n) {
+    std::vector<Snap> keep;
+    for (auto &c : list) {
+      if (c.pos <= n) keep.push_back(c);
+      else spare.push_back(c.buf);
+    }
+    list = keep;
+    if (rollback.pos > n) rollback.pos = -1;
+  }
+  void clear() {
+    for (auto &c : list) spare.push_back(c.buf);
+    list.clear();
+    rollback.pos = -1;
+  }
+  const Snap *find(int pos) const {
+    for (auto &c : list) if (c.pos == pos) return &c;
+    return rollback.pos == pos ? &rollback : nullptr;
+  }
 };
 
 }  // namespace zl
@@ -168,6 +224,15 @@ struct zl_model {
   zl::Act act{};    // quantised input of the q/k/v, attention-output and gate/up GEMVs
   zl::Act act2{};   // quantised FFN hidden state (written by the gate/up GEMV, read by the down GEMV)
   zl::GemvWork gw{};
+  // hybrid (qwen35) models: the live recurrent state, one block [conv windows of every recurrent layer | delta-rule
+  // matrices of every recurrent layer] (convFloats / ssmFloats per layer), its snapshots, the DeltaNet inputs
+  bool hybrid = false;
+  int nAttn = 0, nRec = 0;
+  long convFloats = 0, ssmFloats = 0;
+  float *state = nullptr;
+  zl::Checkpoints ck;
+  bool prevNoLogits = false;
+  float *dqkv = nullptr, *dz = nullptr, *dalpha = nullptr, *dbeta = nullptr;
   zl::Step *dstep = nullptr;
   hipStream_t st = nullptr;
   hipStream_t cst = nullptr;  // graphs are captured on their own stream
@@ -301,30 +366,51 @@ static void finish_model(zl_model *m, const float *ropeFreqs) {
   m->sinT = (float *)m->ar.alloc(sn.size() * 4);
   ZL_HIP(hipMemcpy(m->cosT, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
   ZL_HIP(hipMemcpy(m->sinT, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
-  // K: [layer][kv head][pos][dim]; V: [layer][kv head][dim][vstride] (vstride = ctx rounded up to 16 positions)
+  // KV cache slots: every layer, or only the attention layers of a hybrid model
+  m->nAttn = m->nRec = 0;
+  for (auto &L : m->layers) {
+    L.ai = L.rec ? -1 : m->nAttn++;
+    L.ri = L.rec ? m->nRec++ : -1;
+  }
+  // K: [slot][kv head][pos][dim]; V: [slot][kv head][dim][vstride] (vstride = ctx rounded up to 16 positions)
   m->vstride = (m->ctx + 15) / 16 * 16;
-  const size_t kElems = (size_t)c.n_layer * c.n_head_kv * m->ctx * c.head_dim;
-  const size_t vElems = (size_t)c.n_layer * c.n_head_kv * c.head_dim * m->vstride;
+  const size_t kElems = (size_t)std::max(m->nAttn, 1) * c.n_head_kv * m->ctx * c.head_dim;
+  const size_t vElems = (size_t)std::max(m->nAttn, 1) * c.n_head_kv * c.head_dim * m->vstride;
   m->kcache = m->ar.alloc(kElems * (m->kvF16 ? 2 : 4));
   m->vcache = m->ar.alloc(vElems * (m->kvF16 ? 2 : 4));
   zero_now(m->kcache, kElems * (m->kvF16 ? 2 : 4));
   zero_now(m->vcache, vElems * (m->kvF16 ? 2 : 4));
   const int B = m->maxBatch;
+  const int inner = m->hybrid ? c.ssm_d_inner : 0;
+  if (m->hybrid) {
+    const int D = c.ssm_d_state, convDim = 2 * c.ssm_n_group * D + inner;
+    m->convFloats = (long)c.ssm_dt_rank * 3 * D * (c.ssm_conv_kernel - 1);
+    m->ssmFloats = (long)c.ssm_dt_rank * D * D;
+    const size_t sb = (size_t)m->nRec * (m->convFloats + m->ssmFloats) * 4;
+    m->state = (float *)m->ar.alloc(std::max<size_t>(sb, 16));
+    zero_now(m->state, std::max<size_t>(sb, 16));
+    m->dqkv = (float *)m->ar.alloc((size_t)B * convDim * 4);
+    m->dz = (float *)m->ar.alloc((size_t)B * inner * 4);
+    m->dalpha = (float *)m->ar.alloc((size_t)B * c.ssm_dt_rank * 4);
+    m->dbeta = (float *)m->ar.alloc((size_t)B * c.ssm_dt_rank * 4);
+  }
   m->x = (float *)m->ar.alloc((size_t)B * c.n_embd * 4);
-  m->q = (float *)m->ar.alloc((size_t)B * qdim(m) * 4);
+  m->q = (float *)m->ar.alloc((size_t)B * qdim(m) * (m->hybrid ? 2 : 1) * 4);
   m->k = (float *)m->ar.alloc((size_t)B * kvdim(m) * 4);
   m->v = (float *)m->ar.alloc((size_t)B * kvdim(m) * 4);
   m->hb = (float *)m->ar.alloc((size_t)B * c.n_ff * 4);
   m->logits = (float *)m->ar.alloc((size_t)m->logitsBatch * c.vocab * 4);
   m->scores = (float *)m->ar.alloc((size_t)B * c.n_head * m->ctx * 4);
-  const int ld = pad64(std::max(c.n_embd, std::max(qdim(m), c.n_ff)));
+  const int ld = pad64(std::max(std::max(c.n_embd, inner), std::max(qdim(m), c.n_ff)));
   m->act = alloc_act(m->ar, B, ld, true);
   m->act2 = alloc_act(m->ar, B, pad64(c.n_ff), false);
   m->gw = alloc_gemv_work(m->ar);
   m->dstep = (Step *)m->ar.alloc(sizeof(Step));
   zero_now(m->dstep, sizeof(Step));
   int64_t wb = 0;
-  for (auto &L : m->layers) wb += mat_bytes(L.wq) + mat_bytes(L.wk) + mat_bytes(L.wv) + mat_bytes(L.wo) + mat_bytes(L.wgate) + mat_bytes(L.wup) + mat_bytes(L.wdown);
+  for (auto &L : m->layers)
+    wb += mat_bytes(L.wq) + mat_bytes(L.wk) + mat_bytes(L.wv) + mat_bytes(L.wo) + mat_bytes(L.wgate) + mat_bytes(L.wup) +
+          mat_bytes(L.wdown) + mat_bytes(L.wqkv) + mat_bytes(L.wz) + mat_bytes(L.walpha) + mat_bytes(L.wbeta) + mat_bytes(L.wssmout);
   wb += mat_bytes(m->output);
   m->weightBytes = wb;
   ZL_HIP(hipStreamSynchronize(m->st));
@@ -434,29 +520,57 @@ static void enqueue_forward(zl_model *m, int B, int want) {
   const int d = c.n_embd, qd = qdim(m), kvd = kvdim(m), ff = c.n_ff;
   const double eps = (double)c.rms_eps;
   launch_embed(view(m->tokEmbd), m->dstep, B, m->x, d, m->st);
-  for (int l = 0; l < c.n_layer; l++) {
-    Layer &L = m->layers[l];
-    // q, k, v: consecutive matrices of one type share a launch
-    SegSpec qkv[3] = {{&L.wq, m->q, qd, L.bq}, {&L.wk, m->k, kvd, L.bk}, {&L.wv, m->v, kvd, L.bv}};
+  // consecutive quantised matrices of one type that read the same input share a launch (at most 3 per launch)
+  auto group_by_type = [](const std::vector<SegSpec> &v) {
     std::vector<std::vector<SegSpec>> groups;
-    int i0 = 0;
-    while (i0 < 3) {
-      int i1 = i0 + 1;
-      while (i1 < 3 && qkv[i1].m->type == qkv[i0].m->type && is_quant(qkv[i0].m->type)) i1++;
-      groups.emplace_back(qkv + i0, qkv + i1);
+    size_t i0 = 0;
+    while (i0 < v.size()) {
+      size_t i1 = i0 + 1;
+      while (i1 < v.size() && i1 - i0 < 3 && v[i1].m->type == v[i0].m->type && is_quant(v[i0].m->type)) i1++;
+      groups.emplace_back(v.begin() + i0, v.begin() + i1);
       i0 = i1;
     }
-    gemv_rows(m, groups, std::vector<int>(groups.size(), EPI_STORE), B, Prologue{m->x, d, 0, L.attnNorm, d});
-    AttnArgs aa;
-    aa.q = m->q; aa.ldq = qd; aa.kcache = m->kcache; aa.vcache = m->vcache;
-    aa.k = m->k; aa.v = m->v; aa.ldkv = kvd; aa.qNorm = L.qNorm; aa.kNorm = L.kNorm; aa.eps = eps;
-    aa.cosT = m->cosT; aa.sinT = m->sinT; aa.nRot = c.n_rot; aa.neox = c.neox;
-    aa.nHead = c.n_head; aa.nHeadKv = c.n_head_kv; aa.hd = c.head_dim; aa.ctx = m->ctx; aa.layer = l; aa.kvF16 = m->kvF16;
-    aa.vstride = m->vstride; aa.hpb = 1; aa.scores = m->scores; aa.sld = m->ctx;
-    aa.scale = 1.0 / sqrt((double)c.head_dim);
-    aa.step = m->dstep; aa.out = m->act.f; aa.ldo = m->act.ld; aa.act = m->act;
-    launch_attention(aa, B, m->st);
-    gemv_group(m, {{&L.wo, nullptr, 0, nullptr}}, B, EPI_RESID, m->act, m->act.f, m->act.ld);
+    return groups;
+  };
+  for (int l = 0; l < c.n_layer; l++) {
+    Layer &L = m->layers[l];
+    if (L.rec) {
+      // Gated DeltaNet layer (src/model/forward-qwen35.js:45-61): attn_qkv, attn_gate, ssm_alpha, ssm_beta of the
+      // normed rows; the recurrence; ssm_out added to the residual
+      const int D = c.ssm_d_state, nV = c.ssm_dt_rank, inner = c.ssm_d_inner, convDim = 2 * c.ssm_n_group * D + inner;
+      auto groups = group_by_type({{&L.wqkv, m->dqkv, convDim, nullptr}, {&L.wz, m->dz, inner, nullptr},
+                                   {&L.walpha, m->dalpha, nV, nullptr}, {&L.wbeta, m->dbeta, nV, nullptr}});
+      gemv_rows(m, groups, std::vector<int>(groups.size(), EPI_STORE), B, Prologue{m->x, d, 0, L.attnNorm, d});
+      DeltaArgs da;
+      memset(&da, 0, sizeof(da));
+      da.qkv = m->dqkv; da.ldqkv = convDim; da.z = m->dz; da.ldz = inner; da.alpha = m->dalpha; da.beta = m->dbeta;
+      da.ldab = nV; da.convW = L.conv;
+      da.conv = m->state + (long)L.ri * m->convFloats;
+      da.ssm = m->state + (long)m->nRec * m->convFloats + (long)L.ri * m->ssmFloats;
+      da.dtBias = L.dtBias; da.ssmA = L.ssmA; da.normW = L.ssmNorm;
+      da.nK = c.ssm_n_group; da.nV = nV; da.K = c.ssm_conv_kernel; da.B = B; da.eps = eps;
+      da.act = m->act; da.out = m->act.f; da.ldo = m->act.ld;
+      launch_deltanet(da, D, m->st);
+      gemv_group(m, {{&L.wssmout, nullptr, 0, nullptr}}, B, EPI_RESID, m->act, m->act.f, m->act.ld);
+    } else {
+      // q, k, v (q rows per head [query | gate] in a hybrid model's gated attention)
+      const int qld = m->hybrid ? 2 * qd : qd;
+      auto groups = group_by_type({{&L.wq, m->q, qld, L.bq}, {&L.wk, m->k, kvd, L.bk}, {&L.wv, m->v, kvd, L.bv}});
+      gemv_rows(m, groups, std::vector<int>(groups.size(), EPI_STORE), B, Prologue{m->x, d, 0, L.attnNorm, d});
+      AttnArgs aa;
+      memset(&aa, 0, sizeof(aa));
+      aa.q = m->q; aa.ldq = qld; aa.kcache = m->kcache; aa.vcache = m->vcache;
+      aa.k = m->k; aa.v = m->v; aa.ldkv = kvd; aa.qNorm = L.qNorm; aa.kNorm = L.kNorm; aa.eps = eps;
+      aa.cosT = m->cosT; aa.sinT = m->sinT; aa.nRot = c.n_rot; aa.neox = c.neox;
+      aa.nHead = c.n_head; aa.nHeadKv = c.n_head_kv; aa.hd = c.head_dim; aa.ctx = m->ctx; aa.layer = L.ai; aa.kvF16 = m->kvF16;
+      aa.vstride = m->vstride; aa.hpb = 1; aa.scores = m->scores; aa.sld = m->ctx;
+      aa.scale = 1.0 / sqrt((double)c.head_dim);
+      aa.step = m->dstep; aa.out = m->act.f; aa.ldo = m->act.ld; aa.act = m->act;
+      aa.qhs = m->hybrid ? 2 * c.head_dim : c.head_dim;
+      aa.gate = m->hybrid ? m->q + c.head_dim : nullptr;
+      launch_attention(aa, B, m->st);
+      gemv_group(m, {{&L.wo, nullptr, 0, nullptr}}, B, EPI_RESID, m->act, m->act.f, m->act.ld);
+    }
     ZL_REQUIRE(L.wgate.type == L.wup.type, ZL_ERR_UNSUPPORTED, "ffn_gate and ffn_up must share a type");
     // the gate/up launch quantises hb for a quantised down matrix itself; otherwise it is quantised here
     const bool qdown = is_quant(L.wdown.type), fusedq = qdown && is_quant(L.wgate.type);
@@ -606,11 +720,126 @@ static void check_batch(zl_model *m, const int32_t *tokens, int B, int want) {
                  "; raise the logitsBatch option)");
 }
 
-static void forward(zl_model *m, const int32_t *tokens, int B, int want) {
-  check_batch(m, tokens, B, want);
+// One pass of B tokens at the current position (the caller has checked the batch).
+static void pass(zl_model *m, const int32_t *tokens, int B, int want) {
   set_step(m, (int)m->tokens.size(), tokens, B);
   launch_pass(m, B, want);
   for (int i = 0; i < B; i++) m->tokens.push_back(tokens[i]);
+}
+
+// ---- recurrent-state snapshots of hybrid models (src/model/state-checkpoints.js:42-81), device-to-device copies on the
+// model's stream, ordered with the passes
+static size_t state_bytes(const zl_model *m) { return (size_t)m->nRec * (m->convFloats + m->ssmFloats) * 4; }
+
+static float *snap_buffer(zl_model *m) {
+  if (!m->ck.spare.empty()) {
+    float *b = m->ck.spare.back();
+    m->ck.spare.pop_back();
+    return b;
+  }
+  return (float *)m->ar.alloc(state_bytes(m));
+}
+
+// save (:42-50): a checkpoint of the live state at the current position
+static void checkpoint(zl_model *m) {
+  Checkpoints &ck = m->ck;
+  const int pos = (int)m->tokens.size();
+  if (pos == 0 || ck.max <= 0 || ck.has(pos)) return;
+  float *buf;
+  if ((int)ck.list.size() >= ck.max) {  // drop the smallest position, reuse its buffer
+    buf = ck.list.front().buf;
+    ck.list.erase(ck.list.begin());
+  } else {
+    buf = snap_buffer(m);
+  }
+  ZL_HIP(hipMemcpyAsync(buf, m->state, state_bytes(m), hipMemcpyDeviceToDevice, m->st));
+  Snap sn;
+  sn.pos = pos;
+  sn.buf = buf;
+  ck.list.push_back(sn);
+  std::sort(ck.list.begin(), ck.list.end(), [](const Snap &a, const Snap &b) { return a.pos < b.pos; });
+}
+
+// mark (:53-58): the rollback slot, skipped where a checkpoint holds the position
+static void mark_rollback(zl_model *m) {
+  Checkpoints &ck = m->ck;
+  const int pos = (int)m->tokens.size();
+  if (pos == 0 || ck.has(pos)) { ck.rollback.pos = -1; return; }
+  if (!ck.rollback.buf) ck.rollback.buf = snap_buffer(m);
+  ZL_HIP(hipMemcpyAsync(ck.rollback.buf, m->state, state_bytes(m), hipMemcpyDeviceToDevice, m->st));
+  ck.rollback.pos = pos;
+}
+
+// restore (:76-81): the live state of snapshot position `from` (0: zeros)
+static void restore_state(zl_model *m, int from) {
+  if (from == 0) {
+    ZL_HIP(hipMemsetAsync(m->state, 0, state_bytes(m), m->st));
+    return;
+  }
+  const Snap *c = m->ck.find(from);
+  ZL_REQUIRE(c != nullptr, ZL_ERR_STATE, "no recurrent-state snapshot at position " + std::to_string(from));
+  ZL_HIP(hipMemcpyAsync(m->state, c->buf, state_bytes(m), hipMemcpyDeviceToDevice, m->st));
+}
+
+// PoolModel.#hybridBatch (src/compute/pool.js:182-196): a snapshot before the tokens the policy names; the batch is split
+// there (never when every position returns logits), segments run as separate passes.
+// Returns the size of the last pass.
+static int hybrid_batch(zl_model *m, const int32_t *tokens, int B, int want) {
+  Checkpoints &ck = m->ck;
+  const int pos = (int)m->tokens.size();
+  if (ck.wants_before(pos, tokens[0], want == 2 || (want == 1 && B == 1), m->prevNoLogits)) checkpoint(m);
+  std::vector<int> cuts{0};
+  if (want != 2)
+    for (int i = 1; i < B; i++)
+      if (ck.wants_before(pos + i, tokens[i], want == 1 && i == B - 1, true)) cuts.push_back(i);
+  cuts.push_back(B);
+  for (size_t c = 0; c + 1 < cuts.size(); c++) {
+    if (c > 0) checkpoint(m);
+    const bool last = c + 2 == cuts.size();
+    pass(m, tokens + cuts[c], cuts[c + 1] - cuts[c], last ? want : 0);
+  }
+  m->prevNoLogits = want == 0;
+  return cuts[cuts.size() - 1] - cuts[cuts.size() - 2];
+}
+
+static void forward(zl_model *m, const int32_t *tokens, int B, int want) {
+  check_batch(m, tokens, B, want);
+  if (m->hybrid) hybrid_batch(m, tokens, B, want);
+  else pass(m, tokens, B, want);
+}
+
+// PoolModel.truncate (src/compute/pool.js:278-294): positional KV is bookkeeping; a hybrid model restores the nearest
+// snapshot at or before n and replays the tokens in between (passes of at most maxBatch tokens). Returns the replay count.
+static int truncate_model(zl_model *m, int n) {
+  const int pos = (int)m->tokens.size();
+  if (n >= pos) return 0;
+  if (n < 0) n = 0;
+  if (!m->hybrid) {
+    m->tokens.resize(n);
+    return 0;
+  }
+  ZL_REQUIRE(!m->closed, ZL_ERR_STATE, "model is closed");
+  int from, replay;
+  m->ck.plan(n, pos, &from, &replay);
+  std::vector<int32_t> tail(m->tokens.begin() + from, m->tokens.begin() + n);
+  m->ck.drop_after(n);
+  restore_state(m, from);
+  m->tokens.resize(from);
+  m->prevNoLogits = false;
+  for (size_t i = 0; i < tail.size(); i += m->maxBatch)
+    hybrid_batch(m, tail.data() + i, (int)std::min<size_t>(m->maxBatch, tail.size() - i), 0);
+  if (replay > 0) checkpoint(m);
+  m->prevNoLogits = false;
+  return replay;
+}
+
+static void reset_model(zl_model *m) {
+  m->tokens.clear();
+  if (m->hybrid) {
+    ZL_HIP(hipMemsetAsync(m->state, 0, state_bytes(m), m->st));
+    m->ck.clear();
+    m->prevNoLogits = false;
+  }
 }
 
 // ---------------------------------------------------------------------------------------------- construction
@@ -621,6 +850,9 @@ static zl_model *new_model(const zl_model_opts *o) {
   int lb = o && o->logits_batch > 0 ? o->logits_batch : 16;
   m->logitsBatch = std::max(1, std::min(lb, m->maxBatch));
   m->kvF16 = o ? (o->kv_f16 ? 1 : 0) : 0;
+  if (o && o->max_checkpoints != 0) m->ck.max = std::max(0, o->max_checkpoints);
+  if (o && o->checkpoint_every > 0) m->ck.every = o->checkpoint_every;
+  if (o && o->boundary_ids) for (int i = 0; i < o->n_boundary; i++) m->ck.boundary.insert(o->boundary_ids[i]);
   ZL_HIP(hipStreamCreateWithFlags(&m->st, hipStreamNonBlocking));
   ZL_HIP(hipStreamCreateWithFlags(&m->cst, hipStreamNonBlocking));
   return m.release();
@@ -630,6 +862,14 @@ static void check_config(const zl_config &c) {
   ZL_REQUIRE(c.n_embd > 0 && c.n_layer > 0 && c.n_ff > 0 && c.n_head > 0 && c.n_head_kv > 0 && c.head_dim > 0 && c.vocab > 0,
              ZL_ERR_ARG, "bad model config");
   ZL_REQUIRE(c.n_rot > 0 && c.n_rot <= c.head_dim && c.n_rot % 2 == 0, ZL_ERR_ARG, "bad rope dimension count");
+  if (c.hybrid) {
+    // qwen35 layout checks (src/model/config.js:146-151) and what the DeltaNet kernel takes
+    ZL_REQUIRE(c.full_attn_interval >= 1 && c.ssm_n_group > 0 && c.ssm_dt_rank > 0 && c.ssm_d_state > 0, ZL_ERR_FORMAT, "bad qwen35 layout");
+    ZL_REQUIRE(c.ssm_d_inner % c.ssm_dt_rank == 0, ZL_ERR_FORMAT, "ssm.inner_size is not a multiple of ssm.time_step_rank");
+    ZL_REQUIRE(c.ssm_dt_rank % c.ssm_n_group == 0, ZL_ERR_FORMAT, "ssm.time_step_rank is not a multiple of ssm.group_count");
+    ZL_REQUIRE(c.ssm_d_inner / c.ssm_dt_rank == c.ssm_d_state, ZL_ERR_UNSUPPORTED, "DeltaNet value and key head sizes differ");
+    ZL_REQUIRE(c.ssm_conv_kernel == 4, ZL_ERR_UNSUPPORTED, "DeltaNet conv kernel must be 4");
+  }
 }
 
 static float *upload_vec(zl_model *m, const std::vector<float> &v) {
@@ -644,8 +884,8 @@ static zl_model *load_gguf(const char *path, const zl_model_opts *o) {
   const GGUFValue *av = g.get("general.architecture");
   ZL_REQUIRE(av && av->type == 8, ZL_ERR_FORMAT, "GGUF has no general.architecture");
   const std::string arch = av->str;
-  int archId = arch == "llama" ? 0 : arch == "qwen2" ? 1 : arch == "qwen3" ? 2 : -1;
-  ZL_REQUIRE(archId >= 0, ZL_ERR_UNSUPPORTED, "architecture \"" + arch + "\" is not supported by the HIP path (supported: llama, qwen2, qwen3)");
+  int archId = arch == "llama" ? 0 : arch == "qwen2" ? 1 : arch == "qwen3" ? 2 : arch == "qwen35" ? 3 : -1;
+  ZL_REQUIRE(archId >= 0, ZL_ERR_UNSUPPORTED, "architecture \"" + arch + "\" is not supported by the HIP path (supported: llama, qwen2, qwen3, qwen35)");
   auto need = [&](const std::string &k) {
     const GGUFValue *v = g.get(arch + "." + k);
     ZL_REQUIRE(v != nullptr, ZL_ERR_FORMAT, "GGUF is missing metadata key " + arch + "." + k);
@@ -666,13 +906,24 @@ static zl_model *load_gguf(const char *path, const zl_model_opts *o) {
   ZL_REQUIRE(vs > 0, ZL_ERR_FORMAT, "cannot determine vocab size");
   c.vocab = (int)vs;
   c.n_layer = (int)need("block_count");
+  if (archId == 3) {
+    // qwen35 (src/model/config.js:93-97, 126-156): block_count includes trailing multi-token-prediction blocks
+    c.n_layer -= (int)g.num(arch + ".nextn_predict_layers", 0);
+    c.hybrid = 1;
+    c.full_attn_interval = (int)g.num(arch + ".full_attention_interval", 4);
+    c.ssm_conv_kernel = (int)need("ssm.conv_kernel");
+    c.ssm_d_state = (int)need("ssm.state_size");
+    c.ssm_n_group = (int)need("ssm.group_count");
+    c.ssm_dt_rank = (int)need("ssm.time_step_rank");
+    c.ssm_d_inner = (int)need("ssm.inner_size");
+  }
   c.n_ctx_train = (int)need("context_length");
   c.n_ff = (int)need("feed_forward_length");
   c.n_rot = (int)g.num(arch + ".rope.dimension_count", c.head_dim);
   c.rms_eps = (float)g.num(arch + ".attention.layer_norm_rms_epsilon", 1e-5);
   c.rope_base = (float)g.num(arch + ".rope.freq_base", 10000);
   c.neox = archId != 0;
-  c.qk_norm = g.tensor("blk.0.attn_q_norm.weight") != nullptr;
+  c.qk_norm = c.hybrid || g.tensor("blk.0.attn_q_norm.weight") != nullptr;
   c.qkv_bias = g.tensor("blk.0.attn_q.bias") != nullptr;
   c.tied = g.tensor("output.weight") == nullptr;
   c.has_rope_freqs = g.tensor("rope_freqs.weight") != nullptr;
@@ -728,7 +979,27 @@ static zl_model *load_gguf(const char *path, const zl_model_opts *o) {
     return upload_vec(m.get(), v);
   };
   auto Vopt = [&](const std::string &n, int len) -> float * { return g.tensor(n) ? V(n, len) : nullptr; };
+  // an F32 tensor of any shape with `count` values (ssm_conv1d [kernel, channels])
+  auto VN = [&](const std::string &n, long count) -> float * {
+    const GGUFTensor &t = req(n);
+    long e = 1;
+    for (auto d : t.dims) e *= (long)d;
+    ZL_REQUIRE(t.type == T_F32 && e == count, ZL_ERR_FORMAT, "tensor " + n + " has unexpected type or size");
+    std::vector<float> v(count);
+    if (fseeko(f, (off_t)t.absOffset, SEEK_SET) != 0 || fread(v.data(), 4, count, f) != (size_t)count) throw Error(ZL_ERR_IO, "tensor " + n + ": read failed");
+    return upload_vec(m.get(), v);
+  };
+  auto group = [&](const std::vector<std::string> &nm, const std::vector<int> &rows, int cols) {
+    std::vector<int> types;
+    for (size_t i = 0; i < nm.size(); i++) {
+      const GGUFTensor &t = req(nm[i]);
+      ZL_REQUIRE(t.dims.size() >= 2 && (int)t.dims[0] == cols && (int)t.dims[1] == rows[i], ZL_ERR_FORMAT, "tensor " + nm[i] + " has unexpected shape");
+      types.push_back(t.type);
+    }
+    return make_group(m->ar, types, rows, cols, [&](size_t i) { read_dev(req(nm[i])); }, dstage, m->st);
+  };
   const int qd = c.n_head * c.head_dim, kvd = c.n_head_kv * c.head_dim;
+  m->hybrid = c.hybrid != 0;
   m->tokEmbd = W("token_embd.weight", c.vocab, c.n_embd);
   m->outputNorm = V("output_norm.weight", c.n_embd);
   m->output = c.tied ? m->tokEmbd : W("output.weight", c.vocab, c.n_embd);
@@ -742,22 +1013,26 @@ static zl_model *load_gguf(const char *path, const zl_model_opts *o) {
     const std::string p = "blk." + std::to_string(l) + ".";
     Layer L;
     L.attnNorm = V(p + "attn_norm.weight", c.n_embd);
-    {
-      const std::string nm[3] = {p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"};
-      const std::vector<int> rows{qd, kvd, kvd};
-      std::vector<int> types;
-      for (int i = 0; i < 3; i++) {
-        const GGUFTensor &t = req(nm[i]);
-        ZL_REQUIRE(t.dims.size() >= 2 && (int)t.dims[0] == c.n_embd && (int)t.dims[1] == rows[i], ZL_ERR_FORMAT, "tensor " + nm[i] + " has unexpected shape");
-        types.push_back(t.type);
-      }
-      auto g3 = make_group(m->ar, types, rows, c.n_embd, [&](size_t i) { read_dev(req(nm[i])); }, dstage, m->st);
+    L.rec = m->hybrid && (l + 1) % c.full_attn_interval != 0;
+    if (L.rec) {
+      // Gated DeltaNet layer tensors (src/model/forward-qwen35.js:117-123, 251-254)
+      const int D = c.ssm_d_state, nV = c.ssm_dt_rank, inner = c.ssm_d_inner, convDim = 2 * c.ssm_n_group * D + inner;
+      auto g4 = group({p + "attn_qkv.weight", p + "attn_gate.weight", p + "ssm_alpha.weight", p + "ssm_beta.weight"},
+                      {convDim, inner, nV, nV}, c.n_embd);
+      L.wqkv = g4[0]; L.wz = g4[1]; L.walpha = g4[2]; L.wbeta = g4[3];
+      L.conv = VN(p + "ssm_conv1d.weight", (long)convDim * c.ssm_conv_kernel);
+      L.dtBias = V(p + "ssm_dt.bias", nV);
+      L.ssmA = V(p + "ssm_a", nV);
+      L.ssmNorm = V(p + "ssm_norm.weight", D);
+      L.wssmout = W(p + "ssm_out.weight", c.n_embd, inner);
+    } else {
+      auto g3 = group({p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"}, {m->hybrid ? 2 * qd : qd, kvd, kvd}, c.n_embd);
       L.wq = g3[0]; L.wk = g3[1]; L.wv = g3[2];
+      L.wo = W(p + "attn_output.weight", c.n_embd, qd);
+      L.bq = Vopt(p + "attn_q.bias", qd); L.bk = Vopt(p + "attn_k.bias", kvd); L.bv = Vopt(p + "attn_v.bias", kvd);
+      L.qNorm = Vopt(p + "attn_q_norm.weight", c.head_dim); L.kNorm = Vopt(p + "attn_k_norm.weight", c.head_dim);
     }
-    L.wo = W(p + "attn_output.weight", c.n_embd, qd);
-    L.bq = Vopt(p + "attn_q.bias", qd); L.bk = Vopt(p + "attn_k.bias", kvd); L.bv = Vopt(p + "attn_v.bias", kvd);
-    L.qNorm = Vopt(p + "attn_q_norm.weight", c.head_dim); L.kNorm = Vopt(p + "attn_k_norm.weight", c.head_dim);
-    L.ffnNorm = V(p + "ffn_norm.weight", c.n_embd);
+    L.ffnNorm = V(p + (m->hybrid ? "post_attention_norm.weight" : "ffn_norm.weight"), c.n_embd);
     L.wgate = W(p + "ffn_gate.weight", c.n_ff, c.n_embd);
     L.wup = W(p + "ffn_up.weight", c.n_ff, c.n_embd);
     L.wdown = W(p + "ffn_down.weight", c.n_embd, c.n_ff);
@@ -804,7 +1079,13 @@ static zl_model *build_synth(const zl_config *cfg, const zl_synth_tensor *ts, in
   auto V = [&](const std::string &nm, int len) -> float * {
     const zl_synth_tensor &t = req(nm);
     ZL_REQUIRE(t.rows * t.cols == len, ZL_ERR_ARG, "synthetic vector " + nm + " has unexpected length");
-    if (t.fill) return upload_vec(m.get(), std::vector<float>(len, t.fill_value));
+    if (t.fill == 1) return upload_vec(m.get(), std::vector<float>(len, t.fill_value));
+    if (t.fill == 2) {
+      std::vector<float> v(len);
+      const int rc = zl_synth_tensor_bytes(&t, 0, v.data());
+      ZL_REQUIRE(rc == ZL_OK, rc, "synthetic vector " + nm + ": " + g_err);
+      return upload_vec(m.get(), v);
+    }
     ZL_REQUIRE(t.type == T_F32, ZL_ERR_ARG, "synthetic vector " + nm + " must be F32");
     float *p = (float *)m->ar.alloc((size_t)len * 4);
     synth_to_device(t, (uint8_t *)p, m->st);
@@ -812,29 +1093,50 @@ static zl_model *build_synth(const zl_config *cfg, const zl_synth_tensor *ts, in
   };
   auto Vopt = [&](const std::string &nm, int len) -> float * { return byName.count(nm) ? V(nm, len) : nullptr; };
   const int qd = c.n_head * c.head_dim, kvd = c.n_head_kv * c.head_dim;
+  m->hybrid = c.hybrid != 0;
   m->tokEmbd = W("token_embd.weight", c.vocab, c.n_embd);
   m->outputNorm = V("output_norm.weight", c.n_embd);
   m->output = c.tied ? m->tokEmbd : W("output.weight", c.vocab, c.n_embd);
+  // matrices read by one launch: consecutive ones of a type share an allocation
+  auto group = [&](const std::vector<std::string> &nm, const std::vector<int> &rows, int cols) {
+    std::vector<int> types;
+    for (size_t i = 0; i < nm.size(); i++) {
+      const zl_synth_tensor &t = req(nm[i]);
+      ZL_REQUIRE(t.rows == rows[i] && t.cols == cols && !t.fill, ZL_ERR_ARG, "synthetic tensor " + nm[i] + " has unexpected shape");
+      types.push_back(t.type);
+    }
+    return make_group(m->ar, types, rows, cols, [&](size_t i) { synth_to_device(req(nm[i]), dstage, m->st); }, dstage, m->st);
+  };
   for (int l = 0; l < c.n_layer; l++) {
     const std::string p = "blk." + std::to_string(l) + ".";
     Layer L;
     L.attnNorm = V(p + "attn_norm.weight", c.n_embd);
+    L.rec = m->hybrid && (l + 1) % c.full_attn_interval != 0;
+    if (L.rec) {
+      const int D = c.ssm_d_state, nV = c.ssm_dt_rank, inner = c.ssm_d_inner, convDim = 2 * c.ssm_n_group * D + inner;
+      auto g4 = group({p + "attn_qkv.weight", p + "attn_gate.weight", p + "ssm_alpha.weight", p + "ssm_beta.weight"},
+                      {convDim, inner, nV, nV}, c.n_embd);
+      L.wqkv = g4[0]; L.wz = g4[1]; L.walpha = g4[2]; L.wbeta = g4[3];
+      L.conv = V(p + "ssm_conv1d.weight", convDim * c.ssm_conv_kernel);
+      L.dtBias = V(p + "ssm_dt.bias", nV);
+      L.ssmA = V(p + "ssm_a", nV);
+      L.ssmNorm = V(p + "ssm_norm.weight", D);
+      L.wssmout = W(p + "ssm_out.weight", c.n_embd, inner);
+      L.ffnNorm = V(p + "post_attention_norm.weight", c.n_embd);
+      L.wgate = W(p + "ffn_gate.weight", c.n_ff, c.n_embd);
+      L.wup = W(p + "ffn_up.weight", c.n_ff, c.n_embd);
+      L.wdown = W(p + "ffn_down.weight", c.n_embd, c.n_ff);
+      m->layers.push_back(L);
+      continue;
+    }
     {
-      const std::string nm[3] = {p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"};
-      const std::vector<int> rows{qd, kvd, kvd};
-      std::vector<int> types;
-      for (int i = 0; i < 3; i++) {
-        const zl_synth_tensor &t = req(nm[i]);
-        ZL_REQUIRE(t.rows == rows[i] && t.cols == c.n_embd && !t.fill, ZL_ERR_ARG, "synthetic tensor " + nm[i] + " has unexpected shape");
-        types.push_back(t.type);
-      }
-      auto g3 = make_group(m->ar, types, rows, c.n_embd, [&](size_t i) { synth_to_device(req(nm[i]), dstage, m->st); }, dstage, m->st);
+      auto g3 = group({p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"}, {m->hybrid ? 2 * qd : qd, kvd, kvd}, c.n_embd);
       L.wq = g3[0]; L.wk = g3[1]; L.wv = g3[2];
     }
     L.wo = W(p + "attn_output.weight", c.n_embd, qd);
     L.bq = Vopt(p + "attn_q.bias", qd); L.bk = Vopt(p + "attn_k.bias", kvd); L.bv = Vopt(p + "attn_v.bias", kvd);
     L.qNorm = Vopt(p + "attn_q_norm.weight", c.head_dim); L.kNorm = Vopt(p + "attn_k_norm.weight", c.head_dim);
-    L.ffnNorm = V(p + "ffn_norm.weight", c.n_embd);
+    L.ffnNorm = V(p + (m->hybrid ? "post_attention_norm.weight" : "ffn_norm.weight"), c.n_embd);
     L.wgate = W(p + "ffn_gate.weight", c.n_ff, c.n_embd);
     L.wup = W(p + "ffn_up.weight", c.n_ff, c.n_embd);
     L.wdown = W(p + "ffn_down.weight", c.n_embd, c.n_ff);
@@ -959,19 +1261,26 @@ static void spec_cycle(zl_model *T, zl_model *D, zl_sampler *s, const int32_t *f
   }
   ZL_HIP(hipGetLastError());
   const int *dh = s->sp.penalized ? s->dhist : nullptr;
+  int posF = 0;  // the draft's position after feeding
   if (kk > 0) {
+    ZL_REQUIRE(!D->hybrid || (D->ck.boundary.empty() && D->ck.every == 0), ZL_ERR_UNSUPPORTED,
+               "a hybrid draft with boundary-token or periodic checkpoints is driven with zl_forward, not zl_spec_cycle");
     // feedLogits (src/model/speculative.js:51-61): chunks of maxBatch, logits of the last one
     int lastChunk = 1;
     for (int i = 0; i < nFeed;) {
       int c = std::min(D->maxBatch, nFeed - i);
       bool last = i + c == nFeed;
       check_batch(D, feed + i, c, last ? 1 : 0);
-      set_step(D, (int)D->tokens.size(), feed + i, c);
-      launch_pass(D, c, last ? 1 : 0);
-      for (int t = 0; t < c; t++) D->tokens.push_back(feed[i + t]);
-      lastChunk = c;
+      if (D->hybrid) {
+        lastChunk = hybrid_batch(D, feed + i, c, last ? 1 : 0);
+      } else {
+        pass(D, feed + i, c, last ? 1 : 0);
+        lastChunk = c;
+      }
       i += c;
     }
+    posF = (int)D->tokens.size();
+    if (D->hybrid) mark_rollback(D);  // draft.markRollback after feedLogits (src/model/speculative.js:168)
     for (int j = 0; j < kk; j++) {
       launch_dist_rows(D->logits, D->cfg.vocab, 1, D->cfg.vocab, s->sp, dh, keep + j, 0, s->scratch, s->am, s->qdist + j, st);
       launch_draft_draw(s->qdist + j, s->ss, j, s->dstop, nStop, D->dstep, j == 0 ? lastChunk : 1, T->dstep, s->dhist, keep, st);
@@ -979,6 +1288,10 @@ static void spec_cycle(zl_model *T, zl_model *D, zl_sampler *s, const int32_t *f
     }
   }
   ZL_HIP(hipEventRecord(em, st));
+  if (T->hybrid) {  // the checkpoint policy before the verify pass (#hybridBatch: never split when all rows return logits)
+    if (T->ck.wants_before((int)T->tokens.size(), pending, true, T->prevNoLogits)) checkpoint(T);
+    T->prevNoLogits = false;
+  }
   launch_pass(T, kk + 1, 2);
   launch_dist_rows(T->logits, T->cfg.vocab, kk + 1, T->cfg.vocab, s->sp, dh, keep, 1, s->scratch, s->am, s->pdist, st);
   launch_accept(s->pdist, s->qdist, s->ss, (s->sp.temperature <= 0.0 || s->sp.greedyArgmax) ? 1 : 0, st);
@@ -1001,6 +1314,17 @@ static void spec_cycle(zl_model *T, zl_model *D, zl_sampler *s, const int32_t *f
   for (int j = 0; j + 1 < kkA; j++) D->tokens.push_back(r.drafted[j]);
   T->tokens.push_back(pending);
   for (int j = 0; j < kkA; j++) T->tokens.push_back(r.drafted[j]);
+  if (D->hybrid && kk > 0 && kkA < kk) {
+    // a stop token ended the drafts early, but the captured draft passes ran kk - 1 times: the recurrent state went past
+    // what the reference feeds, so it is rebuilt from the rollback snapshot taken after feeding (a replay of
+    // x_1 .. x_{kkA-1}), as the reference's state stands
+    std::vector<int32_t> tail(D->tokens.begin() + posF, D->tokens.end());
+    restore_state(D, posF);
+    D->tokens.resize(posF);
+    for (size_t i = 0; i < tail.size(); i += D->maxBatch)
+      hybrid_batch(D, tail.data() + i, (int)std::min<size_t>(D->maxBatch, tail.size() - i), 0);
+    D->prevNoLogits = false;
+  }
 }
 
 }  // namespace zl
@@ -1080,6 +1404,7 @@ int zl_model_info_get(const zl_model *m, zl_model_info *out) {
   ZL_REQUIRE(m && out, ZL_ERR_ARG, "null argument");
   out->ctx = m->ctx; out->max_batch = m->maxBatch; out->logits_batch = m->logitsBatch; out->kv_f16 = m->kvF16;
   out->weight_bytes = m->weightBytes; out->device_bytes = m->ar.bytes;
+  out->state_bytes = m->hybrid ? (int64_t)state_bytes(m) : 0;
   ZL_API_END
 }
 
@@ -1111,24 +1436,67 @@ int zl_model_logits(const zl_model *m, int row0, int nrows, float *host_out) {
   ZL_API_END
 }
 
-int zl_truncate(zl_model *m, int n) {
+int zl_truncate(zl_model *m, int n, int *replayed) {
   ZL_API_BEGIN
   ZL_REQUIRE(m, ZL_ERR_ARG, "null argument");
-  if (n < 0) n = 0;
-  if (n < (int)m->tokens.size()) m->tokens.resize(n);
+  const int r = truncate_model(m, n);
+  if (replayed) *replayed = r;
+  ZL_API_END
+}
+
+int zl_truncate_plan(const zl_model *m, int n, int *from, int *replay) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(m && from && replay, ZL_ERR_ARG, "null argument");
+  const int pos = (int)m->tokens.size();
+  if (m->hybrid) m->ck.plan(std::max(n, 0), pos, from, replay);
+  else { *from = std::min(std::max(n, 0), pos); *replay = 0; }
   ZL_API_END
 }
 
 int zl_mark_rollback(zl_model *m) {
   ZL_API_BEGIN
   ZL_REQUIRE(m, ZL_ERR_ARG, "null argument");
+  if (m->hybrid && !m->closed) mark_rollback(m);
   ZL_API_END
 }
 
 int zl_reset(zl_model *m) {
   ZL_API_BEGIN
   ZL_REQUIRE(m, ZL_ERR_ARG, "null argument");
-  m->tokens.clear();
+  reset_model(m);
+  ZL_API_END
+}
+
+int zl_model_checkpoints(const zl_model *m, int32_t *pos, int cap) {
+  if (!m) return -1;
+  const int n = (int)m->ck.list.size();
+  for (int i = 0; i < n && i < cap; i++) pos[i] = m->ck.list[i].pos;
+  return n;
+}
+
+// The live recurrent state in the reference's layout (RecurrentState, src/model/recurrent-state.js:8-37): conv
+// [layer][channel][kernel-1] (q/k channels of key head h from value head h's copy), ssm [layer][vHead][dv][dk].
+int zl_model_recurrent_state(zl_model *m, float *conv, float *ssm) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(m && m->hybrid, ZL_ERR_ARG, "not a hybrid model");
+  const zl_config &c = m->cfg;
+  const int D = c.ssm_d_state, nK = c.ssm_n_group, nV = c.ssm_dt_rank, M = c.ssm_conv_kernel - 1;
+  const long convDim = 2L * nK * D + (long)nV * D;
+  std::vector<float> h((size_t)m->nRec * (m->convFloats + m->ssmFloats));
+  ZL_HIP(hipMemcpyAsync(h.data(), m->state, h.size() * 4, hipMemcpyDeviceToHost, m->st));
+  ZL_HIP(hipStreamSynchronize(m->st));
+  for (int r = 0; r < m->nRec; r++) {
+    const float *w = h.data() + (size_t)r * m->convFloats;
+    float *o = conv ? conv + (size_t)r * convDim * M : nullptr;
+    if (o)
+      for (long ch = 0; ch < convDim; ch++) {
+        int hv, grp, i;
+        if (ch < 2L * nK * D) { grp = (int)(ch / ((long)nK * D)); const int r2 = (int)(ch % ((long)nK * D)); hv = r2 / D; i = r2 % D; }
+        else { grp = 2; hv = (int)((ch - 2L * nK * D) / D); i = (int)((ch - 2L * nK * D) % D); }
+        for (int t = 0; t < M; t++) o[ch * M + t] = w[(((long)hv * 3 + grp) * D + i) * M + t];
+      }
+  }
+  if (ssm) memcpy(ssm, h.data() + (size_t)m->nRec * m->convFloats, (size_t)m->nRec * m->ssmFloats * 4);
   ZL_API_END
 }
 

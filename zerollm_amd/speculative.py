@@ -96,7 +96,7 @@ def generate_speculative(target, draft, prompt_ids, k=4, max_tokens=256, sample=
             if kk > 0:
                 draft.truncate(min(common_prefix(draft.tokens, seq), len(seq) - 1))
                 feed = seq[draft.pos:]
-                draft.mark_rollback()
+                # draft.markRollback after feedLogits (src/model/speculative.js:168) happens inside zl_spec_cycle
             target.mark_rollback()
             feed_arr = np.ascontiguousarray(np.asarray(feed, dtype=np.int32))
             h = hist_of(seq, len(seq))

@@ -308,7 +308,8 @@ def write_gguf(path: str, spec: ModelSpec, use_device=False):
     gguf.write_gguf(path, meta, tensors)
 
 
-def build_on_device(spec: ModelSpec, ctx=None, kv="f32", max_batch=16, logits_batch=None):
+def build_on_device(spec: ModelSpec, ctx=None, kv="f32", max_batch=16, logits_batch=None, **ck):
+    """The model generated directly in HBM; ck: the hybrid checkpoint options of HipModel."""
     from .model import HipModel
     return HipModel.from_synth(spec.config(), [t.c() for t in spec.tensors], ctx=ctx, kv=kv, max_batch=max_batch,
-                               logits_batch=logits_batch)
+                               logits_batch=logits_batch, **ck)
