@@ -57,6 +57,72 @@ def cpu_baseline(t_spec, d_spec, prompt, seconds, threads):
                       f"in {cycles} cycles, {el:.1f}s, f16 KV, context <= 40 positions, same weights"}
 
 
+LONG_PROMPT, LONG_K = 16384, 8
+
+
+def long_context(args):
+    """The same Qwen3-8B / 0.6B-shaped pair with the context pre-filled to 16384 seeded ids, stochastic acceptance
+    (temperature 0.7, top-k 40, top-p 0.9, seeded uniforms for the accept test and residual draws) and k = 8: each verify
+    pass runs 9 rows of GQA attention over a 16K-entry f16 KV cache, and rejected positions are rolled back. A step is
+    one generation of `gen` tokens after the cached prompt; the sampler is re-seeded per step, so every step yields the
+    same tokens."""
+    from zerollm_amd import synth
+    from zerollm_amd.sampler import HipSampler
+    from zerollm_amd.speculative import generate_speculative
+
+    t_spec, d_spec = synth.qwen3_8b_pair()
+    ctx = LONG_PROMPT + args.gen + 2 * (LONG_K + 1)
+    t0 = time.perf_counter()
+    target = synth.build_on_device(t_spec, ctx=ctx, kv="f16")
+    draft = synth.build_on_device(d_spec, ctx=ctx, kv="f16")
+    log(f"models built in HBM in {time.perf_counter() - t0:.1f}s (ctx {ctx})")
+    prompt = synth.seeded_ids(LONG_PROMPT, 2025, t_spec.vocab)
+
+    def run(st):
+        smp = HipSampler(temperature=0.7, top_k=40, top_p=0.9, seed=1234)
+        try:
+            return list(generate_speculative(target, draft, prompt, k=LONG_K, max_tokens=args.gen, sample=smp, stats=st))
+        finally:
+            smp.close()
+
+    t1 = time.perf_counter()
+    first = run({})
+    log(f"first call (prefill {LONG_PROMPT} tokens into both models + {len(first)} tokens) {time.perf_counter() - t1:.1f}s")
+    for w in range(args.warmup):
+        assert run({}) == first, "seeded sampling must reproduce the same tokens"
+    times, cycles, acc, drafted, dms, vms, n_tok = [], 0, 0, 0, 0.0, 0.0, 0
+    for s in range(args.steps):
+        st = {}
+        ts = time.perf_counter()
+        out = run(st)
+        times.append(time.perf_counter() - ts)
+        assert out == first
+        sp = st["speculative"]
+        cycles += sp["cycles"]; acc += sp["accepted"]; drafted += sp["drafted"]; dms += sp["draftMs"]; vms += sp["verifyMs"]
+        n_tok += len(out)
+        log(f"step {s}: {len(out) / times[-1]:.1f} tok/s, {sp['cycles']} cycles, accept {sp['acceptRate']:.3f}")
+    total = sum(times)
+    kv_t = 2 * t_spec.n_layer * t_spec.n_head_kv * t_spec.head_dim * 2 * (LONG_PROMPT + args.gen // 2)
+    kv_d = 2 * d_spec.n_layer * d_spec.n_head_kv * d_spec.head_dim * 2 * (LONG_PROMPT + args.gen // 2)
+    line = {
+        "metric": "spec-decode tok/s, Qwen3-8B-Q4_K_M + 0.6B-Q8_0 draft, k=8, T=0.7, 16K context",
+        "value": round(n_tok / total, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(total * 1e3 / args.steps, 2), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "q4_k/q6_k/q8_0 weights, int8 activations, f64 combine, f16 KV",
+        "data": "synthetic: random-init N(0,0.02) weights of the named shapes, seeded uniform prompt ids",
+        "config": {"workload": "speculative decode with stochastic acceptance (temperature 0.7, top-k 40, top-p 0.9, "
+                               "seeded uniforms), k=8, context pre-filled to 16384 seeded ids, f16 KV, same models as the "
+                               "headline workload", "k": LONG_K, "prompt": LONG_PROMPT, "generate": args.gen,
+                   "accept_rate": round(acc / max(1, drafted), 4), "tokens_per_cycle": round(n_tok / max(1, cycles), 3),
+                   "cycle_ms": round(total * 1e3 / max(1, cycles), 3), "draft_ms_per_cycle": round(dms / max(1, cycles), 3),
+                   "verify_accept_ms_per_cycle": round(vms / max(1, cycles), 3),
+                   "kv_bytes_per_target_pass": kv_t, "kv_bytes_per_draft_pass": kv_d},
+    }
+    target.close()
+    draft.close()
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -65,6 +131,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--gen", type=int, default=GEN, help="tokens generated per step (profiling runs use fewer)")
+    ap.add_argument("--probe-only", action="store_true",
+                    help="only the roofline kernel's timed launches (for hardware-counter runs); prints the roofline")
+    ap.add_argument("--workload", choices=["headline", "long"], default="headline",
+                    help="long: the same pair with a 16384-token context, stochastic acceptance (T 0.7, top-k 40, "
+                         "top-p 0.9) and k = 8")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the speculative step runs on a single MI355X (asked for --gpus {args.gpus}); "
@@ -72,21 +143,29 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
-    from oracle import oracle as O
     from zerollm_amd import model as M, synth
     from zerollm_amd.speculative import generate_speculative
 
     M.init(0)
     dev = M.device_info()
     log("device:", dev)
+    if args.workload == "long":
+        return long_context(args)
     t_spec, d_spec = synth.qwen3_8b_pair()
     t0 = time.perf_counter()
     target = synth.build_on_device(t_spec, ctx=1024, kv="f16")
     draft = synth.build_on_device(d_spec, ctx=1024, kv="f16")
     log(f"models built in HBM in {time.perf_counter() - t0:.1f}s: target {target.weight_bytes / 1e9:.3f} GB/pass, "
         f"draft {draft.weight_bytes / 1e9:.3f} GB/pass")
-    r = O.Rng(2024)
-    prompt = [int(r() * t_spec.vocab) for _ in range(PROMPT)]
+    prompt = synth.seeded_ids(PROMPT, 2024, t_spec.vocab)
+    if args.probe_only:
+        target.forward_batch(prompt[:K + 1], logits="none")
+        ms, b = target.probe_gemv("gate_up", K + 1, 4 * t_spec.n_layer)
+        print(json.dumps({"kernel": "k_gemv_tiles<Q4_K, MT=5, SWIGLU>", "launch_ms": round(ms, 5), "bytes_per_launch": b,
+                          "GBps": round(b / (ms * 1e-3) / 1e9, 1)}), flush=True)
+        target.close()
+        draft.close()
+        return
 
     t1 = time.perf_counter()
     st = {}
@@ -133,7 +212,7 @@ def main():
                    "draft_ms_per_cycle": round(dms / cycles, 3), "verify_accept_ms_per_cycle": round(vms / cycles, 3),
                    "weight_bytes_per_cycle": bytes_cycle,
                    "cycle_weight_bw_frac": round(bytes_cycle / (cycle_ms * 1e-3) / HBM_PEAK, 4)},
-        "roofline": {"bound": "hbm", "kernel": "k_gemv<Q4_K, MT=8, SWIGLU> (ffn_gate+ffn_up, M=k+1=5)",
+        "roofline": {"bound": "hbm", "kernel": "k_gemv_tiles<Q4_K, MT=5, SWIGLU> (ffn_gate+ffn_up, M=k+1=5)",
                      "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
                      "launch_ms": round(probe_ms, 5), "bytes_per_launch": bytes_per, "launches": iters,

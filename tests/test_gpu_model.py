@@ -196,3 +196,47 @@ def test_sampled_speculative_is_reproducible_and_uses_target_distribution(gpu, t
         d.close()
     assert runs[0] == runs[1]
     assert len(runs[0]) == 40
+
+
+def test_long_context_attention_matches_oracle(gpu, tiny_files):
+    """Attention over 1200 cached positions (f16 KV): the last rows against the oracle run token by token."""
+    toks = prompt(1204, seed=17)
+    ref = O.OracleModel(tiny_files[0], ctx=1300, kv="f16")
+    for t in toks[:-4]:
+        ref.forward(t, logits=False)
+    want = np.stack([ref.forward(t) for t in toks[-4:]])
+    print("case long context 1200", flush=True)
+    m = Mdl.HipModel.load(tiny_files[0], ctx=1300, kv="f16")
+    for i in range(0, 1200, 16):
+        m.forward_batch(toks[i:i + 16], logits="none")
+    got = m.forward_batch(toks[-4:], logits="all").copy()
+    m.close()
+    diff = np.abs(got - want)
+    assert diff.max() <= MAX_ABS and diff.mean() <= MEAN_ABS, (diff.max(), diff.mean())
+    assert (got.argmax(1) == want.argmax(1)).all()
+
+
+def test_16k_context_verify_width_9_equals_sequential_and_rolls_back(gpu, tiny_files):
+    """At a 16384-token context a 9-row verify pass (k = 8) equals nine single-token passes bit for bit, and after a
+    rollback to 3 accepted rows the next pass equals a fresh continuation (size-independent checks of the long-context
+    configuration)."""
+    from zerollm_amd import synth
+
+    ctx = 16384 + 32
+    toks = prompt(16384 + 9, seed=18)
+    print("case 16k context", flush=True)
+    spec, _ = synth.tiny_pair()
+    spec.ctx_train = 32768  # the tiny target with a trained context that admits 16K positions
+    a = synth.build_on_device(spec, ctx=ctx, kv="f16")
+    assert a.ctx == ctx
+    for i in range(0, 16384, 16):
+        a.forward_batch(toks[i:i + 16], logits="none")
+    rows = a.forward_batch(toks[16384:], logits="all").copy()
+    a.truncate(16384)
+    seq = np.stack([a.forward(t).copy() for t in toks[16384:]])
+    assert (rows.view(np.uint32) == seq.view(np.uint32)).all()
+    a.truncate(16384 + 3)
+    nxt = a.forward(5).copy()
+    a.truncate(16384 + 3)
+    assert (a.forward(5).view(np.uint32) == nxt.view(np.uint32)).all()
+    a.close()

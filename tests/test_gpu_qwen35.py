@@ -177,3 +177,34 @@ def test_hybrid_speculative_greedy_equals_plain_greedy(gpu):
     assert got3 == want[:16] and st["speculative"]["acceptRate"] == 1.0
     for x in (plain, T, D, D2):
         x.close()
+
+
+def test_4b_shapes_verify_window_matches_oracle(gpu):
+    """The Qwen3.5-4B-shaped Q4_K_M hybrid (the real file's tensor set and types): a short prefix, markRollback, a 5-token
+    verify pass with logits for every row, then rollback to 2 accepted tokens; logits rows and the recurrent state after
+    the rollback against the oracle running the same tokens one at a time."""
+    spec = synth.qwen35_4b()
+    pre, ver = prompt(3, seed=11, vocab=spec.vocab), prompt(5, seed=12, vocab=spec.vocab)
+    print("case qwen35-4b verify window", flush=True)
+    m = synth.build_on_device(spec, ctx=64, kv="f16")
+    m.forward_batch(pre, logits="last")
+    m.mark_rollback()
+    rows = m.forward_batch(ver, logits="all").copy()
+    assert m.truncate(len(pre) + 2) == 2
+    conv, ssm = m.recurrent_state()
+    m.close()
+    arrays = {t.name: synth.tensor_bytes(t, use_device=True) for t in spec.tensors}
+    O.set_threads(16)
+    ref = O.OracleModel(O.ArraySource(spec, arrays), ctx=64, kv="f16", threads=16)
+    for t in pre:
+        ref.forward(t, logits=False)
+    want = []
+    for i, t in enumerate(ver):
+        want.append(ref.forward(t))
+        if i == 1:
+            rconv, rssm = (x.copy() for x in ref.state())
+    d = check_close(np.stack(rows), np.stack(want), "4b verify rows")
+    print(f"qwen35-4b verify rows: max-abs {d.max():.3g}, mean-abs {d.mean():.3g}, bit-exact {np.mean(rows == np.stack(want)):.4f}")
+    np.testing.assert_allclose(conv, rconv, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(ssm, rssm, rtol=1e-4, atol=1e-5)
+    ref.close()

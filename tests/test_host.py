@@ -113,3 +113,12 @@ def test_named_configs():
     e_t = {x.name: x for x in T.tensors}["output.weight"]
     e_d = {x.name: x for x in D.tensors}["output.weight"]
     assert e_d.seed == e_t.seed and e_d.src_cols == 4096 and e_d.cols == 1024 and e_d.type == G.Q8_0
+
+
+def test_seeded_ids_are_mulberry32_prompts():
+    """The package's seeded prompt ids equal floor(mulberry32(seed)() * vocab) of the oracle's restatement."""
+    from oracle import oracle as O
+    from zerollm_amd import synth
+
+    r = O.Rng(2024)
+    assert synth.seeded_ids(300, 2024, 151936) == [int(r() * 151936) for _ in range(300)]

@@ -627,6 +627,21 @@ static void launch_pass(zl_model *m, int B, int want) {
 // Milliseconds per call of `enqueue` (which enqueues work on st), over `iters` calls captured into one HIP graph and
 // replayed once after a warm-up replay: launch gaps are then those of the forward pass's graphs.
 static float time_graph(hipStream_t st, int iters, const std::function<void(int)> &enqueue) {
+  if (!use_graphs()) {
+    // graphs switched off (tracing and counter tools): the same launches one by one, timed with events
+    for (int i = 0; i < iters; i++) enqueue(i);  // warm-up
+    hipEvent_t a, e;
+    ZL_HIP(hipEventCreate(&a));
+    ZL_HIP(hipEventCreate(&e));
+    struct E { hipEvent_t a, b; ~E() { hipEventDestroy(a); hipEventDestroy(b); } } ev{a, e};
+    ZL_HIP(hipEventRecord(a, st));
+    for (int i = 0; i < iters; i++) enqueue(i);
+    ZL_HIP(hipEventRecord(e, st));
+    ZL_HIP(hipEventSynchronize(e));
+    float t = 0;
+    ZL_HIP(hipEventElapsedTime(&t, a, e));
+    return t / iters;
+  }
   hipGraph_t g = nullptr;
   hipGraphExec_t ex = nullptr;
   ZL_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));

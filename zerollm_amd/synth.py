@@ -24,6 +24,18 @@ def _mix(z: int) -> int:
     return z ^ (z >> 31)
 
 
+def seeded_ids(n: int, seed: int, vocab: int) -> list:
+    """n token ids floor(mulberry32(seed)() * vocab), the reference's seeded prompts (src/util/rng.js:4-13)."""
+    a = seed & 0xFFFFFFFF
+    out = []
+    for _ in range(n):
+        a = (a + 0x6D2B79F5) & 0xFFFFFFFF
+        t = ((a ^ (a >> 15)) * (a | 1)) & 0xFFFFFFFF
+        t ^= (t + (((t ^ (t >> 7)) * (t | 61)) & 0xFFFFFFFF)) & 0xFFFFFFFF
+        out.append(int(((t ^ (t >> 14)) & 0xFFFFFFFF) / 4294967296.0 * vocab))
+    return out
+
+
 def tensor_seed(model_seed: int, name: str) -> int:
     """Seed of a named tensor: FNV-1a of the name mixed with the model seed."""
     h = 1469598103934665603
