@@ -17,6 +17,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s
+# HBM bytes per launch of the roofline kernel (k_gemv_tiles<Q4_K, MT=5, SWIGLU>, ffn_gate + ffn_up at M = 5): FETCH_SIZE
+# and WRITE_SIZE counter runs over `bench.py --probe-only`, each scaled by the same counter's reading for a plain copy of
+# known size (profiles/gemv_gate_up_m5_traffic.md). A hardware counter cannot be read inside this timed run.
+ROOFLINE_TRAFFIC_BYTES = 59_381_000
 PROMPT, GEN, K = 512, 256, 4
 
 
@@ -146,6 +150,9 @@ def main():
     from zerollm_amd import model as M, synth
     from zerollm_amd.speculative import generate_speculative
 
+    if args.probe_only:
+        from zerollm_amd.gemv_bench import copy_calibration
+        copy_calibration(256)  # a kernel of known traffic for scaling hardware byte counters (before any other launch)
     M.init(0)
     dev = M.device_info()
     log("device:", dev)
@@ -214,7 +221,7 @@ def main():
                    "cycle_weight_bw_frac": round(bytes_cycle / (cycle_ms * 1e-3) / HBM_PEAK, 4)},
         "roofline": {"bound": "hbm", "kernel": "k_gemv_tiles<Q4_K, MT=5, SWIGLU> (ffn_gate+ffn_up, M=k+1=5)",
                      "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK, 4), "traffic": ROOFLINE_TRAFFIC_BYTES,
                      "launch_ms": round(probe_ms, 5), "bytes_per_launch": bytes_per, "launches": iters,
                      "other_gemvs_GBps": {w: round(b / (ms * 1e-3) / 1e9, 1) for w, (ms, b) in others.items()}},
     }
