@@ -97,13 +97,13 @@ int zl_forward(zl_model *m, const int32_t *tokens, int n, int logits_mode, float
 /* PoolModel.truncate (src/compute/pool.js:278-294): positional KV is bookkeeping only; a hybrid model restores the
  * nearest recurrent-state snapshot at or before n and replays the tokens in between (*replayed, may be NULL). */
 int zl_truncate(zl_model *m, int n, int *replayed);
-/* PoolModel.truncatePlan (src/compute/pool.js:262): the snapshot position truncate(n) restores and the replay count. */
+/* PoolModel.truncatePlan (src/compute/pool.js:256): the snapshot position truncate(n) restores and the replay count. */
 int zl_truncate_plan(const zl_model *m, int n, int *from, int *replay);
 /* PoolModel.markRollback (src/compute/pool.js:269): the rollback snapshot of a hybrid model; no-op for KV-cache models. */
 int zl_mark_rollback(zl_model *m);
-/* PoolModel.checkpointPositions (src/compute/pool.js:259): the count; copies up to cap positions (ascending). */
+/* PoolModel.checkpointPositions (src/compute/pool.js:253): the count; copies up to cap positions (ascending). */
 int zl_model_checkpoints(const zl_model *m, int32_t *pos, int cap);
-/* PoolModel.getRecurrentState (src/compute/pool.js:265) in the reference's layout (src/model/recurrent-state.js:8-37):
+/* PoolModel.getRecurrentState (src/compute/pool.js:259) in the reference's layout (src/model/recurrent-state.js:8-37):
  * conv [recurrent layer][channel][conv_kernel-1], ssm [recurrent layer][value head][value dim][key dim]; either may be
  * NULL. */
 int zl_model_recurrent_state(zl_model *m, float *conv, float *ssm);

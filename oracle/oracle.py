@@ -250,7 +250,7 @@ HYBRID_ARCHS = ("qwen35",)
 
 
 class OracleModel:
-    """RefModel (src/model/forward.js:100-257) and, for arch qwen35, Qwen35Model (src/model/forward-qwen35.js:177-342):
+    """RefModel (src/model/forward.js:100-257) and, for arch qwen35, Qwen35Model (src/model/forward-qwen35.js:158-342):
     single-token forward, f64 math, f32 storage; kv='f16' rounds the cache like the pool's js-kernel path. Hybrid models
     keep the recurrent state, its checkpoints (oracle.checkpoints) and truncate by restore + replay. Weights are
     memory-mapped from the GGUF file (zerollm_amd.gguf reader) or come from an ArraySource."""
@@ -381,7 +381,7 @@ class OracleModel:
 
     def truncate(self, n: int) -> int:
         """Positional for KV-cache models; hybrid models restore the nearest snapshot <= n and replay the tokens in
-        between (Qwen35Model.truncate, src/model/forward-qwen35.js:286-298). Returns the tokens replayed."""
+        between (Qwen35Model.truncate, src/model/forward-qwen35.js:284-300). Returns the tokens replayed."""
         if n >= self.pos:
             return 0
         n = max(0, n)

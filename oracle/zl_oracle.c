@@ -477,7 +477,7 @@ typedef struct {
 typedef struct {
   const float *attnNorm, *ffnNorm, *qNorm, *kNorm, *bq, *bk, *bv;
   orc_w wq, wk, wv, wo, wgate, wup, wdown;
-  /* Gated DeltaNet layer (src/model/forward-qwen35.js:187-207) */
+  /* Gated DeltaNet layer (src/model/forward-qwen35.js:111-132, 186-194) */
   int recurrent;
   orc_w wqkv, wz, walpha, wbeta, wout;
   const float *conv, *dtBias, *ssmA, *ssmNorm;
@@ -567,7 +567,7 @@ void orc_model_set_layer(orc_model *m, int l, const float *attnNorm, const float
   L->wdown = (orc_w){types[6], c->nEmbd, c->nFF, datas[6]};
 }
 
-/* A qwen35 layer (src/model/forward-qwen35.js:187-207). types/datas: recurrent layer [attn_qkv, attn_gate, ssm_alpha,
+/* A qwen35 layer (src/model/forward-qwen35.js:111-132, 186-194). types/datas: recurrent layer [attn_qkv, attn_gate, ssm_alpha,
  * ssm_beta, ssm_out, ffn_gate, ffn_up, ffn_down]; attention layer [attn_q, attn_k, attn_v, attn_output, -, ffn_gate,
  * ffn_up, ffn_down]. ffnNorm is post_attention_norm (the pre-FFN norm). */
 void orc_model_set_layer_hybrid(orc_model *m, int l, const float *attnNorm, const float *ffnNorm, const float *qNorm,
@@ -745,7 +745,7 @@ static void ssm_layer(orc_model *m, orc_layer *L, int ri, const float *xb, float
   mv(m, &L->wout, m->core, out);
 }
 
-/* attnLayerStep (src/model/forward-qwen35.js:73-105): gated attention; attn_q rows per head are [query | gate] */
+/* attnLayerStep (src/model/forward-qwen35.js:71-105): gated attention; attn_q rows per head are [query | gate] */
 static void gated_attn_layer(orc_model *m, orc_layer *L, int ai, int pos, const float *xb, float *out) {
   orc_cfg *c = &m->c;
   int D = c->headDim, nHead = c->nHead;

@@ -1,5 +1,5 @@
 // Causal GQA attention with the reference's arithmetic (src/model/forward.js:115-140; the gated form of
-// src/model/forward-qwen35.js:73-105 when a.gate is set), in two launches per layer:
+// src/model/forward-qwen35.js:71-105 when a.gate is set), in two launches per layer:
 //   k_attn_scores  s_t = f32(sum_i q_i K_t,i (f64, exact products) * 1/sqrt(hd)) for every position t <= pos, one
 //                  block per (64-position chunk, KV head, token): all of K streams in parallel.
 //   k_attn_av      softmax over the scores (e = exp(s - max) in f64, stored f32; p = f32(e * (1/sum e))), then

@@ -1030,7 +1030,7 @@ static zl_model *load_gguf(const char *path, const zl_model_opts *o) {
     L.attnNorm = V(p + "attn_norm.weight", c.n_embd);
     L.rec = m->hybrid && (l + 1) % c.full_attn_interval != 0;
     if (L.rec) {
-      // Gated DeltaNet layer tensors (src/model/forward-qwen35.js:117-123, 251-254)
+      // Gated DeltaNet layer tensors (src/model/forward-qwen35.js:111-132, 186-194)
       const int D = c.ssm_d_state, nV = c.ssm_dt_rank, inner = c.ssm_d_inner, convDim = 2 * c.ssm_n_group * D + inner;
       auto g4 = group({p + "attn_qkv.weight", p + "attn_gate.weight", p + "ssm_alpha.weight", p + "ssm_beta.weight"},
                       {convDim, inner, nV, nV}, c.n_embd);

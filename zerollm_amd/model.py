@@ -137,7 +137,7 @@ class HipModel:
         return r.value
 
     def truncate_plan(self, n: int):
-        """truncatePlan (src/compute/pool.js:262): (from, replay)."""
+        """truncatePlan (src/compute/pool.js:256): (from, replay)."""
         f, r = C.c_int(), C.c_int()
         call("zl_truncate_plan", self._h, int(n), C.byref(f), C.byref(r))
         return f.value, r.value
@@ -152,7 +152,7 @@ class HipModel:
         return list(buf[:n])
 
     def recurrent_state(self):
-        """getRecurrentState (src/compute/pool.js:265): (conv, ssm) float32 arrays in the reference's layout."""
+        """getRecurrentState (src/compute/pool.js:259): (conv, ssm) float32 arrays in the reference's layout."""
         c = self.cfg
         s = c["ssm"]
         n_rec = sum(c["layerIsRecurrent"])
