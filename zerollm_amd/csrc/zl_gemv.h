@@ -172,14 +172,18 @@ __device__ inline const void *recs_of(const Act &a) {
 }
 
 template <int FMT, int MT, int EPI, int DEPTH>
-__global__ __launch_bounds__(EPI == EPI_SWIGLU ? 512 : 1024) void k_gemv_tiles(const GemvArgs a) {
-  constexpr int NR = EPI == EPI_SWIGLU ? 2 : 1;
-  constexpr int WMAX = EPI == EPI_SWIGLU ? 8 : 16;  // waves per workgroup at most
-  __shared__ double red[WMAX / 2][NR * MT][64];
+__global__ __launch_bounds__(1024) void k_gemv_tiles(const GemvArgs a) {
+  constexpr int NR = EPI == EPI_SWIGLU ? 2 : 1;  // matrices per output row: gate and up for SwiGLU
+  __shared__ double red[8][MT][64];
   extern __shared__ __align__(16) uint8_t xl[];  // per token: [nsl][64] int8 values, then [nsl][32] records
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = a.nwave;  // waves of the workgroup (1, 2, 4, 8 or 16)
+  // SwiGLU: the first half of the waves computes the gate rows, the second half the up rows, each half walking the
+  // slabs as a workgroup of W / 2 waves computing one matrix would (so the sums are the same bits)
+  const int WH = NR == 2 ? W >> 1 : W;
+  const int grp = NR == 2 ? __builtin_amdgcn_readfirstlane(wave / WH) : 0;
+  const int wl = wave - grp * WH;
   const int ks = a.ks, kp = blockIdx.x, tile = blockIdx.y;  // grid: (K parts, tiles)
   // segment of the tile, selected field by field (no dynamic indexing into the argument block)
   const int si = __builtin_amdgcn_readfirstlane(
@@ -193,22 +197,20 @@ __global__ __launch_bounds__(EPI == EPI_SWIGLU ? 512 : 1024) void k_gemv_tiles(c
                                  make_rsrc(a.seg[1].m.sc, a.seg[1].nsc), make_rsrc(a.seg[1].m.dd, a.seg[1].ndd)}
                           : R0;
   const int kr = a.kr, s0 = kp * kr, s1 = min(nslab, s0 + kr), nsl = s1 - s0;
-  const int n = nsl > wave ? (nsl - wave + W - 1) / W : 0;  // this wave's slabs: s0 + wave + W i, i < n <= GT_NMAX
+  const int n = nsl > wl ? (nsl - wl + WH - 1) / WH : 0;  // this wave's slabs: s0 + wl + WH i, i < n <= GT_NMAX
   const int M = a.M;
   const uint8_t *xq = (const uint8_t *)a.act.q, *xr = (const uint8_t *)recs_of<FMT>(a.act);
   const long ldq = a.act.ld, ldr = (long)(a.act.ld >> 5) * 16;
 
-  double acc[NR][MT];
+  const Rsrc R = grp == 0 ? R0 : R1;
+  double acc[MT];
   #pragma unroll
-  for (int r = 0; r < NR; r++)
-    #pragma unroll
-    for (int t = 0; t < MT; t++) acc[r][t] = 0.0;
-  Raw<FMT> buf[DEPTH][NR];
-  auto load = [&](int i, Raw<FMT> *b) {
-    const int s = s0 + wave + W * i;
+  for (int t = 0; t < MT; t++) acc[t] = 0.0;
+  Raw<FMT> buf[DEPTH];
+  auto load = [&](int i, Raw<FMT> &b) {
+    const int s = s0 + wl + WH * i;
     const int ts = lt * nslab + s, sbi = lt * nsb + (s >> 2);
-    raw_load<FMT>(R0, ts, sbi, lane, i < n, b[0]);
-    if (NR == 2) raw_load<FMT>(R1, ts, sbi, lane, i < n, b[NR - 1]);
+    raw_load<FMT>(R, ts, sbi, lane, i < n, b);
   };
   #pragma unroll
   for (int d = 0; d < DEPTH; d++) load(d, buf[d]);
@@ -270,14 +272,13 @@ __global__ __launch_bounds__(EPI == EPI_SWIGLU ? 512 : 1024) void k_gemv_tiles(c
     for (int d = 0; d < DEPTH; d++) {
       const int i = i0 + d;
       if (i >= GT_NMAX) break;
-      Unp<FMT> u[NR];
-      #pragma unroll
-      for (int r = 0; r < NR; r++) unpack<FMT>(buf[d][r], u[r]);
+      Unp<FMT> u;
+      unpack<FMT>(buf[d], u);
       // the slot is reloaded only after it has been unpacked (the reload reuses its registers, no copies)
       __builtin_amdgcn_sched_barrier(0);
       load(i + DEPTH, buf[d]);  // past the wave's last slab: no memory access
       if (i < n) {
-        const int sl = wave + W * i;  // slab within the workgroup's range
+        const int sl = wl + WH * i;  // slab within the workgroup's range
         #pragma unroll
         for (int t = 0; t < MT; t++) {
           const int tt = MT == 1 ? 0 : min(t, M - 1);  // a short token tile repeats its last token (not stored)
@@ -288,31 +289,38 @@ __global__ __launch_bounds__(EPI == EPI_SWIGLU ? 512 : 1024) void k_gemv_tiles(c
             const uint4 a0 = xp[2 * h], a1 = xp[2 * h + 1], r = rp[h];
             const u32x8 Xh = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
             const u32x4 Rh = {r.x, r.y, r.z, r.w};
-            #pragma unroll
-            for (int rr = 0; rr < NR; rr++) acc[rr][t] = block_term<FMT>(u[rr], h, Xh, Rh, acc[rr][t]);
+            acc[t] = block_term<FMT>(u, h, Xh, Rh, acc[t]);
           }
         }
       }
     }
   }
 
-  // ---- the workgroup's sum, as a fixed tree over the waves: at each step the upper half of the remaining waves parks
+  // ---- each matrix's sum, as a fixed tree over its waves: at each step the upper half of the remaining waves parks
   // its sums in LDS and the lower half adds them (wave w + half onto wave w)
-  for (int half = W >> 1; half >= 1; half >>= 1) {
-    if (wave >= half && wave < 2 * half) {
+  for (int half = WH >> 1; half >= 1; half >>= 1) {
+    if (wl >= half && wl < 2 * half) {
       #pragma unroll
-      for (int r = 0; r < NR; r++)
-        #pragma unroll
-        for (int t = 0; t < MT; t++) red[wave - half][r * MT + t][lane] = acc[r][t];
+      for (int t = 0; t < MT; t++) red[grp * 4 + wl - half][t][lane] = acc[t];
     }
     __syncthreads();
-    if (wave < half) {
+    if (wl < half) {
       #pragma unroll
-      for (int r = 0; r < NR; r++)
-        #pragma unroll
-        for (int t = 0; t < MT; t++) acc[r][t] += red[wave][r * MT + t][lane];
+      for (int t = 0; t < MT; t++) acc[t] += red[grp * 4 + wl][t][lane];
     }
     __syncthreads();
+  }
+  double accv[NR][MT];  // wave 0: the tile's row sums of each matrix
+  #pragma unroll
+  for (int t = 0; t < MT; t++) accv[0][t] = acc[t];
+  if constexpr (NR == 2) {
+    if (grp == 1 && wl == 0) {
+      #pragma unroll
+      for (int t = 0; t < MT; t++) red[0][t][lane] = acc[t];
+    }
+    __syncthreads();
+    #pragma unroll
+    for (int t = 0; t < MT; t++) accv[NR - 1][t] = red[0][t][lane];
   }
   if (wave > 0) return;
 
@@ -325,7 +333,7 @@ __global__ __launch_bounds__(EPI == EPI_SWIGLU ? 512 : 1024) void k_gemv_tiles(c
     #pragma unroll
     for (int r = 0; r < NR; r++)
       #pragma unroll
-      for (int t = 0; t < MT; t++) __hip_atomic_store(pp + (r * MT + t) * 64 + lane, acc[r][t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int t = 0; t < MT; t++) __hip_atomic_store(pp + (r * MT + t) * 64 + lane, accv[r][t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stores are complete
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -348,7 +356,7 @@ __global__ __launch_bounds__(EPI == EPI_SWIGLU ? 512 : 1024) void k_gemv_tiles(c
         #pragma unroll
         for (int k = 1; k < KSMAX; k++)
           if (k < ks) v += pv[k];
-        acc[r][t] = v;
+        accv[r][t] = v;
       }
     if (lane == 0) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -359,7 +367,7 @@ __global__ __launch_bounds__(EPI == EPI_SWIGLU ? 512 : 1024) void k_gemv_tiles(c
     #pragma unroll
     for (int t = 0; t < MT; t++) {
       if (t >= M) break;
-      const double g = (double)(float)acc[0][t], uu = (double)(float)acc[1][t];
+      const double g = (double)(float)accv[0][t], uu = (double)(float)accv[1][t];
       const float hv = live ? (float)(g / (1.0 + exp(-g)) * uu) : 0.f;  // src/compute/ref-kernels.js:322
       if (live) a.hb[(long)t * a.ldh + row] = hv;
       if (a.qout.q) quant_block32(hv, row, a.qout, t);
@@ -370,7 +378,7 @@ __global__ __launch_bounds__(EPI == EPI_SWIGLU ? 512 : 1024) void k_gemv_tiles(c
       for (int t = 0; t < MT; t++) {
         if (t >= M) break;
         float *o = a.resid + (long)t * a.ldr + row;
-        *o = (float)((double)*o + (double)(float)acc[0][t]);
+        *o = (float)((double)*o + (double)(float)accv[0][t]);
       }
     }
   } else {
@@ -382,7 +390,7 @@ __global__ __launch_bounds__(EPI == EPI_SWIGLU ? 512 : 1024) void k_gemv_tiles(c
       #pragma unroll
       for (int t = 0; t < MT; t++) {
         if (t >= M) break;
-        const float y = (float)acc[0][t];
+        const float y = (float)accv[0][t];
         out[(long)t * ldo + row] = bias ? (float)((double)y + bv) : y;
       }
     }
@@ -402,8 +410,10 @@ inline void allow_big_lds(K kernel) {
 // Launch one chunk of at most GEMV_MAX_MT tokens: token tile MT = M (M = 7 runs as 8).
 template <int FMT, int MT>
 inline void launch_tiles_mt(const GemvArgs &a, int epi, hipStream_t st) {
-  ZL_REQUIRE(a.kr <= GT_KR_MAX && a.M <= MT && a.ks <= 8 && a.nwave >= 1 && a.nwave <= (epi == EPI_SWIGLU ? 8 : 16) &&
-                 (a.kr + a.nwave - 1) / a.nwave <= GT_NMAX && (!a.xf || (a.nwave >= 4 && a.n <= a.nslab * 64)),
+  const int wpm = epi == EPI_SWIGLU ? a.nwave / 2 : a.nwave;  // waves per matrix
+  ZL_REQUIRE(a.kr <= GT_KR_MAX && a.M <= MT && a.ks <= 8 && wpm >= 1 && a.nwave <= 16 &&
+                 (epi != EPI_SWIGLU || (a.nwave % 2 == 0 && wpm <= 8)) && (a.kr + wpm - 1) / wpm <= GT_NMAX &&
+                 (!a.xf || (a.nwave >= 4 && a.n <= a.nslab * 64)),
              ZL_ERR_ARG, "gemv: launch shape out of range");
   const dim3 grid((unsigned)a.ks, (unsigned)a.ntiles), blk((unsigned)a.nwave * 64);
   const size_t lds = (size_t)a.M * a.kr * GT_REC;  // [M][kr] records of 96 bytes

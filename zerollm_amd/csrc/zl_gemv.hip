@@ -43,14 +43,15 @@ __global__ __launch_bounds__(256) void k_gemv_float(const GemvArgs a, int rows_t
 }
 
 // Launch shape, a function of the matrix shape only (so every summation order is independent of the token count):
-// - waves per workgroup: 4 when there are enough tiles to fill the GPU with workgroups, else 16 (8 for gate/up pairs),
-//   so that a small matrix still has many slab loads in flight per CU;
+// - waves per matrix: 4 when there are enough tiles to fill the GPU with workgroups, else 16 (8 for gate/up pairs, whose
+//   workgroup runs the gate and the up rows on two halves of 8), so that a small matrix still has many slab loads in
+//   flight per CU;
 // - K parts: 1 (no cross-workgroup sum) unless a part would exceed the staged-activation limit (GT_KR_MAX slabs) or
 //   give a wave more than GT_NMAX slabs; for large single-output matrices of fewer tiles than CUs, more parts where that
 //   lowers the slabs the busiest CU streams (attn_output 4096 x 4096: 4 parts, 256 workgroups). Not for gate/up pairs:
 //   their 8-wave workgroups hold too many registers to overlap, so rounds of K parts cost more than they save.
 void gemv_shape(int ntiles, int nslab, bool swiglu, int *ks, int *nw) {
-  const int w = ntiles >= 256 ? 4 : swiglu ? 8 : 16;
+  const int w = ntiles >= 256 ? 4 : swiglu ? 8 : 16;  // waves per matrix
   int k = 1;
   while ((nslab + k - 1) / k > 96 || ((nslab + k - 1) / k + w - 1) / w > 16) k *= 2;
   // large matrices of fewer tiles than CUs: more K parts while that lowers the most slabs one CU streams (workgroups
@@ -61,7 +62,7 @@ void gemv_shape(int ntiles, int nslab, bool swiglu, int *ks, int *nw) {
       if (load(kk) < load(k)) k = kk;
   }
   *ks = k;
-  *nw = w;
+  *nw = swiglu ? 2 * w : w;  // a gate/up pair: w waves per matrix
 }
 
 void launch_gemv(const GemvArgs &a0, int epi, const float *xf, int ldx, hipStream_t st) {
