@@ -3,13 +3,14 @@
 // exact int8 block dots (v_dot4_i32_i8), f64 scale combination.
 //
 // Mapping. A wave owns one 64-row tile, one row per lane, and walks slabs (64 values) of the K range its workgroup
-// holds: wave w of the workgroup takes slabs s0 + w, s0 + w + 4, ... The weights' 16-byte planes are contiguous per
-// tile-slab, so each vector load of the wave reads 1 KB without gaps. Every lane of the wave needs the same activation
-// values: the workgroup stages its slab range of the M tokens' int8 values and block records in LDS once (those loads
-// are issued before the weight loads, so they are not queued behind them), and the loop reads them as broadcast LDS
-// loads, which complete in order and pipeline. No cross-lane reduction in the loop. The four waves' f64 sums meet in
-// LDS (added in wave order); with ks > 1 K parts per tile the parts' sums go through `part` and the last part to
-// arrive adds them in part order. Every summation order depends only on the matrix shape, never on M, so a batched
+// holds: wave w of the workgroup's W waves takes slabs s0 + w, s0 + w + W, ... The weights' 16-byte planes are
+// contiguous per tile-slab, so each vector load of the wave reads 1 KB without gaps. Every lane of the wave needs the
+// same activation values: the workgroup stages its slab range of the M tokens' int8 values and block records in LDS
+// once (those loads are issued before the weight loads, so they are not queued behind them). Per token and slab the
+// loop reads the 64 values as one 4-byte word per lane (word k on lane k of each 16-lane row) and the dots take word k
+// from lane k of the row by a DPP broadcast; the block records are broadcast LDS loads. No cross-lane reduction in the
+// loop. The waves' f64 sums meet in LDS (added in a fixed tree order); with ks > 1 K parts per tile the parts' sums go
+// through `part` and the last part to arrive adds them in part order. Every summation order depends only on the matrix shape, never on M, so a batched
 // pass gives the same bits as token-by-token passes. Raw slabs are loaded DEPTH slabs ahead of the one computed.
 #pragma once
 #include "zl_kernels.h"
@@ -138,28 +139,70 @@ __device__ inline double dbl(uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(double, (unsigned long long)lo | ((unsigned long long)hi << 32));
 }
 
-// acc + the term of block h (values 32h..32h+31) of the slab for one token. X: the token's 32 int8 values of the
-// block (uniform); R: the block's record (uniform). In the reference's arithmetic up to where f64 rounds:
+// The 16 int8 dots of one token's slab, in accumulation chains (c[j] += dot4(activation word k, w[k]) for the words k
+// of chain j, back to back). The activation words are spread over each 16-lane row of the wave (lane k of every row
+// holds word k), and each dot takes its word from lane k of the row by a DPP row broadcast, so the wave reads a token's
+// slab from LDS once, 4 bytes per lane, instead of every lane reading all 64 bytes. Wait states: a DPP instruction
+// needs two after a VALU write of a register it reads (the leading s_nop covers writes before the block), and a VALU
+// read of a dot's result needs two after the dot (measured on gfx950: with one, the last dot's sum is not yet there;
+// the trailing s_nop). A dot reading the previous dot's sum as its accumulator needs none.
+//   ORDER 0 (32-value blocks):           c0 words 0-7, c1 words 8-15 (c2, c3 unused)
+//   ORDER 1 (16-value groups, Q6_K):     c0 words 0-3, c1 4-7, c2 8-11, c3 12-15
+#define ZL_DOT(c, k) "v_dot4c_i32_i8_dpp %" #c ", %[x], %[w" #k "] row_newbcast:" #k " row_mask:0xf bank_mask:0xf\n\t"
+#define ZL_WORDS                                                                                                      \
+  [w0] "v"(w[0]), [w1] "v"(w[1]), [w2] "v"(w[2]), [w3] "v"(w[3]), [w4] "v"(w[4]), [w5] "v"(w[5]), [w6] "v"(w[6]), \
+      [w7] "v"(w[7]), [w8] "v"(w[8]), [w9] "v"(w[9]), [w10] "v"(w[10]), [w11] "v"(w[11]), [w12] "v"(w[12]),       \
+      [w13] "v"(w[13]), [w14] "v"(w[14]), [w15] "v"(w[15]), [x] "v"(xw)
+template <int ORDER>
+__device__ inline void slab_dots(uint32_t xw, const uint32_t *w, int c[4]) {
+  if constexpr (ORDER == 0) {
+    asm("s_nop 1\n\t"
+        ZL_DOT(0, 0) ZL_DOT(0, 1) ZL_DOT(0, 2) ZL_DOT(0, 3) ZL_DOT(0, 4) ZL_DOT(0, 5) ZL_DOT(0, 6) ZL_DOT(0, 7)
+        ZL_DOT(1, 8) ZL_DOT(1, 9) ZL_DOT(1, 10) ZL_DOT(1, 11) ZL_DOT(1, 12) ZL_DOT(1, 13) ZL_DOT(1, 14) ZL_DOT(1, 15)
+        "s_nop 1"
+        : "+v"(c[0]), "+v"(c[1])
+        : ZL_WORDS);
+  } else {
+    asm("s_nop 1\n\t"
+        ZL_DOT(0, 0) ZL_DOT(0, 1) ZL_DOT(0, 2) ZL_DOT(0, 3) ZL_DOT(1, 4) ZL_DOT(1, 5) ZL_DOT(1, 6) ZL_DOT(1, 7)
+        ZL_DOT(2, 8) ZL_DOT(2, 9) ZL_DOT(2, 10) ZL_DOT(2, 11) ZL_DOT(3, 12) ZL_DOT(3, 13) ZL_DOT(3, 14) ZL_DOT(3, 15)
+        "s_nop 1"
+        : "+v"(c[0]), "+v"(c[1]), "+v"(c[2]), "+v"(c[3])
+        : ZL_WORDS);
+  }
+}
+#undef ZL_DOT
+#undef ZL_WORDS
+
+// acc + the terms of the slab's two 32-value blocks (block 0, then block 1) for one token. xw: the token's 64 int8
+// values of the slab, word k on lane k of every 16-lane row; R0, R1: the blocks' records (uniform). In the reference's
+// arithmetic up to where f64 rounds:
 //   Q8_0 (s*d)*xd;  Q4_0/Q5_0 ((s - 8|16 sum) * d) * xd;  Q4_K/Q5_K xd*(d*sc*s - dmin*mn*sum);
 //   Q6_K per 16-group (d*scale*(s - 32 sum)) * xd.  The products before the last one are exact; the last multiply
-//   and the accumulation are one fma.
+//   and the accumulation are one fma. The integer dots are exact in any order.
 template <int FMT>
-__device__ inline double block_term(const Unp<FMT> &u, int h, const u32x8 &X, const u32x4 &R, double acc) {
-  const double xd = dbl(R[0], R[1]);
+__device__ inline double slab_terms(const Unp<FMT> &u, uint32_t xw, const u32x4 &R0, const u32x4 &R1, double acc) {
+  const double xd0 = dbl(R0[0], R0[1]), xd1 = dbl(R1[0], R1[1]);
   if constexpr (FMT == T_Q6_K) {
-    int g0 = -(int)R[2], g1 = -(int)R[3];
-    #pragma unroll
-    for (int i = 0; i < 4; i++) g0 = sdot4((int)u.w[8 * h + i], (int)X[i], g0);
-    #pragma unroll
-    for (int i = 4; i < 8; i++) g1 = sdot4((int)u.w[8 * h + i], (int)X[i], g1);
-    acc = fma(u.fa[h] * (double)g0, xd, acc);
-    return fma(u.fb[h] * (double)g1, xd, acc);
+    int c[4] = {-(int)R0[2], -(int)R0[3], -(int)R1[2], -(int)R1[3]};
+    slab_dots<1>(xw, u.w, c);
+    acc = fma(u.fa[0] * (double)c[0], xd0, acc);
+    acc = fma(u.fb[0] * (double)c[1], xd0, acc);
+    acc = fma(u.fa[1] * (double)c[2], xd1, acc);
+    return fma(u.fb[1] * (double)c[3], xd1, acc);
   } else {
-    int lo = (FMT == T_Q4_0 || FMT == T_Q5_0) ? -(int)R[FMT == T_Q4_0 ? 2 : 3] : 0;
-    #pragma unroll
-    for (int i = 0; i < 8; i++) lo = sdot4((int)u.w[8 * h + i], (int)X[i], lo);
-    if constexpr (FMT == T_Q4_K || FMT == T_Q5_K) return fma(xd, fma(u.fa[h], (double)lo, -(u.fb[h] * dbl(R[2], R[3]))), acc);
-    else return fma((double)lo * u.fa[h], xd, acc);
+    constexpr int CI = FMT == T_Q4_0 ? 2 : 3;  // Q4_0 / Q5_0: the block starts at -8 | -16 x its activation sum
+    const bool off = FMT == T_Q4_0 || FMT == T_Q5_0;
+    int c[4] = {off ? -(int)R0[CI] : 0, off ? -(int)R1[CI] : 0, 0, 0};
+    slab_dots<0>(xw, u.w, c);
+    const int lo0 = c[0], lo1 = c[1];
+    if constexpr (FMT == T_Q4_K || FMT == T_Q5_K) {
+      acc = fma(xd0, fma(u.fa[0], (double)lo0, -(u.fb[0] * dbl(R0[2], R0[3]))), acc);
+      return fma(xd1, fma(u.fa[1], (double)lo1, -(u.fb[1] * dbl(R1[2], R1[3]))), acc);
+    } else {
+      acc = fma((double)lo0 * u.fa[0], xd0, acc);
+      return fma((double)lo1 * u.fa[1], xd1, acc);
+    }
   }
 }
 
@@ -283,14 +326,10 @@ __global__ __launch_bounds__(1024) void k_gemv_tiles(const GemvArgs a) {
         for (int t = 0; t < MT; t++) {
           const int tt = MT == 1 ? 0 : min(t, M - 1);  // a short token tile repeats its last token (not stored)
           const uint8_t *tb = xl + tt * nsl * GT_REC;
-          const uint4 *xp = (const uint4 *)(tb + sl * 64), *rp = (const uint4 *)(tb + nsl * 64 + sl * 32);
-          #pragma unroll
-          for (int h = 0; h < 2; h++) {
-            const uint4 a0 = xp[2 * h], a1 = xp[2 * h + 1], r = rp[h];
-            const u32x8 Xh = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-            const u32x4 Rh = {r.x, r.y, r.z, r.w};
-            acc[t] = block_term<FMT>(u, h, Xh, Rh, acc[t]);
-          }
+          const uint32_t xw = ((const uint32_t *)(tb + sl * 64))[lane & 15];
+          const uint4 *rp = (const uint4 *)(tb + nsl * 64 + sl * 32);
+          const uint4 r0 = rp[0], r1 = rp[1];
+          acc[t] = slab_terms<FMT>(u, xw, u32x4{r0.x, r0.y, r0.z, r0.w}, u32x4{r1.x, r1.y, r1.z, r1.w}, acc[t]);
         }
       }
     }
