@@ -217,8 +217,9 @@ __device__ inline const void *recs_of(const Act &a) {
 template <int FMT, int MT, int EPI, int DEPTH>
 __global__ __launch_bounds__(1024) void k_gemv_tiles(const GemvArgs a) {
   constexpr int NR = EPI == EPI_SWIGLU ? 2 : 1;  // matrices per output row: gate and up for SwiGLU
-  __shared__ double red[8][MT][64];
-  extern __shared__ __align__(16) uint8_t xl[];  // per token: [nsl][64] int8 values, then [nsl][32] records
+  // staged activations, per token: [nsl][64] int8 values, then [nsl][32] records; after the slab loop the same bytes
+  // hold the waves' sums for the reduction ([W][MT][64] doubles)
+  extern __shared__ __align__(16) uint8_t xl[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = a.nwave;  // waves of the workgroup (1, 2, 4, 8 or 16)
@@ -262,10 +263,10 @@ __global__ __launch_bounds__(1024) void k_gemv_tiles(const GemvArgs a) {
     // slab range of every token into LDS in the staged layout
     __shared__ double ssr[4][4];
     __shared__ double scl[GEMV_MAX_MT];
-    const int groups = W >> 2 > 0 ? W >> 2 : 1, g = wave >> 2;
+    const int groups = W >> 2, g = wave >> 2;
     for (int t0 = 0; t0 < M; t0 += groups) {
       const int t = t0 + g;
-      const bool act_ = a.nw && g < groups && t < M && W >= 4;
+      const bool act_ = t < M;
       double sc = 1.0;
       if (a.nw) {
         // rms_scale256 synchronises the block: every thread takes part, idle groups with a dummy row
@@ -335,102 +336,80 @@ __global__ __launch_bounds__(1024) void k_gemv_tiles(const GemvArgs a) {
     }
   }
 
-  // ---- each matrix's sum, as a fixed tree over its waves: at each step the upper half of the remaining waves parks
-  // its sums in LDS and the lower half adds them (wave w + half onto wave w)
-  for (int half = WH >> 1; half >= 1; half >>= 1) {
-    if (wl >= half && wl < 2 * half) {
-      #pragma unroll
-      for (int t = 0; t < MT; t++) red[grp * 4 + wl - half][t][lane] = acc[t];
-    }
-    __syncthreads();
-    if (wl < half) {
-      #pragma unroll
-      for (int t = 0; t < MT; t++) acc[t] += red[grp * 4 + wl][t][lane];
-    }
-    __syncthreads();
-  }
-  double accv[NR][MT];  // wave 0: the tile's row sums of each matrix
+  // ---- each matrix's sum over its WH waves in the order of a halving tree (at each level wave w + half is added onto
+  // wave w): every wave parks its sums in LDS once, then the wave of token t adds that token's sums in that order
+  __syncthreads();  // every wave is past its last read of the staged activations, which the sums overwrite
+  double *red = (double *)xl;
   #pragma unroll
-  for (int t = 0; t < MT; t++) accv[0][t] = acc[t];
-  if constexpr (NR == 2) {
-    if (grp == 1 && wl == 0) {
-      #pragma unroll
-      for (int t = 0; t < MT; t++) red[0][t][lane] = acc[t];
-    }
-    __syncthreads();
+  for (int t = 0; t < MT; t++) red[(wave * MT + t) * 64 + lane] = acc[t];
+  __syncthreads();
+  auto tree = [&](int r, int t) {
+    double v[16];
     #pragma unroll
-    for (int t = 0; t < MT; t++) accv[NR - 1][t] = red[0][t][lane];
-  }
-  if (wave > 0) return;
+    for (int w = 0; w < 16; w++) v[w] = red[((r * WH + min(w, WH - 1)) * MT + t) * 64 + lane];  // all loads issued at once
+    #pragma unroll
+    for (int half = 8; half >= 1; half >>= 1)
+      if (2 * half <= WH) {
+        #pragma unroll
+        for (int w = 0; w < half; w++) v[w] = v[w] + v[w + half];
+      }
+    return v[0];
+  };
 
   // ---- K parts: the last part of the tile to arrive adds all parts' sums in part order. Partial sums are written and
   // read with device-scope (agent) atomic accesses, which are coherent across the XCDs' L2 caches without cache-wide
-  // fences; the writer waits for its stores to complete before it counts itself in.
+  // fences; each wave waits for its stores to complete before the workgroup counts itself in.
+  constexpr int PW = NR * MT * 64;  // doubles per part
   if (ks > 1) {
-    constexpr int PW = NR * MT * 64;  // doubles per part
+    __shared__ uint32_t last;
     double *pp = a.part + ((long)tile * ks + kp) * PW;
-    #pragma unroll
-    for (int r = 0; r < NR; r++)
+    for (int t = wave; t < M; t += W) {
       #pragma unroll
-      for (int t = 0; t < MT; t++) __hip_atomic_store(pp + (r * MT + t) * 64 + lane, accv[r][t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int r = 0; r < NR; r++) __hip_atomic_store(pp + (r * MT + t) * 64 + lane, tree(r, t), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stores are complete
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores are complete
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    uint32_t old = 0;
-    if (lane == 0) old = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    old = __shfl(old, 0);
-    if (old != (uint32_t)(ks - 1)) return;
-    const double *pt = a.part + (long)tile * ks * PW;
-    constexpr int KSMAX = 8;  // the parts' loads of one sum are issued together
-    #pragma unroll
-    for (int r = 0; r < NR; r++)
-      #pragma unroll
-      for (int t = 0; t < MT; t++) {
-        double pv[KSMAX];
-        #pragma unroll
-        for (int k = 0; k < KSMAX; k++)
-          pv[k] = __hip_atomic_load(pt + (long)min(k, ks - 1) * PW + (r * MT + t) * 64 + lane, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
-        double v = pv[0];
-        #pragma unroll
-        for (int k = 1; k < KSMAX; k++)
-          if (k < ks) v += pv[k];
-        accv[r][t] = v;
-      }
-    if (lane == 0) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (threadIdx.x == 0) last = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(ks - 1);
+    __syncthreads();
+    if (!last) return;
+    if (threadIdx.x == 0) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  // ---- epilogue: lane = row of the tile
+  auto total = [&](int r, int t) {
+    if (ks == 1) return tree(r, t);
+    const double *pt = a.part + (long)tile * ks * PW + (r * MT + t) * 64 + lane;
+    constexpr int KSMAX = 8;  // the parts' loads of one sum are issued together
+    double pv[KSMAX];
+    #pragma unroll
+    for (int k = 0; k < KSMAX; k++) pv[k] = __hip_atomic_load(pt + (long)min(k, ks - 1) * PW, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    double v = pv[0];
+    #pragma unroll
+    for (int k = 1; k < KSMAX; k++)
+      if (k < ks) v += pv[k];
+    return v;
+  };
+
+  // ---- epilogue of token t on wave t (t, t + W, ...): lane = row of the tile
   const int row = lt * 64 + lane;
   const bool live = row < rows;
-  if constexpr (EPI == EPI_SWIGLU) {
-    #pragma unroll
-    for (int t = 0; t < MT; t++) {
-      if (t >= M) break;
-      const double g = (double)(float)accv[0][t], uu = (double)(float)accv[1][t];
+  for (int t = wave; t < M; t += W) {
+    if constexpr (EPI == EPI_SWIGLU) {
+      const double g = (double)(float)total(0, t), uu = (double)(float)total(1, t);
       const float hv = live ? (float)(g / (1.0 + exp(-g)) * uu) : 0.f;  // src/compute/ref-kernels.js:322
       if (live) a.hb[(long)t * a.ldh + row] = hv;
       if (a.qout.q) quant_block32(hv, row, a.qout, t);
-    }
-  } else if constexpr (EPI == EPI_RESID) {
-    if (live) {
-      #pragma unroll
-      for (int t = 0; t < MT; t++) {
-        if (t >= M) break;
+    } else if constexpr (EPI == EPI_RESID) {
+      const double y = (double)(float)total(0, t);
+      if (live) {
         float *o = a.resid + (long)t * a.ldr + row;
-        *o = (float)((double)*o + (double)(float)accv[0][t]);
+        *o = (float)((double)*o + y);
       }
-    }
-  } else {
-    float *out = ZL_SEG(out);
-    const float *bias = ZL_SEG(bias);
-    const int ldo = ZL_SEG(ldo);
-    if (live) {
-      const double bv = bias ? (double)bias[row] : 0.0;
-      #pragma unroll
-      for (int t = 0; t < MT; t++) {
-        if (t >= M) break;
-        const float y = (float)accv[0][t];
-        out[(long)t * ldo + row] = bias ? (float)((double)y + bv) : y;
+    } else {
+      const float y = (float)total(0, t);
+      if (live) {
+        const float *bias = ZL_SEG(bias);
+        ZL_SEG(out)[(long)t * ZL_SEG(ldo) + row] = bias ? (float)((double)y + (double)bias[row]) : y;
       }
     }
   }
@@ -455,7 +434,8 @@ inline void launch_tiles_mt(const GemvArgs &a, int epi, hipStream_t st) {
                  (!a.xf || (a.nwave >= 4 && a.n <= a.nslab * 64)),
              ZL_ERR_ARG, "gemv: launch shape out of range");
   const dim3 grid((unsigned)a.ks, (unsigned)a.ntiles), blk((unsigned)a.nwave * 64);
-  const size_t lds = (size_t)a.M * a.kr * GT_REC;  // [M][kr] records of 96 bytes
+  // [M][kr] staged records of 96 bytes, then (same bytes) the waves' sums
+  const size_t lds = std::max((size_t)a.M * a.kr * GT_REC, (size_t)a.nwave * MT * 64 * 8);
   if (epi == EPI_STORE) {
     allow_big_lds(k_gemv_tiles<FMT, MT, EPI_STORE, 4>);
     hipLaunchKernelGGL((k_gemv_tiles<FMT, MT, EPI_STORE, 4>), grid, blk, lds, st, a);
