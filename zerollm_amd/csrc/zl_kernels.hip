@@ -174,13 +174,28 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x,
   __shared__ double red[4];
   const int b = blockIdx.y, tid = threadIdx.x;
   const float *xr = x + (long)(row0 + b) * ldx;
-  const double s = w ? rms_scale256(xr, n, eps, tid, red) : 1.0;
+  // the chunk's values and weights are requested before the sum of squares, which does not wait for them
+  constexpr int PER = NQ_CHUNK / 256;
   const int c0 = blockIdx.x * NQ_CHUNK, c1 = min(npad, c0 + NQ_CHUNK);
-  for (int i = c0 + tid; i < c1; i += 256) {
-    float v = 0.f;
-    if (i < n) v = w ? (float)((double)xr[i] * s * (double)w[i]) : xr[i];
-    if (act.f) act.f[(long)b * act.ld + i] = v;
-    quant_block32(v, i, act, b);
+  float xv[PER], wv[PER];
+  #pragma unroll
+  for (int k = 0; k < PER; k++) {
+    const int i = c0 + tid + 256 * k;
+    xv[k] = i < n ? xr[i] : 0.f;
+    wv[k] = (w && i < n) ? w[i] : 0.f;
+  }
+  const double s = w ? rms_scale256(xr, n, eps, tid, red) : 1.0;
+  #pragma unroll
+  for (int k = 0; k < PER; k++) {
+    const int i = c0 + tid + 256 * k;
+    // c1 - c0 is a multiple of 64: a wave's 64 values are all in the chunk or all past it (quant_block32 works on
+    // 32-lane groups)
+    if (i < c1) {
+      float v = 0.f;
+      if (i < n) v = w ? (float)((double)xv[k] * s * (double)wv[k]) : xv[k];
+      if (act.f) act.f[(long)b * act.ld + i] = v;
+      quant_block32(v, i, act, b);
+    }
   }
 }
 
