@@ -56,7 +56,7 @@ void gemv_shape(int ntiles, int nslab, bool swiglu, int *ks, int *nw) {
   while ((nslab + k - 1) / k > 96 || ((nslab + k - 1) / k + w - 1) / w > 16) k *= 2;
   // large matrices of fewer tiles than CUs: more K parts while that lowers the most slabs one CU streams (workgroups
   // run in rounds of 256), keeping at least one slab per wave
-  if (!swiglu && ntiles < 256 && (long)ntiles * nslab >= 2048) {
+  if (!swiglu && ntiles < 256 && (long)ntiles * nslab >= 1024) {
     auto load = [&](int kk) { return (long)((ntiles * kk + 255) / 256) * ((nslab + kk - 1) / kk); };
     for (int kk = k * 2; kk <= 8 && (nslab + kk - 1) / kk >= w; kk *= 2)
       if (load(kk) < load(k)) k = kk;
