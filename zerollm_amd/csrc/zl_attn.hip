@@ -59,10 +59,6 @@ __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
   __shared__ float kf[8 * HD];           // rotated keys of the pass, a batch of up to 8 positions at a time (f32)
   extern __shared__ __align__(16) uint8_t kn[];  // the chunk's new keys in cache format, from position n0: [min(P, B)][HD]
   const int b = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const Step *st = a.step;
-  if (b >= st->B) return;
-  const int pos0 = st->pos0, npos = pos0 + b + 1;
-  if (blockIdx.x * P >= npos) return;
   const int group = a.nHead / a.nHeadKv, hg = a.hpb;
   const int h0 = blockIdx.y * hg;        // first query head of this block
   const int kvh = h0 / group;
@@ -72,20 +68,35 @@ __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
   float *srow = a.scores + ((long)b * a.nHead + h0) * a.sld;
   const int part = tid % LP, sub = tid / LP;
   uint4 u[R];
-  auto fetch = [&](int c0) {  // cached keys only: positions of the pass are filled in from kn
+  // cached keys (positions of the pass are filled in from kn); the first chunk's keys and the query heads are requested
+  // before the pass's step record arrives, so the positions past the cache's valid ones are read too (and unused)
+  auto fetch = [&](int c0, int lim) {
     #pragma unroll
     for (int r = 0; r < R; r++) {
       const int t = c0 + r * PPI + sub;
-      u[r] = t < pos0 ? *(const uint4 *)(kbase + ((long)t * HD + part * EPL) * VB) : make_uint4(0, 0, 0, 0);
+      u[r] = t < lim ? *(const uint4 *)(kbase + ((long)t * HD + part * EPL) * VB) : make_uint4(0, 0, 0, 0);
     }
   };
-  fetch(blockIdx.x * P);  // the first chunk's keys are in flight while q is prepared
-  for (int i = tid; i < hg * HD; i += 256) qs[i] = a.q[(long)b * a.ldq + (long)(h0 + i / HD) * a.qhs + i % HD];
+  fetch(blockIdx.x * P, a.ctx);
+  constexpr int QV = 8 * HD / 256;  // query values per thread (at most 8 heads of HD values per block)
+  float qv[QV];
+  #pragma unroll
+  for (int k = 0; k < QV; k++) {
+    const int i = tid + 256 * k;
+    qv[k] = i < hg * HD ? a.q[(long)b * a.ldq + (long)(h0 + i / HD) * a.qhs + i % HD] : 0.f;
+  }
+  const Step *st = a.step;
+  if (b >= st->B) return;
+  const int pos0 = st->pos0, npos = pos0 + b + 1;
+  if (blockIdx.x * P >= npos) return;
+  #pragma unroll
+  for (int k = 0; k < QV; k++)
+    if (tid + 256 * k < hg * HD) qs[tid + 256 * k] = qv[k];
   __syncthreads();
   for (int h = wave; h < hg; h += 4) norm_rope<HD>(qs + h * HD, a.qNorm, a.eps, a.nRot, a.neox, a.cosT, a.sinT, npos - 1, lane);
   __syncthreads();
   for (int c0 = blockIdx.x * P; c0 < npos; c0 += gridDim.x * P) {
-    if (c0 != blockIdx.x * P) fetch(c0);
+    if (c0 != blockIdx.x * P) fetch(c0, pos0);
     // the pass's keys in this chunk: positions [n0, n1), tokens [n0 - pos0, n1 - pos0)
     const int n0 = max(c0, pos0), n1 = min(c0 + P, npos);
     for (int g0 = n0; g0 < n1; g0 += 8) {
@@ -158,22 +169,21 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
   constexpr int PPR = AV_ROW / 16;       // pieces per row
   constexpr int LPT = AV_DIMS * PPR / 256;   // 16-byte loads per thread per chunk
   const int slice = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const Step *st = a.step;
-  if (b >= st->B) return;
-  const int npos = st->pos0 + b + 1;
   const int hd = a.hd, kvh = h / (a.nHead / a.nHeadKv);
   float *p = (float *)lds;                                // [ctx rounded up to AV_UNIT] probabilities
   uint8_t *vbuf = lds + (size_t)((a.ctx + AV_UNIT - 1) / AV_UNIT * AV_UNIT) * 4;  // [2][AV_DIMS][AV_PITCH] staged V rows
   __shared__ double redd[4];
   __shared__ float redf[4];
   const uint8_t *vbase = (const uint8_t *)a.vcache + (((long)a.layer * a.nHeadKv + kvh) * hd + (long)slice * AV_DIMS) * a.vstride * VB;
-  const int nch = (npos + CT - 1) / CT;
   uint4 pre[LPT];
-  auto fetch = [&](int c) {
+  int npos = 0;
+  // V pieces of chunk c below `lim` positions (inside the cache row); the first chunk and the first 1024 scores are
+  // requested before the pass's step record arrives, and the pieces at or past the last position are zeroed after it
+  auto fetch = [&](int c, int lim) {
     #pragma unroll
     for (int k = 0; k < LPT; k++) {
       const int idx = k * 256 + tid, dim = idx / PPR, t = c * CT + (idx % PPR) * EPP;
-      pre[k] = t < npos ? *(const uint4 *)(vbase + ((long)dim * a.vstride + t) * VB) : make_uint4(0, 0, 0, 0);
+      pre[k] = t < lim ? *(const uint4 *)(vbase + ((long)dim * a.vstride + t) * VB) : make_uint4(0, 0, 0, 0);
     }
   };
   auto store = [&](int buf) {
@@ -183,14 +193,36 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
       *(uint4 *)(vbuf + buf * AV_CHUNK + (idx / PPR) * AV_PITCH + (idx % PPR) * 16) = pre[k];
     }
   };
-  fetch(0);  // the first V chunk is in flight during the softmax
-  // ---- softmax (src/compute/ref-kernels.js:313-320)
+  fetch(0, a.ctx);
   const float *srow = a.scores + ((long)b * a.nHead + h) * a.sld;
+  float v0[4];
+  #pragma unroll
+  for (int k = 0; k < 4; k++) { const int t = k * 256 + tid; v0[k] = t < a.ctx ? srow[t] : -INFINITY; }
+  const Step *st = a.step;
+  if (b >= st->B) return;
+  npos = st->pos0 + b + 1;
+  const int nch = (npos + CT - 1) / CT;
+  #pragma unroll
+  for (int k = 0; k < LPT; k++) {  // the first chunk's pieces from the last position on: zeros, as in later chunks
+    const int t = ((k * 256 + tid) % PPR) * EPP;
+    if (t >= npos) pre[k] = make_uint4(0, 0, 0, 0);
+    else if (t + EPP > npos) {
+      uint32_t w[4] = {pre[k].x, pre[k].y, pre[k].z, pre[k].w};
+      #pragma unroll
+      for (int e = 0; e < EPP; e++)
+        if (t + e >= npos) {
+          if (F16KV) w[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
+          else w[e] = 0u;
+        }
+      pre[k] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+  // ---- softmax (src/compute/ref-kernels.js:313-320)
   float mx = -INFINITY;
   for (int t0 = 0; t0 < npos; t0 += 1024) {
     float v[4];
     #pragma unroll
-    for (int k = 0; k < 4; k++) { const int t = t0 + k * 256 + tid; v[k] = t < npos ? srow[t] : -INFINITY; }
+    for (int k = 0; k < 4; k++) { const int t = t0 + k * 256 + tid; v[k] = t >= npos ? -INFINITY : t0 == 0 ? v0[k] : srow[t]; }
     #pragma unroll
     for (int k = 0; k < 4; k++) { const int t = t0 + k * 256 + tid; if (t < npos) p[t] = v[k]; mx = fmaxf(mx, v[k]); }
   }
@@ -216,7 +248,7 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
   const bool chainLane = wave == 0 && lane < AV_DIMS;
   float o = 0.f;
   for (int c = 0; c < nch; c++) {
-    if (c + 1 < nch) fetch(c + 1);
+    if (c + 1 < nch) fetch(c + 1, npos);
     if (chainLane) {
       // units of UNIT positions: all of a unit's LDS reads are issued first, then its fma steps run back to back
       // (each step waits ~9 cycles on the previous one, so the reads of a unit cost one LDS latency per unit).
