@@ -52,6 +52,7 @@ struct DevMat {
   int type = -1, rows = 0, cols = 0, nslab = 0;
   uint8_t *qs = nullptr, *qx = nullptr, *sc = nullptr;
   uint16_t *dd = nullptr;
+  uint8_t *fq = nullptr;  // Q4_K: the 4-bit plane again, in matrix-core operand order (same size as qs)
 };
 
 __host__ __device__ inline int qs_bytes(int t) { return t == T_Q8_0 ? 64 : 32; }

@@ -97,6 +97,11 @@ void launch_gemv(const GemvArgs &a0, int epi, const float *xf, int ldx, hipStrea
       if (b.qout.q) b.qout = act_rows(a0.qout, t0);
       b.xrow0 += t0;  // fused prologue: the chunk's own input rows
     }
+    if (gemv_mfma_ok(b)) {  // Q4_K at 2..8 tokens: the int8 dots on the matrix cores, same results
+      launch_gemv_mfma(b, epi, st);
+      ZL_HIP(hipGetLastError());
+      continue;
+    }
     switch (fmt) {
       case T_Q8_0: launch_gemv_fmt<T_Q8_0>(b, epi, st); break;
       case T_Q4_0: launch_gemv_fmt<T_Q4_0>(b, epi, st); break;

@@ -1,0 +1,240 @@
+// Q4_K GEMV for 2..8 tokens with the int8 block dots on the matrix cores (v_mfma_i32_16x16x64_i8), the same results
+// bit for bit as k_gemv_tiles (zl_gemv.h): the same slabs per wave, the same f64 block terms per (row, token) in the
+// same order (slab by slab, block 0 then block 1, in the reference's arithmetic, src/compute/ref-kernels.js:210-240),
+// the same halving-tree reduction over the waves and the same K parts.
+//
+// One MFMA multiplies an activation fragment A (16 rows rho = 2 t + b: token t's values of the slab's 32-value block b,
+// zero elsewhere in the slab) by a weight fragment B (16 rows of the tile, the slab's 64 values) into D[rho][row]: the
+// integer dot of every (token, block) with every row at once. Lane l supplies A row l mod 16 and B row l mod 16 for the
+// value quarter l / 16 (16 bytes each), and receives D[4 (l / 16) + v][l mod 16], v = 0..3, i.e. tokens 2 (l / 16) and
+// 2 (l / 16) + 1, both blocks (measured on gfx950). A tile-slab is four MFMAs (row groups j = 0..3). The weights come
+// from a second copy of the matrix's 4-bit plane in that operand order (DevMat::fq: per tile-slab, half h holds row
+// groups 2h and 2h + 1; lane L = n + 16 g of a half holds 8 bytes per group: the values 16 g .. 16 g + 15 of row
+// 16 j + n, value e and e + 4 in the low and high nibble of byte e of each 4-byte word, so two masks and a shift give
+// the operand's 16 bytes in value order). The scale codes and super-block scales are read from the row-layout planes,
+// one row per lane as in k_gemv_tiles; each lane forms its row's four f64 factors once per slab and parks them in LDS,
+// where the lanes of the other row groups read them.
+#include "zl_gemv.h"
+
+namespace zl {
+
+constexpr int MF_SLOTS = 8;  // sums per lane: 4 row groups x 2 tokens
+
+template <int EPI>
+__global__ __launch_bounds__(1024) void k_gemv_mfma(const GemvArgs a) {
+  constexpr int NR = EPI == EPI_SWIGLU ? 2 : 1;
+  constexpr int FMT = T_Q4_K, DEPTH = 4;
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  // staged activations as in k_gemv_tiles; after the slab loop the same bytes hold the waves' sums ([W][8][64])
+  extern __shared__ __align__(16) uint8_t xl[];
+  __shared__ __align__(16) double fac[16][64][4];  // per wave: fa0, fa1, fb0, fb1 of the tile's rows for one slab
+  const int lane = threadIdx.x & 63, n16 = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = a.nwave;
+  const int WH = NR == 2 ? W >> 1 : W;
+  const int grp = NR == 2 ? __builtin_amdgcn_readfirstlane(wave / WH) : 0;
+  const int wl = wave - grp * WH;
+  const int ks = a.ks, kp = blockIdx.x, tile = blockIdx.y;
+  const int si = __builtin_amdgcn_readfirstlane(
+      EPI == EPI_SWIGLU ? 0 : (a.nseg > 2 && tile >= a.seg[2].tile0) ? 2 : (a.nseg > 1 && tile >= a.seg[1].tile0) ? 1 : 0);
+#define ZL_SEG(f) (si == 0 ? a.seg[0].f : si == 1 ? a.seg[1].f : a.seg[2].f)
+  const int lt = tile - ZL_SEG(tile0), rows = ZL_SEG(rows);
+  const int nslab = a.nslab, nsb = nslab >> 2;
+  // the fragment plane takes the place of the row-layout 4-bit plane (same size and per-tile-slab offsets)
+  const Rsrc R0 = {make_rsrc(ZL_SEG(m.fq), ZL_SEG(nqs)), make_rsrc(nullptr, 0), make_rsrc(ZL_SEG(m.sc), ZL_SEG(nsc)),
+                   make_rsrc(ZL_SEG(m.dd), ZL_SEG(ndd))};
+  const Rsrc R1 = NR == 2 ? Rsrc{make_rsrc(a.seg[1].m.fq, a.seg[1].nqs), make_rsrc(nullptr, 0),
+                                 make_rsrc(a.seg[1].m.sc, a.seg[1].nsc), make_rsrc(a.seg[1].m.dd, a.seg[1].ndd)}
+                          : R0;
+  const int kr = a.kr, s0 = kp * kr, s1 = min(nslab, s0 + kr), nsl = s1 - s0;
+  const int n = nsl > wl ? (nsl - wl + WH - 1) / WH : 0;
+  const int M = a.M;
+  const uint8_t *xq = (const uint8_t *)a.act.q, *xr = (const uint8_t *)a.act.ra;
+  const long ldq = a.act.ld, ldr = (long)(a.act.ld >> 5) * 16;
+
+  const Rsrc R = grp == 0 ? R0 : R1;
+  double acc[4][2];
+  #pragma unroll
+  for (int j = 0; j < 4; j++) acc[j][0] = acc[j][1] = 0.0;
+  Raw<FMT> buf[DEPTH];
+  auto load = [&](int i, Raw<FMT> &b) {
+    const int s = s0 + wl + WH * i;
+    const int ts = lt * nslab + s, sbi = lt * nsb + (s >> 2);
+    raw_load<FMT>(R, ts, sbi, lane, i < n, b);
+  };
+  #pragma unroll
+  for (int d = 0; d < DEPTH; d++) load(d, buf[d]);
+  {
+    // ---- stage the activations of the workgroup's slab range in LDS (as k_gemv_tiles does)
+    const int xb = nsl * 64, rb = nsl * 32, xc = (xb + 1023) >> 10, rc = (rb + 1023) >> 10, per = xc + rc;
+    for (int c = wave; c < M * per; c += W) {
+      const int t = c / per, k = c - t * per;
+      const bool isx = k < xc;
+      const int kk = isx ? k : k - xc, off = kk * 1024 + lane * 16;
+      const uint8_t *src = (isx ? xq + t * ldq + s0 * 64 : xr + t * ldr + s0 * 32) + off;
+      uint8_t *dst = xl + t * nsl * GT_REC + (isx ? 0 : xb) + kk * 1024;
+      if (off < (isx ? xb : rb))
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                         (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the staged bytes are in LDS
+  __syncthreads();
+  // A-fragment row rho = n16 of this lane: token n16 / 2, block n16 & 1; its quarter g holds values of that block
+  const int at = n16 >> 1;
+  const bool avalid = at < M && (g >> 1) == (n16 & 1);
+  const uint8_t *abase = xl + (avalid ? at : 0) * nsl * GT_REC + 16 * g;
+  // records of this lane's D elements: tokens 2g and 2g + 1 (a token past M repeats the last one; not stored)
+  const int t0 = min(2 * g, M - 1), t1 = min(2 * g + 1, M - 1);
+  const uint8_t *rb0 = xl + t0 * nsl * GT_REC + nsl * 64, *rb1 = xl + t1 * nsl * GT_REC + nsl * 64;
+  double *fw = &fac[wave][0][0];
+  #pragma unroll
+  for (int i0 = 0; i0 < GT_NMAX; i0 += DEPTH) {
+    if (i0 >= n) break;
+    #pragma unroll
+    for (int d = 0; d < DEPTH; d++) {
+      const int i = i0 + d;
+      if (i >= GT_NMAX) break;
+      // this lane's row (16 g + n16 = lane): its four factors, as k_gemv_tiles forms them
+      const Raw<FMT> &o = buf[d];
+      const double d0 = (double)h2f((uint16_t)(o.dw & 0xffff)), d1 = (double)h2f((uint16_t)(o.dw >> 16));
+      const double f4[4] = {d0 * (double)(o.sc & 0xff), d0 * (double)((o.sc >> 8) & 0xff),
+                            d1 * (double)((o.sc >> 16) & 0xff), d1 * (double)((o.sc >> 24) & 0xff)};
+      const uint32_t q[8] = {o.q[0], o.q[1], o.q[2], o.q[3], o.q[4], o.q[5], o.q[6], o.q[7]};
+      __builtin_amdgcn_sched_barrier(0);
+      load(i + DEPTH, buf[d]);  // past the wave's last slab: no memory access
+      if (i < n) {
+        const int sl = wl + WH * i;
+        *(double4 *)(fw + lane * 4) = make_double4(f4[0], f4[1], f4[2], f4[3]);
+        const uint4 av = avalid ? *(const uint4 *)(abase + sl * 64) : make_uint4(0, 0, 0, 0);
+        const i32x4 A = {(int)av.x, (int)av.y, (int)av.z, (int)av.w};
+        const uint4 r00 = *(const uint4 *)(rb0 + sl * 32), r01 = *(const uint4 *)(rb0 + sl * 32 + 16);
+        const uint4 r10 = *(const uint4 *)(rb1 + sl * 32), r11 = *(const uint4 *)(rb1 + sl * 32 + 16);
+        // (xd, xs) of the elements v = 0..3: (token 2g, block 0), (2g, 1), (2g + 1, 0), (2g + 1, 1)
+        const double xd[4] = {dbl(r00.x, r00.y), dbl(r01.x, r01.y), dbl(r10.x, r10.y), dbl(r11.x, r11.y)};
+        const double xs[4] = {dbl(r00.z, r00.w), dbl(r01.z, r01.w), dbl(r10.z, r10.w), dbl(r11.z, r11.w)};
+        #pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const uint32_t p0 = q[2 * j], p1 = q[2 * j + 1];
+          const i32x4 B = {(int)(p0 & 0x0F0F0F0Fu), (int)((p0 >> 4) & 0x0F0F0F0Fu), (int)(p1 & 0x0F0F0F0Fu),
+                           (int)((p1 >> 4) & 0x0F0F0F0Fu)};
+          const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, (i32x4){0, 0, 0, 0}, 0, 0, 0);
+          const double4 f = *(const double4 *)(fw + (16 * j + n16) * 4);  // row 16 j + n16: fa0, fa1, fb0, fb1
+          #pragma unroll
+          for (int v = 0; v < 4; v++) {
+            const double fa = (v & 1) ? f.y : f.x, fb = (v & 1) ? f.w : f.z;
+            acc[j][v >> 1] = fma(xd[v], fma(fa, (double)D[v], -(fb * xs[v])), acc[j][v >> 1]);
+          }
+        }
+      }
+    }
+  }
+
+  // ---- sums over the WH waves of each matrix in the order of a halving tree; the wave of token t adds that token's
+  __syncthreads();  // every wave is past its last read of the staged activations, which the sums overwrite
+  double *red = (double *)xl;
+  #pragma unroll
+  for (int j = 0; j < 4; j++)
+    #pragma unroll
+    for (int tt = 0; tt < 2; tt++) red[(wave * MF_SLOTS + 2 * j + tt) * 64 + lane] = acc[j][tt];
+  __syncthreads();
+  // (row = lane, token t) lives in lane 16 (t / 2) + row mod 16, slot 2 (row / 16) + t mod 2
+  auto tree = [&](int r, int t) {
+    const int src = 16 * (t >> 1) + n16, slot = 2 * (lane >> 4) + (t & 1);
+    double v[16];
+    #pragma unroll
+    for (int w = 0; w < 16; w++) v[w] = red[((r * WH + min(w, WH - 1)) * MF_SLOTS + slot) * 64 + src];
+    #pragma unroll
+    for (int half = 8; half >= 1; half >>= 1)
+      if (2 * half <= WH) {
+        #pragma unroll
+        for (int w = 0; w < half; w++) v[w] = v[w] + v[w + half];
+      }
+    return v[0];
+  };
+
+  // ---- K parts (as k_gemv_tiles)
+  constexpr int PW = NR * GEMV_MAX_MT * 64;
+  if (ks > 1) {
+    __shared__ uint32_t last;
+    double *pp = a.part + ((long)tile * ks + kp) * PW;
+    for (int t = wave; t < M; t += W) {
+      #pragma unroll
+      for (int r = 0; r < NR; r++) __hip_atomic_store(pp + (r * GEMV_MAX_MT + t) * 64 + lane, tree(r, t), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores are complete
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (threadIdx.x == 0) last = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(ks - 1);
+    __syncthreads();
+    if (!last) return;
+    if (threadIdx.x == 0) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  auto total = [&](int r, int t) {
+    if (ks == 1) return tree(r, t);
+    const double *pt = a.part + (long)tile * ks * PW + (r * GEMV_MAX_MT + t) * 64 + lane;
+    constexpr int KSMAX = 8;
+    double pv[KSMAX];
+    #pragma unroll
+    for (int k = 0; k < KSMAX; k++) pv[k] = __hip_atomic_load(pt + (long)min(k, ks - 1) * PW, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    double v = pv[0];
+    #pragma unroll
+    for (int k = 1; k < KSMAX; k++)
+      if (k < ks) v += pv[k];
+    return v;
+  };
+
+  // ---- epilogue of token t on wave t: lane = row of the tile (as k_gemv_tiles)
+  const int row = lt * 64 + lane;
+  const bool live = row < rows;
+  for (int t = wave; t < M; t += W) {
+    if constexpr (EPI == EPI_SWIGLU) {
+      const double gv = (double)(float)total(0, t), uu = (double)(float)total(1, t);
+      const float hv = live ? (float)(gv / (1.0 + exp(-gv)) * uu) : 0.f;  // src/compute/ref-kernels.js:322
+      if (live) a.hb[(long)t * a.ldh + row] = hv;
+      if (a.qout.q) quant_block32(hv, row, a.qout, t);
+    } else if constexpr (EPI == EPI_RESID) {
+      const double y = (double)(float)total(0, t);
+      if (live) {
+        float *o = a.resid + (long)t * a.ldr + row;
+        *o = (float)((double)*o + y);
+      }
+    } else {
+      const float y = (float)total(0, t);
+      if (live) {
+        const float *bias = ZL_SEG(bias);
+        ZL_SEG(out)[(long)t * ZL_SEG(ldo) + row] = bias ? (float)((double)y + (double)bias[row]) : y;
+      }
+    }
+  }
+#undef ZL_SEG
+}
+
+bool gemv_mfma_ok(const GemvArgs &a) {
+  if (a.seg[0].m.type != T_Q4_K || a.M < 2 || a.M > 8 || a.xf) return false;
+  for (int i = 0; i < a.nseg; i++)
+    if (!a.seg[i].m.fq) return false;
+  return true;
+}
+
+void launch_gemv_mfma(const GemvArgs &a, int epi, hipStream_t st) {
+  const int wpm = epi == EPI_SWIGLU ? a.nwave / 2 : a.nwave;
+  ZL_REQUIRE(gemv_mfma_ok(a) && a.kr <= GT_KR_MAX && a.ks <= 8 && wpm >= 1 && a.nwave <= 16 &&
+                 (epi != EPI_SWIGLU || (a.nwave % 2 == 0 && wpm <= 8)) && (a.kr + wpm - 1) / wpm <= GT_NMAX,
+             ZL_ERR_ARG, "gemv (matrix cores): launch shape out of range");
+  const dim3 grid((unsigned)a.ks, (unsigned)a.ntiles), blk((unsigned)a.nwave * 64);
+  const size_t lds = std::max((size_t)a.M * a.kr * GT_REC, (size_t)a.nwave * MF_SLOTS * 64 * 8);
+  if (epi == EPI_STORE) {
+    allow_big_lds(k_gemv_mfma<EPI_STORE>);
+    hipLaunchKernelGGL((k_gemv_mfma<EPI_STORE>), grid, blk, lds, st, a);
+  } else if (epi == EPI_RESID) {
+    allow_big_lds(k_gemv_mfma<EPI_RESID>);
+    hipLaunchKernelGGL((k_gemv_mfma<EPI_RESID>), grid, blk, lds, st, a);
+  } else {
+    allow_big_lds(k_gemv_mfma<EPI_SWIGLU>);
+    hipLaunchKernelGGL((k_gemv_mfma<EPI_SWIGLU>), grid, blk, lds, st, a);
+  }
+}
+
+}  // namespace zl

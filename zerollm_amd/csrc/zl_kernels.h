@@ -19,8 +19,9 @@ struct MatView {
   int type, rows, cols, nslab;
   const uint8_t *qs, *qx, *sc;
   const uint16_t *dd;
+  const uint8_t *fq;
 };
-inline MatView view(const DevMat &m) { return MatView{m.type, m.rows, m.cols, m.nslab, m.qs, m.qx, m.sc, m.dd}; }
+inline MatView view(const DevMat &m) { return MatView{m.type, m.rows, m.cols, m.nslab, m.qs, m.qx, m.sc, m.dd, m.fq}; }
 
 // Quantised activations of several rows (tokens): int8 values, f32 block scales and int block sums (per 32 values),
 // optionally the f32 values, and per 32-value block one 16-byte record per weight-format family, which the GEMV reads
@@ -155,6 +156,8 @@ void launch_deltanet(const DeltaArgs &a, int D, hipStream_t st);
 void gemv_shape(int ntiles, int nslab, bool swiglu, int *ks, int *nw);
 // Launch a GEMV of a.M tokens (chunks of at most GEMV_MAX_MT); float weights read the f32 activation xf (stride ldx).
 void launch_gemv(const GemvArgs &a, int epi, const float *xf, int ldx, hipStream_t st);
+bool gemv_mfma_ok(const GemvArgs &a);
+void launch_gemv_mfma(const GemvArgs &a, int epi, hipStream_t st);
 template <int FMT>
 void launch_gemv_fmt(const GemvArgs &a, int epi, hipStream_t st);
 
@@ -226,6 +229,7 @@ void launch_norm_quant(const float *x, int ldx, int row0, int nrows, const float
 void launch_embed(const MatView &m, const Step *step, int B, float *x, int ldx, hipStream_t st);
 void launch_dequant_rows(const MatView &m, const int *rowIds, int nrows, float *out, int ldo, hipStream_t st);
 void launch_repack(int type, const uint8_t *raw, long rawRowBytes, int rows, int cols, int nslab, DevMat &m, hipStream_t st);
+void launch_frag(const DevMat &m, hipStream_t st);
 void launch_synth(int type, uint64_t seed, double std, uint64_t srcCols, uint64_t col0, int rows, int cols, uint8_t *out,
                   hipStream_t st);
 void launch_fill(float *p, long n, float v, hipStream_t st);

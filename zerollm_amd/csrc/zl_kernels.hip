@@ -110,6 +110,28 @@ __global__ void k_repack(int type, const uint8_t *__restrict__ raw, long rawRowB
   }
 }
 
+// Q4_K 4-bit plane in matrix-core operand order (zl_gemv_mfma.hip): one thread per (row, slab) of the padded tiles. Row
+// r = 64 T + 16 j + n, value quarter g (values 16 g + e, e < 16) goes to lane L = n + 16 g of half j / 2 of the
+// tile-slab's 2 KB, bytes 8 (j mod 2) .. + 8: byte i of the first word holds values e = i (low nibble) and i + 4 (high),
+// byte i of the second word e = 8 + i and 12 + i.
+__global__ void k_frag(const uint8_t *__restrict__ qs, uint8_t *__restrict__ fq, int rowsPadded, int nslab) {
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)rowsPadded * nslab) return;
+  const int r = (int)(idx / nslab), s = (int)(idx % nslab);
+  uint8_t b[32];
+  for (int j = 0; j < 32; j++) b[j] = qs[qs_off(T_Q4_K, r, s, nslab, j)];
+  auto val = [&](int v) { return v < 32 ? (b[v] & 15) : (b[v - 32] >> 4); };  // value v of the slab (row layout)
+  const int rr = r & 63, jg = rr >> 4, n = rr & 15;
+  const long ts = tile_slab(r, s, nslab);
+  for (int g = 0; g < 4; g++) {
+    uint8_t *dst = fq + ((ts * 2 + (jg >> 1)) * 64 + n + 16 * g) * 16 + (jg & 1) * 8;
+    for (int i = 0; i < 4; i++) {
+      dst[i] = (uint8_t)(val(16 * g + i) | (val(16 * g + i + 4) << 4));
+      dst[4 + i] = (uint8_t)(val(16 * g + 8 + i) | (val(16 * g + 12 + i) << 4));
+    }
+  }
+}
+
 // ================================================================================================ dequantisation
 // dequantRow (src/compute/ref-kernels.js:80-120, src/compute/quant.js:33-202) for value c of row r of the repacked
 // planes, in f64 with one rounding to f32. One element per thread: coalesced stores, no private arrays.
@@ -238,6 +260,13 @@ void launch_repack(int type, const uint8_t *raw, long rawRowBytes, int rows, int
   long n = (long)rows * nslab;
   hipLaunchKernelGGL(k_repack, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, type, raw, rawRowBytes, rows, cols, nslab,
                      m.qs, m.qx, m.sc, m.dd);
+  ZL_HIP(hipGetLastError());
+}
+
+void launch_frag(const DevMat &m, hipStream_t st) {
+  const int rp = tiles_of(m.rows) * 64;
+  const long n = (long)rp * m.nslab;
+  hipLaunchKernelGGL(k_frag, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, m.qs, m.fq, rp, m.nslab);
   ZL_HIP(hipGetLastError());
 }
 

@@ -82,6 +82,7 @@ static DevMat alloc_planes(Arena &ar, int type, int rows, int cols) {
   if (qx_bytes(type)) m.qx = (uint8_t *)zalloc(ns * qx_bytes(type));
   if (sc_bytes(type)) m.sc = (uint8_t *)zalloc(ns * sc_bytes(type));
   m.dd = (uint16_t *)zalloc(T * dd_per_tile(type, m.nslab) * 2);
+  if (type == T_Q4_K) m.fq = (uint8_t *)zalloc(ns * qs_bytes(type));
   return m;
 }
 
@@ -99,6 +100,7 @@ static DevMat row_view(const DevMat &m, int row0, int n) {
   if (m.qx) v.qx = m.qx + ns * qx_bytes(m.type);
   if (m.sc) v.sc = m.sc + ns * sc_bytes(m.type);
   v.dd = m.dd + (long)(row0 / 64) * dd_per_tile(m.type, m.nslab);
+  if (m.fq) v.fq = m.fq + ns * qs_bytes(m.type);
   return v;
 }
 
@@ -111,6 +113,7 @@ static void fill_planes(const DevMat &m, const uint8_t *draw, hipStream_t st) {
   }
   DevMat mm = m;
   launch_repack(m.type, draw, rb, m.rows, m.cols, m.nslab, mm, st);
+  if (m.fq) launch_frag(m, st);
 }
 
 // Allocate the planes of a rows x cols matrix of `type` and repack raw ggml rows (device pointer) into them.
