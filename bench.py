@@ -17,10 +17,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s
-# HBM bytes per launch of the roofline kernel (k_gemv_tiles<Q4_K, MT=5, SWIGLU>, ffn_gate + ffn_up at M = 5): FETCH_SIZE
+# HBM bytes per launch of the roofline kernel (k_gemv_mfma<SWIGLU>, Q4_K ffn_gate + ffn_up at M = 5): FETCH_SIZE
 # and WRITE_SIZE counter runs over `bench.py --probe-only`, each scaled by the same counter's reading for a plain copy of
 # known size (profiles/gemv_gate_up_m5_traffic.md). A hardware counter cannot be read inside this timed run.
-ROOFLINE_TRAFFIC_BYTES = 59_254_000
+ROOFLINE_TRAFFIC_BYTES = 59_153_000
 PROMPT, GEN, K = 512, 256, 4
 
 
@@ -168,7 +168,7 @@ def main():
     if args.probe_only:
         target.forward_batch(prompt[:K + 1], logits="none")
         ms, b = target.probe_gemv("gate_up", K + 1, 4 * t_spec.n_layer)
-        print(json.dumps({"kernel": "k_gemv_tiles<Q4_K, MT=5, SWIGLU>", "launch_ms": round(ms, 5), "bytes_per_launch": b,
+        print(json.dumps({"kernel": "k_gemv_mfma<SWIGLU> (Q4_K, M=5)", "launch_ms": round(ms, 5), "bytes_per_launch": b,
                           "GBps": round(b / (ms * 1e-3) / 1e9, 1)}), flush=True)
         target.close()
         draft.close()
@@ -219,7 +219,7 @@ def main():
                    "draft_ms_per_cycle": round(dms / cycles, 3), "verify_accept_ms_per_cycle": round(vms / cycles, 3),
                    "weight_bytes_per_cycle": bytes_cycle,
                    "cycle_weight_bw_frac": round(bytes_cycle / (cycle_ms * 1e-3) / HBM_PEAK, 4)},
-        "roofline": {"bound": "hbm", "kernel": "k_gemv_tiles<Q4_K, MT=5, SWIGLU> (ffn_gate+ffn_up, M=k+1=5)",
+        "roofline": {"bound": "hbm", "kernel": "k_gemv_mfma<SWIGLU> (Q4_K ffn_gate+ffn_up, M=k+1=5, int8 dots on the matrix cores)",
                      "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK, 4), "traffic": ROOFLINE_TRAFFIC_BYTES,
                      "launch_ms": round(probe_ms, 5), "bytes_per_launch": bytes_per, "launches": iters,
