@@ -250,20 +250,22 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
   for (int c = 0; c < nch; c++) {
     if (c + 1 < nch) fetch(c + 1, npos);
     if (chainLane) {
-      // units of UNIT positions: all of a unit's LDS reads are issued first, then its fma steps run back to back
-      // (each step waits ~9 cycles on the previous one, so the reads of a unit cost one LDS latency per unit).
+      // units of UNIT positions, software pipelined: the LDS reads of unit u + 1 are issued before the fma steps of
+      // unit u, so the chain (one dependent fma per position, ~2.2 ns each) does not wait out an LDS latency per unit.
       // p is zero past the last position, so a unit may run past `cnt`: fmaf(0, v, o) == o for the finite cached
-      // values read there.
-      const int t0 = c * CT, cnt = min(CT, npos - t0);
+      // values read there. The read-ahead index is clamped to the chunk's last unit (a re-read, never past it).
+      const int t0 = c * CT, cnt = min(CT, npos - t0), nu = (cnt + AV_UNIT - 1) / AV_UNIT;
       const uint8_t *row = vbuf + (c & 1) * AV_CHUNK + lane * AV_PITCH;
       const float *pc = p + t0;
-      for (int u = 0; u < cnt; u += AV_UNIT) {
-        float4 pv[AV_UNIT / 4];
-        uint4 vv[AV_UNIT * VB / 16];
+      float4 pa[AV_UNIT / 4], pb[AV_UNIT / 4];
+      uint4 va[AV_UNIT * VB / 16], vb[AV_UNIT * VB / 16];
+      auto read = [&](int u, float4 (&pv)[AV_UNIT / 4], uint4 (&vv)[AV_UNIT * VB / 16]) {
         #pragma unroll
-        for (int k = 0; k < AV_UNIT / 4; k++) pv[k] = *(const float4 *)(pc + u + 4 * k);
+        for (int k = 0; k < AV_UNIT / 4; k++) pv[k] = *(const float4 *)(pc + u * AV_UNIT + 4 * k);
         #pragma unroll
-        for (int k = 0; k < AV_UNIT * VB / 16; k++) vv[k] = *(const uint4 *)(row + (u + k * EPP) * VB);
+        for (int k = 0; k < AV_UNIT * VB / 16; k++) vv[k] = *(const uint4 *)(row + (u * AV_UNIT + k * EPP) * VB);
+      };
+      auto steps = [&](const float4 (&pv)[AV_UNIT / 4], const uint4 (&vv)[AV_UNIT * VB / 16]) {
         #pragma unroll
         for (int k = 0; k < AV_UNIT / 4; k++) {
           float v0, v1, v2, v3;
@@ -278,7 +280,20 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
           }
           o = fmaf(pv[k].x, v0, o); o = fmaf(pv[k].y, v1, o); o = fmaf(pv[k].z, v2, o); o = fmaf(pv[k].w, v3, o);
         }
+      };
+      // two units per iteration and no branch between a unit's reads and its steps (a branch there lets the compiler
+      // sink the reads to their use); an odd last unit is already in (pa, va) after the loop
+      read(0, pa, va);
+      int u = 0;
+      for (; u + 2 <= nu; u += 2) {
+        read(u + 1, pb, vb);
+        __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the steps (the scheduler moves them to their use)
+        steps(pa, va);
+        read(min(u + 2, nu - 1), pa, va);
+        __builtin_amdgcn_sched_barrier(0);
+        steps(pb, vb);
       }
+      if (u < nu) steps(pa, va);
     }
     __syncthreads();
     if (c + 1 < nch) store((c + 1) & 1);
