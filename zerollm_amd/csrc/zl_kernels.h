@@ -212,9 +212,24 @@ __device__ inline void quant_block32(float v, int i, const Act &a, int row) {
 // 256 threads (tid < 256: strided sequential f64 sums, a 64-lane butterfly, then (w0 + w1) + (w2 + w3) through red[4]).
 // Every caller uses this order, so every kernel derives the same scale. All 256 threads return it; the caller
 // synchronises the block between the two uses of red.
+// Sum of squares of this thread's values xr[base + tid + 256 k], k < K, added to ss in k order; the K loads are issued
+// together (unconditionally: a position past n reads xr[0] and adds +0.0, which leaves the f64 sum unchanged).
+template <int K>
+__device__ inline double sumsq_batch(const float *xr, int base, int n, int tid, double ss) {
+  float v[K];
+  #pragma unroll
+  for (int k = 0; k < K; k++) { const int i = base + tid + 256 * k; v[k] = xr[i < n ? i : 0]; }
+  #pragma unroll
+  for (int k = 0; k < K; k++) { const double x = base + tid + 256 * k < n ? (double)v[k] : 0.0; ss += x * x; }
+  return ss;
+}
+
 __device__ inline double rms_scale256(const float *xr, int n, double eps, int tid, double *red) {
+  // thread tid adds x[tid]^2, x[tid + 256]^2, ... in that order (f64), then the 64-lane butterfly and the four waves
   double ss = 0;
-  for (int i = tid; i < n; i += 256) { const double v = (double)xr[i]; ss += v * v; }
+  if (n <= 1024) ss = sumsq_batch<4>(xr, 0, n, tid, ss);
+  else
+    for (int base = 0; base < n; base += 4096) ss = sumsq_batch<16>(xr, base, n, tid, ss);
   ss = wave_sum_xor(ss, 64);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();

@@ -200,11 +200,12 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x,
   constexpr int PER = NQ_CHUNK / 256;
   const int c0 = blockIdx.x * NQ_CHUNK, c1 = min(npad, c0 + NQ_CHUNK);
   float xv[PER], wv[PER];
+  const float *wr = w ? w : xr;  // (no weights: a second read of x, unused)
   #pragma unroll
-  for (int k = 0; k < PER; k++) {
+  for (int k = 0; k < PER; k++) {  // unconditional loads: a branch around a load makes the compiler wait for it there
     const int i = c0 + tid + 256 * k;
-    xv[k] = i < n ? xr[i] : 0.f;
-    wv[k] = (w && i < n) ? w[i] : 0.f;
+    xv[k] = xr[i < n ? i : 0];
+    wv[k] = wr[i < n ? i : 0];
   }
   const double s = w ? rms_scale256(xr, n, eps, tid, red) : 1.0;
   #pragma unroll
@@ -214,7 +215,7 @@ __global__ __launch_bounds__(256) void k_norm_quant(const float *__restrict__ x,
     // 32-lane groups)
     if (i < c1) {
       float v = 0.f;
-      if (i < n) v = w ? (float)((double)xv[k] * s * (double)wv[k]) : xv[k];
+      if (i < n) v = w ? (float)((double)xv[k] * s * (double)wv[k]) : xv[k];  // (positions past n stay 0)
       if (act.f) act.f[(long)b * act.ld + i] = v;
       quant_block32(v, i, act, b);
     }
