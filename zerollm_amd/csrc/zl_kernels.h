@@ -224,17 +224,23 @@ __device__ inline double sumsq_batch(const float *xr, int base, int n, int tid, 
   return ss;
 }
 
+// The RMSNorm scale from each thread's partial sum of squares: the 64-lane butterfly, then the four waves of the
+// 256-thread group (red: 4 doubles of the group; synchronises the block).
+__device__ inline double rms_finish(double ss, int n, double eps, int tid, double *red) {
+  ss = wave_sum_xor(ss, 64);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  ss = (red[0] + red[1]) + (red[2] + red[3]);
+  return 1.0 / sqrt(ss / (double)n + eps);
+}
+
 __device__ inline double rms_scale256(const float *xr, int n, double eps, int tid, double *red) {
   // thread tid adds x[tid]^2, x[tid + 256]^2, ... in that order (f64), then the 64-lane butterfly and the four waves
   double ss = 0;
   if (n <= 1024) ss = sumsq_batch<4>(xr, 0, n, tid, ss);
   else
     for (int base = 0; base < n; base += 4096) ss = sumsq_batch<16>(xr, base, n, tid, ss);
-  ss = wave_sum_xor(ss, 64);
-  if ((tid & 63) == 0) red[tid >> 6] = ss;
-  __syncthreads();
-  ss = (red[0] + red[1]) + (red[2] + red[3]);
-  return 1.0 / sqrt(ss / (double)n + eps);
+  return rms_finish(ss, n, eps, tid, red);
 }
 
 void launch_attention(const AttnArgs &a, int B, hipStream_t st);
