@@ -24,17 +24,36 @@ inline int attn_heads_per_block(int group) {
 template <int HD>
 __device__ inline void norm_rope(float *v, const float *nw, double eps, int nRot, int neox, const float *cosT,
                                  const float *sinT, int pos, int lane) {
+  // the lane's table values and norm weights are requested before the sum of squares, which does not need them
+  const int half = nRot / 2;
+  constexpr int PR = (HD / 2 + 63) / 64;  // rotation pairs per lane at most
+  float cv[PR], sv[PR], wv[(HD + 63) / 64];
+  #pragma unroll
+  for (int r = 0; r < PR; r++) {
+    const int i = lane + 64 * r, ic = i < half ? i : 0;
+    cv[r] = cosT[(long)pos * half + ic];
+    sv[r] = sinT[(long)pos * half + ic];
+  }
+  const float *nwp = nw ? nw : cosT;  // (no norm: a read of the table, unused; no branch around the loads)
+  #pragma unroll
+  for (int r = 0; r < (HD + 63) / 64; r++) wv[r] = nwp[lane + 64 * r < HD ? lane + 64 * r : 0];
   if (nw) {
     double ss = 0;
     for (int i = lane; i < HD; i += 64) { const double x = (double)v[i]; ss += x * x; }
     ss = wave_sum_xor(ss, 64);
     const double sc = 1.0 / sqrt(ss / (double)HD + eps);
-    for (int i = lane; i < HD; i += 64) v[i] = (float)((double)v[i] * sc * (double)nw[i]);
+    #pragma unroll
+    for (int r = 0; r < (HD + 63) / 64; r++) {
+      const int i = lane + 64 * r;
+      if (i < HD) v[i] = (float)((double)v[i] * sc * (double)wv[r]);
+    }
   }
-  const int half = nRot / 2;
-  for (int i = lane; i < half; i += 64) {
+  #pragma unroll
+  for (int r = 0; r < PR; r++) {
+    const int i = lane + 64 * r;
+    if (i >= half) break;
     const int i0 = neox ? i : 2 * i, i1 = neox ? i + half : 2 * i + 1;
-    const double c = (double)cosT[(long)pos * half + i], sn = (double)sinT[(long)pos * half + i];
+    const double c = (double)cv[r], sn = (double)sv[r];
     const double x0 = (double)v[i0], x1 = (double)v[i1];
     v[i0] = (float)(x0 * c - x1 * sn);  // pairs are disjoint across lanes
     v[i1] = (float)(x0 * sn + x1 * c);
