@@ -104,6 +104,16 @@ __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
     const int i = tid + 256 * k;
     qv[k] = i < hg * HD ? a.q[(long)b * a.ldq + (long)(h0 + i / HD) * a.qhs + i % HD] : 0.f;
   }
+  // the pass's first 8 key rows of this KV head (row-major [row][HD], element tid + 256 k), for the blocks that norm
+  // and rotate the pass's keys; unconditional loads (rows past B read row 0, unused)
+  constexpr int KPT = 8 * HD / 256;
+  const int nB = gridDim.z;
+  float kr[KPT];
+  #pragma unroll
+  for (int k = 0; k < KPT; k++) {
+    const int e = tid + 256 * k, row = e / HD < nB ? e / HD : 0;
+    kr[k] = a.k[(long)row * a.ldkv + (long)kvh * HD + e % HD];
+  }
   const Step *st = a.step;
   if (b >= st->B) return;
   const int pos0 = st->pos0, npos = pos0 + b + 1;
@@ -120,8 +130,14 @@ __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
     const int n0 = max(c0, pos0), n1 = min(c0 + P, npos);
     for (int g0 = n0; g0 < n1; g0 += 8) {
       const int g1 = min(n1, g0 + 8);
-      for (int i = tid; i < (g1 - g0) * HD; i += 256)
-        kf[i] = a.k[(long)(g0 - pos0 + i / HD) * a.ldkv + (long)kvh * HD + i % HD];
+      if (g0 == pos0) {  // rows 0 .. g1 - g0 - 1: the prefetched ones
+        #pragma unroll
+        for (int k = 0; k < KPT; k++)
+          if (tid + 256 * k < (g1 - g0) * HD) kf[tid + 256 * k] = kr[k];
+      } else {
+        for (int i = tid; i < (g1 - g0) * HD; i += 256)
+          kf[i] = a.k[(long)(g0 - pos0 + i / HD) * a.ldkv + (long)kvh * HD + i % HD];
+      }
       __syncthreads();
       for (int p = g0 + wave; p < g1; p += 4)
         norm_rope<HD>(kf + (p - g0) * HD, a.kNorm, a.eps, a.nRot, a.neox, a.cosT, a.sinT, p, lane);
