@@ -265,11 +265,20 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
   if (lane == 0) redf[wave] = mx;
   __syncthreads();
   const double m = (double)fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
+  // four independent exponentials per step (their f64 chains overlap), added to the sum in position order as before
   double sum = 0.0;
-  for (int t = tid; t < npos; t += 256) {
-    const double e = exp((double)p[t] - m);
-    p[t] = (float)e;
-    sum += e;
+  for (int t0 = tid; t0 < npos; t0 += 4 * 256) {
+    double e[4];
+    #pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int t = t0 + 256 * k;
+      e[k] = exp((double)p[t < npos ? t : t0] - m);
+    }
+    #pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int t = t0 + 256 * k;
+      if (t < npos) { p[t] = (float)e[k]; sum += e[k]; }
+    }
   }
   sum = wave_sum_xor(sum, 64);
   if (lane == 0) redd[wave] = sum;
