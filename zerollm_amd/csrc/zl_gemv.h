@@ -264,25 +264,49 @@ __global__ __launch_bounds__(1024) void k_gemv_tiles(const GemvArgs a) {
     __shared__ double ssr[4][4];
     __shared__ double scl[GEMV_MAX_MT];
     const int groups = W >> 2, g = wave >> 2;
-    for (int t0 = 0; t0 < M; t0 += groups) {
-      const int t = t0 + g;
-      const bool act_ = t < M;
-      double sc = 1.0;
-      if (a.nw) {
-        // rms_scale256 synchronises the block: every thread takes part, idle groups with a dummy row
-        const float *xr = a.xf + (long)(a.xrow0 + (act_ ? t : 0)) * a.ldxf;
-        sc = rms_scale256(xr, a.n, a.eps, (int)threadIdx.x & 255, ssr[g & 3]);
-      }
-      if (act_ && (threadIdx.x & 255) == 0) scl[t] = sc;
+    // one token, one K part, rows of at most 1024 values: the values this thread quantises (elements e = tid,
+    // tid + 64 W, e < 1024) are among the four it loads for the sum of squares (x[tid mod 256 + 256 k], k = e / 256),
+    // and their norm weights are requested with them, so the quantisation waits for no load
+    const bool own = M == 1 && s0 == 0 && a.n <= 1024 && a.nw && nsl * 64 <= 2 * W * 64;
+    float xo[4], wo[2];
+    if (own) {
+      const int tt = threadIdx.x & 255;
+      const float *xr = a.xf + (long)a.xrow0 * a.ldxf;
+      #pragma unroll
+      for (int k = 0; k < 4; k++) { const int i = tt + 256 * k; xo[k] = xr[i < a.n ? i : 0]; }
+      #pragma unroll
+      for (int q = 0; q < 2; q++) { const int e = threadIdx.x + q * W * 64; wo[q] = a.nw[e < a.n ? e : 0]; }
+      double ss = 0.0;  // rms_scale256's order
+      #pragma unroll
+      for (int k = 0; k < 4; k++) { const double x = tt + 256 * k < a.n ? (double)xo[k] : 0.0; ss += x * x; }
+      const double sc = rms_finish(ss, a.n, a.eps, tt, ssr[g & 3]);
+      if (threadIdx.x == 0) scl[0] = sc;
       __syncthreads();
+    } else {
+      for (int t0 = 0; t0 < M; t0 += groups) {
+        const int t = t0 + g;
+        const bool act_ = t < M;
+        double sc = 1.0;
+        if (a.nw) {
+          // rms_scale256 synchronises the block: every thread takes part, idle groups with a dummy row
+          const float *xr = a.xf + (long)(a.xrow0 + (act_ ? t : 0)) * a.ldxf;
+          sc = rms_scale256(xr, a.n, a.eps, (int)threadIdx.x & 255, ssr[g & 3]);
+        }
+        if (act_ && (threadIdx.x & 255) == 0) scl[t] = sc;
+        __syncthreads();
+      }
     }
     const int per = nsl * 64;  // values of one token in the range (a multiple of 64: each wave holds whole blocks)
     for (int e = threadIdx.x; e < M * per; e += W * 64) {
       const int t = e / per, j = e - t * per, col = s0 * 64 + j;
       float v = 0.f;
       if (col < a.n) {
-        const float xv = a.xf[(long)(a.xrow0 + t) * a.ldxf + col];
-        v = a.nw ? (float)((double)xv * scl[t] * (double)a.nw[col]) : xv;
+        if (own) {
+          v = (float)((double)xo[e >> 8] * scl[0] * (double)wo[e >= W * 64 ? 1 : 0]);
+        } else {
+          const float xv = a.xf[(long)(a.xrow0 + t) * a.ldxf + col];
+          v = a.nw ? (float)((double)xv * scl[t] * (double)a.nw[col]) : xv;
+        }
       }
       const QBlock b = quant32(v);
       uint8_t *tb = xl + t * nsl * GT_REC;
