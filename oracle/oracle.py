@@ -201,6 +201,8 @@ class Sampler:
                                   frequency=0.0 if argmax else frequency_penalty, topK=top_k, repeatLastN=repeat_last_n)
         self.rng = Rng(seed)
         self.greedy = argmax or temperature <= 0
+        # usesHistory (src/sampling/sampler.js:154): only penalties make the history matter
+        self.uses_history = not argmax and (repeat_penalty != 1 or presence_penalty != 0 or frequency_penalty != 0)
 
     def distribution(self, logits: np.ndarray, history=()) -> Dist:
         l = np.ascontiguousarray(logits, dtype=np.float32).copy()

@@ -1,15 +1,24 @@
-"""ORACLE — test infrastructure only. generateSpeculative (src/model/speculative.js:100-240) over oracle models, greedy:
-the draft proposes k tokens one forward at a time, the target checks them one forward at a time (RefModel has no
-batched pass: forwardRows falls back to sequential forwards, src/model/speculative.js:42-47). Used as the CPU baseline
-leg of bench.py and as a reference stream in tests."""
+"""ORACLE — test infrastructure only (tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it; the
+product never imports it).
+
+generateSpeculative (src/model/speculative.js:100-240) restated over oracle models: any object with forward(token,
+logits=True) -> f32 logits | None, truncate(n), tokens, pos, ctx and (optionally) mark_rollback(). The oracle models
+have no batched pass, so forwardRows falls back to one forward per token (src/model/speculative.js:39-48) and
+feedLogits feeds one token at a time (:51-61). Both the greedy path and speculative sampling are restated, with the
+single mulberry32 stream of the sampler consumed in the reference's order: draft draws x_1..x_kk (:173), then the
+accept uniforms (:203), then one residual draw (:204, drawResidual :75-87) or one bonus draw (:207-209).
+"""
 from __future__ import annotations
 
 import time
 
 import numpy as np
 
+from . import oracle as O
+
 
 def common_prefix(a, b):
+    """commonPrefix (src/model/generate.js:34-39)."""
     n = min(len(a), len(b))
     i = 0
     while i < n and a[i] == b[i]:
@@ -17,46 +26,198 @@ def common_prefix(a, b):
     return i
 
 
-def speculative_greedy(target, draft, seq, k, max_tokens, deadline=None):
-    """Continue `seq` (its last token pending; both models hold seq[:-1]) by up to max_tokens greedy tokens.
-    Returns (emitted, cycles). Stops early at `deadline` (time.perf_counter value) after a whole cycle."""
-    seq = list(seq)
-    out = []
-    cycles = 0
-    while len(out) < max_tokens:
-        if deadline is not None and time.perf_counter() > deadline:
-            break
-        kk = max(0, min(k, max_tokens - len(out) - 1))
-        draft.truncate(min(common_prefix(draft.tokens, seq), len(seq) - 1))
-        drafted = []
-        if kk:
-            logits = None
-            for t in seq[draft.pos:]:
-                logits = draft.forward(t)
-            for j in range(kk):
-                x = int(np.argmax(logits))
-                drafted.append(x)
-                if j == kk - 1:
-                    break
-                logits = draft.forward(x)
-        rows = [target.forward(t) for t in [seq[-1]] + drafted]
-        a = 0
-        tok = -1
-        for j in range(len(drafted)):
-            t = int(np.argmax(rows[j]))
-            if t == drafted[j]:
-                a += 1
-                continue
-            tok = t
-            break
-        if a == len(drafted):
-            tok = int(np.argmax(rows[len(drafted)]))
-        emit = drafted[:a] + [tok]
-        for e in emit:
-            seq.append(e)
-            out.append(e)
-            if len(out) >= max_tokens:
+class Argmax:
+    """The plain argmax sampler generate() uses when none is passed (src/model/generate.js:4-8): first maximum."""
+
+    greedy = True
+    uses_history = False
+
+    def sample(self, logits, history=()):
+        return int(np.argmax(logits))
+
+
+def _is_argmax(sample):
+    return isinstance(sample, Argmax)
+
+
+def speculative(target, draft, prompt_ids, k=4, max_tokens=256, sample=None, stop_ids=(), penalize_prompt=True,
+                t_limit=None, cycle_log=None, stats=None, deadline=None):
+    """Yield the token ids generateSpeculative yields after prompt_ids (src/model/speculative.js:100-240).
+
+    sample: an oracle.Sampler (createSampler) or None / Argmax() for plain greedy. t_limit: verifyLimit(target); the
+    oracle models have no forwardBatch, so the reference's value is Infinity (:26-28), but the caller may pass the
+    device model's limit so both run the same kk sequence. cycle_log: a list that receives one
+    (kk, drafted, accepted, token) tuple per cycle. deadline: a time.perf_counter() value after which no new cycle
+    starts (bench sampling only)."""
+    sample = sample if sample is not None else Argmax()
+    greedy = _is_argmax(sample) or bool(sample.greedy)
+    stop = set(stop_ids or ())
+    mx = max_tokens
+    stats = stats if stats is not None else {}
+    k_max = max(1, int(k))
+    n0 = len(prompt_ids)
+    if n0 == 0:
+        raise ValueError("empty prompt")
+    if n0 >= target.ctx:
+        raise ValueError(f"prompt is {n0} tokens but the context window is {target.ctx}; shorten it or raise --ctx")
+    if n0 >= draft.ctx:
+        raise ValueError(f"prompt is {n0} tokens but the draft model's context window is {draft.ctx}; give the draft "
+                         "model at least the target's context")
+    t_limit = float("inf") if t_limit is None else t_limit
+    prompt_ids = [int(t) for t in prompt_ids]
+
+    # ---- prefill everything but the last prompt token on both models (:117-143)
+    body = prompt_ids[:-1]
+    reuse = min(common_prefix(target.tokens, prompt_ids), n0 - 1)
+    target.truncate(reuse)
+    d_reuse = min(common_prefix(draft.tokens, body), len(body))
+    draft.truncate(d_reuse)
+    for t in body[reuse:]:
+        target.forward(t, logits=False)
+    for t in body[d_reuse:]:
+        draft.forward(t, logits=False)
+    spec = stats["speculative"] = {"k": k_max, "cycles": 0, "drafted": 0, "accepted": 0,
+                                   "acceptedHist": [0] * (k_max + 1)}
+    stats["generated"] = 0
+    stats["stopReason"] = "length"
+
+    seq = list(prompt_ids)
+    need_hist = not _is_argmax(sample) and bool(sample.uses_history)
+
+    def hist_of(full, n):
+        if not need_hist:
+            return []
+        return full[n0:n] if penalize_prompt is False else full[:n]
+
+    generated = 0
+    try:
+        while generated < mx:
+            if deadline is not None and time.perf_counter() > deadline:
+                stats["stopReason"] = "deadline"
                 break
-        target.truncate(min(common_prefix(target.tokens, seq), len(seq) - 1))
-        cycles += 1
-    return out, cycles
+            pending = seq[-1]
+            kk = min(k_max, mx - generated - 1, target.ctx - len(seq), t_limit - 1, draft.ctx - len(seq) + 1)
+            kk = max(0, int(kk))
+            # -- draft (:163-179)
+            drafted, qd = [], []
+            if kk > 0:
+                draft.truncate(min(common_prefix(draft.tokens, seq), len(seq) - 1))
+                dl = None
+                for t in seq[draft.pos:]:  # feedLogits, one token per call (:51-61)
+                    dl = draft.forward(t)
+                if hasattr(draft, "mark_rollback"):
+                    draft.mark_rollback()
+                for j in range(kk):
+                    h = hist_of(seq + drafted, len(seq) + j)
+                    if greedy:
+                        x = sample.sample(dl, h)
+                    else:
+                        d = sample.distribution(dl, h)
+                        x = sample.draw(d)
+                        qd.append(d)
+                    drafted.append(x)
+                    if x in stop or j == kk - 1:
+                        break
+                    dl = draft.forward(x)
+                kk = len(drafted)
+            # -- verify: one (sequential) pass over [pending, x_1..x_kk] (:182-190)
+            if hasattr(target, "mark_rollback"):
+                target.mark_rollback()
+            rows = [target.forward(t) for t in [pending] + drafted]
+            full = seq + drafted
+            # -- accept / reject (:192-209)
+            a, tok = 0, -1
+            for j in range(kk):
+                h = hist_of(full, len(seq) + j)
+                if greedy:
+                    t = sample.sample(rows[j], h)
+                    if t == drafted[j]:
+                        a += 1
+                        continue
+                    tok = t
+                    break
+                pd = sample.distribution(rows[j], h)
+                px = O.prob_of(pd, drafted[j])
+                qx = O.prob_of(qd[j], drafted[j])
+                if sample.rand() * qx < px:
+                    a += 1
+                    continue
+                tok = O.draw_residual(sample, pd, qd[j], len(rows[j]))
+                break
+            if a == kk:
+                tok = sample.sample(rows[kk], hist_of(full, len(seq) + kk))
+            spec["cycles"] += 1
+            spec["drafted"] += kk
+            spec["accepted"] += a
+            spec["acceptedHist"][a] += 1
+            if cycle_log is not None:
+                cycle_log.append((kk, tuple(drafted), a, tok))
+            # -- emit and roll back (:211-226)
+            done = False
+            for e in drafted[:a] + [tok]:
+                if e in stop:
+                    stats["stopReason"] = "stop"
+                    done = True
+                    break
+                idx = len(seq)
+                seq.append(e)
+                yield e
+                generated += 1
+                stats["generated"] = generated
+                if generated >= mx:
+                    done = True
+                    break
+                if idx >= target.ctx:
+                    stats["stopReason"] = "context"
+                    done = True
+                    break
+            target.truncate(min(common_prefix(target.tokens, seq), len(seq) - 1))
+            if done:
+                break
+    finally:
+        target.truncate(common_prefix(target.tokens, seq))
+        draft.truncate(common_prefix(draft.tokens, seq))
+        spec["acceptRate"] = spec["accepted"] / spec["drafted"] if spec["drafted"] else 0.0
+        spec["tokensPerCycle"] = generated / spec["cycles"] if spec["cycles"] else 0.0
+
+
+def plain(model, prompt_ids, max_tokens, sample=None, stop_ids=(), penalize_prompt=True, stats=None):
+    """generate() (src/model/generate.js:41-96) over an oracle model, one token per forward: the stream that greedy
+    speculative decoding must reproduce."""
+    sample = sample if sample is not None else Argmax()
+    stop = set(stop_ids or ())
+    stats = stats if stats is not None else {}
+    prompt_ids = [int(t) for t in prompt_ids]
+    n0 = len(prompt_ids)
+    if n0 == 0:
+        raise ValueError("empty prompt")
+    if n0 >= model.ctx:
+        raise ValueError(f"prompt is {n0} tokens but the context window is {model.ctx}; shorten it or raise --ctx")
+    reuse = min(common_prefix(model.tokens, prompt_ids), n0 - 1)
+    model.truncate(reuse)
+    logits = None
+    for i, t in enumerate(prompt_ids[reuse:]):
+        logits = model.forward(t, logits=reuse + i == n0 - 1)
+    history = list(prompt_ids)
+    stats["stopReason"] = "length"
+    for n in range(max_tokens):
+        tok = sample.sample(logits, history[n0:] if penalize_prompt is False else history)
+        if tok in stop:
+            stats["stopReason"] = "stop"
+            break
+        yield tok
+        history.append(tok)
+        if n + 1 >= max_tokens:
+            break
+        if model.pos >= model.ctx:
+            stats["stopReason"] = "context"
+            break
+        logits = model.forward(tok)
+
+
+def speculative_greedy(target, draft, seq, k, max_tokens, deadline=None):
+    """Greedy speculative decoding continuing `seq` whose body both models already hold (bench.py's CPU leg).
+    Returns (emitted, cycles)."""
+    st = {}
+    out = list(speculative(target, draft, seq, k=k, max_tokens=max_tokens, deadline=deadline, stats=st))
+    return out, st["speculative"]["cycles"]

@@ -138,6 +138,23 @@ def test_gemv_matches_oracle(gpu, type_, cols):
     _check_gemv(type_, 300, cols, [1, 2, 5, 9, 17], seed=cols + type_)
 
 
+def float_raw(type_, rows, cols, seed):
+    """Raw F32 / F16 / BF16 rows of N(0, 0.05) values (BF16: the top half of the f32 bits, as ggml truncates)."""
+    w = np.random.default_rng(seed).normal(0, 0.05, (rows, cols)).astype(np.float32)
+    if type_ == G.F32:
+        return w.view(np.uint8).ravel()
+    if type_ == G.F16:
+        return w.astype(np.float16).view(np.uint8).ravel()
+    return (w.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).ravel()
+
+
+@pytest.mark.parametrize("type_", [G.F32, G.F16, G.BF16])
+@pytest.mark.parametrize("cols", [512, 1536])
+def test_gemv_float_weights_match_oracle(gpu, type_, cols):
+    """Float weights take the f32 activations, not their int8 quantisation (src/compute/ref-kernels.js:278-299)."""
+    _check_gemv(type_, 200, cols, [1, 2, 5, 9, 17], seed=cols + type_, raw=float_raw(type_, 200, cols, cols + type_))
+
+
 @pytest.mark.parametrize("type_", [G.Q8_0, G.Q4_0, G.Q5_0])
 def test_gemv_odd_block_count(gpu, type_):
     """cols = 96: the last 64-value slab is half padding."""
@@ -155,20 +172,34 @@ def test_gemv_batched_rows_equal_single_token(gpu):
     m.free()
 
 
-@pytest.mark.parametrize("N,K,type_", [(4096, 4096, G.Q4_K), (1024, 4096, G.Q6_K), (4096, 12288, G.Q6_K)])
+# the verify-width microbenchmark's projection shapes (Qwen3-8B): attn_q / attn_output, attn_k, attn_v, ffn_gate /
+# ffn_up, ffn_down, the output head
+C2_SHAPES = [(4096, 4096, G.Q4_K), (1024, 4096, G.Q4_K), (1024, 4096, G.Q6_K), (12288, 4096, G.Q4_K),
+             (4096, 12288, G.Q6_K), (151936, 4096, G.Q6_K)]
+
+
+@pytest.mark.parametrize("N,K,type_", C2_SHAPES)
 def test_gemv_projection_shapes_synthetic(gpu, N, K, type_):
-    """Projection shapes with this library's quantised N(0, 0.02) weights, checked on a slice of rows against the
-    oracle for M in {1, 5, 9}."""
+    """Projection shapes with this library's quantised N(0, 0.02) weights, at M = k + 1 in {1, 2, 5, 9, 17}: the first
+    and the last 96 rows against the oracle (M = 17 is two weight passes of 9 + 8 tokens; the other rows are covered
+    by the same kernels through the model tests)."""
     t = synth.TensorSpec("w", type_, N, K, seed=99 + N, std=0.02)
     raw = synth.tensor_bytes(t, use_device=True)
+    print(f"case gemv {N}x{K} type {type_}", flush=True)
     m = Mat(type_, raw, N, K)
-    X = np.random.default_rng(N).normal(0, 1, (9, K)).astype(np.float32)
-    rows = 128
+    X = np.random.default_rng(N).normal(0, 1, (17, K)).astype(np.float32)
+    rows = 96
     rb = G.row_size(type_, K)
-    sub = raw[:rows * rb]
-    want = np.stack([O.matvec(type_, sub, rows, K, X[i]) for i in range(9)])
-    for M in (1, 5, 9):
-        y = m.gemv(X[:M])[:, :rows]
-        assert (y.view(np.uint32) == want[:M].view(np.uint32)).mean() >= 0.999
-        assert np.abs(y - want[:M]).max() <= 1e-6 * np.abs(want).max()
+    heads = [(0, raw[:rows * rb]), (N - rows, raw[(N - rows) * rb:])]
+    want = {r0: np.stack([O.matvec(type_, sub, rows, K, X[i]) for i in range(17)]) for r0, sub in heads}
+    for M in (1, 2, 5, 9, 17):
+        y = m.gemv(X[:M])
+        for r0, _ in heads:
+            got, w = y[:, r0:r0 + rows], want[r0][:M]
+            assert (got.view(np.uint32) == w.view(np.uint32)).mean() >= 0.999, (M, r0)
+            assert np.abs(got - w).max() <= 1e-6 * np.abs(w).max(), (M, r0)
+        if M > 1:
+            assert (y[:1].view(np.uint32) == first.view(np.uint32)).all(), M
+        else:
+            first = y[:1].copy()
     m.free()

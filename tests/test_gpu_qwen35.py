@@ -50,8 +50,11 @@ def test_logits_and_state_match_oracle(gpu, quant, kv):
     m = synth.build_on_device(spec, ctx=128, kv=kv)
     got = np.stack([m.forward(t).copy() for t in toks])
     d = check_close(got, want, quant)
-    print(f"{quant} kv={kv}: max-abs {d.max():.3g}, mean-abs {d.mean():.3g}, bit-exact {np.mean(got == want):.4f}")
+    exact = np.mean(got.view(np.uint32) == want.view(np.uint32))
+    print(f"{quant} kv={kv}: max-abs {d.max():.3g}, mean-abs {d.mean():.3g}, bit-exact {exact:.4f}")
     assert (got.argmax(1) == want.argmax(1)).all()
+    # f64 sums in another order than the oracle's: the f32 logits differ only at rare rounding boundaries
+    assert exact >= 0.999 and d.max() <= 1e-6 * np.abs(want).max(), (exact, d.max())
     conv, ssm = m.recurrent_state()
     rconv, rssm = ref.state()
     np.testing.assert_allclose(conv, rconv, rtol=1e-4, atol=1e-5)

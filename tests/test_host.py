@@ -122,3 +122,49 @@ def test_seeded_ids_are_mulberry32_prompts():
 
     r = O.Rng(2024)
     assert synth.seeded_ids(300, 2024, 151936) == [int(r() * 151936) for _ in range(300)]
+
+
+class _Meta:
+    """The get() view of GGUF metadata that vocabFingerprint reads."""
+
+    def __init__(self, tokens, types, arch="qwen3", vocab=None):
+        self.m = {"tokenizer.ggml.tokens": tokens, "tokenizer.ggml.token_type": types, "general.architecture": arch}
+        if vocab is not None:
+            self.m[f"{arch}.vocab_size"] = vocab
+
+    def get(self, k, default=None):
+        return self.m.get(k, default)
+
+
+def test_vocab_fingerprint_and_mismatch_messages():
+    """vocabFingerprint / vocabMismatch (src/model/speculative.js:256-283): sha256 over each token string and a NUL,
+    then '#<n types>:' and '<type>,' per token; the three mismatch messages, token strings quoted as JSON."""
+    import hashlib
+
+    from zerollm_amd.speculative import vocab_fingerprint, vocab_mismatch
+
+    a = _Meta(["a", "b"], [1, 1])
+    fp = vocab_fingerprint(a)
+    assert fp == {"size": 2, "hash": hashlib.sha256(b"a\0b\0#2:1,1,").hexdigest()}
+    assert vocab_mismatch(a, _Meta(["a", "b"], [1, 1])) is None
+    assert vocab_mismatch(a, _Meta(["a"], [1])) == (
+        "the draft model has a vocabulary of 1 tokens but the target has 2: speculative decoding needs two models of "
+        "the same family with the same tokenizer (e.g. Qwen3-0.6B for Qwen3-8B)")
+    assert vocab_mismatch(a, _Meta(["a", "cé"], [1, 1])) == (
+        "the draft model's tokenizer differs from the target's (first difference at token id 1: \"b\" vs \"cé\"): "
+        "speculative decoding needs the same vocabulary")
+    assert vocab_mismatch(a, _Meta(["a", "b"], [1, 3])) == (
+        "the draft model's tokenizer differs from the target's (the token types differ): speculative decoding needs "
+        "the same vocabulary")
+    assert vocab_mismatch(_Meta(["a", "b"], [1, 1], vocab=2), _Meta(["a", "b"], [1, 1], vocab=3)) == \
+        "the models disagree on the logits vocabulary size (2 vs 3)"
+
+
+def test_synthetic_pair_files_share_a_vocabulary(tmp_path):
+    from zerollm_amd.speculative import vocab_mismatch
+
+    t, d = synth.tiny_pair()
+    tp, dp = str(tmp_path / "t.gguf"), str(tmp_path / "d.gguf")
+    synth.write_gguf(tp, t)
+    synth.write_gguf(dp, d)
+    assert vocab_mismatch(G.read_gguf(tp), G.read_gguf(dp)) is None

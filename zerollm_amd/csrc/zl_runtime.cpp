@@ -423,11 +423,11 @@ static void finish_model(zl_model *m, const float *ropeFreqs) {
 struct SegSpec { const DevMat *m; float *out; int ldo; const float *bias; };
 
 // Arguments of one GEMV launch over `segs` (laid end to end in tile order; SWIGLU: gate, up on the same tiles).
-static GemvArgs gemv_args(const std::vector<SegSpec> &segs, int B, int epi, const Act &act, const GemvWork &gw) {
+static GemvArgs gemv_args(const SegSpec *segs, int nseg, int B, int epi, const Act &act, const GemvWork &gw) {
   GemvArgs a;
   memset(&a, 0, sizeof(a));
-  ZL_REQUIRE(segs.size() >= 1 && segs.size() <= 3, ZL_ERR_ARG, "gemv: 1 to 3 matrices per launch");
-  a.nseg = (int)segs.size();
+  ZL_REQUIRE(nseg >= 1 && nseg <= 3, ZL_ERR_ARG, "gemv: 1 to 3 matrices per launch");
+  a.nseg = nseg;
   int t0 = 0;
   for (int i = 0; i < a.nseg; i++) {
     const DevMat &mm = *segs[i].m;
@@ -457,6 +457,9 @@ static GemvArgs gemv_args(const std::vector<SegSpec> &segs, int B, int epi, cons
   a.part = gw.part;
   a.cnt = gw.cnt;
   return a;
+}
+static GemvArgs gemv_args(const std::vector<SegSpec> &segs, int B, int epi, const Act &act, const GemvWork &gw) {
+  return gemv_args(segs.data(), (int)segs.size(), B, epi, act, gw);
 }
 
 // One GEMV launch of the model's pass reading quantised activation `act` (float weights: the f32 rows xf, stride ldx).

@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import ctypes as C
 import hashlib
+import json
 import time
 
 import numpy as np
@@ -22,11 +23,13 @@ DEFAULT_DRAFT_K = 3  # src/model/speculative.js:248
 
 
 def generate_speculative(target, draft, prompt_ids, k=4, max_tokens=256, sample=None, stop_ids=(), signal=None,
-                         stats=None, penalize_prompt=True, on_prefill_progress=None):
+                         stats=None, penalize_prompt=True, on_prefill_progress=None, cycle_log=None):
     """Yield token ids after prompt_ids using `draft` to propose k tokens per cycle and `target` to verify them.
     Same contract as generateSpeculative: greedy output equals plain greedy decoding; sampled output has the target's
     distribution; stats gets promptTokens, cachedTokens, prefillMs, decodeMs, generated, stopReason and
-    speculative = {k, cycles, drafted, accepted, acceptRate, tokensPerCycle, cycleMs, acceptedHist, effectiveTps}."""
+    speculative = {k, cycles, drafted, accepted, acceptRate, tokensPerCycle, cycleMs, acceptedHist, effectiveTps}.
+    cycle_log (not in the reference): a list that receives one (kk, drafted, accepted, token) tuple per cycle, the
+    decisions the device took."""
     if sample is None:
         sample = HipSampler(argmax=True)
     greedy = sample.greedy
@@ -117,6 +120,8 @@ def generate_speculative(target, draft, prompt_ids, k=4, max_tokens=256, sample=
             spec["drafted"] += kk
             spec["accepted"] += a
             spec["acceptedHist"][a] += 1
+            if cycle_log is not None:
+                cycle_log.append((kk, tuple(drafted), a, tok))
             # ---- emit and roll back (:212-226)
             emit = drafted[:a] + [tok]
             done = False
@@ -186,7 +191,10 @@ def vocab_mismatch(target, draft):
         i = 0
         while i < len(ta) and i < len(tb) and ta[i] == tb[i]:
             i += 1
-        detail = f" (first difference at token id {i}: {ta[i]!r} vs {tb[i] if i < len(tb) else None!r})" if i < len(ta) else " (the token types differ)"
+        # JSON.stringify of the two token strings, as the reference formats them
+        detail = (f" (first difference at token id {i}: {json.dumps(ta[i], ensure_ascii=False)} vs "
+                  f"{json.dumps(tb[i], ensure_ascii=False) if i < len(tb) else 'undefined'})") if i < len(ta) \
+            else " (the token types differ)"
         return f"the draft model's tokenizer differs from the target's{detail}: speculative decoding needs the same vocabulary"
     arch_a = target.get("general.architecture")
     arch_b = draft.get("general.architecture")

@@ -121,10 +121,13 @@ class ModelSpec:
 
 
 def build_spec(arch, n_embd, n_layer, n_head, n_head_kv, head_dim, n_ff, vocab, ctx_train, types, seed, std=0.02,
-               embd_from=None, name="synthetic", norm_value=1.0) -> ModelSpec:
+               embd_from=None, name="synthetic", norm_value=1.0, layer_std=None) -> ModelSpec:
     """types: dict with keys embd, output, q, k, v, o, gate, up, down (ggml type ids).
     embd_from: (seed, src_cols) to take token_embd / output values from another model's tensors (their first n_embd
-    columns), e.g. a draft that shares the target's embedding and output head."""
+    columns), e.g. a draft that shares the target's embedding and output head.
+    layer_std: std of the per-layer matrices (default std); a smaller value keeps the residual stream close to the
+    embedding, so a draft made of the first layers agrees with the target more often."""
+    lstd = std if layer_std is None else layer_std
     s = ModelSpec(arch, n_embd, n_layer, n_head, n_head_kv, head_dim, n_ff, vocab, ctx_train, name=name)
     qd, kvd = n_head * head_dim, n_head_kv * head_dim
 
@@ -133,7 +136,8 @@ def build_spec(arch, n_embd, n_layer, n_head, n_head_kv, head_dim, n_ff, vocab, 
             src_seed, src_cols = embd_from
             s.tensors.append(TensorSpec(nm, types[key], rows, cols, tensor_seed(src_seed, nm), std, src_cols, 0))
         else:
-            s.tensors.append(TensorSpec(nm, types[key], rows, cols, tensor_seed(seed, nm), std))
+            sd = std if nm in ("token_embd.weight", "output.weight") else lstd
+            s.tensors.append(TensorSpec(nm, types[key], rows, cols, tensor_seed(seed, nm), sd))
 
     def vec(nm, n):
         s.tensors.append(TensorSpec(nm, gguf.F32, 1, n, fill=True, fill_value=norm_value))
@@ -264,11 +268,12 @@ Q4_K_M = dict(embd=gguf.Q4_K, output=gguf.Q6_K, q=gguf.Q4_K, k=gguf.Q4_K, v=gguf
               up=gguf.Q4_K, down=gguf.Q6_K)
 
 
-def tiny_pair(seed=1, draft_layers=2, quant=gguf.Q8_0):
+def tiny_pair(seed=1, draft_layers=2, quant=gguf.Q8_0, layer_std=None, n_embd=512):
     """Tiny qwen3 target (4 layers, d 512, 8/4 heads, hd 64, FFN 1536, vocab 32000, theta 1e6, all Q8_0, norms 1.0)
-    and a draft made of its first 2 layers plus the same embedding / output head (same seed, so identical tensors)."""
-    kw = dict(arch="qwen3", n_embd=512, n_head=8, n_head_kv=4, head_dim=64, n_ff=1536, vocab=32000, ctx_train=2048,
-              types=all_type(quant), seed=seed)
+    and a draft made of its first 2 layers plus the same embedding / output head (same seed, so identical tensors).
+    layer_std: see build_spec; n_embd: another model width (the heads stay 8 / 4 of 64)."""
+    kw = dict(arch="qwen3", n_embd=n_embd, n_head=8, n_head_kv=4, head_dim=64, n_ff=1536, vocab=32000, ctx_train=2048,
+              types=all_type(quant), seed=seed, layer_std=layer_std)
     return build_spec(n_layer=4, name="tiny-target", **kw), build_spec(n_layer=draft_layers, name="tiny-draft", **kw)
 
 
