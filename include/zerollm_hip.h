@@ -193,6 +193,15 @@ int zl_mat_dequant(zl_mat *m, int64_t row0, int64_t nrows, float *out);
 int zl_mat_gemv(zl_mat *m, const float *x, int M, float *y);
 /* Time `iters` GEMVs with M device-resident tokens, cycling through the copies; returns mean ms per call. */
 int zl_mat_gemv_time(zl_mat *m, int M, int iters, float *ms_per_call);
+/* zl_mat_gemv with nothing allocated. No counterpart in the reference: for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). x: M x cols f32 rows and y:
+ * M x rows f32, both in device memory. The activation quantisation and the split-K partial sums use one static device
+ * array per GPU (under 8 MiB, held until the process ends): at most 16 tokens of at most 16384 values, and matrices
+ * whose split-K partials fit 6 MiB; larger requests fail with ZL_ERR_ARG. stream: a hipStream_t to enqueue on (the
+ * call returns at once; the caller synchronises), or NULL for the matrix's own stream (the call returns when y holds
+ * the result). Every call on one GPU shares the array, so calls that overlap on a GPU race. Same kernels, same bits
+ * as zl_mat_gemv. */
+int zl_mat_gemv_noalloc(zl_mat *m, const float *x, int M, float *y, void *stream);
 /* quantizeAct of M rows of length K (src/compute/ref-kernels.js:44-62). */
 int zl_quant_act(const float *x, int64_t K, int M, int8_t *q, float *d, int32_t *s);
 

@@ -100,6 +100,7 @@ SIGNATURES = [
     ("zl_mat_dequant", C.c_int, [P, C.c_int64, C.c_int64, F32P]),
     ("zl_mat_gemv", C.c_int, [P, F32P, C.c_int, F32P]),
     ("zl_mat_gemv_time", C.c_int, [P, C.c_int, C.c_int, F32P]),
+    ("zl_mat_gemv_noalloc", C.c_int, [P, P, C.c_int, P, P]),
     ("zl_quant_act", C.c_int, [F32P, C.c_int64, C.c_int, C.POINTER(C.c_int8), F32P, I32P]),
     ("zl_probe_gemv", C.c_int, [P, C.c_int, C.c_int, C.c_int, F32P, C.POINTER(C.c_int64)]),
 ]

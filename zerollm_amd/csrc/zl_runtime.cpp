@@ -12,6 +12,7 @@
 #include <map>
 #include <set>
 #include <memory>
+#include <mutex>
 #include <thread>
 #include <vector>
 
@@ -1348,6 +1349,85 @@ static void spec_cycle(zl_model *T, zl_model *D, zl_sampler *s, const int32_t *f
   }
 }
 
+// ---------------------------------------------------------------------------------------------- static work space
+// The work space of zl_mat_gemv_noalloc, for callers that cannot allocate device memory: the quantised activation
+// rows (int8 values, scales, sums, the per-block records and the f32 copy that float weights read) and the split-K
+// partial sums and arrival counters of one GEMV. One array per GPU, held until the process ends; every call on a GPU
+// shares it and leaves its contents behind, so calls that overlap on one GPU race.
+constexpr int NOALLOC_MAX_M = 16;        // tokens per call
+constexpr int NOALLOC_MAX_K = 16384;     // values per row
+constexpr size_t NOALLOC_PART_DOUBLES = 786432;  // 6 MiB of split-K partial sums
+constexpr size_t al256(size_t n) { return (n + 255) / 256 * 256; }
+constexpr size_t NOALLOC_BLOCKS = (size_t)NOALLOC_MAX_M * (NOALLOC_MAX_K / 32);
+constexpr size_t NOALLOC_OFF_Q = 0;
+constexpr size_t NOALLOC_OFF_F = NOALLOC_OFF_Q + al256((size_t)NOALLOC_MAX_M * NOALLOC_MAX_K);
+constexpr size_t NOALLOC_OFF_D = NOALLOC_OFF_F + al256((size_t)NOALLOC_MAX_M * NOALLOC_MAX_K * 4);
+constexpr size_t NOALLOC_OFF_S = NOALLOC_OFF_D + al256(NOALLOC_BLOCKS * 4);
+constexpr size_t NOALLOC_OFF_RA = NOALLOC_OFF_S + al256(NOALLOC_BLOCKS * 4);
+constexpr size_t NOALLOC_OFF_RB = NOALLOC_OFF_RA + al256(NOALLOC_BLOCKS * sizeof(RecA));
+constexpr size_t NOALLOC_OFF_RC = NOALLOC_OFF_RB + al256(NOALLOC_BLOCKS * sizeof(RecB));
+constexpr size_t NOALLOC_OFF_PART = NOALLOC_OFF_RC + al256(NOALLOC_BLOCKS * sizeof(RecC));
+constexpr size_t NOALLOC_OFF_CNT = NOALLOC_OFF_PART + al256(NOALLOC_PART_DOUBLES * 8);
+constexpr size_t NOALLOC_BYTES = NOALLOC_OFF_CNT + al256((size_t)GEMV_CNT_TILES * 4);
+static_assert(NOALLOC_BYTES <= (8u << 20), "the static work space stays within 8 MiB");
+
+static __device__ __align__(256) unsigned char scratch[NOALLOC_BYTES];
+
+// Device address of `scratch` on each GPU (the host-side name is not a device address: host code uses these).
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static unsigned char *g_scratch[NOALLOC_MAX_DEVICES];
+
+// Set-up, once per GPU with that GPU current: look up the array's address and clear the arrival counters (each
+// split-K launch's last workgroup resets its own counters, so they stay zero between calls).
+static unsigned char *noalloc_scratch() {
+  int dev = -1;
+  ZL_HIP(hipGetDevice(&dev));
+  ZL_REQUIRE(dev >= 0 && dev < NOALLOC_MAX_DEVICES, ZL_ERR_UNSUPPORTED, "static work space: device index out of range");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void *p = nullptr;
+    ZL_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    ZL_REQUIRE(p != nullptr, ZL_ERR_HIP, "static work space: no device address");
+    unsigned char *b = (unsigned char *)p;
+    launch_fill((float *)(b + NOALLOC_OFF_CNT), GEMV_CNT_TILES, 0.0f, nullptr);  // 0.0f is all-zero bits
+    ZL_HIP(hipStreamSynchronize(nullptr));
+    g_scratch[dev] = b;
+  }
+  return g_scratch[dev];
+}
+
+// zl_mat_gemv on device rows with the static work space: the same kernels (activation quantisation, then the GEMV
+// dispatch of launch_gemv) as zl_mat_gemv, so the results are the same bits.
+static void mat_gemv_noalloc(zl_mat *m, const float *x, int M, float *y, hipStream_t st) {
+  const DevMat &mm = m->copies[0];
+  ZL_REQUIRE(M >= 1 && M <= NOALLOC_MAX_M && mm.cols <= NOALLOC_MAX_K, ZL_ERR_ARG,
+             "zl_mat_gemv_noalloc: at most " + std::to_string(NOALLOC_MAX_M) + " tokens of at most " +
+                 std::to_string(NOALLOC_MAX_K) + " values (asked for " + std::to_string(M) + " of " +
+                 std::to_string(mm.cols) + ")");
+  unsigned char *b = noalloc_scratch();
+  const int ld = pad64(mm.cols);
+  Act act{};
+  act.ld = ld;
+  act.q = (int8_t *)(b + NOALLOC_OFF_Q);
+  act.f = (float *)(b + NOALLOC_OFF_F);
+  act.d = (float *)(b + NOALLOC_OFF_D);
+  act.s = (int32_t *)(b + NOALLOC_OFF_S);
+  act.ra = (RecA *)(b + NOALLOC_OFF_RA);
+  act.rb = (RecB *)(b + NOALLOC_OFF_RB);
+  act.rc = (RecC *)(b + NOALLOC_OFF_RC);
+  GemvWork gw;
+  gw.part = (double *)(b + NOALLOC_OFF_PART);
+  gw.cnt = (uint32_t *)(b + NOALLOC_OFF_CNT);
+  const SegSpec seg{&mm, y, mm.rows, nullptr};
+  const GemvArgs a = gemv_args(&seg, 1, M, EPI_STORE, act, gw);
+  ZL_REQUIRE(a.ks == 1 || (a.ntiles <= GEMV_CNT_TILES &&
+                           (size_t)a.ntiles * a.ks * 2 * GEMV_MAX_MT * 64 <= NOALLOC_PART_DOUBLES),
+             ZL_ERR_ARG, "zl_mat_gemv_noalloc: this matrix's split-K partial sums exceed the static work space");
+  launch_norm_quant(x, mm.cols, 0, M, nullptr, 0.0, mm.cols, ld, act, st);
+  launch_gemv(a, EPI_STORE, act.f, act.ld, st);
+}
+
 }  // namespace zl
 
 // ================================================================================================ C ABI
@@ -1378,6 +1458,7 @@ int zl_init(int device) {
   ZL_REQUIRE(device >= 0 && device < n, ZL_ERR_ARG, "no such GPU: " + std::to_string(device));
   ZL_HIP(hipSetDevice(device));
   g_device = device;
+  noalloc_scratch();
   ZL_API_END
 }
 
@@ -1746,6 +1827,15 @@ int zl_mat_gemv_time(zl_mat *m, int M, int iters, float *ms_per_call) {
   for (int i = 0; i < nc; i++) probe_gemv(m->copies[i], pa, M, dy, m->st);  // warm-up (outside capture)
   const float ms = time_graph(m->st, iters, [&](int i) { probe_gemv(m->copies[i % nc], pa, M, dy, m->st); });
   *ms_per_call = ms;
+  ZL_API_END
+}
+
+int zl_mat_gemv_noalloc(zl_mat *m, const float *x, int M, float *y, void *stream) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(m && x && y, ZL_ERR_ARG, "bad argument");
+  hipStream_t st = stream ? (hipStream_t)stream : m->st;
+  mat_gemv_noalloc(m, x, M, y, st);
+  if (!stream) ZL_HIP(hipStreamSynchronize(st));
   ZL_API_END
 }
 
