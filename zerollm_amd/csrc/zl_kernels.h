@@ -158,6 +158,10 @@ void gemv_shape(int ntiles, int nslab, bool swiglu, int *ks, int *nw);
 void launch_gemv(const GemvArgs &a, int epi, const float *xf, int ldx, hipStream_t st);
 bool gemv_mfma_ok(const GemvArgs &a);
 void launch_gemv_mfma(const GemvArgs &a, int epi, hipStream_t st);
+// Single-token Q8_0 GEMV in 16-row groups (zl_gemv_rg.hip): takes f32 input rows (a.xf, RMSNorm'd with a.nw when set)
+// and quantises them itself; K <= 3072.
+bool gemv_rg_ok(const GemvArgs &a);
+void launch_gemv_rg(const GemvArgs &a, int epi, hipStream_t st);
 template <int FMT>
 void launch_gemv_fmt(const GemvArgs &a, int epi, hipStream_t st);
 

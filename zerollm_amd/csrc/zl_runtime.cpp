@@ -463,8 +463,25 @@ static GemvArgs gemv_args(const std::vector<SegSpec> &segs, int B, int epi, cons
   return gemv_args(segs.data(), (int)segs.size(), B, epi, act, gw);
 }
 
+// Single-token launches of Q8_0 matrices take the 16-row-group kernel (zl_gemv_rg.hip), which quantises its f32 input
+// itself; ZEROLLM_GEMV_RG=0 keeps them on the tile kernels (timing comparisons).
+static bool use_rg() {
+  static const bool on = [] {
+    const char *e = getenv("ZEROLLM_GEMV_RG");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+static bool rg_path(const std::vector<const DevMat *> &ms, int B) {
+  if (!use_rg() || B != 1) return false;
+  for (const DevMat *d : ms)
+    if (d->type != T_Q8_0 || d->nslab > 48) return false;
+  return true;
+}
+
 // One GEMV launch of the model's pass reading quantised activation `act` (float weights: the f32 rows xf, stride ldx).
-// RESID adds into x; SWIGLU writes hb and, with qout set, its quantisation.
+// RESID adds into x; SWIGLU writes hb and, with qout set, its quantisation. A single-token Q8_0 launch reads the f32
+// rows xf instead and quantises them itself.
 static void gemv_group(zl_model *m, const std::vector<SegSpec> &segs, int B, int epi, const Act &act, const float *xf,
                        int ldx, const Act *qout = nullptr) {
   GemvArgs a = gemv_args(segs, B, epi, act, m->gw);
@@ -473,6 +490,14 @@ static void gemv_group(zl_model *m, const std::vector<SegSpec> &segs, int B, int
   a.hb = m->hb;
   a.ldh = m->cfg.n_ff;
   if (qout) a.qout = *qout;
+  std::vector<const DevMat *> ms;
+  for (const SegSpec &sg : segs) ms.push_back(sg.m);
+  if (rg_path(ms, B) && xf) {
+    a.xf = xf; a.ldxf = ldx; a.xrow0 = 0; a.n = segs[0].m->cols; a.nw = nullptr; a.eps = 0.0;
+    a.qout = Act{};
+    launch_gemv_rg(a, epi, m->st);
+    return;
+  }
   launch_gemv(a, epi, xf, ldx, m->st);
 }
 
@@ -494,17 +519,20 @@ constexpr long FUSE_MAX_VALUES = 4096;
 // With norm unset the k_norm_quant launch is left out (m->act already holds these rows: GEMV timing probes).
 static void gemv_rows(zl_model *m, const std::vector<std::vector<SegSpec>> &groups, const std::vector<int> &epis, int B,
                       const Prologue &p, const Act *qout = nullptr, bool norm = true) {
-  std::vector<bool> fused(groups.size());
+  std::vector<bool> fused(groups.size()), rg(groups.size());
   bool need = false;
   for (size_t i = 0; i < groups.size(); i++) {
     bool q = true;
     int tiles = 0;
+    std::vector<const DevMat *> ms;
     for (size_t k = 0; k < groups[i].size(); k++) {
       q = q && is_quant(groups[i][k].m->type);
       if (epis[i] != EPI_SWIGLU || k == 0) tiles += tiles_of(groups[i][k].m->rows);
+      ms.push_back(groups[i][k].m);
     }
-    fused[i] = q && tiles < 256 && (long)B * pad64(p.n) <= FUSE_MAX_VALUES;
-    need = need || !fused[i];
+    rg[i] = norm && rg_path(ms, B);
+    fused[i] = !rg[i] && q && tiles < 256 && (long)B * pad64(p.n) <= FUSE_MAX_VALUES;
+    need = need || !(fused[i] || rg[i]);
   }
   if (need && norm) norm_quant(m, p.x, p.ldx, p.row0, B, p.nw, p.n, m->act);
   for (size_t i = 0; i < groups.size(); i++) {
@@ -513,11 +541,12 @@ static void gemv_rows(zl_model *m, const std::vector<std::vector<SegSpec>> &grou
     a.ldr = m->cfg.n_embd;
     a.hb = m->hb;
     a.ldh = m->cfg.n_ff;
-    if (qout && epis[i] == EPI_SWIGLU) a.qout = *qout;
-    if (fused[i]) {
+    if (qout && epis[i] == EPI_SWIGLU && !rg[i]) a.qout = *qout;
+    if (fused[i] || rg[i]) {
       a.xf = p.x; a.ldxf = p.ldx; a.xrow0 = p.row0; a.n = p.n; a.nw = p.nw; a.eps = (double)m->cfg.rms_eps;
     }
-    launch_gemv(a, epis[i], m->act.f, m->act.ld, m->st);
+    if (rg[i]) launch_gemv_rg(a, epis[i], m->st);
+    else launch_gemv(a, epis[i], m->act.f, m->act.ld, m->st);
   }
 }
 
@@ -579,11 +608,13 @@ static void enqueue_forward(zl_model *m, int B, int want) {
       gemv_group(m, {{&L.wo, nullptr, 0, nullptr}}, B, EPI_RESID, m->act, m->act.f, m->act.ld);
     }
     ZL_REQUIRE(L.wgate.type == L.wup.type, ZL_ERR_UNSUPPORTED, "ffn_gate and ffn_up must share a type");
-    // the gate/up launch quantises hb for a quantised down matrix itself; otherwise it is quantised here
+    // the gate/up launch quantises hb for a quantised down matrix itself; otherwise it is quantised here (a
+    // single-token Q8_0 down launch quantises hb itself, and a single-token Q8_0 gate/up launch does not quantise it)
     const bool qdown = is_quant(L.wdown.type), fusedq = qdown && is_quant(L.wgate.type);
+    const bool guRg = rg_path({&L.wgate, &L.wup}, B), dnRg = rg_path({&L.wdown}, B);
     gemv_rows(m, {{{&L.wgate, nullptr, 0, nullptr}, {&L.wup, nullptr, 0, nullptr}}}, {EPI_SWIGLU}, B,
-              Prologue{m->x, d, 0, L.ffnNorm, d}, fusedq ? &m->act2 : nullptr);
-    if (qdown && !fusedq) norm_quant(m, m->hb, ff, 0, B, nullptr, ff, m->act2);
+              Prologue{m->x, d, 0, L.ffnNorm, d}, fusedq && !guRg ? &m->act2 : nullptr);
+    if (qdown && !dnRg && (!fusedq || guRg)) norm_quant(m, m->hb, ff, 0, B, nullptr, ff, m->act2);
     gemv_group(m, {{&L.wdown, nullptr, 0, nullptr}}, B, EPI_RESID, m->act2, m->hb, ff);
   }
   if (want == 2) gemv_rows(m, {{{&m->output, m->logits, c.vocab, nullptr}}}, {EPI_STORE}, B, Prologue{m->x, d, 0, m->outputNorm, d});
@@ -1420,10 +1451,15 @@ static void mat_gemv_noalloc(zl_mat *m, const float *x, int M, float *y, hipStre
   gw.part = (double *)(b + NOALLOC_OFF_PART);
   gw.cnt = (uint32_t *)(b + NOALLOC_OFF_CNT);
   const SegSpec seg{&mm, y, mm.rows, nullptr};
-  const GemvArgs a = gemv_args(&seg, 1, M, EPI_STORE, act, gw);
+  GemvArgs a = gemv_args(&seg, 1, M, EPI_STORE, act, gw);
   ZL_REQUIRE(a.ks == 1 || (a.ntiles <= GEMV_CNT_TILES &&
                            (size_t)a.ntiles * a.ks * 2 * GEMV_MAX_MT * 64 <= NOALLOC_PART_DOUBLES),
              ZL_ERR_ARG, "zl_mat_gemv_noalloc: this matrix's split-K partial sums exceed the static work space");
+  if (use_rg() && M == 1 && mm.type == T_Q8_0 && mm.nslab <= 48) {  // the probe's single-token path (no quantisation pass)
+    a.xf = x; a.ldxf = mm.cols; a.xrow0 = 0; a.n = mm.cols; a.nw = nullptr; a.eps = 0.0;
+    launch_gemv_rg(a, EPI_STORE, st);
+    return;
+  }
   launch_norm_quant(x, mm.cols, 0, M, nullptr, 0.0, mm.cols, ld, act, st);
   launch_gemv(a, EPI_STORE, act.f, act.ld, st);
 }
@@ -1796,9 +1832,20 @@ static void probe_act(ProbeAct &pa, const float *x, int64_t K, int M, hipStream_
   launch_norm_quant(pa.x, (int)K, 0, M, nullptr, 0.0, (int)K, ld, pa.act, st);
 }
 
+// A probe GEMV of M rows x (f32, stride = cols; quantised into act) as the model's passes run it: a single-token Q8_0
+// launch takes the 16-row-group kernel on the f32 rows, everything else the tile kernels on act.
+static void launch_probe_gemv(const DevMat &mm, const float *x, const Act &act, const GemvWork &gw, int M, float *y,
+                              hipStream_t st) {
+  GemvArgs a = gemv_args({{&mm, y, mm.rows, nullptr}}, M, EPI_STORE, act, gw);
+  if (rg_path({&mm}, M)) {
+    a.xf = x; a.ldxf = mm.cols; a.xrow0 = 0; a.n = mm.cols; a.nw = nullptr; a.eps = 0.0;
+    launch_gemv_rg(a, EPI_STORE, st);
+    return;
+  }
+  launch_gemv(a, EPI_STORE, act.f, act.ld, st);
+}
 static void probe_gemv(const DevMat &mm, const ProbeAct &pa, int M, float *y, hipStream_t st) {
-  GemvArgs a = gemv_args({{&mm, y, mm.rows, nullptr}}, M, EPI_STORE, pa.act, pa.gw);
-  launch_gemv(a, EPI_STORE, pa.act.f, pa.act.ld, st);
+  launch_probe_gemv(mm, pa.x, pa.act, pa.gw, M, y, st);
 }
 
 int zl_mat_gemv(zl_mat *m, const float *x, int M, float *y) {
