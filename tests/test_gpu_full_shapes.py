@@ -1,0 +1,169 @@
+"""GPU checks at the benchmark configurations' full shapes (test/spec-logits.test.js:13-38, 97-139 and
+test/spec-generate.test.js:29-59 are the reference's versions of these checks):
+- the Qwen3-8B-shaped Q4_K_M target and Qwen3-0.6B-shaped Q8_0 draft (headline configuration): a 5-row verify pass
+  equals 5 single-token passes bit for bit, the first verify rows of both models match the oracle, and greedy
+  speculative decoding equals plain greedy decoding;
+- the same pair at a 16384-token context (long-context configuration): a 9-row verify pass equals 9 single-token
+  passes, rollback leaves what a fresh continuation computes, and seeded stochastic k = 8 runs reproduce;
+- the Qwen3.5-4B-shaped hybrid after a 2048-token prefix: a 5-row verify pass equals 5 single-token passes (logits and
+  recurrent state), and rollback by snapshot restore + replay equals the sequential state.
+The oracle cannot run 16K or 2048-token contexts of these models in seconds, so there the checks are the
+size-independent properties above; the oracle comparisons run on short prefixes of the same models."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from zerollm_amd import synth
+from zerollm_amd.generate import generate
+from zerollm_amd.sampler import HipSampler
+from zerollm_amd.speculative import generate_speculative
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def _oracle(spec, ctx=64):
+    arrays = {t.name: synth.tensor_bytes(t, use_device=True) for t in spec.tensors}
+    O.set_threads(16)
+    return O.OracleModel(O.ArraySource(spec, arrays), ctx=ctx, kv="f16", threads=16)
+
+
+@pytest.fixture(scope="module")
+def pair_8b():
+    t_spec, d_spec = synth.qwen3_8b_pair()
+    return t_spec, d_spec
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("which", ["target", "draft"])
+def test_c3_verify_rows_equal_single_passes_and_oracle(gpu, pair_8b, which):
+    spec = pair_8b[0] if which == "target" else pair_8b[1]
+    pre = synth.seeded_ids(4, 31, spec.vocab)
+    ver = synth.seeded_ids(5, 32, spec.vocab)
+    print(f"case c3 {which}: build", flush=True)
+    m = synth.build_on_device(spec, ctx=64, kv="f16")
+    m.forward_batch(pre, logits="none")
+    rows = m.forward_batch(ver, logits="all").copy()
+    m.truncate(len(pre))
+    seq = np.stack([m.forward(t).copy() for t in ver])
+    m.close()
+    assert (_bits(rows) == _bits(seq)).all(), "a 5-row verify pass must equal 5 single-token passes bit for bit"
+    print(f"case c3 {which}: oracle", flush=True)
+    ref = _oracle(spec)
+    for t in pre:
+        ref.forward(t, logits=False)
+    n_cmp = 3 if which == "target" else 5
+    want = np.stack([ref.forward(t) for t in ver[:n_cmp]])
+    ref.close()
+    got = rows[:n_cmp]
+    d = np.abs(got.astype(np.float64) - want)
+    exact = np.mean(_bits(got) == _bits(want))
+    print(f"c3 {which}: max-abs {d.max():.3g}, mean-abs {d.mean():.3g}, bit-exact {exact:.5f}", flush=True)
+    assert d.max() <= MAX_ABS and d.mean() <= MEAN_ABS
+    assert (got.argmax(1) == want.argmax(1)).all()
+    assert exact >= 0.999 and d.max() <= 1e-6 * np.abs(want).max()
+
+
+@pytest.mark.timeout(600)
+def test_c3_greedy_speculative_equals_plain_greedy(gpu, pair_8b):
+    t_spec, d_spec = pair_8b
+    p = synth.seeded_ids(32, 2024, t_spec.vocab)
+    print("case c3 speculative", flush=True)
+    t = synth.build_on_device(t_spec, ctx=128, kv="f16")
+    d = synth.build_on_device(d_spec, ctx=128, kv="f16")
+    st = {}
+    spec = list(generate_speculative(t, d, p, k=4, max_tokens=12, stats=st))
+    t.reset()
+    plain = list(generate(t, p, max_tokens=12))
+    assert spec == plain and len(spec) == 12
+    assert st["speculative"]["cycles"] >= 3
+    t.close()
+    d.close()
+
+
+@pytest.mark.timeout(900)
+def test_c4_16k_context_verify_rollback_and_sampling(gpu, pair_8b):
+    t_spec, d_spec = pair_8b
+    P = 16384
+    ctx = P + 64
+    prompt = synth.seeded_ids(P, 2025, t_spec.vocab)
+    ver = synth.seeded_ids(9, 33, t_spec.vocab)
+    print("case c4: build and prefill 16384 tokens", flush=True)
+    t = synth.build_on_device(t_spec, ctx=ctx, kv="f16")
+    d = synth.build_on_device(d_spec, ctx=ctx, kv="f16")
+    for i in range(0, P, 16):
+        t.forward_batch(prompt[i:i + 16], logits="none")
+        if i % 4096 == 0:
+            print(f"c4 target prefill {i}", flush=True)
+    # a 9-row verify pass (k = 8) equals nine single-token passes
+    rows = t.forward_batch(ver, logits="all").copy()
+    t.truncate(P)
+    seq = np.stack([t.forward(x).copy() for x in ver])
+    assert (_bits(rows) == _bits(seq)).all()
+    print("c4: 9-row verify == 9 single passes", flush=True)
+    # rollback after a verify pass: 3 rows accepted, then a continuation of 2 tokens equals the sequential one
+    t.truncate(P)
+    t.forward_batch(ver, logits="all")
+    t.truncate(P + 3)
+    cont = t.forward_batch([11, 12], logits="all").copy()
+    t.truncate(P)
+    for x in ver[:3]:
+        t.forward(x)
+    fresh = np.stack([t.forward(11).copy(), t.forward(12).copy()])
+    assert (_bits(cont) == _bits(fresh)).all()
+    print("c4: rollback == fresh continuation", flush=True)
+    # stochastic acceptance, k = 8, temperature 0.7, top-k 40, top-p 0.9: seeded runs reproduce token for token (the
+    # target keeps the prompt's cached prefix; the first run prefills the draft)
+    outs = []
+    for r in range(2):
+        s = HipSampler(temperature=0.7, top_k=40, top_p=0.9, seed=1234)
+        log, st = [], {}
+        outs.append((list(generate_speculative(t, d, prompt, k=8, max_tokens=12, sample=s, stats=st, cycle_log=log)),
+                     log, s.rng_state))
+        s.close()
+        print(f"c4: stochastic run {r}: {len(outs[-1][0])} tokens, {st['speculative']['cycles']} cycles", flush=True)
+    assert outs[0] == outs[1] and len(outs[0][0]) == 12
+    # every cycle consumed kk draft draws, one accept uniform per tested draft and one residual or bonus draw
+    for kk, drafted, a, tok in outs[0][1]:
+        assert 0 <= a <= kk <= 8 and len(drafted) == kk and 0 <= tok < t_spec.vocab
+    t.close()
+    d.close()
+
+
+@pytest.mark.timeout(600)
+def test_c5_4b_hybrid_2048_prefix_verify_state_and_rollback(gpu):
+    spec = synth.qwen35_4b()
+    P = 2048
+    pre = synth.seeded_ids(P, 41, spec.vocab)
+    ver = synth.seeded_ids(5, 42, spec.vocab)
+    print("case c5: build and prefill 2048 tokens", flush=True)
+    m = synth.build_on_device(spec, ctx=P + 64, kv="f16")
+    for i in range(0, P, 16):
+        m.forward_batch(pre[i:i + 16], logits="none")
+    conv0, ssm0 = m.recurrent_state()
+    m.mark_rollback()
+    rows = m.forward_batch(ver, logits="all").copy()
+    conv_b, ssm_b = m.recurrent_state()
+    # rollback to 2 accepted tokens: snapshot restore + replay of the 2 tokens
+    assert m.truncate(P + 2) == 2
+    conv_r, ssm_r = m.recurrent_state()
+    # the sequential path from the same state: restore the prefix state by truncating to P, then single tokens
+    m.truncate(P)
+    c_p, s_p = m.recurrent_state()
+    assert (c_p == conv0).all() and (s_p == ssm0).all()
+    seq = []
+    for i, x in enumerate(ver):
+        seq.append(m.forward(x).copy())
+        if i == 1:
+            conv_2, ssm_2 = m.recurrent_state()
+    conv_s, ssm_s = m.recurrent_state()
+    m.close()
+    assert (_bits(rows) == _bits(np.stack(seq))).all(), "5-row verify == 5 single-token passes"
+    assert (conv_b == conv_s).all() and (ssm_b == ssm_s).all(), "state after the verify == state after 5 passes"
+    assert (conv_r == conv_2).all() and (ssm_r == ssm_2).all(), "rollback to 2 accepted == 2 sequential passes"
+    print("c5: verify, state and rollback checks hold at a 2048-token prefix", flush=True)
