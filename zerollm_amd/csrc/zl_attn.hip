@@ -354,6 +354,100 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
   }
 }
 
+// ---- position-split weighted sum (long contexts). The exact chain above runs one dependent f32 step per position, so
+// at 16K positions it is ~40 us per output element. Here one block per (256-position chunk, query head, token) takes
+// the chunk's scores, its max m_c, e_t = exp(s_t - m_c) and l_c = sum e_t in f64, and o_c[i] = sum e_t V_t,i in f64
+// (V staged through LDS with coalesced loads); k_attn_merge then forms out_i = f32(sum_c w_c o_c[i] / sum_c w_c l_c),
+// w_c = exp(m_c - max_c m_c), adding the chunks in chunk order. Every order is a function of the position count only,
+// so batched and single-token passes agree bit for bit. The result is the softmax-weighted sum in f64, rounded once:
+// it differs from the reference's f32 chain (src/model/forward.js:134-139) by that chain's own rounding error.
+template <bool F16KV>
+__global__ __launch_bounds__(256) void k_attn_av_split(const AttnArgs a) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int VB = F16KV ? 2 : 4, C = ATTN_SPLIT_C, EPP = 16 / VB;
+  __shared__ double e[C];
+  __shared__ double redd[4];
+  __shared__ float redf[4];
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hd = a.hd, kvh = h / (a.nHead / a.nHeadKv), t0 = c * C;
+  const Step *st = a.step;
+  if (b >= st->B) return;
+  const int npos = st->pos0 + b + 1;
+  if (t0 >= npos) return;
+  const int cnt = min(C, npos - t0);
+  // V rows of the chunk [hd][C] (dimension-major cache rows), 16 bytes per load, consecutive threads along a row
+  const uint8_t *vbase = (const uint8_t *)a.vcache + ((long)a.layer * a.nHeadKv + kvh) * hd * a.vstride * VB;
+  // LDS row pitch of C * VB + 4 bytes (an odd number of words): the lanes of a wave, one dimension each, read the same
+  // position of consecutive rows from distinct banks
+  const int ppr = C / EPP, pitch = C * VB + 4;  // 16-byte pieces per row
+  for (int idx = tid; idx < hd * ppr; idx += 256) {
+    const int dim = idx / ppr, t = t0 + (idx % ppr) * EPP;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (t < npos) v = *(const uint4 *)(vbase + ((long)dim * a.vstride + t) * VB);
+    uint32_t *d = (uint32_t *)(lds + (long)dim * pitch + (idx % ppr) * 16);
+    d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+  }
+  const float *srow = a.scores + ((long)b * a.nHead + h) * a.sld + t0;
+  const float s = tid < cnt ? srow[tid] : -INFINITY;
+  float mx = group_fmax(s, 64);
+  if (lane == 0) redf[wave] = mx;
+  __syncthreads();
+  const float m = fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
+  const double ev = tid < cnt ? exp((double)s - (double)m) : 0.0;
+  e[tid] = ev;
+  double l = wave_sum_xor(ev, 64);
+  if (lane == 0) redd[wave] = l;
+  __syncthreads();
+  l = (redd[0] + redd[1]) + (redd[2] + redd[3]);
+  // o_c[i]: thread (i = tid mod hd, q = tid / hd) adds positions q, q + R, ... (R = 256 / hd), then the R partial sums
+  // meet in LDS in q order
+  const int R = 256 / hd, i = tid % hd, q = tid / hd;
+  double o = 0.0;
+  const uint8_t *row = lds + (long)i * pitch;
+  for (int t = q; t < cnt; t += R) {
+    const float v = F16KV ? h2f(((const uint16_t *)row)[t]) : ((const float *)row)[t];
+    o = fma(e[t], (double)v, o);
+  }
+  __syncthreads();  // the staged V is no longer read: its LDS holds the partial sums
+  double *po = (double *)lds;
+  po[tid] = o;
+  __syncthreads();
+  if (tid < hd) {
+    double tot = po[tid];
+    for (int k = 1; k < R; k++) tot += po[k * hd + tid];
+    double *dst = a.part + (((long)b * a.nHead + h) * a.nch + c) * (hd + 2);
+    dst[2 + tid] = tot;
+    if (tid == 0) { dst[0] = (double)m; dst[1] = l; }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_attn_merge(const AttnArgs a) {
+  const int h = blockIdx.x, b = blockIdx.y, i = threadIdx.x, hd = a.hd;
+  const Step *st = a.step;
+  if (b >= st->B || i >= hd) return;
+  const int npos = st->pos0 + b + 1, nch = (npos + ATTN_SPLIT_C - 1) / ATTN_SPLIT_C;
+  const double *pr = a.part + ((long)b * a.nHead + h) * a.nch * (hd + 2);
+  double M = -INFINITY;
+  for (int c = 0; c < nch; c++) M = fmax(M, pr[(long)c * (hd + 2)]);
+  double L = 0.0, O = 0.0;
+  for (int c = 0; c < nch; c++) {
+    const double *pc = pr + (long)c * (hd + 2);
+    const double w = exp(pc[0] - M);
+    L += w * pc[1];
+    O += w * pc[2 + i];
+  }
+  float o = (float)(O / L);
+  const int col = h * hd + i;
+  if (a.gate) {  // gated attention output (src/model/forward-qwen35.js:103): o * sigmoid(gate), f64, stored f32
+    const double g = (double)a.gate[(long)b * a.ldq + (long)h * a.qhs + i];
+    o = (float)((double)o * (1.0 / (1.0 + exp(-g))));
+  }
+  if (a.out) a.out[(long)b * a.ldo + col] = o;
+  quant_block32(o, col, a.act, b);
+}
+
+size_t attention_split_lds(int hd, int kvF16) { return (size_t)hd * (ATTN_SPLIT_C * (kvF16 ? 2 : 4) + 4); }
+
 // Dynamic LDS of one k_attn_av block: the probabilities of ctx positions and two staged V chunks.
 size_t attention_lds(int ctx) { return (size_t)((ctx + AV_UNIT - 1) / AV_UNIT * AV_UNIT) * 4 + 2 * AV_CHUNK; }
 constexpr size_t ATTN_LDS_MAX = 150 * 1024;
@@ -374,10 +468,21 @@ static void launch_av_k(const AttnArgs &a, dim3 grid, size_t lds, hipStream_t st
   hipLaunchKernelGGL((k_attn_av<F16KV>), grid, dim3(256), lds, st, a);
 }
 
+template <bool F16KV>
+static void launch_av_split_k(const AttnArgs &a, dim3 grid, size_t lds, hipStream_t st) {
+  static size_t attr = 64 * 1024;
+  if (lds > attr) {
+    ZL_HIP(hipFuncSetAttribute((const void *)k_attn_av_split<F16KV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    attr = lds;
+  }
+  hipLaunchKernelGGL((k_attn_av_split<F16KV>), grid, dim3(256), lds, st, a);
+}
+
 void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
   AttnArgs a = a0;
-  const size_t lds = attention_lds(a.ctx);
+  const size_t lds = a.part ? attention_split_lds(a.hd, a.kvF16) : attention_lds(a.ctx);
   ZL_REQUIRE(lds <= ATTN_LDS_MAX, ZL_ERR_UNSUPPORTED, "context too long for the attention kernel");
+  ZL_REQUIRE(!a.part || a.nch * ATTN_SPLIT_C >= a.ctx, ZL_ERR_ARG, "attention: split partials below the context");
   ZL_REQUIRE(a.hd == 64 || a.hd == 128 || a.hd == 256, ZL_ERR_UNSUPPORTED, "attention: head_dim must be 64, 128 or 256");
   ZL_REQUIRE(a.sld >= a.ctx, ZL_ERR_ARG, "attention: score stride below the context");
   ZL_REQUIRE(a.qhs >= a.hd && a.ldq >= a.nHead * a.qhs, ZL_ERR_ARG, "attention: query head stride below the head size");
@@ -394,6 +499,15 @@ void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
     case 513: launch_scores_k<256, true>(a, gs, B, st); break;
   }
   ZL_HIP(hipGetLastError());
+  if (a.part) {
+    const dim3 gv(a.nch, a.nHead, B);
+    if (a.kvF16) launch_av_split_k<true>(a, gv, lds, st);
+    else launch_av_split_k<false>(a, gv, lds, st);
+    ZL_HIP(hipGetLastError());
+    hipLaunchKernelGGL(k_attn_merge, dim3(a.nHead, B), dim3(std::max(64, a.hd)), 0, st, a);
+    ZL_HIP(hipGetLastError());
+    return;
+  }
   dim3 ga(a.hd / AV_DIMS, a.nHead, B);
   if (a.kvF16) launch_av_k<true>(a, ga, lds, st);
   else launch_av_k<false>(a, ga, lds, st);

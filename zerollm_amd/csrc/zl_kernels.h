@@ -126,7 +126,13 @@ struct AttnArgs {
   Act act;
   int qhs;              // floats from one query head to the next in q (hd; 2 hd where q rows are [query | gate])
   const float *gate;    // output gate (q + hd for [query | gate] rows, same strides), or null
+  // position-split weighted sum (long contexts): per (token, head, chunk of ATTN_SPLIT_C positions) the chunk's
+  // max score, f64 sum of exponentials and f64 weighted sum of V, [B][nHead][nch][hd + 2] doubles; null: the exact
+  // position-order f32 chain
+  double *part;
+  int nch;              // chunks per (token, head) row of part
 };
+constexpr int ATTN_SPLIT_C = 256;  // positions per chunk of the position-split weighted sum
 
 // One Gated DeltaNet layer over the B tokens of a pass (src/model/forward-qwen35.js:45-61). Conv window and delta-rule
 // matrices of the layer are read, advanced token by token and written back. The conv window is kept per value head:
@@ -249,6 +255,7 @@ __device__ inline double rms_scale256(const float *xr, int n, double eps, int ti
 
 void launch_attention(const AttnArgs &a, int B, hipStream_t st);
 size_t attention_lds(int ctx);
+size_t attention_split_lds(int hd, int kvF16);
 void launch_norm_quant(const float *x, int ldx, int row0, int nrows, const float *w, double eps, int n, int npad,
                        const Act &act, hipStream_t st);
 void launch_embed(const MatView &m, const Step *step, int B, float *x, int ldx, hipStream_t st);
