@@ -80,6 +80,8 @@ typedef struct {
   int64_t weight_bytes;      /* quantised matrix bytes streamed by one pass (all layers + output head) */
   int64_t device_bytes;      /* HBM held by the model */
   int64_t state_bytes;       /* recurrent state of a hybrid model (each snapshot holds as much); 0 otherwise */
+  int state_capture_slots;   /* hybrid: verify passes of up to this many tokens capture the state after each token,
+                                and zl_truncate into such a window copies it instead of replaying (0: restore + replay) */
 } zl_model_info;
 
 /* Load a GGUF model into HBM (RefModel/PoolModel construction: src/model/forward.js:105-153,
@@ -95,7 +97,9 @@ int zl_model_free(zl_model *m);
  * not NULL the logits are copied there (vocab or n*vocab floats); they also stay on the device for zl_sample. */
 int zl_forward(zl_model *m, const int32_t *tokens, int n, int logits_mode, float *host_logits);
 /* PoolModel.truncate (src/compute/pool.js:278-294): positional KV is bookkeeping only; a hybrid model restores the
- * nearest recurrent-state snapshot at or before n and replays the tokens in between (*replayed, may be NULL). */
+ * nearest recurrent-state snapshot at or before n and replays the tokens in between (*replayed, may be NULL). When the
+ * last pass returned every row's logits and n falls inside it, the state the pass captured after token n is copied
+ * instead (the same bits); *replayed and the checkpoints are what the reference's restore + replay leaves. */
 int zl_truncate(zl_model *m, int n, int *replayed);
 /* PoolModel.truncatePlan (src/compute/pool.js:256): the snapshot position truncate(n) restores and the replay count. */
 int zl_truncate_plan(const zl_model *m, int n, int *from, int *replay);

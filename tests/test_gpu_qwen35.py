@@ -211,3 +211,35 @@ def test_4b_shapes_verify_window_matches_oracle(gpu):
     np.testing.assert_allclose(conv, rconv, rtol=1e-4, atol=1e-5)
     np.testing.assert_allclose(ssm, rssm, rtol=1e-4, atol=1e-5)
     ref.close()
+
+
+def test_verify_window_capture_equals_restore_and_replay(gpu, monkeypatch):
+    """A verify pass (every row's logits) captures the recurrent state after each of its tokens, and a rollback into
+    the window copies the captured state instead of restoring the snapshot and replaying the accepted tokens
+    (src/compute/pool.js:278-294). Against the same model with capture off: the same replay count, checkpoint
+    positions, recurrent state and next-token logits, bit for bit, for every accepted count."""
+    spec = synth.tiny_qwen35(seed=23)
+    pre, ver = prompt(20, seed=31), prompt(5, seed=32)
+    models = {}
+    for mode, env in (("capture", "1"), ("replay", "0")):
+        monkeypatch.setenv("ZEROLLM_STATE_CAPTURE", env)
+        models[mode] = synth.build_on_device(spec, ctx=96, kv="f16")
+        models[mode].forward_batch(pre[:16], logits="none")
+        models[mode].forward_batch(pre[16:], logits="last")
+    for a in range(6):
+        print(f"case capture a={a}", flush=True)
+        out = {}
+        for mode, m in models.items():
+            m.truncate(len(pre))
+            m.mark_rollback()
+            m.forward_batch(ver, logits="all")
+            replayed = m.truncate(len(pre) + a)
+            conv, ssm = m.recurrent_state()
+            nxt = m.forward(7).copy()
+            out[mode] = (replayed, list(m.checkpoint_positions), conv, ssm, nxt)
+        c, r = out["capture"], out["replay"]
+        assert c[0] == r[0] and c[1] == r[1], (a, c[:2], r[:2])
+        assert (c[2] == r[2]).all() and (c[3] == r[3]).all()
+        assert (c[4].view(np.uint32) == r[4].view(np.uint32)).all()
+    for m in models.values():
+        m.close()

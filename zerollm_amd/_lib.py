@@ -42,7 +42,8 @@ class zl_config(C.Structure):
 
 class zl_model_info(C.Structure):
     _fields_ = [("ctx", C.c_int), ("max_batch", C.c_int), ("logits_batch", C.c_int), ("kv_f16", C.c_int),
-                ("weight_bytes", C.c_int64), ("device_bytes", C.c_int64), ("state_bytes", C.c_int64)]
+                ("weight_bytes", C.c_int64), ("device_bytes", C.c_int64), ("state_bytes", C.c_int64),
+                ("state_capture_slots", C.c_int)]
 
 
 class zl_synth_tensor(C.Structure):

@@ -42,6 +42,11 @@ __global__ __launch_bounds__(4 * D) void k_deltanet(const DeltaArgs a) {
       #pragma unroll
       for (int t = 0; t + 1 < M; t++) st[t] = st[t + 1];
       if (M > 0) st[M - 1] = cur;
+      if (a.capConv) {  // the window after token b
+        float *cw = a.capConv + (long)b * a.capStride + (((long)hv * 3 + grp) * D + i) * M;
+        #pragma unroll
+        for (int t = 0; t < M; t++) cw[t] = st[t];
+      }
       const float y = (float)(acc / (1.0 + exp(-acc)));
       if (grp == 0) cq[b * ROW + pidx(i)] = y;
       else if (grp == 1) ck[b * ROW + pidx(i)] = y;
@@ -95,6 +100,11 @@ __global__ __launch_bounds__(4 * D) void k_deltanet(const DeltaArgs a) {
     o += __shfl_xor(o, 1);
     o += __shfl_xor(o, 2);
     if (p == 0) core[b * D + j] = (float)o;
+    if (a.capSsm) {  // the state after token b
+      float *cs = a.capSsm + (long)b * a.capStride + ((long)hv * D + j) * D + p * PER;
+      #pragma unroll
+      for (int c = 0; c < PER; c += 4) *(float4 *)(cs + c) = make_float4(S[c], S[c + 1], S[c + 2], S[c + 3]);
+    }
   }
   #pragma unroll
   for (int c = 0; c < PER; c += 4) *(float4 *)(srow + c) = make_float4(S[c], S[c + 1], S[c + 2], S[c + 3]);
@@ -125,6 +135,7 @@ void launch_deltanet(const DeltaArgs &a0, int D, hipStream_t st) {
   ZL_REQUIRE(D == 32 || D == 64 || D == 128, ZL_ERR_UNSUPPORTED, "Gated DeltaNet: head size must be 32, 64 or 128");
   ZL_REQUIRE(a0.nK >= 1 && a0.nV >= 1 && a0.nV % a0.nK == 0, ZL_ERR_ARG, "Gated DeltaNet: value heads must be a multiple of key heads");
   ZL_REQUIRE(a0.act.ld >= a0.nV * D && a0.act.ld % 64 == 0, ZL_ERR_ARG, "Gated DeltaNet: activation rows too short");
+  ZL_REQUIRE(!a0.capConv || a0.B <= DELTA_MAX_B, ZL_ERR_ARG, "Gated DeltaNet: capture holds one launch of tokens");
   for (int t0 = 0; t0 < a0.B; t0 += DELTA_MAX_B) {
     DeltaArgs a = a0;
     a.B = std::min(DELTA_MAX_B, a0.B - t0);

@@ -154,6 +154,10 @@ struct DeltaArgs {
   Act act;             // the quantised core rows (input of ssm_out), columns hv * D + j
   float *out;          // and the f32 core rows (act.f), or null
   int ldo;
+  // per-position capture (verify passes): the layer's conv windows and delta-rule matrices after token b go to
+  // capConv / capSsm + b * capStride (floats; the same layout as conv / ssm), when set
+  float *capConv, *capSsm;
+  long capStride;
 };
 constexpr int DELTA_MAX_B = 16;  // tokens per k_deltanet launch (longer passes run as several launches in order)
 void launch_deltanet(const DeltaArgs &a, int D, hipStream_t st);

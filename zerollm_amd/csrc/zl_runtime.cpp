@@ -236,6 +236,10 @@ struct zl_model {
   int nAttn = 0, nRec = 0;
   long convFloats = 0, ssmFloats = 0;
   float *state = nullptr;
+  // per-position capture of the recurrent state in passes that return every row's logits (verify passes): slot b
+  // holds the state after the pass's token b (capPos0 + b + 1 tokens processed); capN valid slots (0: none)
+  float *capture = nullptr;
+  int capSlots = 0, capPos0 = 0, capN = 0;
   zl::Checkpoints ck;
   bool prevNoLogits = false;
   float *dqkv = nullptr, *dz = nullptr, *dalpha = nullptr, *dbeta = nullptr;
@@ -400,6 +404,11 @@ static void finish_model(zl_model *m, const float *ropeFreqs) {
     const size_t sb = (size_t)m->nRec * (m->convFloats + m->ssmFloats) * 4;
     m->state = (float *)m->ar.alloc(std::max<size_t>(sb, 16));
     zero_now(m->state, std::max<size_t>(sb, 16));
+    const char *ce = getenv("ZEROLLM_STATE_CAPTURE");
+    if (!(ce && ce[0] == '0') && sb > 0) {
+      m->capSlots = std::min(m->logitsBatch, DELTA_MAX_B);
+      m->capture = (float *)m->ar.alloc(sb * m->capSlots);
+    }
     m->dqkv = (float *)m->ar.alloc((size_t)B * convDim * 4);
     m->dz = (float *)m->ar.alloc((size_t)B * inner * 4);
     m->dalpha = (float *)m->ar.alloc((size_t)B * c.ssm_dt_rank * 4);
@@ -597,6 +606,12 @@ static void enqueue_forward(zl_model *m, int B, int want) {
       da.dtBias = L.dtBias; da.ssmA = L.ssmA; da.normW = L.ssmNorm;
       da.nK = c.ssm_n_group; da.nV = nV; da.K = c.ssm_conv_kernel; da.B = B; da.eps = eps;
       da.act = m->act; da.out = m->act.f; da.ldo = m->act.ld;
+      if (want == 2 && m->capture && B <= m->capSlots) {
+        const long stride = (long)m->nRec * (m->convFloats + m->ssmFloats);
+        da.capConv = m->capture + (long)L.ri * m->convFloats;
+        da.capSsm = m->capture + (long)m->nRec * m->convFloats + (long)L.ri * m->ssmFloats;
+        da.capStride = stride;
+      }
       launch_deltanet(da, D, m->st);
       gemv_group(m, {{&L.wssmout, nullptr, 0, nullptr}}, B, EPI_RESID, m->act, m->act.f, m->act.ld);
     } else {
@@ -670,8 +685,13 @@ static bool use_graphs() {
 
 // One pass; the caller has set m->dstep.
 static void launch_pass(zl_model *m, int B, int want) {
+  m->capN = 0;  // the pass moves the recurrent state: earlier captures no longer describe it
   if (use_graphs()) ZL_HIP(hipGraphLaunch(graph_for(m, B, want), m->st));
   else enqueue_forward(m, B, want);
+  if (want == 2 && m->capture && B <= m->capSlots) {
+    m->capPos0 = (int)m->tokens.size();
+    m->capN = B;
+  }
 }
 
 // Milliseconds per call of `enqueue` (which enqueues work on st), over `iters` calls captured into one HIP graph and
@@ -886,6 +906,21 @@ static int truncate_model(zl_model *m, int n) {
   ZL_REQUIRE(!m->closed, ZL_ERR_STATE, "model is closed");
   int from, replay;
   m->ck.plan(n, pos, &from, &replay);
+  // the state after n tokens was captured by the last verify pass: copy it instead of restore + replay (the same bits:
+  // the replay would run the same tokens from the same state). Only without boundary / periodic checkpoints, whose
+  // snapshots a replay would also take; the replay count, the checkpoint after it and the rollback slot are as the
+  // reference leaves them.
+  if (replay > 0 && m->capN > 0 && n > m->capPos0 && n <= m->capPos0 + m->capN && m->ck.boundary.empty() &&
+      m->ck.every == 0) {
+    m->ck.drop_after(n);
+    ZL_HIP(hipMemcpyAsync(m->state, m->capture + (size_t)(n - m->capPos0 - 1) * (state_bytes(m) / 4), state_bytes(m),
+                          hipMemcpyDeviceToDevice, m->st));
+    m->tokens.resize(n);
+    m->capN = n - m->capPos0;  // positions up to n keep their captured states
+    checkpoint(m);
+    m->prevNoLogits = false;
+    return replay;
+  }
   std::vector<int32_t> tail(m->tokens.begin() + from, m->tokens.begin() + n);
   m->ck.drop_after(n);
   restore_state(m, from);
@@ -1555,6 +1590,7 @@ int zl_model_info_get(const zl_model *m, zl_model_info *out) {
   out->ctx = m->ctx; out->max_batch = m->maxBatch; out->logits_batch = m->logitsBatch; out->kv_f16 = m->kvF16;
   out->weight_bytes = m->weightBytes; out->device_bytes = m->ar.bytes;
   out->state_bytes = m->hybrid ? (int64_t)state_bytes(m) : 0;
+  out->state_capture_slots = m->capture ? m->capSlots : 0;
   ZL_API_END
 }
 

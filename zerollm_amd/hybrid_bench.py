@@ -1,8 +1,10 @@
 """Hybrid (qwen35) verify-window benchmark: a Qwen3.5-4B-shaped Q4_K_M target (Gated DeltaNet + gated attention, the real
 file's tensor set) in HBM, a seeded 2048-token prefix prefilled, then cycles of the speculative-decoding target side:
 markRollback (recurrent-state snapshot), one 5-token verify pass with logits for every row, and truncate to the accepted
-length (snapshot restore + replay of the accepted tokens), as generateSpeculative drives a hybrid target
-(src/model/speculative.js:185, 226; src/compute/pool.js:269, 278-294).
+length, as generateSpeculative drives a hybrid target (src/model/speculative.js:185, 226; src/compute/pool.js:269,
+278-294). The verify pass captures the recurrent state after each of its tokens, so the truncate copies the captured
+state where the reference restores the snapshot and replays the accepted tokens (ZEROLLM_STATE_CAPTURE=0: restore +
+replay).
 
 Checks on the way (size-independent, exact): the verify rows equal five single-token passes, and a model rolled back to
 the accepted length holds the same recurrent state as one that only ran those tokens. Prints one JSON line.
@@ -93,7 +95,7 @@ def main(argv=None):
     sync(m)
     verify_ms = (time.perf_counter() - t0) * 1e3 / a.cycles
     # timed (b): whole target-side cycles as generateSpeculative drives a hybrid target: markRollback (snapshot), verify,
-    # truncate to the accepted length (restore + replay of the accepted tokens + a checkpoint there)
+    # truncate to the accepted length (the captured state, or restore + replay of the accepted tokens; a checkpoint there)
     t0 = time.perf_counter()
     for c in range(a.cycles):
         m.mark_rollback()
@@ -111,7 +113,9 @@ def main(argv=None):
         "verify_frac_hbm": round(wb / (verify_ms * 1e-3) / HBM_PEAK, 4),
         "note_verify": "includes one device copy of the recurrent state (restore from the rollback snapshot)",
         "cycle_ms": round(cycle_ms, 3), "accepted_per_cycle": a.accept,
-        "note_cycle": "markRollback snapshot + verify pass + restore + replay pass of the accepted tokens + checkpoint",
+        "note_cycle": ("markRollback snapshot + verify pass (capturing the state after each token) + copy of the captured "
+                       "state at the accepted length + checkpoint" if m.captures else
+                       "markRollback snapshot + verify pass + restore + replay pass of the accepted tokens + checkpoint"),
         "state_bytes": m.state_bytes, "checks": {"batched_equals_sequential": batched_equals_sequential,
                                                  "verify_state_equals_sequential": state_equal,
                                                  "rollback_equals_fresh": rollback_exact},

@@ -64,6 +64,7 @@ class HipModel:
         self.weight_bytes = info.weight_bytes
         self.device_bytes = info.device_bytes
         self.state_bytes = info.state_bytes
+        self.captures = info.state_capture_slots > 0  # rollbacks inside a verify window copy a captured state
         self.closed = False
         self._logits = np.empty((self.logits_batch, c.vocab), dtype=np.float32)
 
