@@ -2,11 +2,13 @@
 product never imports it).
 
 generateSpeculative (src/model/speculative.js:100-240) restated over oracle models: any object with forward(token,
-logits=True) -> f32 logits | None, truncate(n), tokens, pos, ctx and (optionally) mark_rollback(). The oracle models
-have no batched pass, so forwardRows falls back to one forward per token (src/model/speculative.js:39-48) and
-feedLogits feeds one token at a time (:51-61). Both the greedy path and speculative sampling are restated, with the
-single mulberry32 stream of the sampler consumed in the reference's order: draft draws x_1..x_kk (:173), then the
-accept uniforms (:203), then one residual draw (:204, drawResidual :75-87) or one bonus draw (:207-209).
+logits=True) -> f32 logits | None, truncate(n), tokens, pos, ctx and (optionally) mark_rollback(). A model with a batched
+pass (forward_batch(tokens, logits) and max_batch, as oracle.pool.SimdPoolModel) is driven as the reference drives a
+PoolModel: prefill and feedLogits in chunks of max_batch (src/model/generate.js:15-31, src/model/speculative.js:51-61) and
+the k + 1 verify rows in one pass (forwardRows, :39-48; verifyLimit, :25-28). The single-token oracle models fall back
+to one forward per token, as the reference does for RefModel. Both the greedy path and speculative sampling are
+restated, with the single mulberry32 stream of the sampler consumed in the reference's order: draft draws x_1..x_kk
+(:173), then the accept uniforms (:203), then one residual draw (:204, drawResidual :75-87) or one bonus draw (:207-209).
 """
 from __future__ import annotations
 
@@ -40,13 +42,48 @@ def _is_argmax(sample):
     return isinstance(sample, Argmax)
 
 
+def _batched(model):
+    return hasattr(model, "forward_batch")
+
+
+def verify_limit(model):
+    """verifyLimit (src/model/speculative.js:25-28): rows one verify pass can carry; infinite without a batched pass."""
+    if not _batched(model):
+        return float("inf")
+    return min(model.max_batch, getattr(model, "logits_batch", model.max_batch))
+
+
+def feed(model, ids, want_logits):
+    """prefillTokens / feedLogits (src/model/generate.js:15-31, src/model/speculative.js:51-61): ids in chunks of the
+    model's batch (1 without a batched pass); returns the last token's logits when asked."""
+    logits = None
+    chunk = max(1, model.max_batch) if _batched(model) else 1
+    i = 0
+    while i < len(ids):
+        end = min(len(ids), i + chunk)
+        last = want_logits and end == len(ids)
+        if chunk > 1:
+            logits = model.forward_batch(ids[i:end], logits="last" if last else "none")
+        else:
+            logits = model.forward(ids[i], logits=last)
+        i = end
+    return logits
+
+
+def forward_rows(model, tokens):
+    """forwardRows (src/model/speculative.js:39-48): per-position logits of every token, in one pass when it fits."""
+    if _batched(model) and len(tokens) <= verify_limit(model):
+        return list(model.forward_batch(tokens, logits="all"))
+    return [model.forward(t) for t in tokens]
+
+
 def speculative(target, draft, prompt_ids, k=4, max_tokens=256, sample=None, stop_ids=(), penalize_prompt=True,
                 t_limit=None, cycle_log=None, stats=None, deadline=None):
     """Yield the token ids generateSpeculative yields after prompt_ids (src/model/speculative.js:100-240).
 
-    sample: an oracle.Sampler (createSampler) or None / Argmax() for plain greedy. t_limit: verifyLimit(target); the
-    oracle models have no forwardBatch, so the reference's value is Infinity (:26-28), but the caller may pass the
-    device model's limit so both run the same kk sequence. cycle_log: a list that receives one
+    sample: an oracle.Sampler (createSampler) or None / Argmax() for plain greedy. t_limit: verifyLimit(target) by
+    default (Infinity for the single-token oracle models, :26-28); the caller may pass the device model's limit so both
+    run the same kk sequence. cycle_log: a list that receives one
     (kk, drafted, accepted, token) tuple per cycle. deadline: a time.perf_counter() value after which no new cycle
     starts (bench sampling only)."""
     sample = sample if sample is not None else Argmax()
@@ -63,7 +100,7 @@ def speculative(target, draft, prompt_ids, k=4, max_tokens=256, sample=None, sto
     if n0 >= draft.ctx:
         raise ValueError(f"prompt is {n0} tokens but the draft model's context window is {draft.ctx}; give the draft "
                          "model at least the target's context")
-    t_limit = float("inf") if t_limit is None else t_limit
+    t_limit = verify_limit(target) if t_limit is None else t_limit
     prompt_ids = [int(t) for t in prompt_ids]
 
     # ---- prefill everything but the last prompt token on both models (:117-143)
@@ -72,10 +109,8 @@ def speculative(target, draft, prompt_ids, k=4, max_tokens=256, sample=None, sto
     target.truncate(reuse)
     d_reuse = min(common_prefix(draft.tokens, body), len(body))
     draft.truncate(d_reuse)
-    for t in body[reuse:]:
-        target.forward(t, logits=False)
-    for t in body[d_reuse:]:
-        draft.forward(t, logits=False)
+    feed(target, body[reuse:], False)
+    feed(draft, body[d_reuse:], False)
     spec = stats["speculative"] = {"k": k_max, "cycles": 0, "drafted": 0, "accepted": 0,
                                    "acceptedHist": [0] * (k_max + 1)}
     stats["generated"] = 0
@@ -102,9 +137,7 @@ def speculative(target, draft, prompt_ids, k=4, max_tokens=256, sample=None, sto
             drafted, qd = [], []
             if kk > 0:
                 draft.truncate(min(common_prefix(draft.tokens, seq), len(seq) - 1))
-                dl = None
-                for t in seq[draft.pos:]:  # feedLogits, one token per call (:51-61)
-                    dl = draft.forward(t)
+                dl = feed(draft, seq[draft.pos:], True)  # feedLogits (:51-61)
                 if hasattr(draft, "mark_rollback"):
                     draft.mark_rollback()
                 for j in range(kk):
@@ -120,10 +153,10 @@ def speculative(target, draft, prompt_ids, k=4, max_tokens=256, sample=None, sto
                         break
                     dl = draft.forward(x)
                 kk = len(drafted)
-            # -- verify: one (sequential) pass over [pending, x_1..x_kk] (:182-190)
+            # -- verify: one pass over [pending, x_1..x_kk] (:182-190)
             if hasattr(target, "mark_rollback"):
                 target.mark_rollback()
-            rows = [target.forward(t) for t in [pending] + drafted]
+            rows = forward_rows(target, [pending] + drafted)
             full = seq + drafted
             # -- accept / reject (:192-209)
             a, tok = 0, -1

@@ -387,6 +387,15 @@ static void matvec_rows(int type, const uint8_t *u8, long cols, const float *x, 
   }
 }
 
+/* One worker's rows [r0, r1) with the single-thread arithmetic (the CPU baseline's scalar formats). */
+void orc_matvec_rows(int type, const uint8_t *data, long cols, const float *x, const int8_t *xq, const float *xd,
+                     const int32_t *xs, float *y, long r0, long r1) {
+  matvec_rows(type, data, cols, x, xq, xd, xs, y, r0, r1);
+}
+
+/* The f16 table every decoder reads; call once before several threads decode. */
+void orc_tables_init(void) { f16_tbl_init(); }
+
 /* Row-split across threads like the reference pool (src/compute/layout.js:39-43): each row is computed by one
  * thread with the single-thread arithmetic, so the result does not depend on the thread count. */
 static int g_threads = 1;

@@ -40,16 +40,21 @@ def weight_bytes(t, rows, cols):
 
 
 def copy_calibration(mb):
-    """One plain device-to-device copy of `mb` MiB (torch's elementwise copy kernel): a kernel of known traffic, read
-    `mb` MiB and write `mb` MiB, against which FETCH_SIZE / WRITE_SIZE counter readings are scaled."""
-    import torch
+    """A kernel of known traffic, against which FETCH_SIZE / WRITE_SIZE counter readings are scaled: through the HIP
+    runtime the library links (libamdhip64), hipMemset writes `mb` MiB (the runtime's fill kernel) and a
+    device-to-device hipMemcpy then reads `mb` MiB and writes `mb` MiB (the runtime's copy kernel)."""
+    hip = C.CDLL("libamdhip64.so.7")
+    hip.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+    hip.hipMemset.argtypes = [C.c_void_p, C.c_int, C.c_size_t]
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    hip.hipFree.argtypes = [C.c_void_p]
     n = mb << 20
-    a = torch.ones(n, dtype=torch.uint8, device="cuda")
-    b = torch.empty_like(a)
-    torch.cuda.synchronize()
-    b.copy_(a)
-    torch.cuda.synchronize()
-    print(f"copy calibration: {n} B read, {n} B written", flush=True)
+    a, b = C.c_void_p(), C.c_void_p()
+    for rc in (hip.hipMalloc(C.byref(a), n), hip.hipMalloc(C.byref(b), n), hip.hipMemset(a, 1, n),
+               hip.hipMemcpy(b, a, n, 3), hip.hipDeviceSynchronize(), hip.hipFree(a), hip.hipFree(b)):
+        if rc != 0:
+            raise RuntimeError(f"copy calibration: HIP error {rc}")
+    print(f"copy calibration: fill of {n} B written, then a copy of {n} B read and {n} B written", flush=True)
 
 
 def run(shapes, ms_list, min_mb=512, target_ms=40.0, seed=7, iters=None):
