@@ -1255,9 +1255,6 @@ static zl_sampler *new_sampler(const zl_sampler_opts *o) {
   p.presence = o->presence_penalty; p.frequency = o->frequency_penalty; p.topK = o->top_k; p.repeatLastN = o->repeat_last_n;
   p.penalized = (p.repeatPenalty != 1.0 || p.presence != 0.0 || p.frequency != 0.0) ? 1 : 0;
   p.greedyArgmax = o->greedy_argmax ? 1 : 0;
-  if (!(p.temperature <= 0.0) && !p.greedyArgmax)
-    ZL_REQUIRE(p.topK >= 1 && p.topK <= KCAP, ZL_ERR_UNSUPPORTED, "top_k must be 1.." + std::to_string(KCAP) + " on the GPU sampler");
-  ZL_REQUIRE(p.repeatLastN >= 0 && p.repeatLastN <= 64, ZL_ERR_UNSUPPORTED, "repeat_last_n must be 0..64 on the GPU sampler");
   ZL_HIP(hipStreamCreateWithFlags(&s->st, hipStreamNonBlocking));
   s->ss = (SpecState *)s->ar.alloc(sizeof(SpecState));
   zero_now(s->ss, sizeof(SpecState));
@@ -1737,6 +1734,13 @@ int zl_synth_tensor_bytes(const zl_synth_tensor *t, int use_device, void *host_o
 int zl_sampler_create(const zl_sampler_opts *opts, zl_sampler **out) {
   ZL_API_BEGIN
   ZL_REQUIRE(opts && out, ZL_ERR_ARG, "null argument");
+  /* options the device sampler does not take are refused before any device call: a candidate list of KCAP entries,
+   * a history window of 64 ids */
+  if (!(opts->temperature <= 0.0) && !opts->greedy_argmax)
+    ZL_REQUIRE(opts->top_k >= 1 && opts->top_k <= KCAP, ZL_ERR_UNSUPPORTED,
+               "top_k must be 1.." + std::to_string(KCAP) + " on the GPU sampler");
+  ZL_REQUIRE(opts->repeat_last_n >= 0 && opts->repeat_last_n <= 64, ZL_ERR_UNSUPPORTED,
+             "repeat_last_n must be 0..64 on the GPU sampler");
   ensure_init();
   *out = new_sampler(opts);
   ZL_API_END
