@@ -18,46 +18,81 @@ inline int attn_heads_per_block(int group) {
   return 1;
 }
 
+// Score dots: every position's dot is split over HD / ATTN_VPL lanes of ATTN_VPL values each (an f64 fma chain per
+// lane in value order, then an xor butterfly over the position's lanes); both attention forms use this order.
+constexpr int ATTN_VPL = 32;
+// Positions per score block chunk: 64, or one load round of 256 threads where that is more (HD = 64).
+constexpr int attn_score_chunk(int hd) { return 256 / (hd / ATTN_VPL) > 64 ? 256 / (hd / ATTN_VPL) : 64; }
+
 // Per-head RMSNorm (weights nw, when set) and RoPE at position pos of one head vector v[0..HD) in LDS, by one wave,
 // with the arithmetic of src/model/forward.js:203-211 and src/compute/ref-kernels.js:305-310, 344-363 (64-lane strided
 // f64 sum of squares and butterfly; f64 rotation of each (i, i + half) or (2i, 2i + 1) pair, stored f32).
 template <int HD>
-__device__ inline void norm_rope(float *v, const float *nw, double eps, int nRot, int neox, const float *cosT,
-                                 const float *sinT, int pos, int lane) {
-  // the lane's table values and norm weights are requested before the sum of squares, which does not need them
+struct RopeVals {
+  static constexpr int PR = (HD / 2 + 63) / 64;  // rotation pairs per lane at most
+  static constexpr int NW = (HD + 63) / 64;      // norm weights per lane
+  float cv[PR], sv[PR], wv[NW];
+};
+
+// The lane's norm weights (a read of the table when there is no norm: no branch around the loads) ...
+template <int HD>
+__device__ inline void rope_load_w(RopeVals<HD> &r, const float *nw, const float *cosT, int lane) {
+  const float *nwp = nw ? nw : cosT;
+  #pragma unroll
+  for (int k = 0; k < RopeVals<HD>::NW; k++) r.wv[k] = nwp[lane + 64 * k < HD ? lane + 64 * k : 0];
+}
+// ... and its rotation table values at position pos.
+template <int HD>
+__device__ inline void rope_load_cs(RopeVals<HD> &r, int nRot, const float *cosT, const float *sinT, int pos, int lane) {
   const int half = nRot / 2;
-  constexpr int PR = (HD / 2 + 63) / 64;  // rotation pairs per lane at most
-  float cv[PR], sv[PR], wv[(HD + 63) / 64];
   #pragma unroll
-  for (int r = 0; r < PR; r++) {
-    const int i = lane + 64 * r, ic = i < half ? i : 0;
-    cv[r] = cosT[(long)pos * half + ic];
-    sv[r] = sinT[(long)pos * half + ic];
+  for (int k = 0; k < RopeVals<HD>::PR; k++) {
+    const int i = lane + 64 * k, ic = i < half ? i : 0;
+    r.cv[k] = cosT[(long)pos * half + ic];
+    r.sv[k] = sinT[(long)pos * half + ic];
   }
-  const float *nwp = nw ? nw : cosT;  // (no norm: a read of the table, unused; no branch around the loads)
-  #pragma unroll
-  for (int r = 0; r < (HD + 63) / 64; r++) wv[r] = nwp[lane + 64 * r < HD ? lane + 64 * r : 0];
+}
+
+// Per-head RMSNorm (weights nw, when set) and RoPE of one head vector v[0..HD) in LDS, by one wave, with the
+// arithmetic of src/model/forward.js:203-211 and src/compute/ref-kernels.js:305-310, 344-363 (64-lane strided f64 sum
+// of squares and butterfly; f64 rotation of each (i, i + half) or (2i, 2i + 1) pair, stored f32), from values loaded by
+// rope_load_w / rope_load_cs.
+template <int HD>
+__device__ inline void norm_rope_apply(float *v, const RopeVals<HD> &r, const float *nw, double eps, int nRot, int neox,
+                                       int lane) {
+  const int half = nRot / 2;
   if (nw) {
     double ss = 0;
     for (int i = lane; i < HD; i += 64) { const double x = (double)v[i]; ss += x * x; }
     ss = wave_sum_xor(ss, 64);
     const double sc = 1.0 / sqrt(ss / (double)HD + eps);
     #pragma unroll
-    for (int r = 0; r < (HD + 63) / 64; r++) {
-      const int i = lane + 64 * r;
-      if (i < HD) v[i] = (float)((double)v[i] * sc * (double)wv[r]);
+    for (int k = 0; k < RopeVals<HD>::NW; k++) {
+      const int i = lane + 64 * k;
+      if (i < HD) v[i] = (float)((double)v[i] * sc * (double)r.wv[k]);
     }
   }
   #pragma unroll
-  for (int r = 0; r < PR; r++) {
-    const int i = lane + 64 * r;
+  for (int k = 0; k < RopeVals<HD>::PR; k++) {
+    const int i = lane + 64 * k;
     if (i >= half) break;
     const int i0 = neox ? i : 2 * i, i1 = neox ? i + half : 2 * i + 1;
-    const double c = (double)cv[r], sn = (double)sv[r];
+    const double c = (double)r.cv[k], sn = (double)r.sv[k];
     const double x0 = (double)v[i0], x1 = (double)v[i1];
     v[i0] = (float)(x0 * c - x1 * sn);  // pairs are disjoint across lanes
     v[i1] = (float)(x0 * sn + x1 * c);
   }
+}
+
+// Both at position pos; the table values and norm weights are requested before the sum of squares, which does not need
+// them.
+template <int HD>
+__device__ inline void norm_rope(float *v, const float *nw, double eps, int nRot, int neox, const float *cosT,
+                                 const float *sinT, int pos, int lane) {
+  RopeVals<HD> r;
+  rope_load_cs<HD>(r, nRot, cosT, sinT, pos, lane);
+  rope_load_w<HD>(r, nw, cosT, lane);
+  norm_rope_apply<HD>(v, r, nw, eps, nRot, neox, lane);
 }
 
 // Scores of one 64-position chunk of one token for hg query heads sharing a KV head. Keys of positions before the
@@ -68,10 +103,11 @@ __device__ inline void norm_rope(float *v, const float *nw, double eps, int nRot
 template <int HD, bool F16KV>
 __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
   constexpr int VB = F16KV ? 2 : 4;      // bytes per cached value
-  constexpr int EPL = 16 / VB;           // K values per lane per 16-byte load
-  constexpr int LP = HD / EPL;           // lanes per position
+  constexpr int EPW = 16 / VB;           // K values per 16-byte load
+  constexpr int LP = HD / ATTN_VPL;      // lanes per position (ATTN_VPL values each)
+  constexpr int NLD = ATTN_VPL / EPW;    // 16-byte loads per lane and position
   constexpr int PPI = 256 / LP;          // positions per load round
-  constexpr int P = 64;                  // positions per chunk
+  constexpr int P = attn_score_chunk(HD);  // positions per chunk
   constexpr int R = P / PPI;             // load rounds per chunk
   static_assert(R >= 1 && P % PPI == 0, "chunk geometry");
   __shared__ float qs[8 * HD];
@@ -86,14 +122,16 @@ __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
   const uint8_t *kbase = (const uint8_t *)a.kcache + kvoff * VB;
   float *srow = a.scores + ((long)b * a.nHead + h0) * a.sld;
   const int part = tid % LP, sub = tid / LP;
-  uint4 u[R];
+  uint4 u[R][NLD];
   // cached keys (positions of the pass are filled in from kn); the first chunk's keys and the query heads are requested
   // before the pass's step record arrives, so the positions past the cache's valid ones are read too (and unused)
   auto fetch = [&](int c0, int lim) {
     #pragma unroll
     for (int r = 0; r < R; r++) {
       const int t = c0 + r * PPI + sub;
-      u[r] = t < lim ? *(const uint4 *)(kbase + ((long)t * HD + part * EPL) * VB) : make_uint4(0, 0, 0, 0);
+      #pragma unroll
+      for (int k = 0; k < NLD; k++)
+        u[r][k] = t < lim ? *(const uint4 *)(kbase + ((long)t * HD + part * ATTN_VPL) * VB + 16 * k) : make_uint4(0, 0, 0, 0);
     }
   };
   fetch(blockIdx.x * P, a.ctx);
@@ -167,17 +205,23 @@ __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
     #pragma unroll
     for (int r = 0; r < R; r++) {
       const int t = c0 + r * PPI + sub;
-      if (t >= pos0 && t < npos) u[r] = *(const uint4 *)(kn + ((t - n0) * HD + part * EPL) * VB);
-      const uint32_t w4[4] = {u[r].x, u[r].y, u[r].z, u[r].w};
-      double kv[EPL];
+      if (t >= pos0 && t < npos) {
+        #pragma unroll
+        for (int k = 0; k < NLD; k++) u[r][k] = *(const uint4 *)(kn + ((t - n0) * HD + part * ATTN_VPL) * VB + 16 * k);
+      }
+      double kv[ATTN_VPL];
       #pragma unroll
-      for (int e = 0; e < EPL; e++)
-        kv[e] = F16KV ? (double)h2f((uint16_t)((w4[e >> 1] >> (16 * (e & 1))) & 0xffff)) : (double)__uint_as_float(w4[e]);
+      for (int k = 0; k < NLD; k++) {
+        const uint32_t w4[4] = {u[r][k].x, u[r][k].y, u[r][k].z, u[r][k].w};
+        #pragma unroll
+        for (int e = 0; e < EPW; e++)
+          kv[k * EPW + e] = F16KV ? (double)h2f((uint16_t)((w4[e >> 1] >> (16 * (e & 1))) & 0xffff)) : (double)__uint_as_float(w4[e]);
+      }
       for (int h = 0; h < hg; h++) {
-        const float *qh = qs + h * HD + part * EPL;
+        const float *qh = qs + h * HD + part * ATTN_VPL;
         double s = 0.0;
         #pragma unroll
-        for (int e = 0; e < EPL; e++) s = fma((double)qh[e], kv[e], s);
+        for (int e = 0; e < ATTN_VPL; e++) s = fma((double)qh[e], kv[e], s);
         s = wave_sum_xor(s, LP);
         if (part == (h % LP) && t < npos) srow[(long)h * a.sld + t] = (float)(s * a.scale);
       }
@@ -488,7 +532,7 @@ void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
   ZL_REQUIRE(a.qhs >= a.hd && a.ldq >= a.nHead * a.qhs, ZL_ERR_ARG, "attention: query head stride below the head size");
   const int group = a.nHead / a.nHeadKv;
   a.hpb = attn_heads_per_block(group);
-  const int chunks = (a.ctx + 63) / 64;
+  const int chunks = (a.ctx + attn_score_chunk(a.hd) - 1) / attn_score_chunk(a.hd);
   dim3 gs(chunks < 64 ? chunks : 64, a.nHead / a.hpb, B);
   switch (a.hd * 2 + a.kvF16) {
     case 128: launch_scores_k<64, false>(a, gs, B, st); break;
