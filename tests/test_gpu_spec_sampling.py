@@ -114,3 +114,31 @@ def test_oracle_draft_accepts_everything_when_sampling(gpu, close_files):
     assert len(out) == 21 and st["speculative"]["acceptRate"] == 1.0
     for x in (t, d, s):
         x.close()
+
+
+@pytest.mark.parametrize("cfg", ["T0.7-top40-p0.9", "greedy"])
+def test_whole_cycle_graph_equals_launch_by_launch_cycle(gpu, close_files, monkeypatch, cfg):
+    """A cycle captured as two graphs (draft phase, verify phase) makes the decisions the launch-by-launch cycle makes
+    (ZEROLLM_CYCLE_GRAPH=0): the same drafts, accept counts, tokens and final random state, over cycles whose draft
+    feed is one token (after a rejection) or two (after a full acceptance)."""
+    prompt = _prompt(20, 5)
+    c = {} if cfg == "greedy" else CONFIGS[cfg]
+    runs = []
+    for mode in ("1", "0"):
+        monkeypatch.setenv("ZEROLLM_CYCLE_GRAPH", mode)
+        print(f"case whole-cycle graph {cfg} mode {mode}", flush=True)
+        if cfg == "greedy":
+            t = Mdl.HipModel.load(close_files[0], ctx=256, kv="f16")
+            d = Mdl.HipModel.load(close_files[1], ctx=256, kv="f16")
+            log, st = [], {}
+            out = list(generate_speculative(t, d, prompt, k=4, max_tokens=40, stats=st, cycle_log=log))
+            runs.append((out, log))
+            t.close()
+            d.close()
+        else:
+            out, log, rng, st, _ = _run_pair(close_files, prompt, 4, c, 77, 40)
+            runs.append((out, log, rng))
+    assert runs[0] == runs[1]
+    log = runs[0][1]
+    assert any(a == kk for kk, _, a, _ in log) and any(a < kk for kk, _, a, _ in log), \
+        "the run has cycles after a full acceptance (two fed tokens) and after a rejection (one)"

@@ -9,8 +9,10 @@
 #include <algorithm>
 #include <chrono>
 #include <functional>
+#include <atomic>
 #include <map>
 #include <set>
+#include <tuple>
 #include <memory>
 #include <mutex>
 #include <thread>
@@ -212,6 +214,7 @@ struct Checkpoints {
 }  // namespace zl
 
 struct zl_model {
+  uint64_t uid = 0;  // never reused: keys the speculative-cycle graphs that capture this model's passes
   zl_config cfg{};
   int ctx = 0, kvF16 = 0, maxBatch = 16, logitsBatch = 16;
   int vstride = 0;  // positions per V cache row
@@ -266,6 +269,10 @@ struct zl_sampler {
   int scratchVocab = 0;
   zl::ArgmaxWork am{};
   hipStream_t st = nullptr;
+  // whole speculative cycles captured as two graphs (draft phase, verify phase) per (target uid, draft uid, fed
+  // tokens, drafts, stop ids, phase); they capture this sampler's buffers, so they live and die with it
+  hipStream_t cst = nullptr;
+  std::map<std::tuple<uint64_t, uint64_t, int, int, int, int>, std::pair<hipGraphExec_t, hipGraph_t>> cycles;
   ~zl_sampler();
 };
 
@@ -291,6 +298,8 @@ zl_model::~zl_model() {
 
 zl_sampler::~zl_sampler() {
   if (st) hipStreamSynchronize(st);
+  for (auto &c : cycles) { hipGraphExecDestroy(c.second.first); hipGraphDestroy(c.second.second); }
+  if (cst) hipStreamDestroy(cst);
   ar.release();
   if (hss) hipHostFree(hss);
   if (hdist) hipHostFree(hdist);
@@ -944,7 +953,9 @@ static void reset_model(zl_model *m) {
 
 // ---------------------------------------------------------------------------------------------- construction
 static zl_model *new_model(const zl_model_opts *o) {
+  static std::atomic<uint64_t> next_uid{1};
   std::unique_ptr<zl_model> m(new zl_model());
+  m->uid = next_uid++;
   int mb = o && o->max_batch > 0 ? o->max_batch : 16;
   m->maxBatch = std::max(1, std::min(mb, 64));
   int lb = o && o->logits_batch > 0 ? o->logits_batch : 16;
@@ -1314,6 +1325,71 @@ static void dist_of_row(zl_sampler *s, zl_model *m, int row, const int32_t *hist
 }
 
 // ---------------------------------------------------------------------------------------------- speculative cycle
+// The work `body` enqueues on stream cs, captured and instantiated as one graph.
+template <class F>
+static hipGraphExec_t capture_graph(hipStream_t cs, F &&body, hipGraph_t *def) {
+  hipGraph_t g = nullptr;
+  ZL_HIP(hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal));
+  try {
+    body();
+  } catch (...) {
+    hipStreamEndCapture(cs, &g);
+    if (g) hipGraphDestroy(g);
+    throw;
+  }
+  ZL_HIP(hipStreamEndCapture(cs, &g));
+  hipGraphExec_t ex;
+  ZL_HIP(hipGraphInstantiate(&ex, g, nullptr, nullptr, 0));
+  *def = g;
+  return ex;
+}
+
+// One phase of a speculative cycle of dense models as a single graph (whole-cycle capture):
+//   phase 0, the draft: reset of the cycle state, the feed pass of nFeed tokens (whose step record the host has set),
+//            then for j < kk the draft distribution, the on-device draw (which writes the next draft step and the
+//            target's verify row) and, but for the last draft, the next single-token draft pass;
+//   phase 1, the verify: the (kk + 1)-row target pass, its distributions and the acceptance.
+// The kernels are those the per-pass graphs hold, in the same order, so a captured cycle computes what the
+// launch-by-launch cycle computes. Penalised samplers (whose history length is a kernel argument per draw) and hybrid
+// models (whose rollback bookkeeping is host logic) take the launch-by-launch cycle.
+static hipGraphExec_t cycle_graph(zl_model *T, zl_model *D, zl_sampler *s, int nFeed, int kk, int nStop, int phase) {
+  const auto key = std::make_tuple(T->uid, D->uid, nFeed, kk, nStop, phase);
+  auto it = s->cycles.find(key);
+  if (it != s->cycles.end()) return it->second.first;
+  if (!s->cst) ZL_HIP(hipStreamCreateWithFlags(&s->cst, hipStreamNonBlocking));
+  hipStream_t cs = s->cst;
+  hipStream_t ts = T->st, dsv = D->st;
+  T->st = cs;
+  D->st = cs;
+  struct Back { zl_model *T, *D; hipStream_t a, b; ~Back() { T->st = a; D->st = b; } } back{T, D, ts, dsv};
+  const bool greedy = s->sp.temperature <= 0.0 || s->sp.greedyArgmax;
+  hipGraph_t def = nullptr;
+  hipGraphExec_t ex = capture_graph(cs, [&] {
+    if (phase == 0) {
+      hipLaunchKernelGGL(k_spec_reset, dim3(1), dim3(64), 0, cs, s->ss);
+      enqueue_forward(D, nFeed, 1);
+      for (int j = 0; j < kk; j++) {
+        launch_dist_rows(D->logits, D->cfg.vocab, 1, D->cfg.vocab, s->sp, nullptr, j, 0, s->scratch, s->am, s->qdist + j, cs);
+        launch_draft_draw(s->qdist + j, s->ss, j, s->dstop, nStop, D->dstep, j == 0 ? nFeed : 1, T->dstep, s->dhist, 0, cs);
+        if (j < kk - 1) enqueue_forward(D, 1, 1);
+      }
+    } else {
+      enqueue_forward(T, kk + 1, 2);
+      launch_dist_rows(T->logits, T->cfg.vocab, kk + 1, T->cfg.vocab, s->sp, nullptr, 0, 1, s->scratch, s->am, s->pdist, cs);
+      launch_accept(s->pdist, s->qdist, s->ss, greedy ? 1 : 0, cs);
+    }
+    ZL_HIP(hipGetLastError());
+  }, &def);
+  s->cycles[key] = {ex, def};
+  return ex;
+}
+
+// ZEROLLM_CYCLE_GRAPH=0 keeps the launch-by-launch cycle (read per cycle, so a test can compare the two).
+static bool use_cycle_graphs() {
+  const char *e = getenv("ZEROLLM_CYCLE_GRAPH");
+  return !(e && e[0] == '0');
+}
+
 static void spec_cycle(zl_model *T, zl_model *D, zl_sampler *s, const int32_t *feed, int nFeed, int pending, int kk,
                        const int32_t *stopIds, int nStop, const int32_t *hist, int nh, zl_spec_result *out) {
   ZL_REQUIRE(!T->closed && !D->closed, ZL_ERR_STATE, "model is closed");
@@ -1348,7 +1424,9 @@ static void spec_cycle(zl_model *T, zl_model *D, zl_sampler *s, const int32_t *f
     h.pos0 = (int)T->tokens.size(); h.B = kk + 1; h.tokens[0] = pending;
     hipLaunchKernelGGL(k_set_step, dim3(1), dim3(64), 0, st, T->dstep, h);
   }
-  hipLaunchKernelGGL(k_spec_reset, dim3(1), dim3(64), 0, st, s->ss);
+  const bool whole = use_graphs() && use_cycle_graphs() && kk > 0 && !T->hybrid && !D->hybrid && !s->sp.penalized &&
+                     nFeed <= D->maxBatch;
+  if (!whole) hipLaunchKernelGGL(k_spec_reset, dim3(1), dim3(64), 0, st, s->ss);  // (the captured cycle resets it)
   const int keep = upload_hist(s, st, hist, nh);
   {
     StopArgs sa;
@@ -1359,7 +1437,15 @@ static void spec_cycle(zl_model *T, zl_model *D, zl_sampler *s, const int32_t *f
   ZL_HIP(hipGetLastError());
   const int *dh = s->sp.penalized ? s->dhist : nullptr;
   int posF = 0;  // the draft's position after feeding
-  if (kk > 0) {
+  if (whole) {
+    // whole-cycle capture: the host sets the draft's feed step, then two graph launches run the cycle
+    check_batch(D, feed, nFeed, 1);
+    set_step(D, (int)D->tokens.size(), feed, nFeed);
+    for (int i = 0; i < nFeed; i++) D->tokens.push_back(feed[i]);
+    ZL_HIP(hipGraphLaunch(cycle_graph(T, D, s, nFeed, kk, nStop, 0), st));
+    ZL_HIP(hipEventRecord(em, st));
+    ZL_HIP(hipGraphLaunch(cycle_graph(T, D, s, nFeed, kk, nStop, 1), st));
+  } else if (kk > 0) {
     ZL_REQUIRE(!D->hybrid || (D->ck.boundary.empty() && D->ck.every == 0), ZL_ERR_UNSUPPORTED,
                "a hybrid draft with boundary-token or periodic checkpoints is driven with zl_forward, not zl_spec_cycle");
     // feedLogits (src/model/speculative.js:51-61): chunks of maxBatch, logits of the last one
@@ -1384,14 +1470,16 @@ static void spec_cycle(zl_model *T, zl_model *D, zl_sampler *s, const int32_t *f
       if (j < kk - 1) launch_pass(D, 1, 1);
     }
   }
-  ZL_HIP(hipEventRecord(em, st));
-  if (T->hybrid) {  // the checkpoint policy before the verify pass (#hybridBatch: never split when all rows return logits)
-    if (T->ck.wants_before((int)T->tokens.size(), pending, true, T->prevNoLogits)) checkpoint(T);
-    T->prevNoLogits = false;
+  if (!whole) {
+    ZL_HIP(hipEventRecord(em, st));
+    if (T->hybrid) {  // the checkpoint policy before the verify pass (#hybridBatch: never split when all rows return logits)
+      if (T->ck.wants_before((int)T->tokens.size(), pending, true, T->prevNoLogits)) checkpoint(T);
+      T->prevNoLogits = false;
+    }
+    launch_pass(T, kk + 1, 2);
+    launch_dist_rows(T->logits, T->cfg.vocab, kk + 1, T->cfg.vocab, s->sp, dh, keep, 1, s->scratch, s->am, s->pdist, st);
+    launch_accept(s->pdist, s->qdist, s->ss, (s->sp.temperature <= 0.0 || s->sp.greedyArgmax) ? 1 : 0, st);
   }
-  launch_pass(T, kk + 1, 2);
-  launch_dist_rows(T->logits, T->cfg.vocab, kk + 1, T->cfg.vocab, s->sp, dh, keep, 1, s->scratch, s->am, s->pdist, st);
-  launch_accept(s->pdist, s->qdist, s->ss, (s->sp.temperature <= 0.0 || s->sp.greedyArgmax) ? 1 : 0, st);
   ZL_HIP(hipEventRecord(e1, st));
   ZL_HIP(hipMemcpyAsync(s->hss, s->ss, sizeof(SpecState), hipMemcpyDeviceToHost, st));
   ZL_HIP(hipStreamSynchronize(st));
