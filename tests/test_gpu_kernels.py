@@ -135,7 +135,7 @@ def _check_gemv(type_, rows, cols, Ms, seed, raw=None):
 def test_gemv_matches_oracle(gpu, type_, cols):
     if cols % G.TYPE_INFO[type_][1]:
         pytest.skip("not a whole number of blocks")
-    _check_gemv(type_, 300, cols, [1, 2, 5, 9, 17], seed=cols + type_)
+    _check_gemv(type_, 300, cols, [1, 2, 5, 9, 16, 17], seed=cols + type_)
 
 
 def float_raw(type_, rows, cols, seed):
@@ -180,9 +180,10 @@ C2_SHAPES = [(4096, 4096, G.Q4_K), (1024, 4096, G.Q4_K), (1024, 4096, G.Q6_K), (
 
 @pytest.mark.parametrize("N,K,type_", C2_SHAPES)
 def test_gemv_projection_shapes_synthetic(gpu, N, K, type_):
-    """Projection shapes with this library's quantised N(0, 0.02) weights, at M = k + 1 in {1, 2, 5, 9, 17}: the first
-    and the last 96 rows against the oracle (M = 17 is two weight passes of 9 + 8 tokens; the other rows are covered
-    by the same kernels through the model tests)."""
+    """Projection shapes with this library's quantised N(0, 0.02) weights, at M = k + 1 in {1, 2, 5, 9, 17} and the
+    prefill chunk M = 16: the first and the last 96 rows against the oracle (M = 17 is two weight passes of 8 + 9 tokens,
+    M = 16 two of 8, on the matrix cores for Q4_K; the other rows are covered by the same kernels through the model
+    tests)."""
     t = synth.TensorSpec("w", type_, N, K, seed=99 + N, std=0.02)
     raw = synth.tensor_bytes(t, use_device=True)
     print(f"case gemv {N}x{K} type {type_}", flush=True)
@@ -192,7 +193,7 @@ def test_gemv_projection_shapes_synthetic(gpu, N, K, type_):
     rb = G.row_size(type_, K)
     heads = [(0, raw[:rows * rb]), (N - rows, raw[(N - rows) * rb:])]
     want = {r0: np.stack([O.matvec(type_, sub, rows, K, X[i]) for i in range(17)]) for r0, sub in heads}
-    for M in (1, 2, 5, 9, 17):
+    for M in (1, 2, 5, 9, 16, 17):
         y = m.gemv(X[:M])
         for r0, _ in heads:
             got, w = y[:, r0:r0 + rows], want[r0][:M]

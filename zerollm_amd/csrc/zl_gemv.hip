@@ -85,10 +85,14 @@ void launch_gemv(const GemvArgs &a0, int epi, const float *xf, int ldx, hipStrea
              ZL_ERR_ARG, "gemv: split-K work space missing or too small");
   ZL_REQUIRE(a0.act.q && a0.act.ra && a0.act.rb && a0.act.rc && a0.act.ld % 64 == 0 && a0.act.ld >= a0.nslab * 64,
              ZL_ERR_ARG, "gemv: activation records missing");
-  // chunks of at most GEMV_MAX_MT tokens: every input and output row is addressed from offset pointers
-  for (int t0 = 0; t0 < a0.M; t0 += GEMV_MAX_MT) {
+  // as few weight passes as chunks of at most GEMV_MAX_MT tokens allow, with the tokens spread evenly over them (16
+  // prefill tokens: two passes of 8, which a Q4_K matrix runs on the matrix cores); every input and output row is
+  // addressed from offset pointers, and the results do not depend on the chunking
+  const int nch = (a0.M + GEMV_MAX_MT - 1) / GEMV_MAX_MT;
+  for (int c = 0, t0 = 0; c < nch; c++) {
     GemvArgs b = a0;
-    b.M = std::min(GEMV_MAX_MT, a0.M - t0);
+    b.M = (a0.M - t0) / (nch - c);  // the remaining tokens over the remaining chunks, the larger chunks last
+    ZL_REQUIRE(b.M >= 1 && b.M <= GEMV_MAX_MT, ZL_ERR_ARG, "gemv: bad token chunk");
     if (t0) {
       b.act = act_rows(a0.act, t0);
       for (int i = 0; i < b.nseg; i++) if (b.seg[i].out) b.seg[i].out += (long)t0 * b.seg[i].ldo;
@@ -97,6 +101,7 @@ void launch_gemv(const GemvArgs &a0, int epi, const float *xf, int ldx, hipStrea
       if (b.qout.q) b.qout = act_rows(a0.qout, t0);
       b.xrow0 += t0;  // fused prologue: the chunk's own input rows
     }
+    t0 += b.M;
     if (gemv_mfma_ok(b)) {  // Q4_K at 2..8 tokens: the int8 dots on the matrix cores, same results
       launch_gemv_mfma(b, epi, st);
       ZL_HIP(hipGetLastError());
