@@ -241,6 +241,36 @@ def test_long_context_attention_matches_oracle(gpu, tiny_files):
     assert (got.argmax(1) == want.argmax(1)).all()
 
 
+@pytest.mark.parametrize("kv", ["f16", "f32"])
+def test_per_head_weighted_sum_equals_slice_form_and_oracle(gpu, tiny_files, monkeypatch, kv):
+    """The per-head weighted sum (softmax row in the scores buffer, probabilities staged with V; passes of several
+    tokens at contexts beyond 8192 positions take it) forced at a 1300-position context (ZEROLLM_ATTN_HEAD_CTX=1024):
+    its batched rows equal the single-token passes (which keep the slice form) bit for bit, and the oracle's logits."""
+    toks = prompt(1210, seed=19)
+    ref = O.OracleModel(tiny_files[0], ctx=1300, kv=kv)
+    for t in toks[:-6]:
+        ref.forward(t, logits=False)
+    want = np.stack([ref.forward(t) for t in toks[-6:]])
+    rows = {}
+    for form in ("slice", "head"):
+        if form == "head":
+            monkeypatch.setenv("ZEROLLM_ATTN_HEAD_CTX", "1024")
+        print(f"case weighted sum {form} kv {kv}", flush=True)
+        m = Mdl.HipModel.load(tiny_files[0], ctx=1300, kv=kv)
+        for i in range(0, 1200, 16):
+            m.forward_batch(toks[i:i + 16], logits="none")
+        m.forward_batch(toks[1200:1204], logits="none")
+        single = np.stack([m.forward(t).copy() for t in toks[-6:]])
+        m.truncate(1204)
+        batched = m.forward_batch(toks[-6:], logits="all").copy()
+        m.close()
+        assert (single.view(np.uint32) == batched.view(np.uint32)).all(), form
+        rows[form] = single
+    assert (rows["head"].view(np.uint32) == rows["slice"].view(np.uint32)).all()
+    exact = np.mean(rows["head"].view(np.uint32) == want.view(np.uint32))
+    assert exact >= 0.999 and np.abs(rows["head"] - want).max() <= 1e-6 * np.abs(want).max(), exact
+
+
 def test_16k_context_verify_width_9_equals_sequential_and_rolls_back(gpu, tiny_files):
     """At a 16384-token context a 9-row verify pass (k = 8) equals nine single-token passes bit for bit, and after a
     rollback to 3 accepted rows the next pass equals a fresh continuation (size-independent checks of the long-context

@@ -398,6 +398,184 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
   }
 }
 
+// ---- the same weighted sum for long contexts, one block per (query head, token) over all HD dimensions. k_attn_av keeps
+// the block's softmax row in LDS, which at 16K positions leaves room for one block per CU, and its four slice blocks of
+// a head hold four copies. Here the exponentials are written back over the head's scores (one block per row, so no
+// other block reads them), and the probabilities p = f32(e * inv) are staged chunk by chunk with V: LDS no longer grows
+// with the context, and a head's four slices share one softmax. The arithmetic is k_attn_av's (the same max, the same
+// exponentials summed in the same thread order, the same chain per dimension), so the two give the same bits.
+constexpr int AVH_CTX = 8192;  // contexts above this take the per-head form (HD <= 128)
+
+template <int HD, bool F16KV>
+__global__ __launch_bounds__(256) void k_attn_av_head(const AttnArgs a) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int VB = F16KV ? 2 : 4;
+  constexpr int CT = AV_ROW / VB;          // positions per chunk
+  constexpr int EPP = 16 / VB;             // positions per 16-byte piece
+  constexpr int PPR = AV_ROW / 16;         // pieces per row
+  constexpr int CHUNK = HD * AV_PITCH;     // bytes of one staged chunk of V rows
+  constexpr int LPT = HD * PPR / 256;      // pieces per thread per chunk
+  constexpr int PPT = CT / 256 > 0 ? CT / 256 : 1;  // probabilities per thread per chunk
+  static_assert(HD * PPR % 256 == 0 && CT % 256 == 0 || CT == 128, "chunk geometry");
+  float *pb = (float *)(lds + 2 * CHUNK);  // [2][CT] staged probabilities
+  __shared__ double redd[4];
+  __shared__ float redf[4];
+  const int h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int kvh = h / (a.nHead / a.nHeadKv);
+  const uint8_t *vbase = (const uint8_t *)a.vcache + ((long)a.layer * a.nHeadKv + kvh) * HD * a.vstride * VB;
+  float *srow = a.scores + ((long)b * a.nHead + h) * a.sld;
+  uint4 pre[LPT];
+  float pp[PPT];
+  auto fetch = [&](int c, int lim) {
+    #pragma unroll
+    for (int k = 0; k < LPT; k++) {
+      const int idx = k * 256 + tid, dim = idx / PPR, t = c * CT + (idx % PPR) * EPP;
+      pre[k] = t < lim ? *(const uint4 *)(vbase + ((long)dim * a.vstride + t) * VB) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store = [&](int buf) {
+    #pragma unroll
+    for (int k = 0; k < LPT; k++) {
+      const int idx = k * 256 + tid;
+      *(uint4 *)(lds + buf * CHUNK + (idx / PPR) * AV_PITCH + (idx % PPR) * 16) = pre[k];
+    }
+  };
+  fetch(0, a.ctx);
+  const Step *st = a.step;
+  if (b >= st->B) return;
+  const int npos = st->pos0 + b + 1;
+  const int nch = (npos + CT - 1) / CT;
+  #pragma unroll
+  for (int k = 0; k < LPT; k++) {  // the first chunk's pieces from the last position on: zeros, as in later chunks
+    const int t = ((k * 256 + tid) % PPR) * EPP;
+    if (t >= npos) pre[k] = make_uint4(0, 0, 0, 0);
+    else if (t + EPP > npos) {
+      uint32_t w[4] = {pre[k].x, pre[k].y, pre[k].z, pre[k].w};
+      #pragma unroll
+      for (int e = 0; e < EPP; e++)
+        if (t + e >= npos) {
+          if (F16KV) w[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
+          else w[e] = 0u;
+        }
+      pre[k] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+  // ---- softmax (src/compute/ref-kernels.js:313-320) in k_attn_av's order; the exponentials replace the scores
+  float mx = -INFINITY;
+  for (int t = tid; t < npos; t += 256) mx = fmaxf(mx, srow[t]);
+  mx = group_fmax(mx, 64);
+  if (lane == 0) redf[wave] = mx;
+  __syncthreads();
+  const double m = (double)fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
+  double sum = 0.0;
+  for (int t0 = tid; t0 < npos; t0 += 4 * 256) {
+    double e[4];
+    #pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int t = t0 + 256 * k;
+      e[k] = exp((double)srow[t < npos ? t : t0] - m);
+    }
+    #pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int t = t0 + 256 * k;
+      if (t < npos) { srow[t] = (float)e[k]; sum += e[k]; }
+    }
+  }
+  sum = wave_sum_xor(sum, 64);
+  if (lane == 0) redd[wave] = sum;
+  __syncthreads();  // also orders this block's writes of the exponentials before their reads below
+  const double inv = 1.0 / ((redd[0] + redd[1]) + (redd[2] + redd[3]));
+  // probabilities of chunk c (zero past the last position, as k_attn_av's row)
+  auto pload = [&](int c) {
+    #pragma unroll
+    for (int k = 0; k < PPT; k++) {
+      const int t = c * CT + k * 256 + tid;
+      pp[k] = (k * 256 + tid < CT && t < npos) ? srow[t] : 0.f;
+    }
+  };
+  auto pstore = [&](int buf) {
+    #pragma unroll
+    for (int k = 0; k < PPT; k++)
+      if (k * 256 + tid < CT) pb[buf * CT + k * 256 + tid] = (float)((double)pp[k] * inv);
+  };
+  pload(0);
+  store(0);
+  pstore(0);
+  __syncthreads();
+  // ---- weighted sum: output dimension wave * 64 + lane on the first HD / 64 waves, chunk by chunk (double buffered)
+  const bool chainLane = wave < HD / 64;
+  const int dim = wave * 64 + lane;
+  float o = 0.f;
+  for (int c = 0; c < nch; c++) {
+    if (c + 1 < nch) { fetch(c + 1, npos); pload(c + 1); }
+    if (chainLane) {
+      const int cnt = min(CT, npos - c * CT), nu = (cnt + AV_UNIT - 1) / AV_UNIT;
+      const uint8_t *row = lds + (c & 1) * CHUNK + dim * AV_PITCH;
+      const float *pc = pb + (c & 1) * CT;
+      float4 pa[AV_UNIT / 4], pbv[AV_UNIT / 4];
+      uint4 va[AV_UNIT * VB / 16], vb[AV_UNIT * VB / 16];
+      auto read = [&](int u, float4 (&pv)[AV_UNIT / 4], uint4 (&vv)[AV_UNIT * VB / 16]) {
+        #pragma unroll
+        for (int k = 0; k < AV_UNIT / 4; k++) pv[k] = *(const float4 *)(pc + u * AV_UNIT + 4 * k);
+        #pragma unroll
+        for (int k = 0; k < AV_UNIT * VB / 16; k++) vv[k] = *(const uint4 *)(row + (u * AV_UNIT + k * EPP) * VB);
+      };
+      auto steps = [&](const float4 (&pv)[AV_UNIT / 4], const uint4 (&vv)[AV_UNIT * VB / 16]) {
+        #pragma unroll
+        for (int k = 0; k < AV_UNIT / 4; k++) {
+          float v0, v1, v2, v3;
+          if (F16KV) {
+            const uint4 &w = vv[k >> 1];
+            const uint32_t lo = (k & 1) ? w.z : w.x, hi = (k & 1) ? w.w : w.y;
+            v0 = h2f((uint16_t)(lo & 0xffff)); v1 = h2f((uint16_t)(lo >> 16));
+            v2 = h2f((uint16_t)(hi & 0xffff)); v3 = h2f((uint16_t)(hi >> 16));
+          } else {
+            const uint4 &w = vv[k];
+            v0 = __uint_as_float(w.x); v1 = __uint_as_float(w.y); v2 = __uint_as_float(w.z); v3 = __uint_as_float(w.w);
+          }
+          o = fmaf(pv[k].x, v0, o); o = fmaf(pv[k].y, v1, o); o = fmaf(pv[k].z, v2, o); o = fmaf(pv[k].w, v3, o);
+        }
+      };
+      read(0, pa, va);
+      int u = 0;
+      for (; u + 2 <= nu; u += 2) {
+        read(u + 1, pbv, vb);
+        __builtin_amdgcn_sched_barrier(0);
+        steps(pa, va);
+        read(min(u + 2, nu - 1), pa, va);
+        __builtin_amdgcn_sched_barrier(0);
+        steps(pbv, vb);
+      }
+      if (u < nu) steps(pa, va);
+    }
+    __syncthreads();
+    if (c + 1 < nch) { store((c + 1) & 1); pstore((c + 1) & 1); }
+    __syncthreads();
+  }
+  if (chainLane) {
+    const int col = h * HD + dim;
+    if (a.gate) {  // gated attention output (src/model/forward-qwen35.js:103): o * sigmoid(gate), f64, stored f32
+      const double g = (double)a.gate[(long)b * a.ldq + (long)h * a.qhs + dim];
+      o = (float)((double)o * (1.0 / (1.0 + exp(-g))));
+    }
+    if (a.out) a.out[(long)b * a.ldo + col] = o;
+    quant_block32(o, col, a.act, b);
+  }
+}
+
+size_t attention_head_lds(int hd) { return (size_t)2 * hd * AV_PITCH + 2 * 256 * 4; }
+
+template <int HD, bool F16KV>
+static void launch_av_head_k(const AttnArgs &a, int B, hipStream_t st) {
+  static size_t attr = 64 * 1024;
+  const size_t lds = attention_head_lds(HD);
+  if (lds > attr) {
+    ZL_HIP(hipFuncSetAttribute((const void *)k_attn_av_head<HD, F16KV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    attr = lds;
+  }
+  hipLaunchKernelGGL((k_attn_av_head<HD, F16KV>), dim3(1, a.nHead, B), dim3(256), lds, st, a);
+}
+
 // ---- position-split weighted sum (long contexts). The exact chain above runs one dependent f32 step per position, so
 // at 16K positions it is ~40 us per output element. Here one block per (256-position chunk, query head, token) takes
 // the chunk's scores, its max m_c, e_t = exp(s_t - m_c) and l_c = sum e_t in f64, and o_c[i] = sum e_t V_t,i in f64
@@ -494,6 +672,13 @@ size_t attention_split_lds(int hd, int kvF16) { return (size_t)hd * (ATTN_SPLIT_
 
 // Dynamic LDS of one k_attn_av block: the probabilities of ctx positions and two staged V chunks.
 size_t attention_lds(int ctx) { return (size_t)((ctx + AV_UNIT - 1) / AV_UNIT * AV_UNIT) * 4 + 2 * AV_CHUNK; }
+// Contexts above AVH_CTX positions take the per-head weighted sum (heads of at most 128 dimensions), whose LDS does not
+// depend on the context; ZEROLLM_ATTN_HEAD_CTX overrides the threshold (tests).
+bool attention_head_form(int ctx, int hd) {
+  const char *e = getenv("ZEROLLM_ATTN_HEAD_CTX");
+  const int thr = e ? atoi(e) : AVH_CTX;
+  return hd <= 128 && ctx > thr;
+}
 constexpr size_t ATTN_LDS_MAX = 150 * 1024;
 
 template <int HD, bool F16KV>
@@ -524,7 +709,10 @@ static void launch_av_split_k(const AttnArgs &a, dim3 grid, size_t lds, hipStrea
 
 void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
   AttnArgs a = a0;
-  const size_t lds = a.part ? attention_split_lds(a.hd, a.kvF16) : attention_lds(a.ctx);
+  // the per-head form for passes of several tokens at long contexts (single-token passes keep the four slice blocks
+  // per head, which stage a quarter of the rows each, wherever their softmax row fits LDS); both give the same bits
+  const bool head = !a.part && attention_head_form(a.ctx, a.hd) && (B > 1 || attention_lds(a.ctx) > ATTN_LDS_MAX);
+  const size_t lds = a.part ? attention_split_lds(a.hd, a.kvF16) : head ? attention_head_lds(a.hd) : attention_lds(a.ctx);
   ZL_REQUIRE(lds <= ATTN_LDS_MAX, ZL_ERR_UNSUPPORTED, "context too long for the attention kernel");
   ZL_REQUIRE(!a.part || a.nch * ATTN_SPLIT_C >= a.ctx, ZL_ERR_ARG, "attention: split partials below the context");
   ZL_REQUIRE(a.hd == 64 || a.hd == 128 || a.hd == 256, ZL_ERR_UNSUPPORTED, "attention: head_dim must be 64, 128 or 256");
@@ -549,6 +737,16 @@ void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
     else launch_av_split_k<false>(a, gv, lds, st);
     ZL_HIP(hipGetLastError());
     hipLaunchKernelGGL(k_attn_merge, dim3(a.nHead, B), dim3(std::max(64, a.hd)), 0, st, a);
+    ZL_HIP(hipGetLastError());
+    return;
+  }
+  if (head) {
+    switch (a.hd * 2 + a.kvF16) {
+      case 128: launch_av_head_k<64, false>(a, B, st); break;
+      case 129: launch_av_head_k<64, true>(a, B, st); break;
+      case 256: launch_av_head_k<128, false>(a, B, st); break;
+      case 257: launch_av_head_k<128, true>(a, B, st); break;
+    }
     ZL_HIP(hipGetLastError());
     return;
   }

@@ -260,6 +260,7 @@ __device__ inline double rms_scale256(const float *xr, int n, double eps, int ti
 void launch_attention(const AttnArgs &a, int B, hipStream_t st);
 size_t attention_lds(int ctx);
 size_t attention_split_lds(int hd, int kvF16);
+bool attention_head_form(int ctx, int hd);
 void launch_norm_quant(const float *x, int ldx, int row0, int nrows, const float *w, double eps, int n, int npad,
                        const Act &act, hipStream_t st);
 void launch_embed(const MatView &m, const Step *step, int B, float *x, int ldx, hipStream_t st);

@@ -368,13 +368,15 @@ static void finish_model(zl_model *m, const float *ropeFreqs) {
   ZL_REQUIRE(c.head_dim == 128 || c.head_dim == 64 || c.head_dim == 256, ZL_ERR_UNSUPPORTED,
              "head_dim " + std::to_string(c.head_dim) + " is not supported (64, 128 or 256)");
   ZL_REQUIRE(c.n_head % c.n_head_kv == 0, ZL_ERR_UNSUPPORTED, "n_head must be a multiple of n_head_kv");
-  // The weighted sum of attention is the reference's position-order f32 chain, bit for bit, wherever its softmax row
-  // fits the kernel's LDS (contexts up to about 29900 positions). Longer contexts, or contexts beyond
-  // ZEROLLM_ATTN_EXACT_CTX when that is set, take the position-split weighted sum (f64 chunk sums, online-softmax
-  // merge): more accurate than the chain, but not its bits, and on random-weight models the difference is amplified
-  // through the int8 activation quantisation (see the split-path tests).
+  // The weighted sum of attention is the reference's position-order f32 chain, bit for bit: for heads of at most 128
+  // dimensions at any context (the per-head form beyond AVH_CTX positions keeps its softmax row in the scores buffer),
+  // for larger heads wherever the softmax row fits the kernel's LDS (about 29900 positions). Longer contexts of larger
+  // heads, or contexts beyond ZEROLLM_ATTN_EXACT_CTX when that is set, take the position-split weighted sum (f64 chunk
+  // sums, online-softmax merge): more accurate than the chain, but not its bits, and on random-weight models the
+  // difference is amplified through the int8 activation quantisation (see the split-path tests).
   const char *ex = getenv("ZEROLLM_ATTN_EXACT_CTX");
-  const bool split = attention_lds(m->ctx) > 150 * 1024 || (ex && m->ctx > atoi(ex));
+  const bool split = (!attention_head_form(m->ctx, c.head_dim) && attention_lds(m->ctx) > 150 * 1024) ||
+                     (ex && m->ctx > atoi(ex));
   const int half = c.n_rot / 2;
   // RoPE tables exactly as ropeTables (src/compute/ref-kernels.js:329-342), in f64 on the host, stored f32
   std::vector<float> cs((size_t)m->ctx * half), sn((size_t)m->ctx * half);
