@@ -214,12 +214,13 @@ __device__ inline const void *recs_of(const Act &a) {
   else return a.ra;
 }
 
+// The workgroup (kp, tile) of a launch: K part kp of 64-row tile `tile`; xl is the launch's dynamic LDS. Written as a
+// device function so that one kernel can hold two launches of different formats side by side (k_gemv_mix).
 template <int FMT, int MT, int EPI, int DEPTH>
-__global__ __launch_bounds__(1024) void k_gemv_tiles(const GemvArgs a) {
+__device__ __forceinline__ void gemv_tiles_body(const GemvArgs a, const int kp, const int tile, uint8_t *xl) {
   constexpr int NR = EPI == EPI_SWIGLU ? 2 : 1;  // matrices per output row: gate and up for SwiGLU
   // staged activations, per token: [nsl][64] int8 values, then [nsl][32] records; after the slab loop the same bytes
   // hold the waves' sums for the reduction ([W][MT][64] doubles)
-  extern __shared__ __align__(16) uint8_t xl[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = a.nwave;  // waves of the workgroup (1, 2, 4, 8 or 16)
@@ -228,7 +229,7 @@ __global__ __launch_bounds__(1024) void k_gemv_tiles(const GemvArgs a) {
   const int WH = NR == 2 ? W >> 1 : W;
   const int grp = NR == 2 ? __builtin_amdgcn_readfirstlane(wave / WH) : 0;
   const int wl = wave - grp * WH;
-  const int ks = a.ks, kp = blockIdx.x, tile = blockIdx.y;  // grid: (K parts, tiles)
+  const int ks = a.ks;
   // segment of the tile, selected field by field (no dynamic indexing into the argument block)
   const int si = __builtin_amdgcn_readfirstlane(
       EPI == EPI_SWIGLU ? 0 : (a.nseg > 2 && tile >= a.seg[2].tile0) ? 2 : (a.nseg > 1 && tile >= a.seg[1].tile0) ? 1 : 0);
@@ -438,6 +439,12 @@ __global__ __launch_bounds__(1024) void k_gemv_tiles(const GemvArgs a) {
     }
   }
 #undef ZL_SEG
+}
+
+template <int FMT, int MT, int EPI, int DEPTH>
+__global__ __launch_bounds__(1024) void k_gemv_tiles(const GemvArgs a) {
+  extern __shared__ __align__(16) uint8_t xl[];
+  gemv_tiles_body<FMT, MT, EPI, DEPTH>(a, blockIdx.x, blockIdx.y, xl);  // grid: (K parts, tiles)
 }
 
 template <typename K>

@@ -21,12 +21,11 @@ namespace zl {
 constexpr int MF_SLOTS = 8;  // sums per lane: 4 row groups x 2 tokens
 
 template <int EPI>
-__global__ __launch_bounds__(1024) void k_gemv_mfma(const GemvArgs a) {
+__device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, const int tile, uint8_t *xl) {
   constexpr int NR = EPI == EPI_SWIGLU ? 2 : 1;
   constexpr int FMT = T_Q4_K, DEPTH = 4;
   typedef int i32x4 __attribute__((ext_vector_type(4)));
   // staged activations as in k_gemv_tiles; after the slab loop the same bytes hold the waves' sums ([W][8][64])
-  extern __shared__ __align__(16) uint8_t xl[];
   __shared__ __align__(16) double fac[16][64][4];  // per wave: fa0, fa1, fb0, fb1 of the tile's rows for one slab
   const int lane = threadIdx.x & 63, n16 = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -34,7 +33,7 @@ __global__ __launch_bounds__(1024) void k_gemv_mfma(const GemvArgs a) {
   const int WH = NR == 2 ? W >> 1 : W;
   const int grp = NR == 2 ? __builtin_amdgcn_readfirstlane(wave / WH) : 0;
   const int wl = wave - grp * WH;
-  const int ks = a.ks, kp = blockIdx.x, tile = blockIdx.y;
+  const int ks = a.ks;
   const int si = __builtin_amdgcn_readfirstlane(
       EPI == EPI_SWIGLU ? 0 : (a.nseg > 2 && tile >= a.seg[2].tile0) ? 2 : (a.nseg > 1 && tile >= a.seg[1].tile0) ? 1 : 0);
 #define ZL_SEG(f) (si == 0 ? a.seg[0].f : si == 1 ? a.seg[1].f : a.seg[2].f)
@@ -211,6 +210,24 @@ __global__ __launch_bounds__(1024) void k_gemv_mfma(const GemvArgs a) {
 #undef ZL_SEG
 }
 
+template <int EPI>
+__global__ __launch_bounds__(1024) void k_gemv_mfma(const GemvArgs a) {
+  extern __shared__ __align__(16) uint8_t xl[];
+  gemv_mfma_body<EPI>(a, blockIdx.x, blockIdx.y, xl);
+}
+
+// Two store launches reading the same activations in one kernel: a Q4_K launch on the matrix cores (a1) and a launch of
+// another format on the VALU tiles (a2, token tile MT2), workgroups 0 .. a1.ks a1.ntiles - 1 for the first, the rest
+// for the second, each exactly as its own launch would run it (the verify pass's attn_q + attn_k and attn_v: the v
+// launch's workgroups no longer wait for a launch of their own). The launches' split-K work spaces are disjoint.
+template <int FMT2, int MT2>
+__global__ __launch_bounds__(1024) void k_gemv_mix(const GemvArgs a1, const GemvArgs a2) {
+  extern __shared__ __align__(16) uint8_t xl[];
+  const int n1 = a1.ks * a1.ntiles, id = blockIdx.x;
+  if (id < n1) gemv_mfma_body<EPI_STORE>(a1, id % a1.ks, id / a1.ks, xl);
+  else gemv_tiles_body<FMT2, MT2, EPI_STORE, 4>(a2, (id - n1) % a2.ks, (id - n1) / a2.ks, xl);
+}
+
 bool gemv_mfma_ok(const GemvArgs &a) {
   if (a.seg[0].m.type != T_Q4_K || a.M < 2 || a.M > 8 || a.xf) return false;
   for (int i = 0; i < a.nseg; i++)
@@ -235,6 +252,48 @@ void launch_gemv_mfma(const GemvArgs &a, int epi, hipStream_t st) {
     allow_big_lds(k_gemv_mfma<EPI_SWIGLU>);
     hipLaunchKernelGGL((k_gemv_mfma<EPI_SWIGLU>), grid, blk, lds, st, a);
   }
+}
+
+// Whether launch_gemv_mix takes this pair: a1 on the matrix cores, a2 a Q6_K or Q8_0 store launch of the same tokens
+// and workgroup size, neither with a fused prologue, one chunk of tokens.
+bool gemv_mix_ok(const GemvArgs &a1, const GemvArgs &a2) {
+  const int f2 = a2.seg[0].m.type;
+  if (!gemv_mfma_ok(a1) || (f2 != T_Q6_K && f2 != T_Q8_0) || a1.xf || a2.xf || a1.M != a2.M || a1.nwave != a2.nwave)
+    return false;
+  for (int i = 1; i < a2.nseg; i++)
+    if (a2.seg[i].m.type != f2) return false;
+  return a2.kr <= GT_KR_MAX && a2.ks <= 8 && (a2.kr + a2.nwave - 1) / a2.nwave <= GT_NMAX && a1.kr <= GT_KR_MAX &&
+         a1.ks <= 8 && (a1.kr + a1.nwave - 1) / a1.nwave <= GT_NMAX && a1.nwave <= 16;
+}
+
+template <int FMT2, int MT2>
+static void launch_mix_k(const GemvArgs &a1, const GemvArgs &a2, hipStream_t st) {
+  const size_t l1 = std::max((size_t)a1.M * a1.kr * GT_REC, (size_t)a1.nwave * MF_SLOTS * 64 * 8);
+  const size_t l2 = std::max((size_t)a2.M * a2.kr * GT_REC, (size_t)a2.nwave * MT2 * 64 * 8);
+  allow_big_lds(k_gemv_mix<FMT2, MT2>);
+  const unsigned n = (unsigned)(a1.ks * a1.ntiles + a2.ks * a2.ntiles);
+  hipLaunchKernelGGL((k_gemv_mix<FMT2, MT2>), dim3(n), dim3((unsigned)a1.nwave * 64), std::max(l1, l2), st, a1, a2);
+}
+
+template <int FMT2>
+static void launch_mix_fmt(const GemvArgs &a1, const GemvArgs &a2, hipStream_t st) {
+  switch (a1.M) {
+    case 2: launch_mix_k<FMT2, 2>(a1, a2, st); break;
+    case 3: launch_mix_k<FMT2, 3>(a1, a2, st); break;
+    case 4: launch_mix_k<FMT2, 4>(a1, a2, st); break;
+    case 5: launch_mix_k<FMT2, 5>(a1, a2, st); break;
+    case 6: launch_mix_k<FMT2, 6>(a1, a2, st); break;
+    default: launch_mix_k<FMT2, 8>(a1, a2, st); break;  // 7 and 8 tokens (token tile 8, as the tile launch)
+  }
+}
+
+void launch_gemv_mix(const GemvArgs &a1, const GemvArgs &a2, hipStream_t st) {
+  ZL_REQUIRE(gemv_mix_ok(a1, a2), ZL_ERR_ARG, "gemv: launches cannot share a kernel");
+  ZL_REQUIRE(a1.act.q && a1.act.ra && a1.act.rb && a1.act.rc && a2.act.q == a1.act.q, ZL_ERR_ARG, "gemv: activation records missing");
+  ZL_REQUIRE((a1.ks == 1 || a1.part) && (a2.ks == 1 || a2.part), ZL_ERR_ARG, "gemv: split-K work space missing");
+  if (a2.seg[0].m.type == T_Q6_K) launch_mix_fmt<T_Q6_K>(a1, a2, st);
+  else launch_mix_fmt<T_Q8_0>(a1, a2, st);
+  ZL_HIP(hipGetLastError());
 }
 
 }  // namespace zl

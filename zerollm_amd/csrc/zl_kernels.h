@@ -168,6 +168,10 @@ void gemv_shape(int ntiles, int nslab, bool swiglu, int *ks, int *nw);
 void launch_gemv(const GemvArgs &a, int epi, const float *xf, int ldx, hipStream_t st);
 bool gemv_mfma_ok(const GemvArgs &a);
 void launch_gemv_mfma(const GemvArgs &a, int epi, hipStream_t st);
+// Two store launches of the same tokens in one kernel (a1 Q4_K on the matrix cores, a2 Q6_K or Q8_0 on the VALU tiles);
+// their split-K work spaces must be disjoint.
+bool gemv_mix_ok(const GemvArgs &a1, const GemvArgs &a2);
+void launch_gemv_mix(const GemvArgs &a1, const GemvArgs &a2, hipStream_t st);
 // Single-token Q8_0 GEMV in 16-row groups (zl_gemv_rg.hip): takes f32 input rows (a.xf, RMSNorm'd with a.nw when set)
 // and quantises them itself; K <= 3072.
 bool gemv_rg_ok(const GemvArgs &a);

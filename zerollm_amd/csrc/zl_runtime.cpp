@@ -503,6 +503,16 @@ static bool use_rg() {
   }();
   return on;
 }
+// ZEROLLM_GEMV_MIX=0 keeps every store launch a kernel of its own.
+static bool use_mix() {
+  static int v = -1;
+  if (v < 0) {
+    const char *e = getenv("ZEROLLM_GEMV_MIX");
+    v = (e && e[0] == '0') ? 0 : 1;
+  }
+  return v == 1;
+}
+
 static bool rg_path(const std::vector<const DevMat *> &ms, int B) {
   if (!use_rg() || B != 1) return false;
   for (const DevMat *d : ms)
@@ -566,7 +576,7 @@ static void gemv_rows(zl_model *m, const std::vector<std::vector<SegSpec>> &grou
     need = need || !(fused[i] || rg[i]);
   }
   if (need && norm) norm_quant(m, p.x, p.ldx, p.row0, B, p.nw, p.n, m->act);
-  for (size_t i = 0; i < groups.size(); i++) {
+  auto args_of = [&](size_t i) {
     GemvArgs a = gemv_args(groups[i], B, epis[i], m->act, m->gw);
     a.resid = m->x;
     a.ldr = m->cfg.n_embd;
@@ -575,6 +585,22 @@ static void gemv_rows(zl_model *m, const std::vector<std::vector<SegSpec>> &grou
     if (qout && epis[i] == EPI_SWIGLU && !rg[i]) a.qout = *qout;
     if (fused[i] || rg[i]) {
       a.xf = p.x; a.ldxf = p.ldx; a.xrow0 = p.row0; a.n = p.n; a.nw = p.nw; a.eps = (double)m->cfg.rms_eps;
+    }
+    return a;
+  };
+  for (size_t i = 0; i < groups.size(); i++) {
+    GemvArgs a = args_of(i);
+    if (i + 1 < groups.size() && use_mix() && !rg[i] && !rg[i + 1] && epis[i] == EPI_STORE && epis[i + 1] == EPI_STORE) {
+      // a Q4_K store launch on the matrix cores and the next store launch of another format share one kernel
+      GemvArgs b = args_of(i + 1);
+      b.part += (long)a.ntiles * a.ks * GEMV_MAX_MT * 64 * 2;  // disjoint split-K work spaces
+      b.cnt += a.ntiles;
+      if ((long)(a.ntiles + b.ntiles) <= GEMV_CNT_TILES &&
+          (long)(a.ntiles * a.ks + b.ntiles * b.ks) * 2 * GEMV_MAX_MT * 64 <= GEMV_PART_DOUBLES && gemv_mix_ok(a, b)) {
+        launch_gemv_mix(a, b, m->st);
+        i++;
+        continue;
+      }
     }
     if (rg[i]) launch_gemv_rg(a, epis[i], m->st);
     else launch_gemv(a, epis[i], m->act.f, m->act.ld, m->st);
