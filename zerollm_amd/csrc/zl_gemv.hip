@@ -43,22 +43,25 @@ __global__ __launch_bounds__(256) void k_gemv_float(const GemvArgs a, int rows_t
 }
 
 // Launch shape, a function of the matrix shape only (so every summation order is independent of the token count):
-// - waves per matrix: 4 when there are enough tiles to fill the GPU with workgroups, else 16 (8 for gate/up pairs, whose
-//   workgroup runs the gate and the up rows on two halves of 8), so that a small matrix still has many slab loads in
-//   flight per CU;
+// - waves per matrix: 4 when there are enough tiles to fill the GPU with workgroups, else 8 (4 for gate/up pairs, whose
+//   workgroup runs the gate and the up rows on two halves). Against 16 (8 per gate/up half) each wave holds more slabs,
+//   so more of its compute overlaps the loads, and fewer waves meet in the reduction: 5-25 % faster at M = 1, 5, 9 for
+//   every 8B and 0.6B projection shape;
 // - K parts: 1 (no cross-workgroup sum) unless a part would exceed the staged-activation limit (GT_KR_MAX slabs) or
 //   give a wave more than GT_NMAX slabs; for large single-output matrices of fewer tiles than CUs, more parts where that
-//   lowers the slabs the busiest CU streams (attn_output 4096 x 4096: 4 parts, 256 workgroups). Not for gate/up pairs:
-//   their 8-wave workgroups hold too many registers to overlap, so rounds of K parts cost more than they save.
+//   lowers the slabs the busiest CU streams while every wave keeps at least two slabs (attn_output 4096 x 4096: 4 parts,
+//   256 workgroups; attn_v 1024 x 4096: 4 parts, so that its launch mixed with attn_q/attn_k's 160 workgroups stays
+//   within one round of 256). Not for gate/up pairs: their workgroups hold too many registers to overlap, so rounds of
+//   K parts cost more than they save.
 void gemv_shape(int ntiles, int nslab, bool swiglu, int *ks, int *nw) {
-  const int w = ntiles >= 256 ? 4 : swiglu ? 8 : 16;  // waves per matrix
+  const int w = ntiles >= 256 || swiglu ? 4 : 8;  // waves per matrix
   int k = 1;
   while ((nslab + k - 1) / k > 96 || ((nslab + k - 1) / k + w - 1) / w > 16) k *= 2;
   // large matrices of fewer tiles than CUs: more K parts while that lowers the most slabs one CU streams (workgroups
-  // run in rounds of 256), keeping at least one slab per wave
+  // run in rounds of 256), keeping at least two slabs per wave
   if (!swiglu && ntiles < 256 && (long)ntiles * nslab >= 1024) {
     auto load = [&](int kk) { return (long)((ntiles * kk + 255) / 256) * ((nslab + kk - 1) / kk); };
-    for (int kk = k * 2; kk <= 8 && (nslab + kk - 1) / kk >= w; kk *= 2)
+    for (int kk = k * 2; kk <= 8 && (nslab + kk - 1) / kk >= 2 * w; kk *= 2)
       if (load(kk) < load(k)) k = kk;
   }
   *ks = k;
