@@ -105,7 +105,7 @@ void launch_gemv(const GemvArgs &a0, int epi, const float *xf, int ldx, hipStrea
       b.xrow0 += t0;  // fused prologue: the chunk's own input rows
     }
     t0 += b.M;
-    if (gemv_mfma_ok(b)) {  // Q4_K at 2..8 tokens: the int8 dots on the matrix cores, same results
+    if (gemv_mfma_ok(b)) {  // Q4_K and Q8_0 at 2..8 tokens: the int8 dots on the matrix cores, same results
       launch_gemv_mfma(b, epi, st);
       ZL_HIP(hipGetLastError());
       continue;

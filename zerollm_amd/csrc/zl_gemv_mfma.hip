@@ -1,7 +1,7 @@
-// Q4_K GEMV for 2..8 tokens with the int8 block dots on the matrix cores (v_mfma_i32_16x16x64_i8), the same results
-// bit for bit as k_gemv_tiles (zl_gemv.h): the same slabs per wave, the same f64 block terms per (row, token) in the
-// same order (slab by slab, block 0 then block 1, in the reference's arithmetic, src/compute/ref-kernels.js:210-240),
-// the same halving-tree reduction over the waves and the same K parts.
+// Q4_K and Q8_0 GEMVs for 2..8 tokens with the int8 block dots on the matrix cores (v_mfma_i32_16x16x64_i8), the same
+// results bit for bit as k_gemv_tiles (zl_gemv.h): the same slabs per wave, the same f64 block terms per (row, token)
+// in the same order (slab by slab, block 0 then block 1, in the reference's arithmetic, src/compute/ref-kernels.js:
+// 132-152, 210-240), the same halving-tree reduction over the waves and the same K parts.
 //
 // One MFMA multiplies an activation fragment A (16 rows rho = 2 t + b: token t's values of the slab's 32-value block b,
 // zero elsewhere in the slab) by a weight fragment B (16 rows of the tile, the slab's 64 values) into D[rho][row]: the
@@ -13,20 +13,24 @@
 // 16 j + n, value e and e + 4 in the low and high nibble of byte e of each 4-byte word, so two masks and a shift give
 // the operand's 16 bytes in value order). The scale codes and super-block scales are read from the row-layout planes,
 // one row per lane as in k_gemv_tiles; each lane forms its row's four f64 factors once per slab and parks them in LDS,
-// where the lanes of the other row groups read them.
+// where the lanes of the other row groups read them. Q8_0 needs no second plane: its row-layout plane holds part p
+// (values 16 p .. 16 p + 15) of row r at 16-byte unit 64 p + r of a tile-slab, so lane n + 16 g reads its operand bytes
+// for row group j at unit 64 g + 16 j + n; the factors are the two block scales d.
 #include "zl_gemv.h"
 
 namespace zl {
 
 constexpr int MF_SLOTS = 8;  // sums per lane: 4 row groups x 2 tokens
 
-template <int EPI>
+template <int FMT, int EPI>
 __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, const int tile, uint8_t *xl) {
+  static_assert(FMT == T_Q4_K || FMT == T_Q8_0, "matrix-core formats");
   constexpr int NR = EPI == EPI_SWIGLU ? 2 : 1;
-  constexpr int FMT = T_Q4_K, DEPTH = 4;
+  constexpr int DEPTH = FMT == T_Q4_K ? 4 : 3;  // Q8_0 slabs are 64 bytes per lane: three in flight
   typedef int i32x4 __attribute__((ext_vector_type(4)));
   // staged activations as in k_gemv_tiles; after the slab loop the same bytes hold the waves' sums ([W][8][64])
-  __shared__ __align__(16) double fac[16][64][4];  // per wave: fa0, fa1, fb0, fb1 of the tile's rows for one slab
+  __shared__ __align__(16) double fac[16][64][4];  // per wave: the factors of the tile's rows for one slab (Q4_K: fa0,
+                                                   // fa1, fb0, fb1; Q8_0: d0, d1)
   const int lane = threadIdx.x & 63, n16 = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = a.nwave;
@@ -39,10 +43,11 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
 #define ZL_SEG(f) (si == 0 ? a.seg[0].f : si == 1 ? a.seg[1].f : a.seg[2].f)
   const int lt = tile - ZL_SEG(tile0), rows = ZL_SEG(rows);
   const int nslab = a.nslab, nsb = nslab >> 2;
-  // the fragment plane takes the place of the row-layout 4-bit plane (same size and per-tile-slab offsets)
-  const Rsrc R0 = {make_rsrc(ZL_SEG(m.fq), ZL_SEG(nqs)), make_rsrc(nullptr, 0), make_rsrc(ZL_SEG(m.sc), ZL_SEG(nsc)),
-                   make_rsrc(ZL_SEG(m.dd), ZL_SEG(ndd))};
-  const Rsrc R1 = NR == 2 ? Rsrc{make_rsrc(a.seg[1].m.fq, a.seg[1].nqs), make_rsrc(nullptr, 0),
+  // Q4_K: the fragment plane takes the place of the row-layout 4-bit plane (same size and per-tile-slab offsets); Q8_0:
+  // the row-layout plane is already in operand order (part p of row r at 16-byte unit 64 p + r of the tile-slab)
+  const Rsrc R0 = {make_rsrc(FMT == T_Q4_K ? ZL_SEG(m.fq) : ZL_SEG(m.qs), ZL_SEG(nqs)), make_rsrc(nullptr, 0),
+                   make_rsrc(ZL_SEG(m.sc), ZL_SEG(nsc)), make_rsrc(ZL_SEG(m.dd), ZL_SEG(ndd))};
+  const Rsrc R1 = NR == 2 ? Rsrc{make_rsrc(FMT == T_Q4_K ? a.seg[1].m.fq : a.seg[1].m.qs, a.seg[1].nqs), make_rsrc(nullptr, 0),
                                  make_rsrc(a.seg[1].m.sc, a.seg[1].nsc), make_rsrc(a.seg[1].m.dd, a.seg[1].ndd)}
                           : R0;
   const int kr = a.kr, s0 = kp * kr, s1 = min(nslab, s0 + kr), nsl = s1 - s0;
@@ -59,7 +64,19 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
   auto load = [&](int i, Raw<FMT> &b) {
     const int s = s0 + wl + WH * i;
     const int ts = lt * nslab + s, sbi = lt * nsb + (s >> 2);
-    raw_load<FMT>(R, ts, sbi, lane, i < n, b);
+    if constexpr (FMT == T_Q4_K) {
+      raw_load<FMT>(R, ts, sbi, lane, i < n, b);
+    } else {
+      // Q8_0: q[4 j .. 4 j + 3] = part g of row 16 j + n16 (the B operand of row group j); dw = the two block scales of
+      // row `lane` (its factors); past the wave's last slab the offsets leave the planes (zeros, no memory access)
+      const int oob = i < n ? 0 : 0x40000000, tsv = i < n ? ts : 0;
+      #pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(R.qs, oob + (g * 64 + n16) * 16 + j * 256, tsv * 4096, 0));
+        b.q[4 * j] = v.x; b.q[4 * j + 1] = v.y; b.q[4 * j + 2] = v.z; b.q[4 * j + 3] = v.w;
+      }
+      b.dw = __builtin_amdgcn_raw_buffer_load_b32(R.dd, oob + lane * 4, tsv * 256, 0);
+    }
   };
   #pragma unroll
   for (int d = 0; d < DEPTH; d++) load(d, buf[d]);
@@ -94,12 +111,20 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
     for (int d = 0; d < DEPTH; d++) {
       const int i = i0 + d;
       if (i >= GT_NMAX) break;
-      // this lane's row (16 g + n16 = lane): its four factors, as k_gemv_tiles forms them
+      // this lane's row (16 g + n16 = lane): its factors, as k_gemv_tiles forms them
       const Raw<FMT> &o = buf[d];
       const double d0 = (double)h2f((uint16_t)(o.dw & 0xffff)), d1 = (double)h2f((uint16_t)(o.dw >> 16));
-      const double f4[4] = {d0 * (double)(o.sc & 0xff), d0 * (double)((o.sc >> 8) & 0xff),
-                            d1 * (double)((o.sc >> 16) & 0xff), d1 * (double)((o.sc >> 24) & 0xff)};
-      const uint32_t q[8] = {o.q[0], o.q[1], o.q[2], o.q[3], o.q[4], o.q[5], o.q[6], o.q[7]};
+      double f4[4];
+      if constexpr (FMT == T_Q4_K) {
+        f4[0] = d0 * (double)(o.sc & 0xff); f4[1] = d0 * (double)((o.sc >> 8) & 0xff);
+        f4[2] = d1 * (double)((o.sc >> 16) & 0xff); f4[3] = d1 * (double)((o.sc >> 24) & 0xff);
+      } else {
+        f4[0] = d0; f4[1] = d1; f4[2] = 0.0; f4[3] = 0.0;
+      }
+      constexpr int QN = FMT == T_Q4_K ? 8 : 16;
+      uint32_t q[QN];
+      #pragma unroll
+      for (int k = 0; k < QN; k++) q[k] = o.q[k];
       __builtin_amdgcn_sched_barrier(0);
       load(i + DEPTH, buf[d]);  // past the wave's last slab: no memory access
       if (i < n) {
@@ -114,15 +139,21 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
         const double xs[4] = {dbl(r00.z, r00.w), dbl(r01.z, r01.w), dbl(r10.z, r10.w), dbl(r11.z, r11.w)};
         #pragma unroll
         for (int j = 0; j < 4; j++) {
-          const uint32_t p0 = q[2 * j], p1 = q[2 * j + 1];
-          const i32x4 B = {(int)(p0 & 0x0F0F0F0Fu), (int)((p0 >> 4) & 0x0F0F0F0Fu), (int)(p1 & 0x0F0F0F0Fu),
-                           (int)((p1 >> 4) & 0x0F0F0F0Fu)};
+          i32x4 B;
+          if constexpr (FMT == T_Q4_K) {
+            const uint32_t p0 = q[2 * j], p1 = q[2 * j + 1];
+            B = (i32x4){(int)(p0 & 0x0F0F0F0Fu), (int)((p0 >> 4) & 0x0F0F0F0Fu), (int)(p1 & 0x0F0F0F0Fu),
+                        (int)((p1 >> 4) & 0x0F0F0F0Fu)};
+          } else {
+            B = (i32x4){(int)q[4 * j], (int)q[4 * j + 1], (int)q[4 * j + 2], (int)q[4 * j + 3]};
+          }
           const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, (i32x4){0, 0, 0, 0}, 0, 0, 0);
-          const double4 f = *(const double4 *)(fw + (16 * j + n16) * 4);  // row 16 j + n16: fa0, fa1, fb0, fb1
+          const double4 f = *(const double4 *)(fw + (16 * j + n16) * 4);  // row 16 j + n16: its factors
           #pragma unroll
           for (int v = 0; v < 4; v++) {
             const double fa = (v & 1) ? f.y : f.x, fb = (v & 1) ? f.w : f.z;
-            acc[j][v >> 1] = fma(xd[v], fma(fa, (double)D[v], -(fb * xs[v])), acc[j][v >> 1]);
+            if constexpr (FMT == T_Q4_K) acc[j][v >> 1] = fma(xd[v], fma(fa, (double)D[v], -(fb * xs[v])), acc[j][v >> 1]);
+            else acc[j][v >> 1] = fma((double)D[v] * fa, xd[v], acc[j][v >> 1]);  // Q8_0: (s * d) * xd
           }
         }
       }
@@ -210,10 +241,10 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
 #undef ZL_SEG
 }
 
-template <int EPI>
+template <int FMT, int EPI>
 __global__ __launch_bounds__(1024) void k_gemv_mfma(const GemvArgs a) {
   extern __shared__ __align__(16) uint8_t xl[];
-  gemv_mfma_body<EPI>(a, blockIdx.x, blockIdx.y, xl);
+  gemv_mfma_body<FMT, EPI>(a, blockIdx.x, blockIdx.y, xl);
 }
 
 // Two store launches reading the same activations in one kernel: a Q4_K launch on the matrix cores (a1) and a launch of
@@ -224,15 +255,31 @@ template <int FMT2, int MT2>
 __global__ __launch_bounds__(1024) void k_gemv_mix(const GemvArgs a1, const GemvArgs a2) {
   extern __shared__ __align__(16) uint8_t xl[];
   const int n1 = a1.ks * a1.ntiles, id = blockIdx.x;
-  if (id < n1) gemv_mfma_body<EPI_STORE>(a1, id % a1.ks, id / a1.ks, xl);
+  if (id < n1) gemv_mfma_body<T_Q4_K, EPI_STORE>(a1, id % a1.ks, id / a1.ks, xl);
   else gemv_tiles_body<FMT2, MT2, EPI_STORE, 4>(a2, (id - n1) % a2.ks, (id - n1) / a2.ks, xl);
 }
 
+// Q4_K matrices with their fragment plane, and Q8_0 matrices, at 2..8 tokens without a fused prologue.
 bool gemv_mfma_ok(const GemvArgs &a) {
-  if (a.seg[0].m.type != T_Q4_K || a.M < 2 || a.M > 8 || a.xf) return false;
+  const int t = a.seg[0].m.type;
+  if ((t != T_Q4_K && t != T_Q8_0) || a.M < 2 || a.M > 8 || a.xf) return false;
   for (int i = 0; i < a.nseg; i++)
-    if (!a.seg[i].m.fq) return false;
+    if (a.seg[i].m.type != t || (t == T_Q4_K && !a.seg[i].m.fq)) return false;
   return true;
+}
+
+template <int FMT>
+static void launch_mfma_fmt(const GemvArgs &a, int epi, dim3 grid, dim3 blk, size_t lds, hipStream_t st) {
+  if (epi == EPI_STORE) {
+    allow_big_lds(k_gemv_mfma<FMT, EPI_STORE>);
+    hipLaunchKernelGGL((k_gemv_mfma<FMT, EPI_STORE>), grid, blk, lds, st, a);
+  } else if (epi == EPI_RESID) {
+    allow_big_lds(k_gemv_mfma<FMT, EPI_RESID>);
+    hipLaunchKernelGGL((k_gemv_mfma<FMT, EPI_RESID>), grid, blk, lds, st, a);
+  } else {
+    allow_big_lds(k_gemv_mfma<FMT, EPI_SWIGLU>);
+    hipLaunchKernelGGL((k_gemv_mfma<FMT, EPI_SWIGLU>), grid, blk, lds, st, a);
+  }
 }
 
 void launch_gemv_mfma(const GemvArgs &a, int epi, hipStream_t st) {
@@ -242,23 +289,16 @@ void launch_gemv_mfma(const GemvArgs &a, int epi, hipStream_t st) {
              ZL_ERR_ARG, "gemv (matrix cores): launch shape out of range");
   const dim3 grid((unsigned)a.ks, (unsigned)a.ntiles), blk((unsigned)a.nwave * 64);
   const size_t lds = std::max((size_t)a.M * a.kr * GT_REC, (size_t)a.nwave * MF_SLOTS * 64 * 8);
-  if (epi == EPI_STORE) {
-    allow_big_lds(k_gemv_mfma<EPI_STORE>);
-    hipLaunchKernelGGL((k_gemv_mfma<EPI_STORE>), grid, blk, lds, st, a);
-  } else if (epi == EPI_RESID) {
-    allow_big_lds(k_gemv_mfma<EPI_RESID>);
-    hipLaunchKernelGGL((k_gemv_mfma<EPI_RESID>), grid, blk, lds, st, a);
-  } else {
-    allow_big_lds(k_gemv_mfma<EPI_SWIGLU>);
-    hipLaunchKernelGGL((k_gemv_mfma<EPI_SWIGLU>), grid, blk, lds, st, a);
-  }
+  if (a.seg[0].m.type == T_Q4_K) launch_mfma_fmt<T_Q4_K>(a, epi, grid, blk, lds, st);
+  else launch_mfma_fmt<T_Q8_0>(a, epi, grid, blk, lds, st);
 }
 
 // Whether launch_gemv_mix takes this pair: a1 on the matrix cores, a2 a Q6_K or Q8_0 store launch of the same tokens
 // and workgroup size, neither with a fused prologue, one chunk of tokens.
 bool gemv_mix_ok(const GemvArgs &a1, const GemvArgs &a2) {
   const int f2 = a2.seg[0].m.type;
-  if (!gemv_mfma_ok(a1) || (f2 != T_Q6_K && f2 != T_Q8_0) || a1.xf || a2.xf || a1.M != a2.M || a1.nwave != a2.nwave)
+  if (!gemv_mfma_ok(a1) || a1.seg[0].m.type != T_Q4_K || (f2 != T_Q6_K && f2 != T_Q8_0) || a1.xf || a2.xf ||
+      a1.M != a2.M || a1.nwave != a2.nwave)
     return false;
   for (int i = 1; i < a2.nseg; i++)
     if (a2.seg[i].m.type != f2) return false;
