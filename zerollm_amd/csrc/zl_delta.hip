@@ -1,59 +1,103 @@
 // Gated DeltaNet layer step over the B tokens of a pass (src/model/forward-qwen35.js:45-61, per-token arithmetic of
-// src/compute/ref-deltanet.js:42-106), one workgroup per value head, tokens in order:
-//   conv   depthwise causal conv + SiLU of the head's 3 x D channels (q and k of key head hv % nK, v of hv itself):
-//          f64 dot over the window [oldest .. newest, x], stored f32; the window advances token by token;
+// src/compute/ref-deltanet.js:42-106), tokens in order, DELTA_ROWS value rows (of the D) of one value head per
+// workgroup:
+//   conv   depthwise causal conv + SiLU of the head's q and k (key head hv % nK) and of the workgroup's v channels: f64
+//          dot over the window [oldest .. newest, x], stored f32; the window advances token by token;
 //   l2     q normalised and scaled by 1/sqrt(D), k normalised, per token;
 //   delta  S <- exp(g) S; d = beta (v - S^T k); S <- S + k d^T; o = S^T q, with the reference's f64 arithmetic and f32
-//          stores; each row of S is held by 4 lanes (D/4 values each, f64 partial sums joined in a fixed order);
+//          stores; each row of S is held by 8 lanes (D/8 values each, f64 partial sums joined in a fixed order);
 //   norm   gated RMSNorm of o (weights normW, gate silu(z)), then quantizeAct for the ssm_out projection.
-// The head's S (D x D f32) stays in registers across the B tokens: it is read and written once per pass.
+// Row j of the delta rule reads only S[j][.], v_j and the head's q and k, so the rows split over workgroups without any
+// change of arithmetic: every workgroup convolves and normalises the head's q and k itself (the same bits in each), and
+// holds its rows of S in registers across the B tokens (read and written once per pass, captured per token when asked).
+// The gated norm needs the head's whole output row: each workgroup stores its rows' outputs to an exchange buffer at
+// agent scope and counts its arrival; the last to arrive for the head reads the other rows, norms, gates and quantises
+// the head's B rows, and writes back the head's q and k conv windows, which every workgroup of the head read at its
+// start, before it arrived. The arrival counter is back at zero when the launch ends.
 #include "zl_kernels.h"
 
 namespace zl {
 
+constexpr int DELTA_ROWS = 32;  // value rows of a head per workgroup
+constexpr int DELTA_LPR = 8;    // lanes per row (DELTA_ROWS x DELTA_LPR = 256 threads)
+
 template <int D, int CK>
-__global__ __launch_bounds__(4 * D) void k_deltanet(const DeltaArgs a) {
-  constexpr int NT = 4 * D, NW = NT / 64, PER = D / 4;
-  constexpr int ROW = D + 16;  // LDS row of q or k: the four row parts padded apart by 4 floats (distinct banks)
+__global__ __launch_bounds__(DELTA_LPR * DELTA_ROWS) void k_deltanet(const DeltaArgs a) {
+  constexpr int RW = DELTA_ROWS, R = D / RW, LPR = DELTA_LPR, NT = LPR * RW, NW = NT / 64, PER = D / LPR;
+  constexpr int ROW = D + 4 * LPR;  // LDS row of q or k: the row parts padded apart by 4 floats (distinct banks)
   constexpr int M = CK - 1;    // window length
-  __shared__ float cq[DELTA_MAX_B * ROW], ck[DELTA_MAX_B * ROW], cv[DELTA_MAX_B * D], core[DELTA_MAX_B * D];
+  static_assert(D % RW == 0, "head size is a multiple of the rows per workgroup");
+  constexpr int NCH = 2 * D + RW;      // channels of the workgroup: the head's q and k, then its RW rows of v
+  constexpr int EXT = M + DELTA_MAX_B;  // per channel: the window (oldest first), then the launch's inputs
+  __shared__ float cq[DELTA_MAX_B * ROW], ck[DELTA_MAX_B * ROW], cv[DELTA_MAX_B * RW], core[DELTA_MAX_B * D];
+  __shared__ float ext[NCH * EXT], wts[NCH * CK];
   __shared__ double gexp[DELTA_MAX_B], bet[DELTA_MAX_B];
-  const int hv = blockIdx.x, kh = hv % a.nK, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ uint32_t last;
+  const int hv = blockIdx.x / R, r = blockIdx.x - hv * R, kh = hv % a.nK, tid = threadIdx.x, lane = tid & 63,
+            wave = tid >> 6;
   const int B = a.B;
   auto pidx = [](int i) { return i + (i / PER) * 4; };
-
-  // ---- conv + SiLU (convStep, src/compute/ref-deltanet.js:42-55)
   const int keyDim = a.nK * D;
-  if (tid < 3 * D) {
-    const int grp = tid / D, i = tid - grp * D;
-    const int ch = grp == 0 ? kh * D + i : grp == 1 ? keyDim + kh * D + i : 2 * keyDim + hv * D + i;
-    float *win = a.conv + (((long)hv * 3 + grp) * D + i) * M;
-    float w[CK], st[M > 0 ? M : 1];
+  // channel c of the workgroup: group (0 q, 1 k, 2 v), index within the head, conv channel, window
+  auto chan = [&](int c, int &grp, int &i) {
+    grp = c < D ? 0 : c < 2 * D ? 1 : 2;
+    i = grp < 2 ? c - grp * D : r * RW + (c - 2 * D);
+    return grp == 0 ? kh * D + i : grp == 1 ? keyDim + kh * D + i : 2 * keyDim + hv * D + i;
+  };
+
+  // lane (j, p) holds S[jg][p*PER .. p*PER+PER) of the head's row jg = r RW + j (requested first: it is used last)
+  const int j = tid / LPR, p = tid % LPR, jg = r * RW + j;
+  float S[PER];
+  float *srow = a.ssm + ((long)hv * D + jg) * D + p * PER;
+  #pragma unroll
+  for (int c = 0; c < PER; c += 4) {
+    const float4 v4 = *(const float4 *)(srow + c);
+    S[c] = v4.x; S[c + 1] = v4.y; S[c + 2] = v4.z; S[c + 3] = v4.w;
+  }
+
+  // ---- stage the windows, the B inputs and the conv weights of the workgroup's channels (every load issued up front)
+  {
+    // all loads first (registers), then the LDS stores: a load per loop iteration would wait out its latency each time
+    constexpr int SE = ((M + DELTA_MAX_B) * NCH + NT - 1) / NT, SW = (CK * NCH + NT - 1) / NT;
+    float ve[SE], vw[SW];
     #pragma unroll
-    for (int t = 0; t < CK; t++) w[t] = a.convW[(long)ch * CK + t];
-    #pragma unroll
-    for (int t = 0; t < M; t++) st[t] = win[t];
-    for (int b = 0; b < B; b++) {
-      const float cur = a.qkv[(long)b * a.ldqkv + ch];
-      double acc = 0.0;
-      #pragma unroll
-      for (int t = 0; t < M; t++) acc += (double)w[t] * (double)st[t];
-      acc += (double)w[M] * (double)cur;
-      #pragma unroll
-      for (int t = 0; t + 1 < M; t++) st[t] = st[t + 1];
-      if (M > 0) st[M - 1] = cur;
-      if (a.capConv) {  // the window after token b
-        float *cw = a.capConv + (long)b * a.capStride + (((long)hv * 3 + grp) * D + i) * M;
-        #pragma unroll
-        for (int t = 0; t < M; t++) cw[t] = st[t];
-      }
-      const float y = (float)(acc / (1.0 + exp(-acc)));
-      if (grp == 0) cq[b * ROW + pidx(i)] = y;
-      else if (grp == 1) ck[b * ROW + pidx(i)] = y;
-      else cv[b * D + i] = y;
+    for (int k = 0; k < SE; k++) {
+      const int idx = tid + k * NT, t = idx / NCH, c = idx - t * NCH;
+      int grp, i;
+      const int ch = chan(c, grp, i);
+      ve[k] = idx >= (M + B) * NCH ? 0.f
+              : t < M ? a.conv[(((long)hv * 3 + grp) * D + i) * M + t] : a.qkv[(long)(t - M) * a.ldqkv + ch];
     }
     #pragma unroll
-    for (int t = 0; t < M; t++) win[t] = st[t];
+    for (int k = 0; k < SW; k++) {
+      const int idx = tid + k * NT, t = idx / NCH, c = idx - t * NCH;
+      int grp, i;
+      const int ch = chan(c, grp, i);
+      vw[k] = idx < CK * NCH ? a.convW[(long)ch * CK + t] : 0.f;
+    }
+    #pragma unroll
+    for (int k = 0; k < SE; k++) {
+      const int idx = tid + k * NT, t = idx / NCH, c = idx - t * NCH;
+      if (idx < (M + B) * NCH) ext[c * EXT + t] = ve[k];
+    }
+    #pragma unroll
+    for (int k = 0; k < SW; k++) {
+      const int idx = tid + k * NT, t = idx / NCH, c = idx - t * NCH;
+      if (idx < CK * NCH) wts[c * CK + t] = vw[k];
+    }
+  }
+  // the gate values and norm weights of the lane's outputs in the gated norm (token wave + NW k, value 64 q + lane)
+  constexpr int ZB = ((DELTA_MAX_B + NW - 1) / NW + 1) / 2 * 2, ZI = (D + 63) / 64;
+  float zr[ZB][ZI], nwr[ZI];
+  #pragma unroll
+  for (int q = 0; q < ZI; q++) {
+    const int i = 64 * q + lane;
+    nwr[q] = a.normW[i < D ? i : 0];
+    #pragma unroll
+    for (int k = 0; k < ZB; k++) {
+      const int b = wave + NW * k;
+      zr[k][q] = a.z[(long)(b < B ? b : 0) * a.ldz + hv * D + (i < D ? i : 0)];
+    }
   }
   // decay and write strength per token (src/model/forward-qwen35.js:55-56): beta = sigmoid(b),
   // exp(softplus(alpha + dt_bias) * ssm_a)
@@ -65,66 +109,149 @@ __global__ __launch_bounds__(4 * D) void k_deltanet(const DeltaArgs a) {
   }
   __syncthreads();
 
-  // ---- L2 norms (l2normHeads, src/compute/ref-deltanet.js:61-69): one wave per (token, q or k) row
-  for (int r = wave; r < 2 * B; r += NW) {
-    float *row = ((r & 1) ? ck : cq) + (r >> 1) * ROW;
-    double ss = 0.0;
-    for (int i = lane; i < D; i += 64) { const double x = (double)row[pidx(i)]; ss += x * x; }
-    ss = wave_sum_xor(ss, 64);
-    const double s = ((r & 1) ? 1.0 : 1.0 / sqrt((double)D)) / sqrt(ss + a.eps);
-    for (int i = lane; i < D; i += 64) row[pidx(i)] = (float)((double)row[pidx(i)] * s);
+  // ---- conv + SiLU (convStep, src/compute/ref-deltanet.js:42-55) of every (channel, token): the window of token b is
+  // ext[b .. b + M), its input ext[b + M]; f64 products added in window order, then the input's
+  #pragma unroll 2
+  for (int idx = tid; idx < B * NCH; idx += NT) {
+    const int b = idx / NCH, c = idx - b * NCH;
+    int grp, i;
+    chan(c, grp, i);
+    const float *e = ext + c * EXT + b, *w = wts + c * CK;
+    double acc = 0.0;
+    #pragma unroll
+    for (int t = 0; t < M; t++) acc += (double)w[t] * (double)e[t];
+    acc += (double)w[M] * (double)e[M];
+    if (a.capConv && (grp == 2 || r == 0)) {  // the window after token b (q and k by the head's first workgroup)
+      float *cw = a.capConv + (long)b * a.capStride + (((long)hv * 3 + grp) * D + i) * M;
+      #pragma unroll
+      for (int t = 0; t < M; t++) cw[t] = e[t + 1];
+    }
+    const float y = (float)(acc / (1.0 + exp(-acc)));
+    if (grp == 0) cq[b * ROW + pidx(i)] = y;
+    else if (grp == 1) ck[b * ROW + pidx(i)] = y;
+    else cv[b * RW + (i - r * RW)] = y;
+  }
+  for (int idx = tid; idx < RW * M; idx += NT) {  // the v windows of the workgroup's rows after the last token
+    const int c = 2 * D + idx / M, t = idx - (idx / M) * M;
+    int grp, i;
+    chan(c, grp, i);
+    a.conv[(((long)hv * 3 + grp) * D + i) * M + t] = ext[c * EXT + B + t];
   }
   __syncthreads();
 
-  // ---- delta rule (deltaRuleHead, src/compute/ref-deltanet.js:86-96): lane (j, p) holds S[j][p*PER .. p*PER+PER)
-  const int j = tid >> 2, p = tid & 3;
-  float S[PER];
-  float *srow = a.ssm + ((long)hv * D + j) * D + p * PER;
-  #pragma unroll
-  for (int c = 0; c < PER; c += 4) {
-    const float4 v4 = *(const float4 *)(srow + c);
-    S[c] = v4.x; S[c + 1] = v4.y; S[c + 2] = v4.z; S[c + 3] = v4.w;
+  // ---- L2 norms (l2normHeads, src/compute/ref-deltanet.js:61-69): one wave per (token, q or k) row
+  // (two rows per wave at a time, rr and rr + NW, as independent chains)
+  for (int rr = wave; rr < 2 * B; rr += 2 * NW) {
+    const int r1 = rr + NW < 2 * B ? rr + NW : rr;
+    float *row0 = ((rr & 1) ? ck : cq) + (rr >> 1) * ROW, *row1 = ((r1 & 1) ? ck : cq) + (r1 >> 1) * ROW;
+    double s0 = 0.0, s1 = 0.0;
+    for (int i = lane; i < D; i += 64) {
+      const double x0 = (double)row0[pidx(i)], x1 = (double)row1[pidx(i)];
+      s0 += x0 * x0;
+      s1 += x1 * x1;
+    }
+    s0 = wave_sum_xor(s0, 64);
+    s1 = wave_sum_xor(s1, 64);
+    const double f0 = ((rr & 1) ? 1.0 : 1.0 / sqrt((double)D)) / sqrt(s0 + a.eps);
+    const double f1 = ((r1 & 1) ? 1.0 : 1.0 / sqrt((double)D)) / sqrt(s1 + a.eps);
+    for (int i = lane; i < D; i += 64) {
+      const float y0 = (float)((double)row0[pidx(i)] * f0), y1 = (float)((double)row1[pidx(i)] * f1);
+      row0[pidx(i)] = y0;
+      if (r1 != rr) row1[pidx(i)] = y1;
+    }
   }
+  __syncthreads();
+
+  // ---- delta rule (deltaRuleHead, src/compute/ref-deltanet.js:86-96) on the lane's part of row jg
   for (int b = 0; b < B; b++) {
     const double g = gexp[b], be = bet[b];
     const float *kp = ck + b * ROW + p * (PER + 4), *qp = cq + b * ROW + p * (PER + 4);
     double sk = 0.0;
     #pragma unroll
     for (int c = 0; c < PER; c++) { const double s = (double)S[c] * g; S[c] = (float)s; sk += s * (double)kp[c]; }
-    sk += __shfl_xor(sk, 1);  // (p0 + p1) + (p2 + p3) on all four lanes of the row
+    sk += __shfl_xor(sk, 1);  // ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)) on all eight lanes of the row
     sk += __shfl_xor(sk, 2);
-    const double d = ((double)cv[b * D + j] - sk) * be;
+    sk += __shfl_xor(sk, 4);
+    const double d = ((double)cv[b * RW + j] - sk) * be;
     double o = 0.0;
     #pragma unroll
     for (int c = 0; c < PER; c++) { const double s = (double)S[c] + (double)kp[c] * d; S[c] = (float)s; o += s * (double)qp[c]; }
     o += __shfl_xor(o, 1);
     o += __shfl_xor(o, 2);
-    if (p == 0) core[b * D + j] = (float)o;
+    o += __shfl_xor(o, 4);
+    if (p == 0) {
+      core[b * D + jg] = (float)o;
+      if (R > 1) __hip_atomic_store(a.xcore + ((long)hv * DELTA_MAX_B + b) * D + jg, (float)o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     if (a.capSsm) {  // the state after token b
-      float *cs = a.capSsm + (long)b * a.capStride + ((long)hv * D + j) * D + p * PER;
+      float *cs = a.capSsm + (long)b * a.capStride + ((long)hv * D + jg) * D + p * PER;
       #pragma unroll
       for (int c = 0; c < PER; c += 4) *(float4 *)(cs + c) = make_float4(S[c], S[c + 1], S[c + 2], S[c + 3]);
     }
   }
   #pragma unroll
   for (int c = 0; c < PER; c += 4) *(float4 *)(srow + c) = make_float4(S[c], S[c + 1], S[c + 2], S[c + 3]);
+
+  // ---- the head's last workgroup to arrive continues with the whole head
+  if constexpr (R > 1) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores are complete
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (tid == 0) last = __hip_atomic_fetch_add(a.xcnt + hv, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(R - 1);
+    __syncthreads();
+    if (!last) return;
+    if (tid == 0) __hip_atomic_store(a.xcnt + hv, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    constexpr int XJ = (DELTA_MAX_B * D + NT - 1) / NT;
+    float xv[XJ];
+    #pragma unroll
+    for (int k = 0; k < XJ; k++) {  // every load issued before the first store
+      const int idx = tid + k * NT, b = idx / D, jj = idx - b * D;
+      xv[k] = idx < B * D && jj / RW != r ? __hip_atomic_load(a.xcore + ((long)hv * DELTA_MAX_B + b) * D + jj, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+    }
+    #pragma unroll
+    for (int k = 0; k < XJ; k++) {
+      const int idx = tid + k * NT, b = idx / D, jj = idx - b * D;
+      if (idx < B * D && jj / RW != r) core[b * D + jj] = xv[k];
+    }
+  }
+  for (int idx = tid; idx < 2 * D * M; idx += NT) {  // the head's q and k windows after the last token
+    const int c = idx / M, t = idx - c * M, grp = c < D ? 0 : 1, i = c - grp * D;
+    a.conv[(((long)hv * 3 + grp) * D + i) * M + t] = ext[c * EXT + B + t];
+  }
   __syncthreads();
 
   // ---- gated RMSNorm (gatedRmsNormHead, src/compute/ref-deltanet.js:102-106) + quantisation, one wave per token
-  for (int b = wave; b < B; b += NW) {
-    const float *o = core + b * D;
-    double ss = 0.0;
-    for (int i = lane; i < D; i += 64) { const double x = (double)o[i]; ss += x * x; }
-    ss = wave_sum_xor(ss, 64);
-    const double s = 1.0 / sqrt(ss / (double)D + a.eps);
-    for (int i0 = 0; i0 < D; i0 += 64) {
-      const int i = i0 + lane;
-      if (i < D) {  // D = 32: lanes 32-63 idle, a whole 32-lane block group
-        const double zz = (double)a.z[(long)b * a.ldz + hv * D + i];
-        const float v = (float)((double)o[i] * s * (double)a.normW[i] * (zz / (1.0 + exp(-zz))));
-        const int col = hv * D + i;
-        if (a.out) a.out[(long)b * a.ldo + col] = v;
-        quant_block32(v, col, a.act, b);
+  // (the wave's tokens in pairs k, k + 1, their scales as independent chains)
+  #pragma unroll
+  for (int k = 0; k < ZB; k += 2) {
+    const int b0 = wave + NW * k;
+    if (b0 >= B) break;
+    const int b1 = b0 + NW < B ? b0 + NW : b0;
+    const float *o0 = core + b0 * D, *o1 = core + b1 * D;
+    double s0 = 0.0, s1 = 0.0;
+    for (int i = lane; i < D; i += 64) {
+      const double x0 = (double)o0[i], x1 = (double)o1[i];
+      s0 += x0 * x0;
+      s1 += x1 * x1;
+    }
+    s0 = wave_sum_xor(s0, 64);
+    s1 = wave_sum_xor(s1, 64);
+    const double f[2] = {1.0 / sqrt(s0 / (double)D + a.eps), 1.0 / sqrt(s1 / (double)D + a.eps)};
+    #pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int b = h ? b1 : b0;
+      if (h && b1 == b0) break;
+      #pragma unroll
+      for (int q = 0; q < ZI; q++) {
+        const int i = 64 * q + lane;
+        if (i < D) {  // D = 32: lanes 32-63 idle, a whole 32-lane block group
+          const double zz = (double)zr[k + h][q];
+          const float v = (float)((double)core[b * D + i] * f[h] * (double)nwr[q] * (zz / (1.0 + exp(-zz))));
+          const int col = hv * D + i;
+          if (a.out) a.out[(long)b * a.ldo + col] = v;
+          quant_block32(v, col, a.act, b);
+        }
       }
     }
   }
@@ -136,6 +263,7 @@ void launch_deltanet(const DeltaArgs &a0, int D, hipStream_t st) {
   ZL_REQUIRE(a0.nK >= 1 && a0.nV >= 1 && a0.nV % a0.nK == 0, ZL_ERR_ARG, "Gated DeltaNet: value heads must be a multiple of key heads");
   ZL_REQUIRE(a0.act.ld >= a0.nV * D && a0.act.ld % 64 == 0, ZL_ERR_ARG, "Gated DeltaNet: activation rows too short");
   ZL_REQUIRE(!a0.capConv || a0.B <= DELTA_MAX_B, ZL_ERR_ARG, "Gated DeltaNet: capture holds one launch of tokens");
+  ZL_REQUIRE(D <= DELTA_ROWS || (a0.xcore && a0.xcnt), ZL_ERR_ARG, "Gated DeltaNet: exchange buffer missing");
   for (int t0 = 0; t0 < a0.B; t0 += DELTA_MAX_B) {
     DeltaArgs a = a0;
     a.B = std::min(DELTA_MAX_B, a0.B - t0);
@@ -145,9 +273,10 @@ void launch_deltanet(const DeltaArgs &a0, int D, hipStream_t st) {
     a.beta += (long)t0 * a.ldab;
     a.act = act_rows(a0.act, t0);
     if (a.out) a.out += (long)t0 * a.ldo;
-    if (D == 128) hipLaunchKernelGGL((k_deltanet<128, 4>), dim3(a.nV), dim3(512), 0, st, a);
-    else if (D == 64) hipLaunchKernelGGL((k_deltanet<64, 4>), dim3(a.nV), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((k_deltanet<32, 4>), dim3(a.nV), dim3(128), 0, st, a);
+    const dim3 grid((unsigned)(a.nV * (D / DELTA_ROWS))), blk(DELTA_LPR * DELTA_ROWS);
+    if (D == 128) hipLaunchKernelGGL((k_deltanet<128, 4>), grid, blk, 0, st, a);
+    else if (D == 64) hipLaunchKernelGGL((k_deltanet<64, 4>), grid, blk, 0, st, a);
+    else hipLaunchKernelGGL((k_deltanet<32, 4>), grid, blk, 0, st, a);
     ZL_HIP(hipGetLastError());
   }
 }
