@@ -125,7 +125,11 @@ def test_device_sampler_matches_oracle(gpu, tiny_files):
     toks = prompt(6, seed=8)
     for cfg in [dict(temperature=0.7, top_k=40, top_p=0.9), dict(temperature=1.0, top_k=5, top_p=1.0, min_p=0.05),
                 dict(temperature=0.8, top_k=40, top_p=0.95, repeat_penalty=1.3, presence_penalty=0.2, frequency_penalty=0.1),
-                dict(temperature=0)]:
+                dict(temperature=0),
+                # full candidate lists (topK 0: every id sorted, src/sampling/sampler.js:115-118) and topK above 256
+                dict(temperature=0.7, top_k=0, top_p=0.9), dict(temperature=1.5, top_k=0, top_p=1.0),
+                dict(temperature=1.0, top_k=0, top_p=0.95, min_p=0.001, repeat_penalty=1.3, presence_penalty=0.2),
+                dict(temperature=1.0, top_k=1000, top_p=1.0)]:
         ds = HipSampler(seed=77, **cfg)
         hs = O.Sampler(seed=77, **cfg)
         for t in toks:
@@ -137,6 +141,44 @@ def test_device_sampler_matches_oracle(gpu, tiny_files):
             assert np.allclose(dd.probs, hd.probs, rtol=1e-14, atol=0)
             assert dd.greedy == hd.greedy
             assert ds.sample(m, 0, hist) == hs.sample(logits, hist)
+        m.reset()
+    m.close()
+
+
+def test_device_sampler_ties_match_oracle(gpu, tiny_files, tmp_path):
+    """Logit ties at the k-th value: which tied ids stay is decided by the reference's heap history (topKSelect,
+    src/sampling/sampler.js:21-43), and a full list keeps equal logits in id order (src/sampling/sampler.js:115-118).
+    An output head whose rows come in equal pairs makes every logit appear twice, so an odd top-k always cuts a pair:
+    the fixed lists' heap fallback (top_k 41), the full lists' heap replay (top_k 301) and the sort's tie order
+    (top_k 0) all run."""
+    import shutil
+    from zerollm_amd import gguf as G
+    path = str(tmp_path / "paired_head.gguf")
+    shutil.copy(tiny_files[0], path)
+    t = G.read_gguf(path).require_tensor("output.weight")
+    rb, rows = G.row_size(t.type, t.dims[0]), t.dims[1]
+    with open(path, "r+b") as f:
+        f.seek(t.abs_offset)
+        raw = bytearray(f.read(rb * rows))
+        for r in range(1, rows, 2):
+            raw[r * rb:(r + 1) * rb] = raw[(r - 1) * rb:r * rb]
+        f.seek(t.abs_offset)
+        f.write(raw)
+    m = Mdl.HipModel.load(path, ctx=64)
+    toks = prompt(4, seed=9)
+    for cfg in [dict(temperature=0.8, top_k=41, top_p=1.0), dict(temperature=0.8, top_k=301, top_p=1.0),
+                dict(temperature=0.9, top_k=0, top_p=0.9)]:
+        ds = HipSampler(seed=5, **cfg)
+        hs = O.Sampler(seed=5, **cfg)
+        for tk in toks:
+            logits = m.forward(tk).copy()
+            assert np.array_equal(logits[0::2], logits[1::2])
+            dd = ds.distribution(m, 0, [])
+            hd = hs.distribution(logits, [])
+            assert list(dd.ids) == list(hd.ids)
+            assert np.allclose(dd.probs, hd.probs, rtol=1e-14, atol=0)
+            assert ds.sample(m, 0, []) == hs.sample(logits, [])
+        ds.close()
         m.reset()
     m.close()
 

@@ -21,6 +21,10 @@ CONFIGS = {
     "T1-top10-penalties": dict(temperature=1.0, top_k=10, top_p=0.95, repeat_penalty=1.3, repeat_last_n=16,
                                 presence_penalty=-0.5, frequency_penalty=0.1),
     "T0.8-top40-minp": dict(temperature=0.8, top_k=40, top_p=1.0, min_p=0.05),
+    # full candidate lists (src/sampling/sampler.js:115-118) and a top-k above the fixed lists' 256
+    "T0.9-all-p0.95": dict(temperature=0.9, top_k=0, top_p=0.95),
+    "T1-all-penalties-minp": dict(temperature=1.0, top_k=0, top_p=1.0, min_p=0.002, repeat_penalty=1.2, repeat_last_n=16),
+    "T1.2-top300-p0.98": dict(temperature=1.2, top_k=300, top_p=0.98),
 }
 
 
@@ -70,7 +74,8 @@ def test_sampled_cycles_match_oracle(gpu, close_files, k, seed):
     print(f"k={k} seed={seed}: {len(log)} cycles, accept {st['speculative']['acceptRate']:.3f}", flush=True)
 
 
-@pytest.mark.parametrize("name", ["T1-top10-penalties", "T0.8-top40-minp"])
+@pytest.mark.parametrize("name", ["T1-top10-penalties", "T0.8-top40-minp", "T0.9-all-p0.95", "T1-all-penalties-minp",
+                                  "T1.2-top300-p0.98"])
 def test_sampled_cycles_match_oracle_other_samplers(gpu, close_files, name):
     """Repetition / presence / frequency penalties (the tentative tokens of a block enter the history of the later
     rows) and min-p, with the stop-token and max-token bookkeeping of the host loop."""

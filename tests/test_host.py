@@ -40,13 +40,11 @@ def test_errors_without_gpu_are_reported_not_crashing():
 
 
 @pytest.mark.parametrize("opts,msg", [
-    (dict(top_k=0), "top_k must be 1..256 on the GPU sampler"),
-    (dict(top_k=257), "top_k must be 1..256 on the GPU sampler"),
     (dict(top_k=40, repeat_last_n=65), "repeat_last_n must be 0..64 on the GPU sampler"),
 ])
 def test_sampler_options_the_device_does_not_take_are_refused(opts, msg):
-    """createSampler's topK 0 (no top-k cut, src/sampling/sampler.js:111-118) and topK above the device candidate list
-    are refused with a message before any device call; at temperature <= 0 (greedy) top_k is not used."""
+    """A repetition window above the device history's 64 ids is refused with a message before any device call
+    (every topK is taken: 0 and values above 256 keep full candidate lists)."""
     o = _lib.zl_sampler_opts(temperature=0.8, top_p=0.95, min_p=0.0, repeat_penalty=1.0, presence_penalty=0.0,
                              frequency_penalty=0.0, top_k=opts["top_k"], repeat_last_n=opts.get("repeat_last_n", 64),
                              seed=1, greedy_argmax=0)

@@ -283,12 +283,29 @@ void launch_fill(float *p, long n, float v, hipStream_t st);
 constexpr int KCAP = 256;  // largest top-k (candidate list) the device sampler supports
 
 // Sparse distribution (zerollm's TokenDist, src/sampling/sampler.js:52-62): ids[i] has probability probs[i] / total.
+// A sampler with top_k 0 or above KCAP (the reference's full candidate list) keeps up to a vocabulary of entries in
+// storage of its own: wids / wprobs in rank order, wpos[id] = rank + 1 of a kept id (0 otherwise), and wres for the
+// residual draw; these pointers are null for the fixed lists.
 struct DevDist {
   int n;
   int greedy;
   double total;
   int ids[KCAP];
   double probs[KCAP];
+  int *wids;
+  double *wprobs;
+  int *wpos;
+  double *wres;
+};
+
+// Work space of full-list distributions: the rows' sort keys and ids (two buffers each, [rows][vocab]) and per-chunk
+// digit counts ([rows][256][chunks]).
+constexpr int WIDE_CHUNK = 4096;  // keys per sort workgroup
+struct WideWork {
+  uint32_t *keyA, *keyB;
+  int *idA, *idB;
+  uint32_t *hist;
+  int vocab, rows;
 };
 
 struct SamplerParams {
@@ -315,8 +332,12 @@ struct ArgmaxWork {
 };
 
 // Row r uses history hist[0 .. histLen0 + r * histInc).
+// ww: the full-list work space when the sampler keeps full lists (top_k 0 or above KCAP), else null.
 void launch_dist_rows(const float *logits, int ldl, int nrows, int vocab, const SamplerParams &sp, const int *hist,
-                      int histLen0, int histInc, float *scratch, const ArgmaxWork &aw, DevDist *out, hipStream_t st);
+                      int histLen0, int histInc, float *scratch, const ArgmaxWork &aw, const WideWork *ww, DevDist *out,
+                      hipStream_t st);
+// Point rows [0, n) of d at full-list storage of `vocab` entries per row (ids, probs, pos, res), or at null.
+void launch_set_wide(DevDist *d, int n, int vocab, int *ids, double *probs, int *pos, double *res, hipStream_t st);
 void launch_draft_draw(const DevDist *dist, SpecState *ss, int j, const int *stopIds, int nStop, Step *draftStep,
                        int advance, Step *targetStep, int *hist, int histLen0, hipStream_t st);
 void launch_accept(const DevDist *pdist, const DevDist *qdist, SpecState *ss, int greedy, hipStream_t st);

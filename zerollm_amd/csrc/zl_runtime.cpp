@@ -270,6 +270,8 @@ struct zl_sampler {
   float *scratch = nullptr;
   int scratchVocab = 0;
   zl::ArgmaxWork am{};
+  bool wide = false;      // full candidate lists (top_k 0 or above KCAP)
+  zl::WideWork ww{};      // their sort work space ([65 rows][vocab])
   hipStream_t st = nullptr;
   // whole speculative cycles captured as two graphs (draft phase, verify phase) per (target uid, draft uid, fed
   // tokens, drafts, stop ids, phase); they capture this sampler's buffers, so they live and die with it
@@ -1300,6 +1302,7 @@ static zl_sampler *new_sampler(const zl_sampler_opts *o) {
   p.presence = o->presence_penalty; p.frequency = o->frequency_penalty; p.topK = o->top_k; p.repeatLastN = o->repeat_last_n;
   p.penalized = (p.repeatPenalty != 1.0 || p.presence != 0.0 || p.frequency != 0.0) ? 1 : 0;
   p.greedyArgmax = o->greedy_argmax ? 1 : 0;
+  s->wide = !(p.temperature <= 0.0 || p.greedyArgmax) && (p.topK <= 0 || p.topK > KCAP);
   ZL_HIP(hipStreamCreateWithFlags(&s->st, hipStreamNonBlocking));
   s->ss = (SpecState *)s->ar.alloc(sizeof(SpecState));
   zero_now(s->ss, sizeof(SpecState));
@@ -1307,6 +1310,9 @@ static zl_sampler *new_sampler(const zl_sampler_opts *o) {
   s->pdist = (DevDist *)s->ar.alloc(sizeof(DevDist) * 65);
   s->qdist = (DevDist *)s->ar.alloc(sizeof(DevDist) * 64);
   s->tmpdist = (DevDist *)s->ar.alloc(sizeof(DevDist));
+  zero_now(s->pdist, sizeof(DevDist) * 65);  // fixed lists: null full-list pointers
+  zero_now(s->qdist, sizeof(DevDist) * 64);
+  zero_now(s->tmpdist, sizeof(DevDist));
   ZL_HIP(hipHostMalloc((void **)&s->hdist, sizeof(DevDist)));
   s->dhist = (int *)s->ar.alloc(sizeof(int) * 256);
   s->dstop = (int *)s->ar.alloc(sizeof(int) * 64);
@@ -1321,10 +1327,33 @@ static zl_sampler *new_sampler(const zl_sampler_opts *o) {
   return s.release();
 }
 
+// The sampler's work space for rows of `vocab` logits: the penalised copies of up to 65 rows, and for full candidate
+// lists their sort buffers and each distribution's storage (65 target rows, 64 draft rows, one for single draws).
+// Allocated before any graph capture that uses them; storage for a smaller vocabulary stays allocated (graphs
+// captured with it keep their pointers).
 static void ensure_scratch(zl_sampler *s, int vocab) {
-  if (!s->sp.penalized || s->scratchVocab >= vocab) return;
-  s->scratch = (float *)s->ar.alloc((size_t)65 * vocab * 4);
-  s->scratchVocab = vocab;
+  if ((s->sp.penalized || s->wide) && s->scratchVocab < vocab) {
+    s->scratch = (float *)s->ar.alloc((size_t)65 * vocab * 4);
+    s->scratchVocab = vocab;
+  }
+  if (!s->wide || s->ww.vocab >= vocab) return;
+  const size_t n = (size_t)65 * vocab, nch = (vocab + WIDE_CHUNK - 1) / WIDE_CHUNK;
+  s->ww.keyA = (uint32_t *)s->ar.alloc(n * 4);
+  s->ww.keyB = (uint32_t *)s->ar.alloc(n * 4);
+  s->ww.idA = (int *)s->ar.alloc(n * 4);
+  s->ww.idB = (int *)s->ar.alloc(n * 4);
+  s->ww.hist = (uint32_t *)s->ar.alloc((size_t)65 * 256 * nch * 4);
+  s->ww.vocab = vocab;
+  s->ww.rows = 65;
+  auto give = [&](DevDist *d, int cnt) {
+    const size_t m = (size_t)cnt * vocab;
+    launch_set_wide(d, cnt, vocab, (int *)s->ar.alloc(m * 4), (double *)s->ar.alloc(m * 8), (int *)s->ar.alloc(m * 4),
+                    (double *)s->ar.alloc(m * 8), s->st);
+  };
+  give(s->pdist, 65);
+  give(s->qdist, 64);
+  give(s->tmpdist, 1);
+  ZL_HIP(hipStreamSynchronize(s->st));
 }
 
 // Upload the last repeatLastN ids of a history (only those can matter) and return how many were kept.
@@ -1355,7 +1384,7 @@ static void dist_of_row(zl_sampler *s, zl_model *m, int row, const int32_t *hist
   ensure_scratch(s, m->cfg.vocab);
   const int keep = upload_hist(s, m->st, hist, nh);
   launch_dist_rows(m->logits + (size_t)row * m->cfg.vocab, m->cfg.vocab, 1, m->cfg.vocab, s->sp, keep ? s->dhist : nullptr, keep, 0,
-                   s->scratch, s->am, out, m->st);
+                   s->scratch, s->am, s->wide ? &s->ww : nullptr, out, m->st);
 }
 
 // ---------------------------------------------------------------------------------------------- speculative cycle
@@ -1403,13 +1432,13 @@ static hipGraphExec_t cycle_graph(zl_model *T, zl_model *D, zl_sampler *s, int n
       hipLaunchKernelGGL(k_spec_reset, dim3(1), dim3(64), 0, cs, s->ss);
       enqueue_forward(D, nFeed, 1);
       for (int j = 0; j < kk; j++) {
-        launch_dist_rows(D->logits, D->cfg.vocab, 1, D->cfg.vocab, s->sp, nullptr, j, 0, s->scratch, s->am, s->qdist + j, cs);
+        launch_dist_rows(D->logits, D->cfg.vocab, 1, D->cfg.vocab, s->sp, nullptr, j, 0, s->scratch, s->am, s->wide ? &s->ww : nullptr, s->qdist + j, cs);
         launch_draft_draw(s->qdist + j, s->ss, j, s->dstop, nStop, D->dstep, j == 0 ? nFeed : 1, T->dstep, s->dhist, 0, cs);
         if (j < kk - 1) enqueue_forward(D, 1, 1);
       }
     } else {
       enqueue_forward(T, kk + 1, 2);
-      launch_dist_rows(T->logits, T->cfg.vocab, kk + 1, T->cfg.vocab, s->sp, nullptr, 0, 1, s->scratch, s->am, s->pdist, cs);
+      launch_dist_rows(T->logits, T->cfg.vocab, kk + 1, T->cfg.vocab, s->sp, nullptr, 0, 1, s->scratch, s->am, s->wide ? &s->ww : nullptr, s->pdist, cs);
       launch_accept(s->pdist, s->qdist, s->ss, greedy ? 1 : 0, cs);
     }
     ZL_HIP(hipGetLastError());
@@ -1499,7 +1528,7 @@ static void spec_cycle(zl_model *T, zl_model *D, zl_sampler *s, const int32_t *f
     posF = (int)D->tokens.size();
     if (D->hybrid) mark_rollback(D);  // draft.markRollback after feedLogits (src/model/speculative.js:168)
     for (int j = 0; j < kk; j++) {
-      launch_dist_rows(D->logits, D->cfg.vocab, 1, D->cfg.vocab, s->sp, dh, keep + j, 0, s->scratch, s->am, s->qdist + j, st);
+      launch_dist_rows(D->logits, D->cfg.vocab, 1, D->cfg.vocab, s->sp, dh, keep + j, 0, s->scratch, s->am, s->wide ? &s->ww : nullptr, s->qdist + j, st);
       launch_draft_draw(s->qdist + j, s->ss, j, s->dstop, nStop, D->dstep, j == 0 ? lastChunk : 1, T->dstep, s->dhist, keep, st);
       if (j < kk - 1) launch_pass(D, 1, 1);
     }
@@ -1511,7 +1540,7 @@ static void spec_cycle(zl_model *T, zl_model *D, zl_sampler *s, const int32_t *f
       T->prevNoLogits = false;
     }
     launch_pass(T, kk + 1, 2);
-    launch_dist_rows(T->logits, T->cfg.vocab, kk + 1, T->cfg.vocab, s->sp, dh, keep, 1, s->scratch, s->am, s->pdist, st);
+    launch_dist_rows(T->logits, T->cfg.vocab, kk + 1, T->cfg.vocab, s->sp, dh, keep, 1, s->scratch, s->am, s->wide ? &s->ww : nullptr, s->pdist, st);
     launch_accept(s->pdist, s->qdist, s->ss, (s->sp.temperature <= 0.0 || s->sp.greedyArgmax) ? 1 : 0, st);
   }
   ZL_HIP(hipEventRecord(e1, st));
@@ -1856,11 +1885,7 @@ int zl_synth_tensor_bytes(const zl_synth_tensor *t, int use_device, void *host_o
 int zl_sampler_create(const zl_sampler_opts *opts, zl_sampler **out) {
   ZL_API_BEGIN
   ZL_REQUIRE(opts && out, ZL_ERR_ARG, "null argument");
-  /* options the device sampler does not take are refused before any device call: a candidate list of KCAP entries,
-   * a history window of 64 ids */
-  if (!(opts->temperature <= 0.0) && !opts->greedy_argmax)
-    ZL_REQUIRE(opts->top_k >= 1 && opts->top_k <= KCAP, ZL_ERR_UNSUPPORTED,
-               "top_k must be 1.." + std::to_string(KCAP) + " on the GPU sampler");
+  /* options the device sampler does not take are refused before any device call: a history window above 64 ids */
   ZL_REQUIRE(opts->repeat_last_n >= 0 && opts->repeat_last_n <= 64, ZL_ERR_UNSUPPORTED,
              "repeat_last_n must be 0..64 on the GPU sampler");
   ensure_init();
@@ -1913,7 +1938,12 @@ int zl_distribution(zl_sampler *s, zl_model *m, int row, const int32_t *hist, in
   ZL_HIP(hipStreamSynchronize(m->st));
   const DevDist &d = *s->hdist;
   ZL_REQUIRE(d.n <= cap, ZL_ERR_ARG, "distribution capacity too small");
-  for (int i = 0; i < d.n; i++) { ids[i] = d.ids[i]; probs[i] = d.probs[i]; }
+  if (d.wids) {  // a full list: its kept entries from the list's own storage
+    ZL_HIP(hipMemcpy(ids, d.wids, sizeof(int32_t) * d.n, hipMemcpyDeviceToHost));
+    ZL_HIP(hipMemcpy(probs, d.wprobs, sizeof(double) * d.n, hipMemcpyDeviceToHost));
+  } else {
+    for (int i = 0; i < d.n; i++) { ids[i] = d.ids[i]; probs[i] = d.probs[i]; }
+  }
   *n = d.n; *total = d.total; *greedy = d.greedy;
   ZL_API_END
 }

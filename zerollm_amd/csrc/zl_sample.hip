@@ -51,6 +51,34 @@ __device__ int heap_topk(const float *l, int n, int k, int *ids, double *vals) {
 
 constexpr int DT = 1024;  // threads of the distribution kernel
 
+// The row's logits copied to cp with the repetition / presence / frequency penalties of the last repeatLastN history ids
+// applied (src/sampling/sampler.js:96-110), in the reference's order (distinct ids in first-occurrence order). Every
+// thread of the block calls it.
+__device__ void penalized_copy(const float *l, float *cp, int vocab, const SamplerParams &sp, const int *hist, int hl,
+                               bool penalize) {
+  const int tid = threadIdx.x;
+  for (int i = tid; i < vocab; i += blockDim.x) cp[i] = l[i];
+  __syncthreads();
+  if (penalize && tid == 0) {
+    int start = hl - sp.repeatLastN;
+    if (start < 0) start = 0;
+    for (int i = start; i < hl; i++) {
+      int t = hist[i];
+      bool seen = false;
+      for (int j = start; j < i; j++) if (hist[j] == t) { seen = true; break; }
+      if (seen) continue;
+      int c = 0;
+      for (int j = i; j < hl; j++) c += hist[j] == t;
+      double lv = (double)cp[t];
+      double v = sp.repeatPenalty != 1.0 ? (lv > 0 ? lv / sp.repeatPenalty : lv * sp.repeatPenalty) : lv;
+      v -= (double)c * sp.frequency + sp.presence;
+      cp[t] = (float)v;
+    }
+  }
+  __syncthreads();
+  __threadfence_block();
+}
+
 // distribution(logits row, history) for nrows rows (src/sampling/sampler.js:94-142).
 __global__ __launch_bounds__(DT) void k_dist_rows(const float *__restrict__ logits, int ldl, int vocab, SamplerParams sp,
                                                  const int *hist, int histLen0, int histInc, float *scratch, DevDist *out) {
@@ -70,26 +98,7 @@ __global__ __launch_bounds__(DT) void k_dist_rows(const float *__restrict__ logi
   const int hl = hist ? histLen0 + r * histInc : 0;
   if (sp.penalized && hl > 0) {
     float *cp = scratch + (long)r * vocab;
-    for (int i = tid; i < vocab; i += DT) cp[i] = l[i];
-    __syncthreads();
-    if (tid == 0) {
-      int start = hl - sp.repeatLastN;
-      if (start < 0) start = 0;
-      for (int i = start; i < hl; i++) {
-        int t = hist[i];
-        bool seen = false;
-        for (int j = start; j < i; j++) if (hist[j] == t) { seen = true; break; }
-        if (seen) continue;
-        int c = 0;
-        for (int j = i; j < hl; j++) c += hist[j] == t;
-        double lv = (double)cp[t];
-        double v = sp.repeatPenalty != 1.0 ? (lv > 0 ? lv / sp.repeatPenalty : lv * sp.repeatPenalty) : lv;
-        v -= (double)c * sp.frequency + sp.presence;
-        cp[t] = (float)v;
-      }
-    }
-    __syncthreads();
-    __threadfence_block();
+    penalized_copy(l, cp, vocab, sp, hist, hl, true);
     l = cp;
   }
   // ---- greedy: first maximum (src/sampling/sampler.js:46-50)
@@ -195,31 +204,38 @@ __global__ __launch_bounds__(DT) void k_dist_rows(const float *__restrict__ logi
   }
 }
 
+// Entry i of a distribution, from its fixed list or its full-list storage.
+__device__ inline int dist_id(const DevDist &d, int i) { return d.wids ? d.wids[i] : d.ids[i]; }
+__device__ inline double dist_p(const DevDist &d, int i) { return d.wprobs ? d.wprobs[i] : d.probs[i]; }
+
 // draw(dist) (src/sampling/sampler.js:145-151)
 __device__ inline int draw_dist(const DevDist &d, uint32_t &rng) {
-  if (d.greedy) return d.ids[0];
+  if (d.greedy) return dist_id(d, 0);
   double r = rng_next(rng) * d.total;
   for (int i = 0; i < d.n; i++) {
-    r -= d.probs[i];
-    if (r <= 0) return d.ids[i];
+    r -= dist_p(d, i);
+    if (r <= 0) return dist_id(d, i);
   }
-  return d.ids[d.n - 1];
+  return dist_id(d, d.n - 1);
 }
 
-// probOf (src/model/speculative.js:64-67)
+// probOf (src/model/speculative.js:64-67); a full list finds the id's rank in wpos
 __device__ inline double prob_of(const DevDist &d, int id) {
+  if (d.wpos) {
+    const int k = d.wpos[id];
+    return k ? d.wprobs[k - 1] / d.total : 0.0;
+  }
   for (int i = 0; i < d.n; i++) if (d.ids[i] == id) return d.probs[i] / d.total;
   return 0.0;
 }
 
 // drawResidual (src/model/speculative.js:75-87); the dense scratch of the reference is a lookup into q's support
 __device__ int draw_residual(const DevDist &p, const DevDist &q, uint32_t &rng) {
-  double res[KCAP];
+  double resl[KCAP];
+  double *res = p.wres ? p.wres : resl;
   double sum = 0;
   for (int i = 0; i < p.n; i++) {
-    double qv = 0.0;
-    for (int j = 0; j < q.n; j++) if (q.ids[j] == p.ids[i]) { qv = q.probs[j] / q.total; break; }
-    double v = p.probs[i] / p.total - qv;
+    const double v = dist_p(p, i) / p.total - prob_of(q, dist_id(p, i));
     res[i] = 0.0;
     if (v > 0) { res[i] = v; sum += v; }
   }
@@ -230,10 +246,10 @@ __device__ int draw_residual(const DevDist &p, const DevDist &q, uint32_t &rng) 
     if (res[i] > 0) {
       last = i;
       r -= res[i];
-      if (r <= 0) return p.ids[i];
+      if (r <= 0) return dist_id(p, i);
     }
   }
-  return p.ids[last];
+  return dist_id(p, last);
 }
 
 // Draft proposal j (src/model/speculative.js:169-177): draw x_j from the draft's distribution, record it, stop after a
@@ -267,7 +283,7 @@ __global__ void k_accept(const DevDist *pdist, const DevDist *qdist, SpecState *
     const DevDist &P = pdist[j];
     const int x = ss->drafted[j];
     if (greedy) {
-      int t = P.ids[0];
+      int t = dist_id(P, 0);
       if (t == x) { a++; continue; }
       tok = t;
       break;
@@ -350,13 +366,219 @@ __global__ __launch_bounds__(AM_THREADS) void k_argmax_rows(const float *__restr
   }
 }
 
+// ---- full candidate lists (topK 0 or at least the vocabulary: every id, sorted by logit descending, then id ascending,
+// src/sampling/sampler.js:115-118; topK above KCAP: the K best, src/sampling/sampler.js:21-43). The order is an LSD radix
+// sort of (~key of the penalised logit) with the ids as payload, four 8-bit passes, each stable, over ids taken in
+// ascending order, so equal logits stay in id order. The softmax, min-p, top-p and total then follow the reference's
+// order in one lane, as the fixed lists do.
+constexpr int WT = 256;                          // threads of the sort kernels
+constexpr int WPT = WIDE_CHUNK / WT;             // keys per thread and chunk
+
+// the penalised logits of each row (scratch) and the first sort buffers: key ~fkey(logit), payload the id
+__global__ __launch_bounds__(DT) void k_wide_prep(const float *__restrict__ logits, int ldl, int vocab, SamplerParams sp,
+                                                  const int *hist, int histLen0, int histInc, float *scratch, WideWork ww) {
+  const int r = blockIdx.x;
+  const int hl = hist ? histLen0 + r * histInc : 0;
+  float *cp = scratch + (long)r * vocab;
+  penalized_copy(logits + (long)r * ldl, cp, vocab, sp, hist, hl, sp.penalized && hl > 0);
+  for (int i = threadIdx.x; i < vocab; i += DT) {
+    ww.keyA[(long)r * vocab + i] = ~fkey(cp[i]);
+    ww.idA[(long)r * vocab + i] = i;
+  }
+}
+
+// digit counts of one chunk: hist[row][digit][chunk]
+__global__ __launch_bounds__(WT) void k_rs_hist(const uint32_t *__restrict__ keys, int vocab, int shift, uint32_t *hist) {
+  __shared__ uint32_t h[256];
+  const int ch = blockIdx.x, r = blockIdx.y, nch = gridDim.x, tid = threadIdx.x;
+  h[tid] = 0;
+  __syncthreads();
+  const uint32_t *k = keys + (long)r * vocab;
+  #pragma unroll
+  for (int j = 0; j < WPT; j++) {
+    const int i = ch * WIDE_CHUNK + j * WT + tid;
+    if (i < vocab) atomicAdd(&h[(k[i] >> shift) & 255u], 1u);
+  }
+  __syncthreads();
+  hist[((long)r * 256 + tid) * nch + ch] = h[tid];
+}
+
+// exclusive scan of a row's counts in (digit, chunk) order: the first output position of each (digit, chunk)
+__global__ __launch_bounds__(DT) void k_rs_scan(uint32_t *hist, int nch) {
+  __shared__ uint32_t ws[DT / 64];
+  const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t *h = hist + (long)r * 256 * nch;
+  const int E = 256 * nch, per = (E + DT - 1) / DT, i0 = min(E, tid * per), i1 = min(E, i0 + per);
+  uint32_t sum = 0;
+  for (int i = i0; i < i1; i++) sum += h[i];
+  uint32_t inc = sum;  // inclusive scan over the wave
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t v = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += v;
+  }
+  if (lane == 63) ws[wave] = inc;
+  __syncthreads();
+  uint32_t before = inc - sum;
+  for (int w = 0; w < wave; w++) before += ws[w];
+  for (int i = i0; i < i1; i++) { const uint32_t c = h[i]; h[i] = before; before += c; }
+}
+
+// stable scatter of one chunk by the pass's digit: the chunk's keys in 256-key steps; within a step a key's place is
+// the digit's running position, plus the same-digit keys of lower waves, plus those of lower lanes of its own wave
+__global__ __launch_bounds__(WT) void k_rs_scatter(const uint32_t *__restrict__ kin, const int *__restrict__ iin,
+                                                   uint32_t *kout, int *iout, int vocab, int shift,
+                                                   const uint32_t *__restrict__ hist) {
+  __shared__ uint32_t base[256];
+  __shared__ uint32_t wcnt[WT / 64][256];
+  const int ch = blockIdx.x, r = blockIdx.y, nch = gridDim.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const long ro = (long)r * vocab;
+  base[tid] = hist[((long)r * 256 + tid) * nch + ch];
+  for (int j = 0; j < WPT; j++) {
+    const int i = ch * WIDE_CHUNK + j * WT + tid;
+    const bool valid = i < vocab;
+    const uint32_t key = valid ? kin[ro + i] : 0u;
+    const int id = valid ? iin[ro + i] : 0;
+    const uint32_t d = (key >> shift) & 255u;
+    #pragma unroll
+    for (int w = 0; w < WT / 64; w++) wcnt[w][tid] = 0;
+    __syncthreads();
+    unsigned long long m = __ballot(valid);
+    #pragma unroll
+    for (int b = 0; b < 8; b++) {
+      const unsigned long long bal = __ballot((d >> b) & 1u);
+      m &= ((d >> b) & 1u) ? bal : ~bal;
+    }
+    const int rank = __popcll(m & ((1ull << lane) - 1ull));
+    if (valid && rank == 0) wcnt[wave][d] = (uint32_t)__popcll(m);
+    __syncthreads();
+    if (valid) {
+      uint32_t pos = base[d] + (uint32_t)rank;
+      for (int w = 0; w < wave; w++) pos += wcnt[w][d];
+      kout[ro + pos] = key;
+      iout[ro + pos] = id;
+    }
+    __syncthreads();
+    uint32_t add = 0;
+    #pragma unroll
+    for (int w = 0; w < WT / 64; w++) add += wcnt[w][tid];
+    base[tid] += add;
+    __syncthreads();
+  }
+}
+
+// distribution of each row from its sorted ids (src/sampling/sampler.js:111-142)
+__global__ __launch_bounds__(DT) void k_wide_dist(int vocab, SamplerParams sp, const float *__restrict__ scratch,
+                                                  WideWork ww, DevDist *out) {
+  __shared__ double s_sum;
+  __shared__ int s_keep;
+  const int r = blockIdx.x, tid = threadIdx.x;
+  DevDist *D = out + r;
+  int *wids = D->wids, *wpos = D->wpos;
+  double *wprobs = D->wprobs;
+  const float *cp = scratch + (long)r * vocab;
+  const uint32_t *key = ww.keyA + (long)r * vocab;
+  const int *sid = ww.idA + (long)r * vocab;
+  const int K = sp.topK;
+  const bool full = K <= 0 || K >= vocab;
+  const int m = full ? vocab : K;
+  if (!full && key[K - 1] == key[K]) {
+    // a tie at the K-th value: which tied ids the reference's heap keeps depends on its history, so it is replayed
+    // (wpos / wres as its ids / values), then its ids are listed in the sorted order
+    if (tid == 0) heap_topk(cp, vocab, K, wpos, D->wres);
+    __syncthreads();
+    for (int i = tid; i < vocab; i += DT) wids[i] = 0;
+    __syncthreads();
+    for (int j = tid; j < K; j += DT) wids[wpos[j]] = 1;
+    __syncthreads();
+    if (tid == 0) {
+      int c = 0;
+      for (int i = 0; i < vocab && c < K; i++) if (wids[sid[i]]) wpos[c++] = sid[i];
+    }
+    __syncthreads();
+    for (int i = tid; i < K; i += DT) wids[i] = wpos[i];
+  } else {
+    for (int i = tid; i < m; i += DT) wids[i] = sid[i];
+  }
+  __syncthreads();
+  // softmax with temperature: exponentials in parallel, their sum in rank order
+  const double mx = (double)cp[wids[0]];
+  for (int i = tid; i < m; i += DT) wprobs[i] = exp(((double)cp[wids[i]] - mx) / sp.temperature);
+  __syncthreads();
+  if (tid == 0) {
+    double sum = 0;
+    for (int i = 0; i < m; i++) sum += wprobs[i];
+    s_sum = sum;
+    s_keep = m;
+  }
+  __syncthreads();
+  const double sum = s_sum;
+  for (int i = tid; i < m; i += DT) wprobs[i] = wprobs[i] / sum;
+  __syncthreads();
+  // min-p: the first rank from 1 on whose probability is below minP * probs[0]
+  if (sp.minP > 0) {
+    const double thr = sp.minP * wprobs[0];
+    for (int i = 1 + tid; i < m; i += DT)
+      if (wprobs[i] < thr) atomicMin(&s_keep, i);
+    __syncthreads();
+  }
+  if (tid == 0) {
+    int keep = s_keep;
+    double total = 0;
+    if (sp.topP < 1) {  // the running sum at the cut is the reference's total over the kept prefix
+      int i = 0;
+      while (i < keep) { total += wprobs[i]; i++; if (total >= sp.topP) break; }
+      keep = i > 1 ? i : 1;
+    } else {
+      for (int i = 0; i < keep; i++) total += wprobs[i];
+    }
+    D->n = keep; D->greedy = 0; D->total = total;
+    s_keep = keep;
+  }
+  for (int i = tid; i < vocab; i += DT) wpos[i] = 0;
+  __syncthreads();
+  const int keep = s_keep;
+  for (int i = tid; i < keep; i += DT) wpos[wids[i]] = i + 1;
+}
+
+__global__ void k_set_wide(DevDist *d, int n, int vocab, int *ids, double *probs, int *pos, double *res) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  d[i].wids = ids ? ids + (long)i * vocab : nullptr;
+  d[i].wprobs = probs ? probs + (long)i * vocab : nullptr;
+  d[i].wpos = pos ? pos + (long)i * vocab : nullptr;
+  d[i].wres = res ? res + (long)i * vocab : nullptr;
+}
+
+void launch_set_wide(DevDist *d, int n, int vocab, int *ids, double *probs, int *pos, double *res, hipStream_t st) {
+  hipLaunchKernelGGL(k_set_wide, dim3((n + 63) / 64), dim3(64), 0, st, d, n, vocab, ids, probs, pos, res);
+  ZL_HIP(hipGetLastError());
+}
+
 void launch_dist_rows(const float *logits, int ldl, int nrows, int vocab, const SamplerParams &sp, const int *hist,
-                      int histLen0, int histInc, float *scratch, const ArgmaxWork &aw, DevDist *out, hipStream_t st) {
+                      int histLen0, int histInc, float *scratch, const ArgmaxWork &aw, const WideWork *ww, DevDist *out,
+                      hipStream_t st) {
   const bool greedy = sp.temperature <= 0.0 || sp.greedyArgmax;
   const int nb = (vocab + AM_CHUNK - 1) / AM_CHUNK;
   if (greedy && !(sp.penalized && hist && histLen0 + (nrows - 1) * histInc > 0) && nb <= ARGMAX_MAX_BLOCKS &&
       nrows <= ARGMAX_MAX_ROWS) {
     hipLaunchKernelGGL(k_argmax_rows, dim3(nb, nrows), dim3(AM_THREADS), 0, st, logits, ldl, vocab, aw.keys, aw.count, out);
+    ZL_HIP(hipGetLastError());
+    return;
+  }
+  if (!greedy && ww) {
+    ZL_REQUIRE(scratch && ww->vocab >= vocab && ww->rows >= nrows, ZL_ERR_STATE, "sampler work space too small");
+    const int nch = (vocab + WIDE_CHUNK - 1) / WIDE_CHUNK;
+    hipLaunchKernelGGL(k_wide_prep, dim3(nrows), dim3(DT), 0, st, logits, ldl, vocab, sp, hist, histLen0, histInc, scratch, *ww);
+    for (int pass = 0; pass < 4; pass++) {
+      const uint32_t *kin = pass & 1 ? ww->keyB : ww->keyA;
+      const int *iin = pass & 1 ? ww->idB : ww->idA;
+      uint32_t *kout = pass & 1 ? ww->keyA : ww->keyB;
+      int *iout = pass & 1 ? ww->idA : ww->idB;
+      hipLaunchKernelGGL(k_rs_hist, dim3(nch, nrows), dim3(WT), 0, st, kin, vocab, 8 * pass, ww->hist);
+      hipLaunchKernelGGL(k_rs_scan, dim3(nrows), dim3(DT), 0, st, ww->hist, nch);
+      hipLaunchKernelGGL(k_rs_scatter, dim3(nch, nrows), dim3(WT), 0, st, kin, iin, kout, iout, vocab, 8 * pass, ww->hist);
+    }
+    hipLaunchKernelGGL(k_wide_dist, dim3(nrows), dim3(DT), 0, st, vocab, sp, scratch, *ww, out);
     ZL_HIP(hipGetLastError());
     return;
   }

@@ -51,7 +51,7 @@ class HipSampler:
 
     def distribution(self, model, row: int = 0, history=()) -> TokenDist:
         hp, nh, keep = self._hist(history)
-        cap = 256
+        cap = int(model._logits.shape[1])  # a full candidate list (top_k 0) keeps up to the vocabulary
         ids = np.zeros(cap, np.int32)
         probs = np.zeros(cap, np.float64)
         n = C.c_int()
