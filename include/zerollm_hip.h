@@ -143,8 +143,9 @@ int zl_model_synth(const zl_config *cfg, const zl_synth_tensor *tensors, int n, 
 /* ---------------------------------------------------------------------------------------------- sampler */
 typedef struct zl_sampler zl_sampler;
 
-/* createSampler options (src/sampling/sampler.js:4-15, 81-92). top_k must be 1..256 (device candidate list) unless
- * the temperature is <= 0. greedy_argmax = 1 makes it the plain argmax sampler (src/model/generate.js:4-8). */
+/* createSampler options (src/sampling/sampler.js:4-15, 81-92). Any top_k: 0 (or at least the vocabulary) keeps every
+ * id as a candidate, as the reference does; repeat_last_n must be 0..64. greedy_argmax = 1 makes it the plain argmax
+ * sampler (src/model/generate.js:4-8). */
 typedef struct {
   double temperature, top_p, min_p, repeat_penalty, presence_penalty, frequency_penalty;
   int top_k, repeat_last_n;
