@@ -231,26 +231,30 @@ __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
 }
 
 // One block per (32-dim slice, query head, token). The slice's V rows (dimension-major in the cache) are staged
-// through LDS in chunks of 256 (f16) or 128 (f32) positions, double buffered, the first chunk during the softmax. The
+// through LDS in chunks of ROWB bytes per dimension (1024: 512 f16 or 256 f32 positions, at long contexts where the
+// softmax row leaves room; else 512), double buffered, the first chunk during the softmax; fewer chunks, fewer barriers in the
+// chain. The
 // chain runs on lanes 0-31 of wave 0, one output dimension each, reading 16 bytes of consecutive positions at a time.
 constexpr int AV_DIMS = 32;       // output dimensions per block
-constexpr int AV_ROW = 512;       // bytes of one dimension's positions per chunk
+constexpr int AV_ROW = 512;       // bytes of one dimension's positions per chunk (the smaller chunk)
+constexpr int AV_ROW_BIG = 1024;  // the larger chunk
 constexpr int AV_PITCH = AV_ROW + 16;   // LDS row pitch (the pad spreads the chain's rows over the banks)
 constexpr int AV_CHUNK = AV_DIMS * AV_PITCH;
 constexpr int AV_UNIT = 32;       // positions per unrolled step of the weighted sum
 
-template <bool F16KV>
+template <bool F16KV, int ROWB>
 __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int PITCH = ROWB + 16, CHUNKB = AV_DIMS * PITCH;  // LDS row pitch and bytes of one staged chunk
   constexpr int VB = F16KV ? 2 : 4;
-  constexpr int CT = AV_ROW / VB;        // positions per chunk
+  constexpr int CT = ROWB / VB;        // positions per chunk
   constexpr int EPP = 16 / VB;           // positions per 16-byte piece
-  constexpr int PPR = AV_ROW / 16;       // pieces per row
+  constexpr int PPR = ROWB / 16;       // pieces per row
   constexpr int LPT = AV_DIMS * PPR / 256;   // 16-byte loads per thread per chunk
   const int slice = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int hd = a.hd, kvh = h / (a.nHead / a.nHeadKv);
   float *p = (float *)lds;                                // [ctx rounded up to AV_UNIT] probabilities
-  uint8_t *vbuf = lds + (size_t)((a.ctx + AV_UNIT - 1) / AV_UNIT * AV_UNIT) * 4;  // [2][AV_DIMS][AV_PITCH] staged V rows
+  uint8_t *vbuf = lds + (size_t)((a.ctx + AV_UNIT - 1) / AV_UNIT * AV_UNIT) * 4;  // [2][AV_DIMS][PITCH] staged V rows
   __shared__ double redd[4];
   __shared__ float redf[4];
   const uint8_t *vbase = (const uint8_t *)a.vcache + (((long)a.layer * a.nHeadKv + kvh) * hd + (long)slice * AV_DIMS) * a.vstride * VB;
@@ -269,7 +273,7 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
     #pragma unroll
     for (int k = 0; k < LPT; k++) {
       const int idx = k * 256 + tid;
-      *(uint4 *)(vbuf + buf * AV_CHUNK + (idx / PPR) * AV_PITCH + (idx % PPR) * 16) = pre[k];
+      *(uint4 *)(vbuf + buf * CHUNKB + (idx / PPR) * PITCH + (idx % PPR) * 16) = pre[k];
     }
   };
   fetch(0, a.ctx);
@@ -343,7 +347,7 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
       // p is zero past the last position, so a unit may run past `cnt`: fmaf(0, v, o) == o for the finite cached
       // values read there. The read-ahead index is clamped to the chunk's last unit (a re-read, never past it).
       const int t0 = c * CT, cnt = min(CT, npos - t0), nu = (cnt + AV_UNIT - 1) / AV_UNIT;
-      const uint8_t *row = vbuf + (c & 1) * AV_CHUNK + lane * AV_PITCH;
+      const uint8_t *row = vbuf + (c & 1) * CHUNKB + lane * PITCH;
       const float *pc = p + t0;
       float4 pa[AV_UNIT / 4], pb[AV_UNIT / 4];
       uint4 va[AV_UNIT * VB / 16], vb[AV_UNIT * VB / 16];
@@ -670,8 +674,12 @@ __global__ __launch_bounds__(256) void k_attn_merge(const AttnArgs a) {
 
 size_t attention_split_lds(int hd, int kvF16) { return (size_t)hd * (ATTN_SPLIT_C * (kvF16 ? 2 : 4) + 4); }
 
-// Dynamic LDS of one k_attn_av block: the probabilities of ctx positions and two staged V chunks.
-size_t attention_lds(int ctx) { return (size_t)((ctx + AV_UNIT - 1) / AV_UNIT * AV_UNIT) * 4 + 2 * AV_CHUNK; }
+// Dynamic LDS of one k_attn_av block: the probabilities of ctx positions and two staged V chunks (of AV_ROW or rowb
+// bytes per dimension).
+size_t attention_lds(int ctx, int rowb) {
+  return (size_t)((ctx + AV_UNIT - 1) / AV_UNIT * AV_UNIT) * 4 + 2 * (size_t)AV_DIMS * (rowb + 16);
+}
+size_t attention_lds(int ctx) { return attention_lds(ctx, AV_ROW); }
 // Contexts above AVH_CTX positions take the per-head weighted sum (heads of at most 128 dimensions), whose LDS does not
 // depend on the context; ZEROLLM_ATTN_HEAD_CTX overrides the threshold (tests).
 bool attention_head_form(int ctx, int hd) {
@@ -687,14 +695,24 @@ static void launch_scores_k(const AttnArgs &a, dim3 grid, int B, hipStream_t st)
   hipLaunchKernelGGL((k_attn_scores<HD, F16KV>), grid, dim3(256), kn, st, a);
 }
 
-template <bool F16KV>
-static void launch_av_k(const AttnArgs &a, dim3 grid, size_t lds, hipStream_t st) {
+template <bool F16KV, int ROWB>
+static void launch_av_rows(const AttnArgs &a, dim3 grid, size_t lds, hipStream_t st) {
   static size_t attr = 64 * 1024;  // dynamic LDS above 64 KB must be requested per kernel
   if (lds > attr) {
-    ZL_HIP(hipFuncSetAttribute((const void *)k_attn_av<F16KV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    ZL_HIP(hipFuncSetAttribute((const void *)k_attn_av<F16KV, ROWB>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     attr = lds;
   }
-  hipLaunchKernelGGL((k_attn_av<F16KV>), grid, dim3(256), lds, st, a);
+  hipLaunchKernelGGL((k_attn_av<F16KV, ROWB>), grid, dim3(256), lds, st, a);
+}
+
+// the larger chunk for long contexts where it fits (the same bits: only the staging changes); at short contexts its
+// LDS would halve the blocks a CU holds (measured: 5-token verify pass 3.11 -> 3.32 ms at 1024 positions)
+constexpr int AV_BIG_CTX = 4096;
+template <bool F16KV>
+static void launch_av_k(const AttnArgs &a, dim3 grid, size_t lds, hipStream_t st) {
+  const size_t big = attention_lds(a.ctx, AV_ROW_BIG);
+  if (a.ctx >= AV_BIG_CTX && big <= ATTN_LDS_MAX) launch_av_rows<F16KV, AV_ROW_BIG>(a, grid, big, st);
+  else launch_av_rows<F16KV, AV_ROW>(a, grid, lds, st);
 }
 
 template <bool F16KV>
