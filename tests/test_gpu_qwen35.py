@@ -63,6 +63,38 @@ def test_logits_and_state_match_oracle(gpu, quant, kv):
     ref.close()
 
 
+@pytest.mark.parametrize("d_state", [32, 128])
+def test_deltanet_head_sizes_match_oracle(gpu, d_state):
+    """DeltaNet heads of 32 values (one workgroup per head: no exchange among workgroups) and of 128 (four workgroups
+    per head, the gated norm by the last to arrive): single-token logits and state against the oracle, and a 5-token
+    pass equal to single-token passes bit for bit."""
+    from zerollm_amd import gguf
+    spec = synth.build_qwen35_spec(256, 2, 4, 2, 64, 32, 512, 2048, 4096, synth.qwen35_types(gguf.Q8_0), 23, interval=2,
+                                   d_state=d_state, n_group=2, dt_rank=4, name=f"qwen35-dstate{d_state}")
+    toks = prompt(12, seed=7)
+    print(f"case deltanet d_state={d_state}", flush=True)
+    ref = oracle(spec)
+    want = np.stack([ref.forward(t) for t in toks])
+    m = synth.build_on_device(spec, ctx=64)
+    got = np.stack([m.forward(t).copy() for t in toks])
+    check_close(got, want, f"d_state {d_state}")
+    assert (got.argmax(1) == want.argmax(1)).all()
+    assert np.mean(got.view(np.uint32) == want.view(np.uint32)) >= 0.999
+    conv, ssm = m.recurrent_state()
+    rconv, rssm = ref.state()
+    np.testing.assert_allclose(conv, rconv, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(ssm, rssm, rtol=1e-4, atol=1e-5)
+    b = synth.build_on_device(spec, ctx=64)
+    for t in toks[:7]:
+        b.forward(t)
+    rows = b.forward_batch(toks[7:], logits="all").copy()
+    assert np.array_equal(rows.view(np.uint32), got[7:].view(np.uint32))
+    bconv, bssm = b.recurrent_state()
+    assert np.array_equal(bconv, conv) and np.array_equal(bssm, ssm)
+    for x in (m, b, ref):
+        x.close()
+
+
 def test_verify_width_batch_over_prefix_equals_sequential_and_oracle(gpu):
     """A 5-token verify pass (logits for every row) after a prefix: the rows equal five single-token passes bit for bit,
     and the oracle within the contract."""
