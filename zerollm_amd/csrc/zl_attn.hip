@@ -569,6 +569,204 @@ __global__ __launch_bounds__(256) void k_attn_av_head(const AttnArgs a) {
 
 size_t attention_head_lds(int hd) { return (size_t)2 * hd * AV_PITCH + 2 * 256 * 4; }
 
+// ---- the weighted sum of multi-token passes at long contexts, grouped by KV head. The per-head form above stages its
+// KV head's V once per (query head, token) row: at 16K positions, 4 query heads per KV head and 9 tokens that is 36
+// reads of 4 MB per KV head, 1.2 GB per layer, and the launch runs at the speed of those reads. Here the softmax runs
+// first, one block per row (k_attn_softmax_rows: the per-head form's code; the exponentials replace the scores and
+// 1 / sum goes to pinv), then one block per (32-dimension slice, KV head, group of AVG_ROWS rows) stages each V chunk
+// once for the chains of all its rows: lanes 0-31 of wave w run row 2w's 32 dimensions, lanes 32-63 row 2w + 1's. Every
+// chain is the same position-order f32 chain as in the per-head form, with the same probabilities f32(e * inv); past
+// a row's last position its probabilities are 0 (fmaf(0, v, o) leaves o as it is, V staged there being finite cache
+// values or zeros), so the bits are the per-head form's.
+constexpr int AVG_ROWS = 8;   // rows (query head, token) per block of the grouped weighted sum
+constexpr int AVG_DIMS = 32;  // dimensions per block
+
+__global__ __launch_bounds__(256) void k_attn_softmax_rows(const AttnArgs a) {
+  __shared__ double redd[4];
+  __shared__ float redf[4];
+  const int h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const Step *st = a.step;
+  if (b >= st->B) return;
+  const int npos = st->pos0 + b + 1;
+  float *srow = a.scores + ((long)b * a.nHead + h) * a.sld;
+  float mx = -INFINITY;
+  for (int t = tid; t < npos; t += 256) mx = fmaxf(mx, srow[t]);
+  mx = group_fmax(mx, 64);
+  if (lane == 0) redf[wave] = mx;
+  __syncthreads();
+  const double m = (double)fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
+  double sum = 0.0;
+  for (int t0 = tid; t0 < npos; t0 += 4 * 256) {
+    double e[4];
+    #pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int t = t0 + 256 * k;
+      e[k] = exp((double)srow[t < npos ? t : t0] - m);
+    }
+    #pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int t = t0 + 256 * k;
+      if (t < npos) { srow[t] = (float)e[k]; sum += e[k]; }
+    }
+  }
+  sum = wave_sum_xor(sum, 64);
+  if (lane == 0) redd[wave] = sum;
+  __syncthreads();
+  if (tid == 0) a.pinv[(long)b * a.nHead + h] = 1.0 / ((redd[0] + redd[1]) + (redd[2] + redd[3]));
+}
+
+// nrows: query heads per KV head x the launch's tokens (rows r = b G + g: token b, query head kvh G + g)
+template <bool F16KV>
+__global__ __launch_bounds__(256) void k_attn_av_group(const AttnArgs a, int nrows) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int VB = F16KV ? 2 : 4;
+  constexpr int CT = AV_ROW / VB;                     // positions per chunk
+  constexpr int EPP = 16 / VB;                        // positions per 16-byte piece
+  constexpr int PPR = AV_ROW / 16;                    // pieces per row
+  constexpr int CHUNK = AVG_DIMS * AV_PITCH;          // bytes of one staged chunk of V rows
+  constexpr int LPT = AVG_DIMS * PPR / 256;           // V pieces per thread per chunk
+  constexpr int PPT = AVG_ROWS * CT / 256;            // probabilities per thread per chunk
+  static_assert(AVG_DIMS * PPR % 256 == 0 && AVG_ROWS * CT % 256 == 0 && AVG_ROWS == 8, "chunk geometry");
+  float *pb = (float *)(lds + 2 * CHUNK);             // [2][AVG_ROWS][CT] staged probabilities
+  __shared__ int rnpos[AVG_ROWS];
+  __shared__ long roff[AVG_ROWS];
+  __shared__ double rinv[AVG_ROWS];
+  const int slice = blockIdx.x, kvh = blockIdx.y, r0 = blockIdx.z * AVG_ROWS, tid = threadIdx.x, wave = tid >> 6,
+            lane = tid & 63;
+  const int G = a.nHead / a.nHeadKv;
+  const uint8_t *vbase = (const uint8_t *)a.vcache +
+                         (((long)a.layer * a.nHeadKv + kvh) * a.hd + (long)slice * AVG_DIMS) * a.vstride * VB;
+  uint4 pre[LPT];
+  float pp[PPT];
+  auto fetch = [&](int c, int lim) {
+    #pragma unroll
+    for (int k = 0; k < LPT; k++) {
+      const int idx = k * 256 + tid, dim = idx / PPR, t = c * CT + (idx % PPR) * EPP;
+      pre[k] = t < lim ? *(const uint4 *)(vbase + ((long)dim * a.vstride + t) * VB) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store = [&](int buf) {
+    #pragma unroll
+    for (int k = 0; k < LPT; k++) {
+      const int idx = k * 256 + tid;
+      *(uint4 *)(lds + buf * CHUNK + (idx / PPR) * AV_PITCH + (idx % PPR) * 16) = pre[k];
+    }
+  };
+  fetch(0, a.ctx);
+  const Step *st = a.step;
+  const int Bd = st->B, pos0 = st->pos0;
+  // the group's rows: their scores rows, last positions (0: no row) and 1 / sum
+  if (tid < AVG_ROWS) {
+    const int r = r0 + tid, b = r / G, h = kvh * G + r % G;
+    const bool live = r < nrows && b < Bd;
+    rnpos[tid] = live ? pos0 + b + 1 : 0;
+    roff[tid] = live ? ((long)b * a.nHead + h) * a.sld : 0;
+    rinv[tid] = live ? a.pinv[(long)b * a.nHead + h] : 0.0;
+  }
+  __syncthreads();
+  int nmax = 0;
+  #pragma unroll
+  for (int i = 0; i < AVG_ROWS; i++) nmax = max(nmax, rnpos[i]);
+  if (nmax == 0) return;  // (uniform over the block)
+  const int nch = (nmax + CT - 1) / CT;
+  #pragma unroll
+  for (int k = 0; k < LPT; k++) {  // the first chunk's pieces from the group's last position on: zeros
+    const int t = ((k * 256 + tid) % PPR) * EPP;
+    if (t >= nmax) pre[k] = make_uint4(0, 0, 0, 0);
+    else if (t + EPP > nmax) {
+      uint32_t w[4] = {pre[k].x, pre[k].y, pre[k].z, pre[k].w};
+      #pragma unroll
+      for (int e = 0; e < EPP; e++)
+        if (t + e >= nmax) {
+          if (F16KV) w[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
+          else w[e] = 0u;
+        }
+      pre[k] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+  // probabilities of chunk c for the group's rows (zero past each row's last position)
+  auto pload = [&](int c) {
+    #pragma unroll
+    for (int k = 0; k < PPT; k++) {
+      const int idx = k * 256 + tid, rr = idx / CT, t = c * CT + idx % CT;
+      pp[k] = t < rnpos[rr] ? a.scores[roff[rr] + t] : 0.f;
+    }
+  };
+  auto pstore = [&](int buf) {
+    #pragma unroll
+    for (int k = 0; k < PPT; k++) {
+      const int idx = k * 256 + tid, rr = idx / CT;
+      pb[buf * AVG_ROWS * CT + idx] = (float)((double)pp[k] * rinv[rr]);
+    }
+  };
+  pload(0);
+  store(0);
+  pstore(0);
+  __syncthreads();
+  // ---- weighted sum: row rl = 2 wave + lane / 32, dimension d = lane mod 32 of the slice, chunk by chunk
+  const int rl = 2 * wave + (lane >> 5), d = lane & 31;
+  float o = 0.f;
+  for (int c = 0; c < nch; c++) {
+    if (c + 1 < nch) { fetch(c + 1, nmax); pload(c + 1); }
+    {
+      const int cnt = min(CT, nmax - c * CT), nu = (cnt + AV_UNIT - 1) / AV_UNIT;
+      const uint8_t *row = lds + (c & 1) * CHUNK + d * AV_PITCH;
+      const float *pc = pb + ((c & 1) * AVG_ROWS + rl) * CT;
+      float4 pa[AV_UNIT / 4], pbv[AV_UNIT / 4];
+      uint4 va[AV_UNIT * VB / 16], vb[AV_UNIT * VB / 16];
+      auto read = [&](int u, float4 (&pv)[AV_UNIT / 4], uint4 (&vv)[AV_UNIT * VB / 16]) {
+        #pragma unroll
+        for (int k = 0; k < AV_UNIT / 4; k++) pv[k] = *(const float4 *)(pc + u * AV_UNIT + 4 * k);
+        #pragma unroll
+        for (int k = 0; k < AV_UNIT * VB / 16; k++) vv[k] = *(const uint4 *)(row + (u * AV_UNIT + k * EPP) * VB);
+      };
+      auto steps = [&](const float4 (&pv)[AV_UNIT / 4], const uint4 (&vv)[AV_UNIT * VB / 16]) {
+        #pragma unroll
+        for (int k = 0; k < AV_UNIT / 4; k++) {
+          float v0, v1, v2, v3;
+          if (F16KV) {
+            const uint4 &w = vv[k >> 1];
+            const uint32_t lo = (k & 1) ? w.z : w.x, hi = (k & 1) ? w.w : w.y;
+            v0 = h2f((uint16_t)(lo & 0xffff)); v1 = h2f((uint16_t)(lo >> 16));
+            v2 = h2f((uint16_t)(hi & 0xffff)); v3 = h2f((uint16_t)(hi >> 16));
+          } else {
+            const uint4 &w = vv[k];
+            v0 = __uint_as_float(w.x); v1 = __uint_as_float(w.y); v2 = __uint_as_float(w.z); v3 = __uint_as_float(w.w);
+          }
+          o = fmaf(pv[k].x, v0, o); o = fmaf(pv[k].y, v1, o); o = fmaf(pv[k].z, v2, o); o = fmaf(pv[k].w, v3, o);
+        }
+      };
+      read(0, pa, va);
+      int u = 0;
+      for (; u + 2 <= nu; u += 2) {
+        read(u + 1, pbv, vb);
+        __builtin_amdgcn_sched_barrier(0);
+        steps(pa, va);
+        read(min(u + 2, nu - 1), pa, va);
+        __builtin_amdgcn_sched_barrier(0);
+        steps(pbv, vb);
+      }
+      if (u < nu) steps(pa, va);
+    }
+    __syncthreads();
+    if (c + 1 < nch) { store((c + 1) & 1); pstore((c + 1) & 1); }
+    __syncthreads();
+  }
+  if (rnpos[rl] > 0) {  // (the same for the 32 lanes of the row)
+    const int r = r0 + rl, b = r / G, h = kvh * G + r % G, dim = slice * AVG_DIMS + d, col = h * a.hd + dim;
+    if (a.gate) {  // gated attention output (src/model/forward-qwen35.js:103): o * sigmoid(gate), f64, stored f32
+      const double g = (double)a.gate[(long)b * a.ldq + (long)h * a.qhs + dim];
+      o = (float)((double)o * (1.0 / (1.0 + exp(-g))));
+    }
+    if (a.out) a.out[(long)b * a.ldo + col] = o;
+    quant_block32(o, col, a.act, b);
+  }
+}
+
+size_t attention_group_lds(int kvF16) {
+  return (size_t)2 * AVG_DIMS * AV_PITCH + (size_t)2 * AVG_ROWS * (AV_ROW / (kvF16 ? 2 : 4)) * 4;
+}
+
 template <int HD, bool F16KV>
 static void launch_av_head_k(const AttnArgs &a, int B, hipStream_t st) {
   static size_t attr = 64 * 1024;
@@ -755,6 +953,17 @@ void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
     else launch_av_split_k<false>(a, gv, lds, st);
     ZL_HIP(hipGetLastError());
     hipLaunchKernelGGL(k_attn_merge, dim3(a.nHead, B), dim3(std::max(64, a.hd)), 0, st, a);
+    ZL_HIP(hipGetLastError());
+    return;
+  }
+  if (head && B > 1 && a.pinv) {
+    // grouped by KV head: the softmax rows, then each V chunk staged once for a group's rows
+    hipLaunchKernelGGL(k_attn_softmax_rows, dim3(1, a.nHead, B), dim3(256), 0, st, a);
+    const int nrows = (a.nHead / a.nHeadKv) * B;
+    const dim3 gg(a.hd / AVG_DIMS, a.nHeadKv, (nrows + AVG_ROWS - 1) / AVG_ROWS);
+    const size_t gl = attention_group_lds(a.kvF16);
+    if (a.kvF16) hipLaunchKernelGGL(k_attn_av_group<true>, gg, dim3(256), gl, st, a, nrows);
+    else hipLaunchKernelGGL(k_attn_av_group<false>, gg, dim3(256), gl, st, a, nrows);
     ZL_HIP(hipGetLastError());
     return;
   }

@@ -131,6 +131,7 @@ struct AttnArgs {
   // position-order f32 chain
   double *part;
   int nch;              // chunks per (token, head) row of part
+  double *pinv;         // [token][head] 1 / sum of a row's exponentials (grouped weighted sum of long multi-token passes)
 };
 constexpr int ATTN_SPLIT_C = 256;  // positions per chunk of the position-split weighted sum
 

@@ -229,6 +229,7 @@ struct zl_model {
   float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *hb = nullptr, *logits = nullptr;
   float *scores = nullptr;  // attention scores [maxBatch][n_head][ctx]
   double *attnPart = nullptr;  // position-split weighted-sum partials (contexts beyond ZEROLLM_ATTN_EXACT_CTX), or null
+  double *attnInv = nullptr;   // [maxBatch][n_head] 1 / sum of exponentials (grouped weighted sum)
   int attnNch = 0;
   zl::Act act{};    // quantised input of the q/k/v, attention-output and gate/up GEMVs
   zl::Act act2{};   // quantised FFN hidden state (written by the gate/up GEMV, read by the down GEMV)
@@ -439,6 +440,7 @@ static void finish_model(zl_model *m, const float *ropeFreqs) {
   m->hb = (float *)m->ar.alloc((size_t)B * c.n_ff * 4);
   m->logits = (float *)m->ar.alloc((size_t)m->logitsBatch * c.vocab * 4);
   m->scores = (float *)m->ar.alloc((size_t)B * c.n_head * m->ctx * 4);
+  m->attnInv = (double *)m->ar.alloc((size_t)B * c.n_head * 8);
   if (split) {
     m->attnNch = (m->ctx + ATTN_SPLIT_C - 1) / ATTN_SPLIT_C;
     m->attnPart = (double *)m->ar.alloc((size_t)B * c.n_head * m->attnNch * (c.head_dim + 2) * 8);
@@ -675,7 +677,7 @@ static void enqueue_forward(zl_model *m, int B, int want) {
       aa.step = m->dstep; aa.out = m->act.f; aa.ldo = m->act.ld; aa.act = m->act;
       aa.qhs = m->hybrid ? 2 * c.head_dim : c.head_dim;
       aa.gate = m->hybrid ? m->q + c.head_dim : nullptr;
-      aa.part = m->attnPart; aa.nch = m->attnNch;
+      aa.part = m->attnPart; aa.nch = m->attnNch; aa.pinv = m->attnInv;
       launch_attention(aa, B, m->st);
       gemv_group(m, {{&L.wo, nullptr, 0, nullptr}}, B, EPI_RESID, m->act, m->act.f, m->act.ld);
     }
