@@ -302,12 +302,14 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
   }
   // ---- softmax (src/compute/ref-kernels.js:313-320)
   float mx = -INFINITY;
-  for (int t0 = 0; t0 < npos; t0 += 1024) {
-    float v[4];
+  #pragma unroll
+  for (int k = 0; k < 4; k++) { const int t = k * 256 + tid; if (t < npos) p[t] = v0[k]; else v0[k] = -INFINITY; mx = fmaxf(mx, v0[k]); }
+  for (int t0 = 1024; t0 < npos; t0 += 16 * 256) {  // 16 loads per thread in flight at a time
+    float v[16];
     #pragma unroll
-    for (int k = 0; k < 4; k++) { const int t = t0 + k * 256 + tid; v[k] = t >= npos ? -INFINITY : t0 == 0 ? v0[k] : srow[t]; }
+    for (int k = 0; k < 16; k++) { const int t = t0 + k * 256 + tid; v[k] = srow[t < npos ? t : 0]; }
     #pragma unroll
-    for (int k = 0; k < 4; k++) { const int t = t0 + k * 256 + tid; if (t < npos) p[t] = v[k]; mx = fmaxf(mx, v[k]); }
+    for (int k = 0; k < 16; k++) { const int t = t0 + k * 256 + tid; if (t < npos) { p[t] = v[k]; mx = fmaxf(mx, v[k]); } }
   }
   mx = group_fmax(mx, 64);
   if (lane == 0) redf[wave] = mx;
@@ -466,23 +468,32 @@ __global__ __launch_bounds__(256) void k_attn_av_head(const AttnArgs a) {
   }
   // ---- softmax (src/compute/ref-kernels.js:313-320) in k_attn_av's order; the exponentials replace the scores
   float mx = -INFINITY;
-  for (int t = tid; t < npos; t += 256) mx = fmaxf(mx, srow[t]);
+  for (int t0 = tid; t0 < npos; t0 += 16 * 256) {  // 16 loads per thread in flight at a time
+    float v[16];
+    #pragma unroll
+    for (int k = 0; k < 16; k++) { const int t = t0 + 256 * k; v[k] = srow[t < npos ? t : t0]; }
+    #pragma unroll
+    for (int k = 0; k < 16; k++) mx = fmaxf(mx, v[k]);  // (a clamped reload repeats a value already counted)
+  }
   mx = group_fmax(mx, 64);
   if (lane == 0) redf[wave] = mx;
   __syncthreads();
   const double m = (double)fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
   double sum = 0.0;
-  for (int t0 = tid; t0 < npos; t0 += 4 * 256) {
-    double e[4];
+  for (int t0 = tid; t0 < npos; t0 += 16 * 256) {  // positions tid + 256 j added in j order, as k_attn_av does
+    float v[16];
     #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const int t = t0 + 256 * k;
-      e[k] = exp((double)srow[t < npos ? t : t0] - m);
-    }
+    for (int k = 0; k < 16; k++) { const int t = t0 + 256 * k; v[k] = srow[t < npos ? t : t0]; }
     #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const int t = t0 + 256 * k;
-      if (t < npos) { srow[t] = (float)e[k]; sum += e[k]; }
+    for (int q = 0; q < 16; q += 4) {
+      double e[4];
+      #pragma unroll
+      for (int k = 0; k < 4; k++) e[k] = exp((double)v[q + k] - m);
+      #pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int t = t0 + 256 * (q + k);
+        if (t < npos) { srow[t] = (float)e[k]; sum += e[k]; }
+      }
     }
   }
   sum = wave_sum_xor(sum, 64);
@@ -590,23 +601,32 @@ __global__ __launch_bounds__(256) void k_attn_softmax_rows(const AttnArgs a) {
   const int npos = st->pos0 + b + 1;
   float *srow = a.scores + ((long)b * a.nHead + h) * a.sld;
   float mx = -INFINITY;
-  for (int t = tid; t < npos; t += 256) mx = fmaxf(mx, srow[t]);
+  for (int t0 = tid; t0 < npos; t0 += 16 * 256) {  // 16 loads per thread in flight at a time
+    float v[16];
+    #pragma unroll
+    for (int k = 0; k < 16; k++) { const int t = t0 + 256 * k; v[k] = srow[t < npos ? t : t0]; }
+    #pragma unroll
+    for (int k = 0; k < 16; k++) mx = fmaxf(mx, v[k]);  // (a clamped reload repeats a value already counted)
+  }
   mx = group_fmax(mx, 64);
   if (lane == 0) redf[wave] = mx;
   __syncthreads();
   const double m = (double)fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
   double sum = 0.0;
-  for (int t0 = tid; t0 < npos; t0 += 4 * 256) {
-    double e[4];
+  for (int t0 = tid; t0 < npos; t0 += 16 * 256) {  // positions tid + 256 j added in j order, as k_attn_av does
+    float v[16];
     #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const int t = t0 + 256 * k;
-      e[k] = exp((double)srow[t < npos ? t : t0] - m);
-    }
+    for (int k = 0; k < 16; k++) { const int t = t0 + 256 * k; v[k] = srow[t < npos ? t : t0]; }
     #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const int t = t0 + 256 * k;
-      if (t < npos) { srow[t] = (float)e[k]; sum += e[k]; }
+    for (int q = 0; q < 16; q += 4) {
+      double e[4];
+      #pragma unroll
+      for (int k = 0; k < 4; k++) e[k] = exp((double)v[q + k] - m);
+      #pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int t = t0 + 256 * (q + k);
+        if (t < npos) { srow[t] = (float)e[k]; sum += e[k]; }
+      }
     }
   }
   sum = wave_sum_xor(sum, 64);
@@ -627,7 +647,9 @@ __global__ __launch_bounds__(256) void k_attn_av_group(const AttnArgs a, int nro
   constexpr int LPT = AVG_DIMS * PPR / 256;           // V pieces per thread per chunk
   constexpr int PPT = AVG_ROWS * CT / 256;            // probabilities per thread per chunk
   static_assert(AVG_DIMS * PPR % 256 == 0 && AVG_ROWS * CT % 256 == 0 && AVG_ROWS == 8, "chunk geometry");
-  float *pb = (float *)(lds + 2 * CHUNK);             // [2][AVG_ROWS][CT] staged probabilities
+  constexpr int CTP = CT + 4;                         // row pitch of the staged probabilities (the two rows a wave
+                                                      // reads at once fall on different banks)
+  float *pb = (float *)(lds + 2 * CHUNK);             // [2][AVG_ROWS][CTP] staged probabilities
   __shared__ int rnpos[AVG_ROWS];
   __shared__ long roff[AVG_ROWS];
   __shared__ double rinv[AVG_ROWS];
@@ -696,7 +718,7 @@ __global__ __launch_bounds__(256) void k_attn_av_group(const AttnArgs a, int nro
     #pragma unroll
     for (int k = 0; k < PPT; k++) {
       const int idx = k * 256 + tid, rr = idx / CT;
-      pb[buf * AVG_ROWS * CT + idx] = (float)((double)pp[k] * rinv[rr]);
+      pb[(buf * AVG_ROWS + rr) * CTP + idx % CT] = (float)((double)pp[k] * rinv[rr]);
     }
   };
   pload(0);
@@ -711,7 +733,7 @@ __global__ __launch_bounds__(256) void k_attn_av_group(const AttnArgs a, int nro
     {
       const int cnt = min(CT, nmax - c * CT), nu = (cnt + AV_UNIT - 1) / AV_UNIT;
       const uint8_t *row = lds + (c & 1) * CHUNK + d * AV_PITCH;
-      const float *pc = pb + ((c & 1) * AVG_ROWS + rl) * CT;
+      const float *pc = pb + ((c & 1) * AVG_ROWS + rl) * CTP;
       float4 pa[AV_UNIT / 4], pbv[AV_UNIT / 4];
       uint4 va[AV_UNIT * VB / 16], vb[AV_UNIT * VB / 16];
       auto read = [&](int u, float4 (&pv)[AV_UNIT / 4], uint4 (&vv)[AV_UNIT * VB / 16]) {
@@ -764,7 +786,7 @@ __global__ __launch_bounds__(256) void k_attn_av_group(const AttnArgs a, int nro
 }
 
 size_t attention_group_lds(int kvF16) {
-  return (size_t)2 * AVG_DIMS * AV_PITCH + (size_t)2 * AVG_ROWS * (AV_ROW / (kvF16 ? 2 : 4)) * 4;
+  return (size_t)2 * AVG_DIMS * AV_PITCH + (size_t)2 * AVG_ROWS * (AV_ROW / (kvF16 ? 2 : 4) + 4) * 4;
 }
 
 template <int HD, bool F16KV>
