@@ -636,14 +636,15 @@ __global__ __launch_bounds__(256) void k_attn_softmax_rows(const AttnArgs a) {
 }
 
 // nrows: query heads per KV head x the launch's tokens (rows r = b G + g: token b, query head kvh G + g)
-template <bool F16KV>
+template <bool F16KV, int ROWB>
 __global__ __launch_bounds__(256) void k_attn_av_group(const AttnArgs a, int nrows) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int VB = F16KV ? 2 : 4;
-  constexpr int CT = AV_ROW / VB;                     // positions per chunk
+  constexpr int CT = ROWB / VB;                       // positions per chunk
   constexpr int EPP = 16 / VB;                        // positions per 16-byte piece
-  constexpr int PPR = AV_ROW / 16;                    // pieces per row
-  constexpr int CHUNK = AVG_DIMS * AV_PITCH;          // bytes of one staged chunk of V rows
+  constexpr int PPR = ROWB / 16;                      // pieces per row
+  constexpr int PITCH = ROWB + 16;                    // LDS pitch of a staged V row
+  constexpr int CHUNK = AVG_DIMS * PITCH;             // bytes of one staged chunk of V rows
   constexpr int LPT = AVG_DIMS * PPR / 256;           // V pieces per thread per chunk
   constexpr int PPT = AVG_ROWS * CT / 256;            // probabilities per thread per chunk
   static_assert(AVG_DIMS * PPR % 256 == 0 && AVG_ROWS * CT % 256 == 0 && AVG_ROWS == 8, "chunk geometry");
@@ -671,7 +672,7 @@ __global__ __launch_bounds__(256) void k_attn_av_group(const AttnArgs a, int nro
     #pragma unroll
     for (int k = 0; k < LPT; k++) {
       const int idx = k * 256 + tid;
-      *(uint4 *)(lds + buf * CHUNK + (idx / PPR) * AV_PITCH + (idx % PPR) * 16) = pre[k];
+      *(uint4 *)(lds + buf * CHUNK + (idx / PPR) * PITCH + (idx % PPR) * 16) = pre[k];
     }
   };
   fetch(0, a.ctx);
@@ -732,7 +733,7 @@ __global__ __launch_bounds__(256) void k_attn_av_group(const AttnArgs a, int nro
     if (c + 1 < nch) { fetch(c + 1, nmax); pload(c + 1); }
     {
       const int cnt = min(CT, nmax - c * CT), nu = (cnt + AV_UNIT - 1) / AV_UNIT;
-      const uint8_t *row = lds + (c & 1) * CHUNK + d * AV_PITCH;
+      const uint8_t *row = lds + (c & 1) * CHUNK + d * PITCH;
       const float *pc = pb + ((c & 1) * AVG_ROWS + rl) * CTP;
       float4 pa[AV_UNIT / 4], pbv[AV_UNIT / 4];
       uint4 va[AV_UNIT * VB / 16], vb[AV_UNIT * VB / 16];
@@ -785,8 +786,20 @@ __global__ __launch_bounds__(256) void k_attn_av_group(const AttnArgs a, int nro
   }
 }
 
-size_t attention_group_lds(int kvF16) {
-  return (size_t)2 * AVG_DIMS * AV_PITCH + (size_t)2 * AVG_ROWS * (AV_ROW / (kvF16 ? 2 : 4) + 4) * 4;
+// LDS of a grouped block with chunks of rowb bytes per dimension: two staged V chunks and two chunks of probabilities
+size_t attention_group_lds(int kvF16, int rowb) {
+  return (size_t)2 * AVG_DIMS * (rowb + 16) + (size_t)2 * AVG_ROWS * (rowb / (kvF16 ? 2 : 4) + 4) * 4;
+}
+
+template <bool F16KV, int ROWB>
+static void launch_av_group_k(const AttnArgs &a, dim3 grid, int nrows, hipStream_t st) {
+  static size_t attr = 64 * 1024;  // dynamic LDS above 64 KB must be requested per kernel
+  const size_t lds = attention_group_lds(F16KV, ROWB);
+  if (lds > attr) {
+    ZL_HIP(hipFuncSetAttribute((const void *)k_attn_av_group<F16KV, ROWB>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    attr = lds;
+  }
+  hipLaunchKernelGGL((k_attn_av_group<F16KV, ROWB>), grid, dim3(256), lds, st, a, nrows);
 }
 
 template <int HD, bool F16KV>
@@ -983,9 +996,9 @@ void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
     hipLaunchKernelGGL(k_attn_softmax_rows, dim3(1, a.nHead, B), dim3(256), 0, st, a);
     const int nrows = (a.nHead / a.nHeadKv) * B;
     const dim3 gg(a.hd / AVG_DIMS, a.nHeadKv, (nrows + AVG_ROWS - 1) / AVG_ROWS);
-    const size_t gl = attention_group_lds(a.kvF16);
-    if (a.kvF16) hipLaunchKernelGGL(k_attn_av_group<true>, gg, dim3(256), gl, st, a, nrows);
-    else hipLaunchKernelGGL(k_attn_av_group<false>, gg, dim3(256), gl, st, a, nrows);
+    // 1024-byte chunks (512 f16 / 256 f32 positions): each chunk's chain is long enough to cover the next chunk's loads
+    if (a.kvF16) launch_av_group_k<true, AV_ROW_BIG>(a, gg, nrows, st);
+    else launch_av_group_k<false, AV_ROW_BIG>(a, gg, nrows, st);
     ZL_HIP(hipGetLastError());
     return;
   }
