@@ -133,9 +133,14 @@ __global__ __launch_bounds__(DT) void k_dist_rows(const float *__restrict__ logi
     for (int i = tid; i < 256; i += DT) hcount[i] = 0;
     __syncthreads();
     const uint32_t prefix = s_prefix, mask = s_mask;
-    for (int i = tid; i < vocab; i += DT) {
-      uint32_t k = fkey(l[i]);
-      if ((k & mask) == prefix) atomicAdd(&hcount[(k >> shift) & 255], 1u);
+    // 8 keys per thread requested at a time
+    for (int i0 = 0; i0 < vocab; i0 += 8 * DT) {
+      uint32_t kv[8];
+      #pragma unroll
+      for (int j = 0; j < 8; j++) { const int i = i0 + j * DT + tid; kv[j] = i < vocab ? fkey(l[i]) : 0u; }
+      #pragma unroll
+      for (int j = 0; j < 8; j++)
+        if (i0 + j * DT + tid < vocab && (kv[j] & mask) == prefix) atomicAdd(&hcount[(kv[j] >> shift) & 255u], 1u);
     }
     __syncthreads();
     if (tid == 0) {
@@ -157,11 +162,17 @@ __global__ __launch_bounds__(DT) void k_dist_rows(const float *__restrict__ logi
   if (tid == 0) s_ncand = 0;
   __syncthreads();
   if (!tie) {
-    for (int i = tid; i < vocab; i += DT) {
-      uint32_t k = fkey(l[i]);
-      if (k >= T) {
-        int p = atomicAdd(&s_ncand, 1);
-        if (p < KCAP) { s_ids[p] = i; s_vals[p] = (double)l[i]; }
+    for (int i0 = 0; i0 < vocab; i0 += 8 * DT) {
+      float v[8];
+      #pragma unroll
+      for (int j = 0; j < 8; j++) { const int i = i0 + j * DT + tid; v[j] = l[i < vocab ? i : 0]; }
+      #pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int i = i0 + j * DT + tid;
+        if (i < vocab && fkey(v[j]) >= T) {
+          int p = atomicAdd(&s_ncand, 1);
+          if (p < KCAP) { s_ids[p] = i; s_vals[p] = (double)v[j]; }
+        }
       }
     }
   } else if (tid == 0) {
