@@ -95,6 +95,9 @@ __device__ inline void norm_rope(float *v, const float *nw, double eps, int nRot
   norm_rope_apply<HD>(v, r, nw, eps, nRot, neox, lane);
 }
 
+// Contexts from which the long-context launch forms are used (KV cache capacity in positions).
+constexpr int AV_BIG_CTX = 4096;
+
 // Scores of one 64-position chunk of one token for hg query heads sharing a KV head. Keys of positions before the
 // pass (pos0) come from the cache; the pass's own keys (positions pos0 .. pos0 + b) are normed and rotated here from the
 // projection output, rounded as the cache stores them, and the block of token b appends its own key and value to the
@@ -113,9 +116,25 @@ __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
   __shared__ float qs[8 * HD];
   __shared__ float kf[8 * HD];           // rotated keys of the pass, a batch of up to 8 positions at a time (f32)
   extern __shared__ __align__(16) uint8_t kn[];  // the chunk's new keys in cache format, from position n0: [min(P, B)][HD]
-  const int b = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // Workgroups go to the 8 XCDs round robin (linear id mod 8). At long contexts, where a layer's keys outgrow the
+  // L2s, the blocks of the pass's tokens that read the same key chunks are given consecutive linear ids of one XCD, so
+  // their K reads meet in that XCD's L2 instead of each token streaming the keys from memory again (measured: 16K
+  // context, 9 tokens, 0.24 ms less per verify pass; at ~700 positions the keys stay in L2 and the order costs 0.02 ms).
+  const int X = gridDim.x, XY = X * gridDim.y, Z = gridDim.z;
+  const int L = blockIdx.x + X * (blockIdx.y + gridDim.y * blockIdx.z);
+  int xy, b;
+  if (a.ctx >= AV_BIG_CTX && XY % 8 == 0) {
+    const int q = L >> 3;
+    b = q % Z;
+    xy = (L & 7) + 8 * (q / Z);
+  } else {
+    b = L / XY;
+    xy = L - b * XY;
+  }
+  const int bx = xy % X, by = xy / X;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int group = a.nHead / a.nHeadKv, hg = a.hpb;
-  const int h0 = blockIdx.y * hg;        // first query head of this block
+  const int h0 = by * hg;        // first query head of this block
   const int kvh = h0 / group;
   const bool writer = h0 % group == 0;   // the first head group of a KV head appends the pass's K and V
   const long kvoff = ((long)a.layer * a.nHeadKv + kvh) * a.ctx * HD;
@@ -134,7 +153,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
         u[r][k] = t < lim ? *(const uint4 *)(kbase + ((long)t * HD + part * ATTN_VPL) * VB + 16 * k) : make_uint4(0, 0, 0, 0);
     }
   };
-  fetch(blockIdx.x * P, a.ctx);
+  fetch(bx * P, a.ctx);
   constexpr int QV = 8 * HD / 256;  // query values per thread (at most 8 heads of HD values per block)
   float qv[QV];
   #pragma unroll
@@ -145,7 +164,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
   // the pass's first 8 key rows of this KV head (row-major [row][HD], element tid + 256 k), for the blocks that norm
   // and rotate the pass's keys; unconditional loads (rows past B read row 0, unused)
   constexpr int KPT = 8 * HD / 256;
-  const int nB = gridDim.z;
+  const int nB = Z;
   float kr[KPT];
   #pragma unroll
   for (int k = 0; k < KPT; k++) {
@@ -155,15 +174,15 @@ __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
   const Step *st = a.step;
   if (b >= st->B) return;
   const int pos0 = st->pos0, npos = pos0 + b + 1;
-  if (blockIdx.x * P >= npos) return;
+  if (bx * P >= npos) return;
   #pragma unroll
   for (int k = 0; k < QV; k++)
     if (tid + 256 * k < hg * HD) qs[tid + 256 * k] = qv[k];
   __syncthreads();
   for (int h = wave; h < hg; h += 4) norm_rope<HD>(qs + h * HD, a.qNorm, a.eps, a.nRot, a.neox, a.cosT, a.sinT, npos - 1, lane);
   __syncthreads();
-  for (int c0 = blockIdx.x * P; c0 < npos; c0 += gridDim.x * P) {
-    if (c0 != blockIdx.x * P) fetch(c0, pos0);
+  for (int c0 = bx * P; c0 < npos; c0 += X * P) {
+    if (c0 != bx * P) fetch(c0, pos0);
     // the pass's keys in this chunk: positions [n0, n1), tokens [n0 - pos0, n1 - pos0)
     const int n0 = max(c0, pos0), n1 = min(c0 + P, npos);
     for (int g0 = n0; g0 < n1; g0 += 8) {
@@ -940,7 +959,6 @@ static void launch_av_rows(const AttnArgs &a, dim3 grid, size_t lds, hipStream_t
 
 // the larger chunk for long contexts where it fits (the same bits: only the staging changes); at short contexts its
 // LDS would halve the blocks a CU holds (measured: 5-token verify pass 3.11 -> 3.32 ms at 1024 positions)
-constexpr int AV_BIG_CTX = 4096;
 template <bool F16KV>
 static void launch_av_k(const AttnArgs &a, dim3 grid, size_t lds, hipStream_t st) {
   const size_t big = attention_lds(a.ctx, AV_ROW_BIG);
