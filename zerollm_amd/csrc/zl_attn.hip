@@ -654,9 +654,12 @@ __global__ __launch_bounds__(256) void k_attn_softmax_rows(const AttnArgs a) {
   if (tid == 0) a.pinv[(long)b * a.nHead + h] = 1.0 / ((redd[0] + redd[1]) + (redd[2] + redd[3]));
 }
 
-// nrows: query heads per KV head x the launch's tokens (rows r = b G + g: token b, query head kvh G + g)
+// nrows: query heads per KV head x the launch's tokens (rows r = b G + g: token b, query head kvh G + g).
+// 512 threads: waves 0-3 run the chains of chunk c while waves 4-7 store chunk c + 1 (V and probabilities) into the
+// other buffer and request chunk c + 2, so the staging never stands between two chunks' chains (one barrier per chunk).
+constexpr int AVG_THREADS = 512;
 template <bool F16KV, int ROWB>
-__global__ __launch_bounds__(256) void k_attn_av_group(const AttnArgs a, int nrows) {
+__global__ __launch_bounds__(AVG_THREADS) void k_attn_av_group(const AttnArgs a, int nrows) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int VB = F16KV ? 2 : 4;
   constexpr int CT = ROWB / VB;                       // positions per chunk
@@ -664,8 +667,8 @@ __global__ __launch_bounds__(256) void k_attn_av_group(const AttnArgs a, int nro
   constexpr int PPR = ROWB / 16;                      // pieces per row
   constexpr int PITCH = ROWB + 16;                    // LDS pitch of a staged V row
   constexpr int CHUNK = AVG_DIMS * PITCH;             // bytes of one staged chunk of V rows
-  constexpr int LPT = AVG_DIMS * PPR / 256;           // V pieces per thread per chunk
-  constexpr int PPT = AVG_ROWS * CT / 256;            // probabilities per thread per chunk
+  constexpr int LPT = AVG_DIMS * PPR / 256;           // V pieces per staging thread per chunk
+  constexpr int PPT = AVG_ROWS * CT / 256;            // probabilities per staging thread per chunk
   static_assert(AVG_DIMS * PPR % 256 == 0 && AVG_ROWS * CT % 256 == 0 && AVG_ROWS == 8, "chunk geometry");
   constexpr int CTP = CT + 4;                         // row pitch of the staged probabilities (the two rows a wave
                                                       // reads at once fall on different banks)
@@ -675,6 +678,8 @@ __global__ __launch_bounds__(256) void k_attn_av_group(const AttnArgs a, int nro
   __shared__ double rinv[AVG_ROWS];
   const int slice = blockIdx.x, kvh = blockIdx.y, r0 = blockIdx.z * AVG_ROWS, tid = threadIdx.x, wave = tid >> 6,
             lane = tid & 63;
+  const bool stager = tid >= 256;
+  const int sid = tid - 256;                          // staging thread index (stagers only)
   const int G = a.nHead / a.nHeadKv;
   const uint8_t *vbase = (const uint8_t *)a.vcache +
                          (((long)a.layer * a.nHeadKv + kvh) * a.hd + (long)slice * AVG_DIMS) * a.vstride * VB;
@@ -683,18 +688,18 @@ __global__ __launch_bounds__(256) void k_attn_av_group(const AttnArgs a, int nro
   auto fetch = [&](int c, int lim) {
     #pragma unroll
     for (int k = 0; k < LPT; k++) {
-      const int idx = k * 256 + tid, dim = idx / PPR, t = c * CT + (idx % PPR) * EPP;
+      const int idx = k * 256 + sid, dim = idx / PPR, t = c * CT + (idx % PPR) * EPP;
       pre[k] = t < lim ? *(const uint4 *)(vbase + ((long)dim * a.vstride + t) * VB) : make_uint4(0, 0, 0, 0);
     }
   };
   auto store = [&](int buf) {
     #pragma unroll
     for (int k = 0; k < LPT; k++) {
-      const int idx = k * 256 + tid;
+      const int idx = k * 256 + sid;
       *(uint4 *)(lds + buf * CHUNK + (idx / PPR) * PITCH + (idx % PPR) * 16) = pre[k];
     }
   };
-  fetch(0, a.ctx);
+  if (stager) fetch(0, a.ctx);
   const Step *st = a.step;
   const int Bd = st->B, pos0 = st->pos0;
   // the group's rows: their scores rows, last positions (0: no row) and 1 / sum
@@ -711,46 +716,55 @@ __global__ __launch_bounds__(256) void k_attn_av_group(const AttnArgs a, int nro
   for (int i = 0; i < AVG_ROWS; i++) nmax = max(nmax, rnpos[i]);
   if (nmax == 0) return;  // (uniform over the block)
   const int nch = (nmax + CT - 1) / CT;
-  #pragma unroll
-  for (int k = 0; k < LPT; k++) {  // the first chunk's pieces from the group's last position on: zeros
-    const int t = ((k * 256 + tid) % PPR) * EPP;
-    if (t >= nmax) pre[k] = make_uint4(0, 0, 0, 0);
-    else if (t + EPP > nmax) {
-      uint32_t w[4] = {pre[k].x, pre[k].y, pre[k].z, pre[k].w};
-      #pragma unroll
-      for (int e = 0; e < EPP; e++)
-        if (t + e >= nmax) {
-          if (F16KV) w[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
-          else w[e] = 0u;
-        }
-      pre[k] = make_uint4(w[0], w[1], w[2], w[3]);
-    }
-  }
   // probabilities of chunk c for the group's rows (zero past each row's last position)
   auto pload = [&](int c) {
     #pragma unroll
     for (int k = 0; k < PPT; k++) {
-      const int idx = k * 256 + tid, rr = idx / CT, t = c * CT + idx % CT;
+      const int idx = k * 256 + sid, rr = idx / CT, t = c * CT + idx % CT;
       pp[k] = t < rnpos[rr] ? a.scores[roff[rr] + t] : 0.f;
     }
   };
   auto pstore = [&](int buf) {
     #pragma unroll
     for (int k = 0; k < PPT; k++) {
-      const int idx = k * 256 + tid, rr = idx / CT;
+      const int idx = k * 256 + sid, rr = idx / CT;
       pb[(buf * AVG_ROWS + rr) * CTP + idx % CT] = (float)((double)pp[k] * rinv[rr]);
     }
   };
-  pload(0);
-  store(0);
-  pstore(0);
+  if (stager) {
+    #pragma unroll
+    for (int k = 0; k < LPT; k++) {  // the first chunk's pieces from the group's last position on: zeros
+      const int t = ((k * 256 + sid) % PPR) * EPP;
+      if (t >= nmax) pre[k] = make_uint4(0, 0, 0, 0);
+      else if (t + EPP > nmax) {
+        uint32_t w[4] = {pre[k].x, pre[k].y, pre[k].z, pre[k].w};
+        #pragma unroll
+        for (int e = 0; e < EPP; e++)
+          if (t + e >= nmax) {
+            if (F16KV) w[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
+            else w[e] = 0u;
+          }
+        pre[k] = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    }
+    pload(0);
+    store(0);
+    pstore(0);
+    if (nch > 1) { fetch(1, nmax); pload(1); }
+  }
   __syncthreads();
-  // ---- weighted sum: row rl = 2 wave + lane / 32, dimension d = lane mod 32 of the slice, chunk by chunk
-  const int rl = 2 * wave + (lane >> 5), d = lane & 31;
+  // ---- weighted sum: row rl = 2 wave + lane / 32, dimension d = lane mod 32 of the slice, chunk by chunk (waves 0-3)
+  const int rl = 2 * (wave & 3) + (lane >> 5), d = lane & 31;
   float o = 0.f;
   for (int c = 0; c < nch; c++) {
-    if (c + 1 < nch) { fetch(c + 1, nmax); pload(c + 1); }
-    {
+    if (stager) {
+      // chunk c + 1 into the buffer the chains left at the last barrier, then the loads of chunk c + 2
+      if (c + 1 < nch) {
+        store((c + 1) & 1);
+        pstore((c + 1) & 1);
+        if (c + 2 < nch) { fetch(c + 2, nmax); pload(c + 2); }
+      }
+    } else {
       const int cnt = min(CT, nmax - c * CT), nu = (cnt + AV_UNIT - 1) / AV_UNIT;
       const uint8_t *row = lds + (c & 1) * CHUNK + d * PITCH;
       const float *pc = pb + ((c & 1) * AVG_ROWS + rl) * CTP;
@@ -791,10 +805,8 @@ __global__ __launch_bounds__(256) void k_attn_av_group(const AttnArgs a, int nro
       if (u < nu) steps(pa, va);
     }
     __syncthreads();
-    if (c + 1 < nch) { store((c + 1) & 1); pstore((c + 1) & 1); }
-    __syncthreads();
   }
-  if (rnpos[rl] > 0) {  // (the same for the 32 lanes of the row)
+  if (!stager && rnpos[rl] > 0) {  // (the same for the 32 lanes of the row)
     const int r = r0 + rl, b = r / G, h = kvh * G + r % G, dim = slice * AVG_DIMS + d, col = h * a.hd + dim;
     if (a.gate) {  // gated attention output (src/model/forward-qwen35.js:103): o * sigmoid(gate), f64, stored f32
       const double g = (double)a.gate[(long)b * a.ldq + (long)h * a.qhs + dim];
@@ -818,7 +830,7 @@ static void launch_av_group_k(const AttnArgs &a, dim3 grid, int nrows, hipStream
     ZL_HIP(hipFuncSetAttribute((const void *)k_attn_av_group<F16KV, ROWB>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     attr = lds;
   }
-  hipLaunchKernelGGL((k_attn_av_group<F16KV, ROWB>), grid, dim3(256), lds, st, a, nrows);
+  hipLaunchKernelGGL((k_attn_av_group<F16KV, ROWB>), grid, dim3(AVG_THREADS), lds, st, a, nrows);
 }
 
 template <int HD, bool F16KV>
