@@ -309,6 +309,20 @@ struct WideWork {
   int vocab, rows;
 };
 
+// Work space of two-stage top-k selection (top_k <= KCAP, no penalties): blocks of CAND_CHUNK logits each keep every
+// logit at or above their own k-th largest ([rows][blocks][cmax] ids and values, [rows][blocks] counts); the row's
+// selection then runs over those candidates only.
+constexpr int CAND_CHUNK = 2048;              // logits per candidate block
+constexpr int CAND_MAXB = 128;                // candidate blocks per row at most (vocabularies up to 262144)
+constexpr int CAND_SLACK = 32;                // list room above top_k for ties at a block's k-th value
+constexpr int CAND_CMAX = KCAP + CAND_SLACK;  // list length the work space is sized for
+struct CandWork {
+  int *ids;
+  float *vals;
+  int *cnt;
+  int vocab, rows;
+};
+
 struct SamplerParams {
   double temperature, topP, minP, repeatPenalty, presence, frequency;
   int topK, repeatLastN, penalized, greedyArgmax;
@@ -333,10 +347,11 @@ struct ArgmaxWork {
 };
 
 // Row r uses history hist[0 .. histLen0 + r * histInc).
-// ww: the full-list work space when the sampler keeps full lists (top_k 0 or above KCAP), else null.
+// ww: the full-list work space when the sampler keeps full lists (top_k 0 or above KCAP), else null; cw: the two-stage
+// selection's work space (unpenalized samplers with top_k <= KCAP), else null.
 void launch_dist_rows(const float *logits, int ldl, int nrows, int vocab, const SamplerParams &sp, const int *hist,
-                      int histLen0, int histInc, float *scratch, const ArgmaxWork &aw, const WideWork *ww, DevDist *out,
-                      hipStream_t st);
+                      int histLen0, int histInc, float *scratch, const ArgmaxWork &aw, const WideWork *ww,
+                      const CandWork *cw, DevDist *out, hipStream_t st);
 // Point rows [0, n) of d at full-list storage of `vocab` entries per row (ids, probs, pos, res), or at null.
 void launch_set_wide(DevDist *d, int n, int vocab, int *ids, double *probs, int *pos, double *res, hipStream_t st);
 void launch_draft_draw(const DevDist *dist, SpecState *ss, int j, const int *stopIds, int nStop, Step *draftStep,

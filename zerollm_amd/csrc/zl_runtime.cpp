@@ -273,6 +273,7 @@ struct zl_sampler {
   zl::ArgmaxWork am{};
   bool wide = false;      // full candidate lists (top_k 0 or above KCAP)
   zl::WideWork ww{};      // their sort work space ([65 rows][vocab])
+  zl::CandWork cw{};      // two-stage top-k selection work space (unpenalized samplers with top_k <= KCAP)
   hipStream_t st = nullptr;
   // whole speculative cycles captured as two graphs (draft phase, verify phase) per (target uid, draft uid, fed
   // tokens, drafts, stop ids, phase); they capture this sampler's buffers, so they live and die with it
@@ -1338,6 +1339,15 @@ static void ensure_scratch(zl_sampler *s, int vocab) {
     s->scratch = (float *)s->ar.alloc((size_t)65 * vocab * 4);
     s->scratchVocab = vocab;
   }
+  const bool sampled = !(s->sp.temperature <= 0.0 || s->sp.greedyArgmax);
+  if (sampled && !s->wide && !s->sp.penalized && s->cw.vocab < vocab) {
+    const size_t nb = (size_t)(vocab + CAND_CHUNK - 1) / CAND_CHUNK, n = 65 * nb * CAND_CMAX;
+    s->cw.ids = (int *)s->ar.alloc(n * 4);
+    s->cw.vals = (float *)s->ar.alloc(n * 4);
+    s->cw.cnt = (int *)s->ar.alloc(65 * nb * 4);
+    s->cw.vocab = vocab;
+    s->cw.rows = 65;
+  }
   if (!s->wide || s->ww.vocab >= vocab) return;
   const size_t n = (size_t)65 * vocab, nch = (vocab + WIDE_CHUNK - 1) / WIDE_CHUNK;
   s->ww.keyA = (uint32_t *)s->ar.alloc(n * 4);
@@ -1386,7 +1396,7 @@ static void dist_of_row(zl_sampler *s, zl_model *m, int row, const int32_t *hist
   ensure_scratch(s, m->cfg.vocab);
   const int keep = upload_hist(s, m->st, hist, nh);
   launch_dist_rows(m->logits + (size_t)row * m->cfg.vocab, m->cfg.vocab, 1, m->cfg.vocab, s->sp, keep ? s->dhist : nullptr, keep, 0,
-                   s->scratch, s->am, s->wide ? &s->ww : nullptr, out, m->st);
+                   s->scratch, s->am, s->wide ? &s->ww : nullptr, &s->cw, out, m->st);
 }
 
 // ---------------------------------------------------------------------------------------------- speculative cycle
@@ -1434,13 +1444,13 @@ static hipGraphExec_t cycle_graph(zl_model *T, zl_model *D, zl_sampler *s, int n
       hipLaunchKernelGGL(k_spec_reset, dim3(1), dim3(64), 0, cs, s->ss);
       enqueue_forward(D, nFeed, 1);
       for (int j = 0; j < kk; j++) {
-        launch_dist_rows(D->logits, D->cfg.vocab, 1, D->cfg.vocab, s->sp, nullptr, j, 0, s->scratch, s->am, s->wide ? &s->ww : nullptr, s->qdist + j, cs);
+        launch_dist_rows(D->logits, D->cfg.vocab, 1, D->cfg.vocab, s->sp, nullptr, j, 0, s->scratch, s->am, s->wide ? &s->ww : nullptr, &s->cw, s->qdist + j, cs);
         launch_draft_draw(s->qdist + j, s->ss, j, s->dstop, nStop, D->dstep, j == 0 ? nFeed : 1, T->dstep, s->dhist, 0, cs);
         if (j < kk - 1) enqueue_forward(D, 1, 1);
       }
     } else {
       enqueue_forward(T, kk + 1, 2);
-      launch_dist_rows(T->logits, T->cfg.vocab, kk + 1, T->cfg.vocab, s->sp, nullptr, 0, 1, s->scratch, s->am, s->wide ? &s->ww : nullptr, s->pdist, cs);
+      launch_dist_rows(T->logits, T->cfg.vocab, kk + 1, T->cfg.vocab, s->sp, nullptr, 0, 1, s->scratch, s->am, s->wide ? &s->ww : nullptr, &s->cw, s->pdist, cs);
       launch_accept(s->pdist, s->qdist, s->ss, greedy ? 1 : 0, cs);
     }
     ZL_HIP(hipGetLastError());
@@ -1530,7 +1540,7 @@ static void spec_cycle(zl_model *T, zl_model *D, zl_sampler *s, const int32_t *f
     posF = (int)D->tokens.size();
     if (D->hybrid) mark_rollback(D);  // draft.markRollback after feedLogits (src/model/speculative.js:168)
     for (int j = 0; j < kk; j++) {
-      launch_dist_rows(D->logits, D->cfg.vocab, 1, D->cfg.vocab, s->sp, dh, keep + j, 0, s->scratch, s->am, s->wide ? &s->ww : nullptr, s->qdist + j, st);
+      launch_dist_rows(D->logits, D->cfg.vocab, 1, D->cfg.vocab, s->sp, dh, keep + j, 0, s->scratch, s->am, s->wide ? &s->ww : nullptr, &s->cw, s->qdist + j, st);
       launch_draft_draw(s->qdist + j, s->ss, j, s->dstop, nStop, D->dstep, j == 0 ? lastChunk : 1, T->dstep, s->dhist, keep, st);
       if (j < kk - 1) launch_pass(D, 1, 1);
     }
@@ -1542,7 +1552,7 @@ static void spec_cycle(zl_model *T, zl_model *D, zl_sampler *s, const int32_t *f
       T->prevNoLogits = false;
     }
     launch_pass(T, kk + 1, 2);
-    launch_dist_rows(T->logits, T->cfg.vocab, kk + 1, T->cfg.vocab, s->sp, dh, keep, 1, s->scratch, s->am, s->wide ? &s->ww : nullptr, s->pdist, st);
+    launch_dist_rows(T->logits, T->cfg.vocab, kk + 1, T->cfg.vocab, s->sp, dh, keep, 1, s->scratch, s->am, s->wide ? &s->ww : nullptr, &s->cw, s->pdist, st);
     launch_accept(s->pdist, s->qdist, s->ss, (s->sp.temperature <= 0.0 || s->sp.greedyArgmax) ? 1 : 0, st);
   }
   ZL_HIP(hipEventRecord(e1, st));

@@ -7,6 +7,8 @@
 // and takes the same decisions as the reference given the same logits.
 #include "zl_kernels.h"
 
+#include <algorithm>
+
 namespace zl {
 
 // mulberry32 (src/util/rng.js:4-13)
@@ -51,6 +53,96 @@ __device__ int heap_topk(const float *l, int n, int k, int *ids, double *vals) {
 
 constexpr int DT = 1024;  // threads of the distribution kernel
 
+// The digit step of the radix select, on the 64 lanes of one wave: d = the largest digit whose keys, with those of all
+// larger digits, number at least rem (0 if there is none), which a scan from digit 255 down finds first; above = the
+// number of keys of the digits above d. Lane L holds digits 4L .. 4L + 3; the suffix counts are integer sums, so the
+// result is the scan's.
+__device__ inline void radix_digit(const uint32_t *hc, uint32_t rem, int lane, int &d, uint32_t &above) {
+  const uint32_t h0 = hc[4 * lane], h1 = hc[4 * lane + 1], h2 = hc[4 * lane + 2], h3 = hc[4 * lane + 3];
+  const uint32_t loc = h0 + h1 + h2 + h3;
+  uint32_t suf = loc;  // keys of the digits of lanes L' >= L
+  #pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t t = __shfl_down(suf, o, 64);
+    if (lane + o < 64) suf += t;
+  }
+  const uint32_t s3 = suf - loc + h3, s2 = s3 + h2, s1 = s2 + h1, s0 = s1 + h0;  // keys of digits >= 4L + 3 .. >= 4L
+  int c = (s0 >= rem) + (s1 >= rem) + (s2 >= rem) + (s3 >= rem);  // the digits that qualify are 0 .. d
+  #pragma unroll
+  for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+  d = c > 0 ? c - 1 : 0;
+  uint32_t a = (4 * lane > d ? h0 : 0u) + (4 * lane + 1 > d ? h1 : 0u) + (4 * lane + 2 > d ? h2 : 0u) +
+               (4 * lane + 3 > d ? h3 : 0u);
+  #pragma unroll
+  for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o, 64);
+  above = a;
+}
+
+// First stage of the two-stage selection: block (c, r) radix-selects the K-th largest key among logits
+// [c CAND_CHUNK, (c + 1) CAND_CHUNK) of row r and lists every logit at or above it (all of them when the block holds at
+// most K). Every logit of the row's top K is in its block's list (fewer than K logits of the row, hence of the block, lie
+// above it), and so is every logit equal to the row's K-th largest: the row's selection over the lists finds the same
+// K-th key, the same count of keys equal to it and the same candidates as over the whole row. A list longer than cmax
+// is reported by its count, and the row then selects over the whole row.
+constexpr int CT_T = 256;                   // threads of the candidate kernel (one per digit)
+constexpr int CT_PER = CAND_CHUNK / CT_T;   // logits per thread
+__global__ __launch_bounds__(CT_T) void k_topk_cand(const float *__restrict__ logits, int ldl, int vocab, int K,
+                                                  int cmax, CandWork cw) {
+  __shared__ uint32_t hc[256];
+  __shared__ uint32_t s_prefix, s_mask, s_rem;
+  __shared__ int s_n;
+  const int c = blockIdx.x, r = blockIdx.y, nb = gridDim.x, tid = threadIdx.x;
+  const int i0 = c * CAND_CHUNK, n = min(vocab - i0, CAND_CHUNK);
+  const float *l = logits + (long)r * ldl + i0;
+  float v[CT_PER];
+  uint32_t k[CT_PER];
+  #pragma unroll
+  for (int j = 0; j < CT_PER; j++) {
+    const int i = j * CT_T + tid;
+    v[j] = l[i < n ? i : 0];
+    k[j] = fkey(v[j]);
+  }
+  if (tid == 0) { s_prefix = 0; s_mask = 0; s_rem = (uint32_t)K; s_n = 0; }
+  __syncthreads();
+  if (n > K) {  // (uniform over the block)
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      hc[tid] = 0;
+      __syncthreads();
+      const uint32_t prefix = s_prefix, mask = s_mask;
+      #pragma unroll
+      for (int j = 0; j < CT_PER; j++)
+        if (j * CT_T + tid < n && (k[j] & mask) == prefix) atomicAdd(&hc[(k[j] >> shift) & 255u], 1u);
+      __syncthreads();
+      if (tid < 64) {
+        int d;
+        uint32_t above;
+        radix_digit(hc, s_rem, tid, d, above);
+        if (tid == 0) {
+          s_rem -= above;
+          s_prefix = prefix | ((uint32_t)d << shift);
+          s_mask = mask | (255u << shift);
+        }
+      }
+      __syncthreads();
+    }
+  }
+  const uint32_t T = n > K ? s_prefix : 0u;
+  const long base = ((long)r * nb + c) * cmax;
+  #pragma unroll
+  for (int j = 0; j < CT_PER; j++) {
+    const int i = j * CT_T + tid;
+    if (i < n && k[j] >= T) {
+      const int p = atomicAdd(&s_n, 1);
+      if (p < cmax) { cw.ids[base + p] = i0 + i; cw.vals[base + p] = v[j]; }
+    }
+  }
+  __syncthreads();
+  if (tid == 0) cw.cnt[r * nb + c] = s_n;
+}
+
+// Candidates of a row the distribution kernel gathers into LDS (more: it selects over the whole row).
+constexpr int CAND_LDS = 6144;
+
 // The row's logits copied to cp with the repetition / presence / frequency penalties of the last repeatLastN history ids
 // applied (src/sampling/sampler.js:96-110), in the reference's order (distinct ids in first-occurrence order). Every
 // thread of the block calls it.
@@ -80,8 +172,10 @@ __device__ void penalized_copy(const float *l, float *cp, int vocab, const Sampl
 }
 
 // distribution(logits row, history) for nrows rows (src/sampling/sampler.js:94-142).
+// cw.ids set: the first stage's lists of nb blocks per row (cmax entries each) to select from.
 __global__ __launch_bounds__(DT) void k_dist_rows(const float *__restrict__ logits, int ldl, int vocab, SamplerParams sp,
-                                                 const int *hist, int histLen0, int histInc, float *scratch, DevDist *out) {
+                                                 const int *hist, int histLen0, int histInc, float *scratch, CandWork cw,
+                                                 int nb, int cmax, DevDist *out) {
   __shared__ uint32_t hcount[256];
   __shared__ int s_ids[KCAP];
   __shared__ double s_vals[KCAP];
@@ -127,33 +221,90 @@ __global__ __launch_bounds__(DT) void k_dist_rows(const float *__restrict__ logi
     return;
   }
   const int K = sp.topK;
+  // ---- the first stage's candidates of this row into LDS, unless a list overflowed or they are too many
+  __shared__ float c_val[CAND_LDS];
+  __shared__ int c_id[CAND_LDS];
+  __shared__ int s_off[CAND_MAXB + 1];
+  __shared__ int s_cand;
+  bool cand = cw.ids != nullptr;
+  if (cand) {
+    if (tid < 64) {  // exclusive prefix of the blocks' counts, two blocks per lane
+      const int b0 = 2 * tid, b1 = 2 * tid + 1;
+      const int n0 = b0 < nb ? cw.cnt[r * nb + b0] : 0, n1 = b1 < nb ? cw.cnt[r * nb + b1] : 0;
+      int ovf = n0 > cmax || n1 > cmax;
+      const int loc = n0 + n1;
+      int inc = loc;
+      #pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(inc, o, 64);
+        if (tid >= o) inc += t;
+      }
+      if (b0 < nb) s_off[b0] = inc - loc;
+      if (b1 < nb) s_off[b1] = inc - loc + n0;
+      #pragma unroll
+      for (int o = 32; o > 0; o >>= 1) ovf |= __shfl_xor(ovf, o, 64);
+      const int total = __shfl(inc, 63, 64);
+      if (tid == 0) { s_off[nb] = total; s_cand = !ovf && total <= CAND_LDS; }
+    }
+    __syncthreads();
+    cand = s_cand;
+    if (cand) {
+      const int b = tid >> 3, q = tid & 7;  // eight threads per block's list, eight entries each in flight
+      if (b < nb) {
+        const int cn = s_off[b + 1] - s_off[b], dst = s_off[b];
+        const long src = ((long)r * nb + b) * cmax;
+        for (int j0 = q; j0 < cn; j0 += 64) {
+          float vv[8];
+          int ii[8];
+          #pragma unroll
+          for (int m = 0; m < 8; m++) {
+            const int j = j0 + 8 * m;
+            vv[m] = j < cn ? cw.vals[src + j] : 0.f;
+            ii[m] = j < cn ? cw.ids[src + j] : 0;
+          }
+          #pragma unroll
+          for (int m = 0; m < 8; m++) {
+            const int j = j0 + 8 * m;
+            if (j < cn) { c_val[dst + j] = vv[m]; c_id[dst + j] = ii[m]; }
+          }
+        }
+      }
+    }
+  }
+  const int NC = cand ? s_off[nb] : 0;
   // ---- radix select of the K-th largest key
   if (tid == 0) { s_prefix = 0; s_mask = 0; s_remaining = (uint32_t)K; }
   for (int shift = 24; shift >= 0; shift -= 8) {
     for (int i = tid; i < 256; i += DT) hcount[i] = 0;
     __syncthreads();
     const uint32_t prefix = s_prefix, mask = s_mask;
-    // 8 keys per thread requested at a time
-    for (int i0 = 0; i0 < vocab; i0 += 8 * DT) {
-      uint32_t kv[8];
-      #pragma unroll
-      for (int j = 0; j < 8; j++) { const int i = i0 + j * DT + tid; kv[j] = i < vocab ? fkey(l[i]) : 0u; }
-      #pragma unroll
-      for (int j = 0; j < 8; j++)
-        if (i0 + j * DT + tid < vocab && (kv[j] & mask) == prefix) atomicAdd(&hcount[(kv[j] >> shift) & 255u], 1u);
+    if (cand) {
+      for (int i = tid; i < NC; i += DT) {
+        const uint32_t kv = fkey(c_val[i]);
+        if ((kv & mask) == prefix) atomicAdd(&hcount[(kv >> shift) & 255u], 1u);
+      }
+    } else {
+      // 8 keys per thread requested at a time
+      for (int i0 = 0; i0 < vocab; i0 += 8 * DT) {
+        uint32_t kv[8];
+        #pragma unroll
+        for (int j = 0; j < 8; j++) { const int i = i0 + j * DT + tid; kv[j] = i < vocab ? fkey(l[i]) : 0u; }
+        #pragma unroll
+        for (int j = 0; j < 8; j++)
+          if (i0 + j * DT + tid < vocab && (kv[j] & mask) == prefix) atomicAdd(&hcount[(kv[j] >> shift) & 255u], 1u);
+      }
     }
     __syncthreads();
-    if (tid == 0) {
-      uint32_t rem = s_remaining, above = 0;
-      int d = 255;
-      for (; d > 0; d--) {
-        if (above + hcount[d] >= rem) break;
-        above += hcount[d];
+    if (tid < 64) {
+      int d;
+      uint32_t above;
+      radix_digit(hcount, s_remaining, tid, d, above);
+      if (tid == 0) {
+        s_remaining -= above;
+        s_eqcount = hcount[d];
+        s_prefix = prefix | ((uint32_t)d << shift);
+        s_mask = mask | (255u << shift);
       }
-      s_remaining = rem - above;
-      s_eqcount = hcount[d];
-      s_prefix = prefix | ((uint32_t)d << shift);
-      s_mask = mask | (255u << shift);
     }
     __syncthreads();
   }
@@ -161,7 +312,15 @@ __global__ __launch_bounds__(DT) void k_dist_rows(const float *__restrict__ logi
   const bool tie = s_eqcount != s_remaining;
   if (tid == 0) s_ncand = 0;
   __syncthreads();
-  if (!tie) {
+  if (!tie && cand) {
+    for (int i = tid; i < NC; i += DT) {
+      const float v = c_val[i];
+      if (fkey(v) >= T) {
+        const int p = atomicAdd(&s_ncand, 1);
+        if (p < KCAP) { s_ids[p] = c_id[i]; s_vals[p] = (double)v; }
+      }
+    }
+  } else if (!tie) {
     for (int i0 = 0; i0 < vocab; i0 += 8 * DT) {
       float v[8];
       #pragma unroll
@@ -566,8 +725,8 @@ void launch_set_wide(DevDist *d, int n, int vocab, int *ids, double *probs, int 
 }
 
 void launch_dist_rows(const float *logits, int ldl, int nrows, int vocab, const SamplerParams &sp, const int *hist,
-                      int histLen0, int histInc, float *scratch, const ArgmaxWork &aw, const WideWork *ww, DevDist *out,
-                      hipStream_t st) {
+                      int histLen0, int histInc, float *scratch, const ArgmaxWork &aw, const WideWork *ww,
+                      const CandWork *cw, DevDist *out, hipStream_t st) {
   const bool greedy = sp.temperature <= 0.0 || sp.greedyArgmax;
   const int nb = (vocab + AM_CHUNK - 1) / AM_CHUNK;
   if (greedy && !(sp.penalized && hist && histLen0 + (nrows - 1) * histInc > 0) && nb <= ARGMAX_MAX_BLOCKS &&
@@ -593,7 +752,17 @@ void launch_dist_rows(const float *logits, int ldl, int nrows, int vocab, const 
     ZL_HIP(hipGetLastError());
     return;
   }
-  hipLaunchKernelGGL(k_dist_rows, dim3(nrows), dim3(DT), 0, st, logits, ldl, vocab, sp, hist, histLen0, histInc, scratch, out);
+  // two stages (candidate lists of CAND_CHUNK-logit blocks, then the selection over them) where the work space fits;
+  // one block per row over the whole row otherwise
+  const int ncb = (vocab + CAND_CHUNK - 1) / CAND_CHUNK, cmax = std::min(sp.topK + CAND_SLACK, CAND_CMAX);
+  const bool two = !greedy && cw && !sp.penalized && sp.topK >= 1 && sp.topK <= KCAP && ncb <= CAND_MAXB &&
+                   cw->vocab >= vocab && cw->rows >= nrows;
+  if (two) {
+    hipLaunchKernelGGL(k_topk_cand, dim3(ncb, nrows), dim3(CT_T), 0, st, logits, ldl, vocab, sp.topK, cmax, *cw);
+    ZL_HIP(hipGetLastError());
+  }
+  hipLaunchKernelGGL(k_dist_rows, dim3(nrows), dim3(DT), 0, st, logits, ldl, vocab, sp, hist, histLen0, histInc, scratch,
+                     two ? *cw : CandWork{}, ncb, cmax, out);
   ZL_HIP(hipGetLastError());
 }
 
