@@ -350,28 +350,33 @@ __global__ __launch_bounds__(DT) void k_dist_rows(const float *__restrict__ logi
     o_ids[rank] = ii; o_vals[rank] = vi;
   }
   __syncthreads();
-  // ---- softmax with temperature, min-p, top-p (one lane, the reference's order)
+  // ---- softmax with temperature, min-p, top-p (one lane, the reference's order, on LDS; s_vals is free again), then the
+  // kept entries written out by all threads
+  __shared__ int s_keep;
+  double *pr = s_vals;
   if (tid == 0) {
     double mx = o_vals[0], sum = 0;
-    for (int i = 0; i < m; i++) { double pr = exp((o_vals[i] - mx) / sp.temperature); D->probs[i] = pr; sum += pr; }
-    for (int i = 0; i < m; i++) D->probs[i] = D->probs[i] / sum;
+    for (int i = 0; i < m; i++) { const double e = exp((o_vals[i] - mx) / sp.temperature); pr[i] = e; sum += e; }
+    for (int i = 0; i < m; i++) pr[i] = pr[i] / sum;
     int keep = m;
     if (sp.minP > 0) {
-      double thr = sp.minP * D->probs[0];
+      double thr = sp.minP * pr[0];
       keep = 1;
-      while (keep < m && D->probs[keep] >= thr) keep++;
+      while (keep < m && pr[keep] >= thr) keep++;
     }
     if (sp.topP < 1) {
       double c = 0;
       int i = 0;
-      while (i < keep) { c += D->probs[i]; i++; if (c >= sp.topP) break; }
+      while (i < keep) { c += pr[i]; i++; if (c >= sp.topP) break; }
       keep = i > 1 ? i : 1;
     }
     double total = 0;
-    for (int i = 0; i < keep; i++) total += D->probs[i];
-    for (int i = 0; i < keep; i++) D->ids[i] = o_ids[i];
+    for (int i = 0; i < keep; i++) total += pr[i];
+    s_keep = keep;
     D->n = keep; D->greedy = 0; D->total = total;
   }
+  __syncthreads();
+  for (int i = tid; i < s_keep; i += DT) { D->ids[i] = o_ids[i]; D->probs[i] = pr[i]; }
 }
 
 // Entry i of a distribution, from its fixed list or its full-list storage.
@@ -444,8 +449,92 @@ __global__ void k_draft_draw(const DevDist *dist, SpecState *ss, int j, const in
 
 // Acceptance (src/model/speculative.js:192-209): greedy compare, or accept with probability min(1, p/q) and on the first
 // rejection draw from the residual; when every draft is accepted the bonus token comes from the last row.
+// The fixed-list form of the acceptance (distributions of at most KCAP entries): the wave copies each distribution it
+// needs into LDS and finds q's probability of every entry of p in parallel; lane 0 then takes the same decisions in
+// the same order, with the same arithmetic, as the one-lane form below (prob_of, draw_residual, draw_dist).
+__device__ void accept_lists(const DevDist *pdist, const DevDist *qdist, SpecState *ss) {
+  __shared__ int pid[KCAP], qid[KCAP];
+  __shared__ double ppr[KCAP], qpr[KCAP], qat[KCAP];
+  __shared__ double s_px, s_qx;
+  const int lane = threadIdx.x;
+  auto stage = [&](const DevDist &d, int *ids, double *pr) {
+    for (int i = lane; i < d.n; i += 64) { ids[i] = d.ids[i]; pr[i] = d.probs[i]; }
+  };
+  uint32_t rng = ss->rng;  // every lane steps its own copy of the stream the same way
+  const int kk = ss->kk;
+  int a = 0, tok = -1;
+  for (int j = 0; j < kk; j++) {
+    const DevDist &P = pdist[j], &Q = qdist[j];
+    const int x = ss->drafted[j], pn = P.n, qn = Q.n;
+    stage(P, pid, ppr);
+    stage(Q, qid, qpr);
+    if (lane == 0) { s_px = 0.0; s_qx = 0.0; }
+    __syncthreads();
+    for (int i = lane; i < pn; i += 64) if (pid[i] == x) s_px = ppr[i] / P.total;  // ids of a list are distinct
+    for (int i = lane; i < qn; i += 64) if (qid[i] == x) s_qx = qpr[i] / Q.total;
+    __syncthreads();
+    if (rng_next(rng) * s_qx < s_px) { a++; __syncthreads(); continue; }
+    // rejected: the residual max(0, p - q) over p's entries
+    for (int i = lane; i < pn; i += 64) {
+      double v = 0.0;
+      for (int k = 0; k < qn; k++) if (qid[k] == pid[i]) { v = qpr[k] / Q.total; break; }
+      qat[i] = v;
+    }
+    __syncthreads();
+    if (lane == 0) {
+      double *res = ppr;  // each entry's residual replaces its probability once read
+      double sum = 0;
+      for (int i = 0; i < pn; i++) {
+        const double v = ppr[i] / P.total - qat[i];
+        res[i] = 0.0;
+        if (v > 0) { res[i] = v; sum += v; }
+      }
+      if (!(sum > 0)) {
+        tok = draw_dist(P, rng);
+      } else {
+        double r = rng_next(rng) * sum;
+        int last = 0;
+        tok = -1;
+        for (int i = 0; i < pn; i++) {
+          if (res[i] > 0) {
+            last = i;
+            r -= res[i];
+            if (r <= 0) { tok = pid[i]; break; }
+          }
+        }
+        if (tok < 0) tok = pid[last];
+      }
+    }
+    break;
+  }
+  if (a == kk) {  // (a is the same in every lane) the bonus draw from the last row, as draw_dist takes it
+    const DevDist &P = pdist[kk];
+    const int pn = P.n;
+    stage(P, pid, ppr);
+    __syncthreads();
+    if (lane == 0) {
+      if (P.greedy) {
+        tok = pid[0];
+      } else {
+        double r = rng_next(rng) * P.total;
+        tok = pid[pn - 1];
+        for (int i = 0; i < pn; i++) {
+          r -= ppr[i];
+          if (r <= 0) { tok = pid[i]; break; }
+        }
+      }
+    }
+  }
+  if (lane != 0) return;
+  ss->a = a;
+  ss->tok = tok;
+  ss->rng = rng;
+}
+
 __global__ void k_accept(const DevDist *pdist, const DevDist *qdist, SpecState *ss, int greedy) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  if (blockIdx.x != 0) return;
+  if (!greedy && !pdist[0].wids) { accept_lists(pdist, qdist, ss); return; }
+  if (threadIdx.x != 0) return;
   uint32_t rng = ss->rng;
   const int kk = ss->kk;
   int a = 0, tok = -1;
