@@ -183,6 +183,38 @@ def test_device_sampler_ties_match_oracle(gpu, tiny_files, tmp_path):
     m.close()
 
 
+def test_device_sampler_all_equal_logits_match_oracle(gpu, tiny_files, tmp_path):
+    """Every logit equal (an output head of identical rows): each 2048-logit block of the two-stage selection then holds
+    more ties at its k-th value than its candidate list, so the row is selected over the whole vocabulary, and the
+    reference's heap keeps the first k ids it met (topKSelect, src/sampling/sampler.js:21-43)."""
+    import shutil
+    from zerollm_amd import gguf as G
+    path = str(tmp_path / "flat_head.gguf")
+    shutil.copy(tiny_files[0], path)
+    t = G.read_gguf(path).require_tensor("output.weight")
+    rb, rows = G.row_size(t.type, t.dims[0]), t.dims[1]
+    with open(path, "r+b") as f:
+        f.seek(t.abs_offset)
+        row0 = f.read(rb)
+        f.seek(t.abs_offset)
+        f.write(row0 * rows)
+    m = Mdl.HipModel.load(path, ctx=64)
+    for cfg in [dict(temperature=0.8, top_k=40, top_p=1.0), dict(temperature=1.0, top_k=5, top_p=0.9)]:
+        ds = HipSampler(seed=3, **cfg)
+        hs = O.Sampler(seed=3, **cfg)
+        for tk in prompt(2, seed=4):
+            logits = m.forward(tk).copy()
+            assert np.all(logits == logits[0])
+            dd = ds.distribution(m, 0, [])
+            hd = hs.distribution(logits, [])
+            assert list(dd.ids) == list(hd.ids)
+            assert np.allclose(dd.probs, hd.probs, rtol=1e-14, atol=0)
+            assert ds.sample(m, 0, []) == hs.sample(logits, [])
+        ds.close()
+        m.reset()
+    m.close()
+
+
 @pytest.mark.parametrize("k", [1, 2, 4, 7])
 def test_greedy_speculative_equals_plain_greedy(gpu, tiny_files, k):
     """test/spec-generate.test.js:29-59: greedy speculative output is plain greedy output."""
