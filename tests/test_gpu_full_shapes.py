@@ -86,6 +86,29 @@ def test_c3_greedy_speculative_equals_plain_greedy(gpu, pair_8b):
     d.close()
 
 
+def test_sampler_at_the_full_vocabulary_matches_oracle(gpu, pair_8b):
+    """Sampled distributions over the 151,936 logits of the 0.6B-shaped draft against the oracle sampler on the same
+    logits: top_k 40 selects over the 75 blocks' candidate lists in LDS; top_k 200 and 256 have more candidates than
+    LDS holds and select over the whole row."""
+    d_spec = pair_8b[1]
+    print("case sampler at the full vocabulary", flush=True)
+    d = synth.build_on_device(d_spec, ctx=64, kv="f16")
+    for cfg in [dict(temperature=0.7, top_k=40, top_p=0.9), dict(temperature=1.0, top_k=200, top_p=1.0),
+                dict(temperature=1.2, top_k=256, top_p=0.95, min_p=0.01)]:
+        ds = HipSampler(seed=21, **cfg)
+        hs = O.Sampler(seed=21, **cfg)
+        for tk in synth.seeded_ids(3, 77, d_spec.vocab):
+            logits = d.forward(tk).copy()
+            dd = ds.distribution(d, 0, [])
+            hd = hs.distribution(logits, [])
+            assert list(dd.ids) == list(hd.ids)
+            assert np.allclose(dd.probs, hd.probs, rtol=1e-14, atol=0)
+            assert ds.sample(d, 0, []) == hs.sample(logits, [])
+        ds.close()
+        d.reset()
+    d.close()
+
+
 @pytest.mark.timeout(900)
 def test_c4_16k_context_verify_rollback_and_sampling(gpu, pair_8b):
     t_spec, d_spec = pair_8b
