@@ -1,4 +1,4 @@
-"""CPU BASELINE — benchmark and test infrastructure only (bench.py's cpu_baseline leg and tests/ use it; the product
+"""CPU baseline — benchmark and test infrastructure only (bench.py's cpu_baseline leg and tests/ use it; the product
 never imports it).
 
 SimdPoolModel: ctypes wrapper of oracle/pool_simd.c, a multi-threaded AVX-512 VNNI restatement of the reference's

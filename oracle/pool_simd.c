@@ -1,5 +1,5 @@
 /*
- * CPU BASELINE — benchmark and test infrastructure only (bench.py's cpu_baseline leg and tests/ use it; nothing in
+ * CPU baseline — benchmark and test infrastructure only (bench.py's cpu_baseline leg and tests/ use it; nothing in
  * zerollm_amd/ links or calls it). A multi-threaded AVX-512 VNNI restatement of the reference's worker-pool pass
  * (PoolModel.forwardBatch, src/compute/pool.js:145-160, run by every worker in src/compute/worker.js:278-445):
  *  - one SPMD region per pass (OpenMP threads = the pool's workers), barriers between the phases of a layer
