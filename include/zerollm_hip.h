@@ -122,7 +122,8 @@ int zl_model_logits(const zl_model *m, int row0, int nrows, float *host_out);
 /* ---------------------------------------------------------------------------------------------- synthetic models */
 /* One tensor of a synthetic model: values std * N(0,1) from stream `seed` (element (r, c) is deviate
  * r * src_cols + col0 + c), quantised with this library's quantisers into ggml type `type`; with fill = 1 a
- * constant F32 tensor of fill_value (norm weights); with fill = 2 an F32 tensor of fill_value + std * N(0,1).
+ * constant F32 tensor of fill_value (norm weights); with fill = 2 an F32 tensor of fill_value + std * N(0,1); with
+ * fill = 3 an F32 tensor of fill_value in its first src_cols elements and std in the rest (a two-level norm weight).
  * Mirrors the reference generators' role (tools/make-tiny-gguf.js:28-149, tools/make-synth-qwen35.js:30-60). */
 typedef struct {
   const char *name;
@@ -158,6 +159,9 @@ int zl_sampler_free(zl_sampler *s);
 /* mulberry32 state of the sampler's single random stream (src/util/rng.js:4-13). */
 int zl_sampler_get_rng(zl_sampler *s, uint32_t *state);
 int zl_sampler_set_rng(zl_sampler *s, uint32_t state);
+/* Diagnostic, no counterpart in the reference: the whole-cycle graphs this sampler holds. Freeing a model drops the
+ * graphs that captured it; past 64 graphs the cache starts over. */
+int zl_sampler_cycle_graphs(zl_sampler *s, int *n);
 /* sample(logits, history) = draw(distribution(...)) on logits row `row` of the model's last forward
  * (src/sampling/sampler.js:94-153). Only the id crosses to the host. */
 int zl_sample(zl_sampler *s, zl_model *m, int row, const int32_t *hist, int n_hist, int32_t *token);

@@ -133,9 +133,22 @@ def _check_gemv(type_, rows, cols, Ms, seed, raw=None):
 @pytest.mark.parametrize("type_", QTYPES)
 @pytest.mark.parametrize("cols", [512, 1024, 1536, 4096])
 def test_gemv_matches_oracle(gpu, type_, cols):
+    """1..9 tokens on the GEMV kernels, 10..64 on the GEMM (Q8_0, Q4_K, Q5_K, Q6_K: one launch of up to 64 tokens by
+    default); every token's row equals its single-token row bit for bit and the oracle's."""
     if cols % G.TYPE_INFO[type_][1]:
         pytest.skip("not a whole number of blocks")
-    _check_gemv(type_, 300, cols, [1, 2, 5, 9, 16, 17], seed=cols + type_)
+    _check_gemv(type_, 300, cols, [1, 2, 5, 9, 16, 17, 32, 33, 64], seed=cols + type_)
+
+
+@pytest.mark.parametrize("maxm", ["64", "48", "16", "0"])
+@pytest.mark.parametrize("type_", [G.Q8_0, G.Q4_K, G.Q5_K, G.Q6_K])
+def test_gemm_launch_widths_give_the_same_bits(gpu, monkeypatch, type_, maxm):
+    """The GEMM at every token-group count (ZEROLLM_GEMM_MAXM = 64: one launch of 64 tokens, four groups of 16; 48:
+    three groups; 16: one; 0: the GEMV kernels alone) gives the rows of single-token launches bit for bit, and the
+    oracle's."""
+    monkeypatch.setenv("ZEROLLM_GEMM_MAXM", maxm)
+    print(f"case gemm width {maxm} type {type_}", flush=True)
+    _check_gemv(type_, 200, 2048, [1, 10, 16, 31, 48, 64], seed=7 + type_)
 
 
 def float_raw(type_, rows, cols, seed):
@@ -181,19 +194,19 @@ C2_SHAPES = [(4096, 4096, G.Q4_K), (1024, 4096, G.Q4_K), (1024, 4096, G.Q6_K), (
 @pytest.mark.parametrize("N,K,type_", C2_SHAPES)
 def test_gemv_projection_shapes_synthetic(gpu, N, K, type_):
     """Projection shapes with this library's quantised N(0, 0.02) weights, at M = k + 1 in {1, 2, 5, 9, 17} and the
-    prefill chunk M = 16: the first and the last 96 rows against the oracle (M = 17 is two weight passes of 8 + 9 tokens,
-    M = 16 two of 8, on the matrix cores for Q4_K; the other rows are covered by the same kernels through the model
-    tests)."""
+    prefill chunks M = 16, 32, 64: the first and the last 96 rows against the oracle, every M's first row equal to the
+    single-token row bit for bit (M = 16, 17, 32 and 64 are one GEMM launch each; the other rows are covered by the same
+    kernels through the model tests)."""
     t = synth.TensorSpec("w", type_, N, K, seed=99 + N, std=0.02)
     raw = synth.tensor_bytes(t, use_device=True)
     print(f"case gemv {N}x{K} type {type_}", flush=True)
     m = Mat(type_, raw, N, K)
-    X = np.random.default_rng(N).normal(0, 1, (17, K)).astype(np.float32)
+    X = np.random.default_rng(N).normal(0, 1, (64, K)).astype(np.float32)
     rows = 96
     rb = G.row_size(type_, K)
     heads = [(0, raw[:rows * rb]), (N - rows, raw[(N - rows) * rb:])]
-    want = {r0: np.stack([O.matvec(type_, sub, rows, K, X[i]) for i in range(17)]) for r0, sub in heads}
-    for M in (1, 2, 5, 9, 16, 17):
+    want = {r0: np.stack([O.matvec(type_, sub, rows, K, X[i]) for i in range(64)]) for r0, sub in heads}
+    for M in (1, 2, 5, 9, 16, 17, 32, 64):
         y = m.gemv(X[:M])
         for r0, _ in heads:
             got, w = y[:, r0:r0 + rows], want[r0][:M]

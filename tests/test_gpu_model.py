@@ -282,7 +282,7 @@ def test_stop_token_and_limits(gpu, tiny_files):
         x.close()
 
 
-def test_sampled_speculative_is_reproducible_and_uses_target_distribution(gpu, tiny_files):
+def test_sampled_speculative_is_reproducible(gpu, tiny_files):
     p = prompt(32, seed=11)
     runs = []
     for _ in range(2):
@@ -317,18 +317,24 @@ def test_long_context_attention_matches_oracle(gpu, tiny_files):
 
 @pytest.mark.parametrize("kv", ["f16", "f32"])
 def test_per_head_weighted_sum_equals_slice_form_and_oracle(gpu, tiny_files, monkeypatch, kv):
-    """The per-head weighted sum (softmax row in the scores buffer, probabilities staged with V; passes of several
-    tokens at contexts beyond 8192 positions take it) forced at a 1300-position context (ZEROLLM_ATTN_HEAD_CTX=1024):
-    its batched rows equal the single-token passes (which keep the slice form) bit for bit, and the oracle's logits."""
+    """The long-context weighted sums forced at a 1300-position context, each against the slice form (k_attn_av) and
+    the oracle:
+    - "grouped": ZEROLLM_ATTN_HEAD_CTX=1024 sends passes of several tokens to k_attn_softmax_rows + k_attn_av_group
+      (single-token passes keep k_attn_av);
+    - "head": ZEROLLM_ATTN_HEAD1_CTX=1024 in addition sends single-token passes to the per-head kernel k_attn_av_head
+      (what single-token passes take beyond ~29,900 positions).
+    In every form the batched rows equal the single-token passes bit for bit, and the rows equal the slice form's."""
     toks = prompt(1210, seed=19)
     ref = O.OracleModel(tiny_files[0], ctx=1300, kv=kv)
     for t in toks[:-6]:
         ref.forward(t, logits=False)
     want = np.stack([ref.forward(t) for t in toks[-6:]])
     rows = {}
-    for form in ("slice", "head"):
-        if form == "head":
+    for form in ("slice", "grouped", "head"):
+        if form == "grouped":
             monkeypatch.setenv("ZEROLLM_ATTN_HEAD_CTX", "1024")
+        if form == "head":
+            monkeypatch.setenv("ZEROLLM_ATTN_HEAD1_CTX", "1024")
         print(f"case weighted sum {form} kv {kv}", flush=True)
         m = Mdl.HipModel.load(tiny_files[0], ctx=1300, kv=kv)
         for i in range(0, 1200, 16):
@@ -340,7 +346,8 @@ def test_per_head_weighted_sum_equals_slice_form_and_oracle(gpu, tiny_files, mon
         m.close()
         assert (single.view(np.uint32) == batched.view(np.uint32)).all(), form
         rows[form] = single
-    assert (rows["head"].view(np.uint32) == rows["slice"].view(np.uint32)).all()
+    for form in ("grouped", "head"):
+        assert (rows[form].view(np.uint32) == rows["slice"].view(np.uint32)).all(), form
     exact = np.mean(rows["head"].view(np.uint32) == want.view(np.uint32))
     assert exact >= 0.999 and np.abs(rows["head"] - want).max() <= 1e-6 * np.abs(want).max(), exact
 

@@ -147,3 +147,30 @@ def test_whole_cycle_graph_equals_launch_by_launch_cycle(gpu, close_files, monke
     log = runs[0][1]
     assert any(a == kk for kk, _, a, _ in log) and any(a < kk for kk, _, a, _ in log), \
         "the run has cycles after a full acceptance (two fed tokens) and after a rejection (one)"
+
+
+def test_freeing_a_model_drops_its_cycle_graphs(gpu, close_files):
+    """The whole-cycle graphs a sampler caches capture the models' buffers: freeing either model drops the entries
+    that captured it, and a new pair starts its own."""
+    import ctypes as C
+
+    from zerollm_amd._lib import call
+
+    def cached(s):
+        n = C.c_int()
+        call("zl_sampler_cycle_graphs", s._h, C.byref(n))
+        return n.value
+
+    prompt = _prompt(20, 5)
+    s = HipSampler(argmax=True)
+    for rnd in range(2):
+        print(f"case cycle graph cache pair {rnd}", flush=True)
+        t = Mdl.HipModel.load(close_files[0], ctx=256, kv="f16")
+        d = Mdl.HipModel.load(close_files[1], ctx=256, kv="f16")
+        out = list(generate_speculative(t, d, prompt, k=4, max_tokens=12, sample=s))
+        assert len(out) == 12
+        assert cached(s) > 0
+        d.close()
+        assert cached(s) == 0, "the draft's graphs are gone"
+        t.close()
+    s.close()

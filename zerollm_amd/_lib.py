@@ -92,6 +92,7 @@ SIGNATURES = [
     ("zl_sampler_free", C.c_int, [P]),
     ("zl_sampler_get_rng", C.c_int, [P, C.POINTER(C.c_uint32)]),
     ("zl_sampler_set_rng", C.c_int, [P, C.c_uint32]),
+    ("zl_sampler_cycle_graphs", C.c_int, [P, C.POINTER(C.c_int)]),
     ("zl_sample", C.c_int, [P, P, C.c_int, I32P, C.c_int, I32P]),
     ("zl_distribution", C.c_int, [P, P, C.c_int, I32P, C.c_int, I32P, F64P, C.c_int, C.POINTER(C.c_int), F64P, C.POINTER(C.c_int)]),
     ("zl_spec_cycle", C.c_int, [P, P, P, I32P, C.c_int, C.c_int32, C.c_int, I32P, C.c_int, I32P, C.c_int, C.POINTER(zl_spec_result)]),

@@ -9,7 +9,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 SOURCES = ["zl_attn.hip", "zl_delta.hip", "zl_gemv_q4k.hip", "zl_gemv_q6k.hip", "zl_gemv_q8.hip", "zl_gemv_q40.hip", "zl_gemv_q50.hip", "zl_gemv_q5k.hip",
-           "zl_gemv_mfma.hip", "zl_gemv_rg.hip", "zl_gemv.hip", "zl_kernels.hip", "zl_sample.hip", "zl_runtime.cpp", "gguf.cpp"]
+           "zl_gemv_mfma.hip", "zl_gemm_q4k.hip", "zl_gemm_q5k.hip", "zl_gemm_q6k.hip", "zl_gemm_q8.hip", "zl_gemv_rg.hip", "zl_gemv.hip", "zl_kernels.hip", "zl_sample.hip", "zl_runtime.cpp", "gguf.cpp"]
 LIB = os.path.join(HERE, "libzerollm_hip.so")
 
 # -ffp-contract=off: every f64/f32 step rounds where the reference's arithmetic rounds; fusions are explicit fma().

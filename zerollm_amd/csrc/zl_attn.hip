@@ -8,6 +8,8 @@
 // Scores live in a [token][head][ctx] f32 buffer between the two. The weighted sum keeps the reference's f32 rounding
 // after every position: a random-weight network turns a 1e-7 change there into a visible logit difference.
 #include "zl_kernels.h"
+#include <algorithm>
+#include <climits>
 
 namespace zl {
 
@@ -944,14 +946,22 @@ size_t attention_lds(int ctx, int rowb) {
   return (size_t)((ctx + AV_UNIT - 1) / AV_UNIT * AV_UNIT) * 4 + 2 * (size_t)AV_DIMS * (rowb + 16);
 }
 size_t attention_lds(int ctx) { return attention_lds(ctx, AV_ROW); }
-// Contexts above AVH_CTX positions take the per-head weighted sum (heads of at most 128 dimensions), whose LDS does not
-// depend on the context; ZEROLLM_ATTN_HEAD_CTX overrides the threshold (tests).
-bool attention_head_form(int ctx, int hd) {
-  const char *e = getenv("ZEROLLM_ATTN_HEAD_CTX");
-  const int thr = e ? atoi(e) : AVH_CTX;
-  return hd <= 128 && ctx > thr;
-}
 constexpr size_t ATTN_LDS_MAX = 150 * 1024;
+
+// Contexts above AVH_CTX positions take the per-head weighted sum (heads of at most 128 dimensions), whose LDS does not
+// depend on the context, for passes of several tokens; single-token passes keep the slice form wherever its softmax
+// row fits LDS. ZEROLLM_ATTN_HEAD_CTX / ZEROLLM_ATTN_HEAD1_CTX override the two thresholds (tests). Read once per model.
+AttnForm attention_form(int ctx, int hd) {
+  const char *e = getenv("ZEROLLM_ATTN_HEAD_CTX"), *e1 = getenv("ZEROLLM_ATTN_HEAD1_CTX");
+  AttnForm f;
+  f.headCtx = hd > 128 ? INT_MAX : e ? atoi(e) : AVH_CTX;
+  // single-token passes: the per-head form once the slice form's LDS no longer holds the row
+  int fit = 0;
+  while (fit < ctx && attention_lds(fit + AV_UNIT) <= ATTN_LDS_MAX) fit += AV_UNIT;
+  f.head1Ctx = hd > 128 ? INT_MAX : e1 ? atoi(e1) : std::max(f.headCtx, fit);
+  f.split = ctx > f.headCtx ? false : attention_lds(ctx) > ATTN_LDS_MAX;
+  return f;
+}
 
 template <int HD, bool F16KV>
 static void launch_scores_k(const AttnArgs &a, dim3 grid, int B, hipStream_t st) {
@@ -992,7 +1002,7 @@ void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
   AttnArgs a = a0;
   // the per-head form for passes of several tokens at long contexts (single-token passes keep the four slice blocks
   // per head, which stage a quarter of the rows each, wherever their softmax row fits LDS); both give the same bits
-  const bool head = !a.part && attention_head_form(a.ctx, a.hd) && (B > 1 || attention_lds(a.ctx) > ATTN_LDS_MAX);
+  const bool head = !a.part && a.ctx > (B > 1 ? a.headCtx : a.head1Ctx);
   const size_t lds = a.part ? attention_split_lds(a.hd, a.kvF16) : head ? attention_head_lds(a.hd) : attention_lds(a.ctx);
   ZL_REQUIRE(lds <= ATTN_LDS_MAX, ZL_ERR_UNSUPPORTED, "context too long for the attention kernel");
   ZL_REQUIRE(!a.part || a.nch * ATTN_SPLIT_C >= a.ctx, ZL_ERR_ARG, "attention: split partials below the context");

@@ -194,13 +194,13 @@ __global__ __launch_bounds__(DELTA_LPR * DELTA_ROWS) void k_deltanet(const Delta
 
   // ---- the head's last workgroup to arrive continues with the whole head
   if constexpr (R > 1) {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores are complete
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    // the workgroup's exchange stores happen before its arrival (barrier), the arrival releases them at agent scope,
+    // and the last workgroup to arrive acquires every other workgroup's before it reads them
     __syncthreads();
-    if (tid == 0) last = __hip_atomic_fetch_add(a.xcnt + hv, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(R - 1);
+    if (tid == 0) last = __hip_atomic_fetch_add(a.xcnt + hv, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(R - 1);
     __syncthreads();
     if (!last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (tid == 0) __hip_atomic_store(a.xcnt + hv, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     constexpr int XJ = (DELTA_MAX_B * D + NT - 1) / NT;
     float xv[XJ];

@@ -68,6 +68,29 @@ void gemv_shape(int ntiles, int nslab, bool swiglu, int *ks, int *nw) {
   *nw = swiglu ? 2 * w : w;  // a gate/up pair: w waves per matrix
 }
 
+// Tokens per GEMM launch (ZEROLLM_GEMM_MAXM, read when a launch is enqueued, so a captured graph keeps the value of its
+// capture; below GEMM_MIN_M every launch stays on the GEMV kernels in chunks of at most GEMV_MAX_MT tokens: the same
+// bits, more weight passes). Default 64, one launch per prefill chunk: measured against two launches of 32 (whose
+// sums fit a wave's registers, where 64 tokens spill a few), 16K-token prefill 6.47 -> 6.21 s (target), 2.69 -> 2.32 s
+// (draft).
+static int gemm_max_m() {
+  const char *e = getenv("ZEROLLM_GEMM_MAXM");
+  const int m = e ? atoi(e) : 64;
+  return m < GEMM_MIN_M ? 0 : std::min(m, 64);
+}
+
+// Launches of at least GEMM_MIN_M tokens of the formats the GEMM takes, without a fused prologue.
+bool gemm_takes(const GemvArgs &a) {
+  const int t = a.seg[0].m.type;
+  return gemm_max_m() > 0 && a.M >= GEMM_MIN_M && !a.xf && (t == T_Q8_0 || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K);
+}
+
+long gemv_part_need(const GemvArgs &a) {
+  if (a.ks == 1) return 0;
+  if (gemm_takes(a)) return (long)a.ntiles * a.ks * 2 * 16 * ((std::min(a.M, gemm_max_m()) + 15) / 16) * 64;
+  return (long)a.ntiles * a.ks * 2 * GEMV_MAX_MT * 64;
+}
+
 void launch_gemv(const GemvArgs &a0, int epi, const float *xf, int ldx, hipStream_t st) {
   const int fmt = a0.seg[0].m.type;
   for (int i = 1; i < a0.nseg; i++)
@@ -83,19 +106,20 @@ void launch_gemv(const GemvArgs &a0, int epi, const float *xf, int ldx, hipStrea
     return;
   }
   ZL_REQUIRE(a0.ks >= 1 && a0.ntiles >= 1, ZL_ERR_ARG, "gemv: bad launch shape");
-  ZL_REQUIRE(a0.ks == 1 || (a0.part && a0.cnt && a0.ntiles <= GEMV_CNT_TILES &&
-                            (long)a0.ntiles * a0.ks * 2 * GEMV_MAX_MT * 64 <= GEMV_PART_DOUBLES),
+  ZL_REQUIRE(a0.ks == 1 || (a0.part && a0.cnt && a0.ntiles <= GEMV_CNT_TILES && gemv_part_need(a0) <= GEMV_PART_DOUBLES),
              ZL_ERR_ARG, "gemv: split-K work space missing or too small");
   ZL_REQUIRE(a0.act.q && a0.act.ra && a0.act.rb && a0.act.rc && a0.act.ld % 64 == 0 && a0.act.ld >= a0.nslab * 64,
              ZL_ERR_ARG, "gemv: activation records missing");
-  // as few weight passes as chunks of at most GEMV_MAX_MT tokens allow, with the tokens spread evenly over them (16
-  // prefill tokens: two passes of 8, which a Q4_K matrix runs on the matrix cores); every input and output row is
-  // addressed from offset pointers, and the results do not depend on the chunking
-  const int nch = (a0.M + GEMV_MAX_MT - 1) / GEMV_MAX_MT;
+  // as few weight passes as chunks of at most 64 (GEMM) or GEMV_MAX_MT tokens allow, with the tokens spread evenly
+  // over them; every input and output row is addressed from offset pointers, and the results do not depend on the
+  // chunking
+  const bool gemm = gemm_takes(a0);
+  const int cap = gemm ? gemm_max_m() : GEMV_MAX_MT;
+  const int nch = (a0.M + cap - 1) / cap;
   for (int c = 0, t0 = 0; c < nch; c++) {
     GemvArgs b = a0;
     b.M = (a0.M - t0) / (nch - c);  // the remaining tokens over the remaining chunks, the larger chunks last
-    ZL_REQUIRE(b.M >= 1 && b.M <= GEMV_MAX_MT, ZL_ERR_ARG, "gemv: bad token chunk");
+    ZL_REQUIRE(b.M >= 1 && b.M <= cap, ZL_ERR_ARG, "gemv: bad token chunk");
     if (t0) {
       b.act = act_rows(a0.act, t0);
       for (int i = 0; i < b.nseg; i++) if (b.seg[i].out) b.seg[i].out += (long)t0 * b.seg[i].ldo;
@@ -105,6 +129,16 @@ void launch_gemv(const GemvArgs &a0, int epi, const float *xf, int ldx, hipStrea
       b.xrow0 += t0;  // fused prologue: the chunk's own input rows
     }
     t0 += b.M;
+    if (gemm) {  // every weight read once for all the chunk's tokens, on the matrix cores; same results
+      switch (fmt) {
+        case T_Q8_0: launch_gemm_fmt<T_Q8_0>(b, epi, st); break;
+        case T_Q4_K: launch_gemm_fmt<T_Q4_K>(b, epi, st); break;
+        case T_Q5_K: launch_gemm_fmt<T_Q5_K>(b, epi, st); break;
+        default: launch_gemm_fmt<T_Q6_K>(b, epi, st); break;
+      }
+      ZL_HIP(hipGetLastError());
+      continue;
+    }
     if (gemv_mfma_ok(b)) {  // Q4_K and Q8_0 at 2..8 tokens: the int8 dots on the matrix cores, same results
       launch_gemv_mfma(b, epi, st);
       ZL_HIP(hipGetLastError());

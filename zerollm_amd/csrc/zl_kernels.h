@@ -132,6 +132,9 @@ struct AttnArgs {
   double *part;
   int nch;              // chunks per (token, head) row of part
   double *pinv;         // [token][head] 1 / sum of a row's exponentials (grouped weighted sum of long multi-token passes)
+  // contexts above headCtx take the per-head / grouped weighted sum for passes of several tokens, contexts above
+  // head1Ctx also for single-token passes (decided once per model when it is loaded: attention_form)
+  int headCtx, head1Ctx;
 };
 constexpr int ATTN_SPLIT_C = 256;  // positions per chunk of the position-split weighted sum
 
@@ -183,6 +186,14 @@ bool gemv_rg_ok(const GemvArgs &a);
 void launch_gemv_rg(const GemvArgs &a, int epi, hipStream_t st);
 template <int FMT>
 void launch_gemv_fmt(const GemvArgs &a, int epi, hipStream_t st);
+constexpr int GEMM_MIN_M = 10;  // launches of at least this many tokens take the GEMM (zl_gemm.h)
+// GEMM of 10..64 tokens (zl_gemm.h): Q8_0, Q4_K, Q5_K and Q6_K, every weight read once for all the launch's tokens,
+// the same bits per token as the GEMV kernels.
+template <int FMT>
+void launch_gemm_fmt(const GemvArgs &a, int epi, hipStream_t st);
+// Whether launch_gemv runs a launch of a.M tokens on the GEMM, and the split-K partial sums (doubles) a launch needs.
+bool gemm_takes(const GemvArgs &a);
+long gemv_part_need(const GemvArgs &a);
 
 // quantizeAct of one 32-value block (src/compute/ref-kernels.js:44-62) held by 32 consecutive lanes: d = amax/127 (f64,
 // stored f32), q = round-half-away(v * (1/d)). Every lane gets its q; the block's first lane (i & 31 == 0) also gets
@@ -269,7 +280,11 @@ __device__ inline double rms_scale256(const float *xr, int n, double eps, int ti
 void launch_attention(const AttnArgs &a, int B, hipStream_t st);
 size_t attention_lds(int ctx);
 size_t attention_split_lds(int hd, int kvF16);
-bool attention_head_form(int ctx, int hd);
+// The attention form of a model, decided once at load from its context and head size (the environment overrides
+// ZEROLLM_ATTN_HEAD_CTX and ZEROLLM_ATTN_HEAD1_CTX move the thresholds, for tests): headCtx / head1Ctx as in AttnArgs
+// (INT_MAX: never), split = whether the model needs the position-split weighted sum (its exact chain would not fit).
+struct AttnForm { int headCtx, head1Ctx; bool split; };
+AttnForm attention_form(int ctx, int hd);
 void launch_norm_quant(const float *x, int ldx, int row0, int nrows, const float *w, double eps, int n, int npad,
                        const Act &act, hipStream_t st);
 void launch_embed(const MatView &m, const Step *step, int B, float *x, int ldx, hipStream_t st);

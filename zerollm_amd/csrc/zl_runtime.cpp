@@ -231,6 +231,7 @@ struct zl_model {
   double *attnPart = nullptr;  // position-split weighted-sum partials (contexts beyond ZEROLLM_ATTN_EXACT_CTX), or null
   double *attnInv = nullptr;   // [maxBatch][n_head] 1 / sum of exponentials (grouped weighted sum)
   int attnNch = 0;
+  int attnHeadCtx = 0, attnHead1Ctx = 0;  // the attention form's thresholds, decided at load (attention_form)
   zl::Act act{};    // quantised input of the q/k/v, attention-output and gate/up GEMVs
   zl::Act act2{};   // quantised FFN hidden state (written by the gate/up GEMV, read by the down GEMV)
   zl::GemvWork gw{};
@@ -293,7 +294,30 @@ struct zl_mat {
   }
 };
 
+// Live samplers, so that freeing a model can drop the cycle graphs that captured its buffers.
+static std::mutex g_samplers_mu;
+static std::set<zl_sampler *> g_samplers;
+constexpr size_t CYCLE_GRAPHS_MAX = 64;  // cached cycle graphs per sampler; beyond it the cache starts over
+
+static void drop_cycles(zl_sampler *s, uint64_t uid) {  // uid 0: every entry
+  if (s->st) hipStreamSynchronize(s->st);
+  if (s->cst) hipStreamSynchronize(s->cst);
+  for (auto it = s->cycles.begin(); it != s->cycles.end();) {
+    if (uid == 0 || std::get<0>(it->first) == uid || std::get<1>(it->first) == uid) {
+      hipGraphExecDestroy(it->second.first);
+      hipGraphDestroy(it->second.second);
+      it = s->cycles.erase(it);
+    } else {
+      ++it;
+    }
+  }
+}
+
 zl_model::~zl_model() {
+  {
+    std::lock_guard<std::mutex> lk(g_samplers_mu);
+    for (zl_sampler *s : g_samplers) drop_cycles(s, uid);
+  }
   if (st) hipStreamSynchronize(st);
   for (auto &g : graphs) hipGraphExecDestroy(g.second);
   for (auto &g : graphDefs) hipGraphDestroy(g.second);
@@ -303,6 +327,10 @@ zl_model::~zl_model() {
 }
 
 zl_sampler::~zl_sampler() {
+  {
+    std::lock_guard<std::mutex> lk(g_samplers_mu);
+    g_samplers.erase(this);
+  }
   if (st) hipStreamSynchronize(st);
   for (auto &c : cycles) { hipGraphExecDestroy(c.second.first); hipGraphDestroy(c.second.second); }
   if (cst) hipStreamDestroy(cst);
@@ -381,8 +409,10 @@ static void finish_model(zl_model *m, const float *ropeFreqs) {
   // sums, online-softmax merge): more accurate than the chain, but not its bits, and on random-weight models the
   // difference is amplified through the int8 activation quantisation (see the split-path tests).
   const char *ex = getenv("ZEROLLM_ATTN_EXACT_CTX");
-  const bool split = (!attention_head_form(m->ctx, c.head_dim) && attention_lds(m->ctx) > 150 * 1024) ||
-                     (ex && m->ctx > atoi(ex));
+  const AttnForm form = attention_form(m->ctx, c.head_dim);
+  const bool split = form.split || (ex && m->ctx > atoi(ex));
+  m->attnHeadCtx = form.headCtx;
+  m->attnHead1Ctx = form.head1Ctx;
   const int half = c.n_rot / 2;
   // RoPE tables exactly as ropeTables (src/compute/ref-kernels.js:329-342), in f64 on the host, stored f32
   std::vector<float> cs((size_t)m->ctx * half), sn((size_t)m->ctx * half);
@@ -679,6 +709,7 @@ static void enqueue_forward(zl_model *m, int B, int want) {
       aa.qhs = m->hybrid ? 2 * c.head_dim : c.head_dim;
       aa.gate = m->hybrid ? m->q + c.head_dim : nullptr;
       aa.part = m->attnPart; aa.nch = m->attnNch; aa.pinv = m->attnInv;
+      aa.headCtx = m->attnHeadCtx; aa.head1Ctx = m->attnHead1Ctx;
       launch_attention(aa, B, m->st);
       gemv_group(m, {{&L.wo, nullptr, 0, nullptr}}, B, EPI_RESID, m->act, m->act.f, m->act.ld);
     }
@@ -1230,7 +1261,7 @@ static zl_model *build_synth(const zl_config *cfg, const zl_synth_tensor *ts, in
     const zl_synth_tensor &t = req(nm);
     ZL_REQUIRE(t.rows * t.cols == len, ZL_ERR_ARG, "synthetic vector " + nm + " has unexpected length");
     if (t.fill == 1) return upload_vec(m.get(), std::vector<float>(len, t.fill_value));
-    if (t.fill == 2) {
+    if (t.fill == 2 || t.fill == 3) {
       std::vector<float> v(len);
       const int rc = zl_synth_tensor_bytes(&t, 0, v.data());
       ZL_REQUIRE(rc == ZL_OK, rc, "synthetic vector " + nm + ": " + g_err);
@@ -1429,8 +1460,12 @@ static hipGraphExec_t capture_graph(hipStream_t cs, F &&body, hipGraph_t *def) {
 // models (whose rollback bookkeeping is host logic) take the launch-by-launch cycle.
 static hipGraphExec_t cycle_graph(zl_model *T, zl_model *D, zl_sampler *s, int nFeed, int kk, int nStop, int phase) {
   const auto key = std::make_tuple(T->uid, D->uid, nFeed, kk, nStop, phase);
-  auto it = s->cycles.find(key);
-  if (it != s->cycles.end()) return it->second.first;
+  {
+    std::lock_guard<std::mutex> lk(g_samplers_mu);  // a model freed on another thread drops entries under this lock
+    auto it = s->cycles.find(key);
+    if (it != s->cycles.end()) return it->second.first;
+    if (s->cycles.size() >= CYCLE_GRAPHS_MAX) drop_cycles(s, 0);
+  }
   if (!s->cst) ZL_HIP(hipStreamCreateWithFlags(&s->cst, hipStreamNonBlocking));
   hipStream_t cs = s->cst;
   hipStream_t ts = T->st, dsv = D->st;
@@ -1455,6 +1490,7 @@ static hipGraphExec_t cycle_graph(zl_model *T, zl_model *D, zl_sampler *s, int n
     }
     ZL_HIP(hipGetLastError());
   }, &def);
+  std::lock_guard<std::mutex> lk(g_samplers_mu);
   s->cycles[key] = {ex, def};
   return ex;
 }
@@ -1659,8 +1695,7 @@ static void mat_gemv_noalloc(zl_mat *m, const float *x, int M, float *y, hipStre
   gw.cnt = (uint32_t *)(b + NOALLOC_OFF_CNT);
   const SegSpec seg{&mm, y, mm.rows, nullptr};
   GemvArgs a = gemv_args(&seg, 1, M, EPI_STORE, act, gw);
-  ZL_REQUIRE(a.ks == 1 || (a.ntiles <= GEMV_CNT_TILES &&
-                           (size_t)a.ntiles * a.ks * 2 * GEMV_MAX_MT * 64 <= NOALLOC_PART_DOUBLES),
+  ZL_REQUIRE(a.ks == 1 || (a.ntiles <= GEMV_CNT_TILES && (size_t)gemv_part_need(a) <= NOALLOC_PART_DOUBLES),
              ZL_ERR_ARG, "zl_mat_gemv_noalloc: this matrix's split-K partial sums exceed the static work space");
   if (use_rg() && M == 1 && mm.type == T_Q8_0 && mm.nslab <= 48) {  // the probe's single-token path (no quantisation pass)
     a.xf = x; a.ldxf = mm.cols; a.xrow0 = 0; a.n = mm.cols; a.nw = nullptr; a.eps = 0.0;
@@ -1862,6 +1897,10 @@ int zl_synth_tensor_bytes(const zl_synth_tensor *t, int use_device, void *host_o
     for (int64_t i = 0; i < t->rows * t->cols; i++) ((float *)host_out)[i] = t->fill_value;
     return ZL_OK;
   }
+  if (t->fill == 3) {
+    for (int64_t i = 0; i < t->rows * t->cols; i++) ((float *)host_out)[i] = i < t->src_cols ? t->fill_value : (float)t->std;
+    return ZL_OK;
+  }
   ZL_REQUIRE(t->fill == 0 || (t->fill == 2 && t->type == T_F32), ZL_ERR_ARG, "fill 2 (offset normal values) needs type F32");
   const int bv = zl_synth::block_values(t->type), bb = zl_synth::block_bytes(t->type);
   ZL_REQUIRE(bv > 0 && t->cols % bv == 0, ZL_ERR_UNSUPPORTED, "unsupported synthetic tensor type/shape");
@@ -1902,6 +1941,16 @@ int zl_sampler_create(const zl_sampler_opts *opts, zl_sampler **out) {
              "repeat_last_n must be 0..64 on the GPU sampler");
   ensure_init();
   *out = new_sampler(opts);
+  std::lock_guard<std::mutex> lk(g_samplers_mu);
+  g_samplers.insert(*out);
+  ZL_API_END
+}
+
+int zl_sampler_cycle_graphs(zl_sampler *s, int *n) {
+  ZL_API_BEGIN
+  ZL_REQUIRE(s && n, ZL_ERR_ARG, "null argument");
+  std::lock_guard<std::mutex> lk(g_samplers_mu);
+  *n = (int)s->cycles.size();
   ZL_API_END
 }
 

@@ -64,10 +64,14 @@ def generate_speculative(target, draft, prompt_ids, k=4, max_tokens=256, sample=
                                    "tokensPerCycle": 0.0, "cycleMs": 0.0, "draftMs": 0.0, "verifyMs": 0.0, "otherMs": 0.0,
                                    "acceptedHist": [0] * (k_max + 1), "draftCachedTokens": d_reuse, "draftPrefillMs": 0.0}
     t0 = time.perf_counter()
-    _, aborted = prefill_tokens(target, body, start=reuse, want_logits=False, signal=signal)
+    t_todo, d_todo = len(body) - reuse, len(body) - d_reuse
+    prog = on_prefill_progress
+    _, aborted = prefill_tokens(target, body, start=reuse, want_logits=False, signal=signal,
+                                on_progress=(lambda d, _n: prog(d, t_todo + d_todo)) if prog else None)
     if not aborted:
         td = time.perf_counter()
-        _, aborted = prefill_tokens(draft, body, start=d_reuse, want_logits=False, signal=signal)
+        _, aborted = prefill_tokens(draft, body, start=d_reuse, want_logits=False, signal=signal,
+                                    on_progress=(lambda d, _n: prog(t_todo + d, t_todo + d_todo)) if prog else None)
         spec["draftPrefillMs"] = (time.perf_counter() - td) * 1e3
     stats["prefillMs"] = (time.perf_counter() - t0) * 1e3
     if aborted:

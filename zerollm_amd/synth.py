@@ -55,7 +55,7 @@ class TensorSpec:
     std: float = 0.02
     src_cols: int = 0
     col0: int = 0
-    fill: int = 0  # 1 constant fill_value, 2 fill_value + std * N(0, 1) (F32)
+    fill: int = 0  # 1 constant fill_value, 2 fill_value + std * N(0, 1), 3 fill_value then std from element src_cols
     fill_value: float = 1.0
 
     @property
@@ -283,6 +283,23 @@ def qwen3_8b_pair(seed=8, draft_seed=6, ctx_train=32768):
     t = build_spec("qwen3", 4096, 36, 32, 8, 128, 12288, 151936, ctx_train, Q4_K_M, seed, name="qwen3-8b-shaped")
     d = build_spec("qwen3", 1024, 28, 16, 8, 128, 3072, 151936, ctx_train, all_type(gguf.Q8_0), draft_seed,
                    embd_from=(seed, 4096), name="qwen3-0.6b-shaped")
+    return t, d
+
+
+def qwen3_8b_close_pair(layer_std=0.002, tail=0.05, seed=8, draft_seed=6, ctx_train=32768):
+    """The headline pair's shapes, formats and bytes, made to agree: small per-layer matrices (layer_std) keep both
+    residual streams close to the token embedding, and the target's output norm weighs the 3072 embedding columns its
+    draft does not have by `tail` (1.0 on the first 1024), so the target's head mostly sees what the draft's head sees.
+    The reference's generator builds agreeing pairs the same way, by damping what the draft lacks
+    (tools/make-tiny-gguf.js:22-23, 80-81: fadeAfter / fade)."""
+    t = build_spec("qwen3", 4096, 36, 32, 8, 128, 12288, 151936, ctx_train, Q4_K_M, seed, name="qwen3-8b-shaped-close",
+                   layer_std=layer_std)
+    for i, ts in enumerate(t.tensors):
+        if ts.name == "output_norm.weight":
+            t.tensors[i] = TensorSpec("output_norm.weight", gguf.F32, 1, 4096, std=tail, src_cols=1024, fill=3,
+                                      fill_value=1.0)
+    d = build_spec("qwen3", 1024, 28, 16, 8, 128, 3072, 151936, ctx_train, all_type(gguf.Q8_0), draft_seed,
+                   embd_from=(seed, 4096), name="qwen3-0.6b-shaped-close", layer_std=layer_std)
     return t, d
 
 
