@@ -37,7 +37,7 @@ def cpu_baseline(t_spec, d_spec, prompt, seconds, threads):
     runs instead, at a context of 8 prompt tokens."""
     from oracle import oracle as O
     from oracle import pool as P
-    from oracle.spec import feed, speculative_greedy
+    from oracle.spec import feed, plain, speculative_greedy
     from zerollm_amd import synth
 
     simd = P.supported()
@@ -61,6 +61,14 @@ def cpu_baseline(t_spec, d_spec, prompt, seconds, threads):
     ts = time.perf_counter()
     out, cycles = speculative_greedy(tm, dm, ctx_prompt, K, 256, deadline=ts + seconds)
     el = time.perf_counter() - ts
+    # plain greedy decoding of the same prompt on the same target, for half as long
+    tp = time.perf_counter()
+    n_plain = 0
+    for _ in plain(tm, ctx_prompt, len(out)):
+        n_plain += 1
+        if time.perf_counter() - tp > seconds / 2:
+            break
+    el_plain = time.perf_counter() - tp
     for m in models:
         m.close()
     if simd:
@@ -71,7 +79,45 @@ def cpu_baseline(t_spec, d_spec, prompt, seconds, threads):
     else:
         sample = (f"scalar oracle (no AVX-512 VNNI on {P.cpu_name()}), greedy speculative decoding k={K} of {len(out)} "
                   f"tokens in {cycles} cycles, {el:.1f}s, f16 KV, context <= 40 positions, same weights")
-    return {"value": round(len(out) / el, 3), "unit": "tok/s", "cores": threads, "kind": "port", "sample": sample}
+    return {"value": round(len(out) / el, 3), "unit": "tok/s", "cores": threads, "kind": "port", "sample": sample,
+            "plain_tok_s": round(n_plain / el_plain, 3),
+            "plain_sample": f"plain greedy decoding of the same prompt on the same target: {n_plain} tokens in {el_plain:.1f}s"}
+
+
+def _stats(v):
+    v = sorted(v)
+    return {"median": round(v[len(v) // 2] if len(v) % 2 else 0.5 * (v[len(v) // 2 - 1] + v[len(v) // 2]), 2),
+            "min": round(v[0], 2), "max": round(v[-1], 2)}
+
+
+def paired_rounds(target, draft, prompt, rounds, gen, k=K):
+    """Plain greedy decoding (generate) against greedy speculative decoding (generateSpeculative) of the same prompt on
+    the same models, in interleaved rounds whose order alternates, medians with min-max, as the reference's own
+    comparison does (tools/specbench.mjs:67-106). Both reuse the cached prompt, so each round times decoding alone."""
+    from zerollm_amd.generate import generate
+    from zerollm_amd.speculative import generate_speculative
+
+    spec, plain, ratio, acc = [], [], [], []
+    ref = None
+    for r in range(rounds):
+        res = {}
+        for mode in (("spec", "plain") if r % 2 == 0 else ("plain", "spec")):
+            st = {}
+            t0 = time.perf_counter()
+            if mode == "spec":
+                out = list(generate_speculative(target, draft, prompt, k=k, max_tokens=gen, stats=st))
+                acc.append(st["speculative"]["acceptRate"])
+            else:
+                out = list(generate(target, prompt, max_tokens=gen, stats=st))
+            res[mode] = len(out) / (time.perf_counter() - t0)
+            ref = out if ref is None else ref
+            assert out == ref, "greedy speculative decoding must emit the plain greedy stream"
+        spec.append(res["spec"])
+        plain.append(res["plain"])
+        ratio.append(res["spec"] / res["plain"])
+        log(f"paired round {r}: speculative {res['spec']:.1f} tok/s, plain {res['plain']:.1f} tok/s")
+    return {"rounds": rounds, "tokens": gen, "speculative_tok_s": _stats(spec), "plain_tok_s": _stats(plain),
+            "speedup": _stats(ratio), "accept_rate": round(sum(acc) / len(acc), 4)}
 
 
 def modeled(cycle_ms, k=K):
@@ -87,6 +133,7 @@ def modeled(cycle_ms, k=K):
 
 
 LONG_PROMPT, LONG_K = 16384, 8
+CLOSE_LAYER_STD, CLOSE_TAIL = 0.0003, 0.01
 
 
 def long_context(args):
@@ -161,6 +208,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--gen", type=int, default=GEN, help="tokens generated per step (profiling runs use fewer)")
+    ap.add_argument("--rounds", type=int, default=5,
+                    help="paired rounds of plain vs speculative decoding after the timed steps (0: none)")
     ap.add_argument("--probe-only", action="store_true",
                     help="only the roofline kernel's timed launches (for hardware-counter runs); prints the roofline")
     ap.add_argument("--workload", choices=["headline", "long"], default="headline",
@@ -252,8 +301,24 @@ def main():
                      "launch_ms": round(probe_ms, 5), "bytes_per_launch": bytes_per, "launches": iters,
                      "other_gemvs_GBps": {w: round(b / (ms * 1e-3) / 1e9, 1) for w, (ms, b) in others.items()}},
     }
+    speculation = {"headline_pair": paired_rounds(target, draft, prompt, args.rounds, args.gen)}
     target.close()
     draft.close()
+    if args.rounds:
+        # an agreeing pair of the same shapes, formats and bytes per pass (so the same cycle cost), to measure what
+        # speculation buys when the draft is accepted
+        c_spec, cd_spec = synth.qwen3_8b_close_pair(layer_std=CLOSE_LAYER_STD, tail=CLOSE_TAIL)
+        ct = synth.build_on_device(c_spec, ctx=1024, kv="f16")
+        cd = synth.build_on_device(cd_spec, ctx=1024, kv="f16")
+        list(generate_speculative(ct, cd, prompt, k=K, max_tokens=args.gen))  # prefill, graph capture
+        ap = paired_rounds(ct, cd, prompt, args.rounds, args.gen)
+        ap["pair"] = (f"the headline shapes and formats with per-layer matrices N(0, {CLOSE_LAYER_STD}) and the target's "
+                      f"output norm weighing the 3072 embedding columns the draft lacks by {CLOSE_TAIL} "
+                      "(synth.qwen3_8b_close_pair)")
+        speculation["agreeing_pair"] = ap
+        ct.close()
+        cd.close()
+    line["speculation"] = speculation
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
         line["cpu_baseline"] = cpu_baseline(t_spec, d_spec, prompt, args.cpu_seconds, threads)

@@ -125,3 +125,29 @@ def naive_qwen35_logits(spec, W, V, tokens):
         ff = _silu(h2 @ W(p + "ffn_gate.weight").T) * (h2 @ W(p + "ffn_up.weight").T)
         xs = xs + ff @ W(p + "ffn_down.weight").T
     return _rms(xs, V("output_norm.weight"), eps) @ E.T
+
+
+def chunked_gated_delta_rule(q, k, v, gam, beta, chunk=64):
+    """The chunkwise form of one head's gated delta rule with the state carried between chunks (what a chunked
+    prefill would run; test/naive-qwen35.js:111-135 is its single-chunk, zero-state case). S is [dv][dk], o_t = S_t q_t.
+    Inside a chunk with decay products b_r = gam_1 ... gam_r the writes d_r solve (I + A) D = B, A[r][s] = beta_r
+    (b_r / b_s) k_r.k_s (s < r), B_r = beta_r (v_r - b_r S_0 k_r); then o_r = b_r S_0 q_r + sum_{s<=r} (b_r / b_s)
+    (k_s.q_r) d_s and S_C = b_C S_0 + sum_s (b_C / b_s) d_s k_s^T. Returns (outputs [T][dv], final state), float64."""
+    from scipy.linalg import solve_triangular
+
+    q, k, v, gam, beta = (np.asarray(x, np.float64) for x in (q, k, v, gam, beta))
+    T, dk = k.shape
+    dv = v.shape[1]
+    S = np.zeros((dv, dk))
+    out = np.zeros((T, dv))
+    for c0 in range(0, T, chunk):
+        Q, K, V, g, bt = q[c0:c0 + chunk], k[c0:c0 + chunk], v[c0:c0 + chunk], gam[c0:c0 + chunk], beta[c0:c0 + chunk]
+        n = len(g)
+        b = np.cumprod(g)
+        ratio = b[:, None] / b[None, :]
+        A = np.tril(bt[:, None] * ratio * (K @ K.T), -1)
+        B = bt[:, None] * (V - b[:, None] * (K @ S.T))
+        D = solve_triangular(np.eye(n) + A, B, lower=True, unit_diagonal=True)
+        out[c0:c0 + n] = b[:, None] * (Q @ S.T) + (np.tril(ratio) * (Q @ K.T)) @ D
+        S = b[-1] * S + ((b[-1] / b)[:, None] * D).T @ K
+    return out, S

@@ -114,6 +114,42 @@ def test_c3_greedy_speculative_equals_plain_greedy(gpu, pair_8b):
     d.close()
 
 
+@pytest.mark.timeout(1200)
+def test_sampled_cycles_at_the_full_vocabulary_match_oracle(gpu):
+    """Stochastic acceptance with the long-context configuration's sampler (temperature 0.7, top-k 40, top-p 0.9, k = 8)
+    on the 8B / 0.6B shapes, 151,936 logits per row: the two-stage candidate selection over 75 blocks, the acceptance
+    over fixed candidate lists and the residual and bonus draws, cycle by cycle against the oracle's
+    generateSpeculative (src/model/speculative.js:155-209): the same drafts, accept counts and tokens, and the same final
+    mulberry32 state. The agreeing pair of the same shapes (synth.qwen3_8b_close_pair) is used so that cycles both
+    accept and reject."""
+    from oracle import spec as OS
+    from zerollm_amd import model as Mdl
+
+    t_spec, d_spec = synth.qwen3_8b_close_pair()
+    prompt = synth.seeded_ids(6, 57, t_spec.vocab)
+    cfg = dict(temperature=0.7, top_k=40, top_p=0.9)
+    print("case full-vocabulary sampled cycles: device", flush=True)
+    t = synth.build_on_device(t_spec, ctx=64, kv="f16")
+    d = synth.build_on_device(d_spec, ctx=64, kv="f16")
+    s = HipSampler(seed=1234, **cfg)
+    log, st = [], {}
+    out = list(generate_speculative(t, d, prompt, k=8, max_tokens=10, sample=s, stats=st, cycle_log=log))
+    rng, limit = s.rng_state, Mdl.verify_limit(t)
+    for x in (t, d, s):
+        x.close()
+    print(f"device: {len(log)} cycles {log}", flush=True)
+    print("case full-vocabulary sampled cycles: oracle", flush=True)
+    ot, od = _oracle(t_spec), _oracle(d_spec)
+    os_ = O.Sampler(seed=1234, **cfg)
+    o_log = []
+    o_out = list(OS.speculative(ot, od, prompt, k=8, max_tokens=10, sample=os_, cycle_log=o_log, t_limit=limit))
+    ot.close()
+    od.close()
+    for c, (g, w) in enumerate(zip(log, o_log)):
+        assert g == w, f"cycle {c}: device {g} vs oracle {w}"
+    assert log == o_log and out == o_out and rng == os_.rng.state
+
+
 def test_sampler_at_the_full_vocabulary_matches_oracle(gpu, pair_8b):
     """Sampled distributions over the 151,936 logits of the 0.6B-shaped draft against the oracle sampler on the same
     logits: top_k 40 selects over the 75 blocks' candidate lists in LDS; top_k 200 and 256 have more candidates than

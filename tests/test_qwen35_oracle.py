@@ -160,6 +160,52 @@ def test_forward_tracks_naive_with_quantized_weights(quant):
     m.close()
 
 
+@pytest.mark.parametrize("decay", [(0.5, 0.7), (0.9, 0.999)])
+def test_chunked_delta_rule_is_not_the_recurrence_bits(decay):
+    """Why a chunked (WY) prefill of the Gated DeltaNet is not used: over 2048 tokens of a 128 x 128 head, the chunk form
+    equals the exact recurrence in f64 to 1e-15, but the reference's recurrence (deltaRuleHead,
+    src/compute/ref-deltanet.js:79-90) rounds the state to f32 after every decay and every write, and those roundings are
+    part of its result. Measured: the chunk form's outputs carry ~1e-7 of relative deviation from the reference's and
+    equal its bits in only 46 % (fast decay) / 23 % (slow decay) of elements; per-element perturbations of this kind are
+    what the random-weight networks amplify through the int8 activation rounding of every later layer (the
+    position-split attention sum: ~1e-6 per element became 0.028 max-abs in the logits). The GPU runs the recurrence
+    itself, token by token inside each workgroup, and captures the state per position instead."""
+    from tests.naive_qwen35 import chunked_gated_delta_rule
+
+    rng = np.random.default_rng(1)
+    T, D = 2048, 128
+
+    def l2(x):
+        return x / np.sqrt((x * x).sum(-1, keepdims=True) + 1e-6)
+
+    k = l2(rng.normal(size=(T, D))).astype(np.float32)
+    q = (l2(rng.normal(size=(T, D))) / np.sqrt(D)).astype(np.float32)
+    v = (rng.normal(size=(T, D)) * 0.5).astype(np.float32)
+    gam = rng.uniform(decay[0], decay[1], T)
+    beta = 1.0 / (1.0 + np.exp(-rng.normal(size=T)))
+    # the reference's recurrence: f64 arithmetic, the state stored f32 after the decay and after the write
+    S = np.zeros((D, D), np.float32)
+    ref = np.zeros((T, D), np.float32)
+    ex = np.zeros((T, D))
+    Se = np.zeros((D, D))
+    for t in range(T):
+        s = (S.astype(np.float64) * gam[t]).astype(np.float32)
+        d = (v[t] - s.astype(np.float64) @ k[t].astype(np.float64)) * beta[t]
+        S = (s.astype(np.float64) + np.outer(d, k[t].astype(np.float64))).astype(np.float32)
+        ref[t] = (S.astype(np.float64) @ q[t].astype(np.float64)).astype(np.float32)
+        Se = Se * gam[t]
+        de = (v[t] - Se @ k[t]) * beta[t]
+        Se = Se + np.outer(de, k[t])
+        ex[t] = Se @ q[t]
+    wy, Swy = chunked_gated_delta_rule(q, k, v, gam, beta, chunk=64)
+    assert np.abs(wy - ex).max() <= 1e-12 * np.abs(ex).max() and np.abs(Swy - Se).max() <= 1e-12 * np.abs(Se).max()
+    got = wy.astype(np.float32)
+    rel = np.abs(got - ref).max() / np.abs(ref).max()
+    same = np.mean(got.view(np.uint32) == ref.view(np.uint32))
+    print(f"decay {decay}: chunk form vs the reference's recurrence: max-abs {rel:.2e} of max, bit-equal {same:.3f}")
+    assert 1e-8 < rel < 1e-5 and same < 0.6
+
+
 def test_prefill_without_logits_equals_token_by_token_and_state_is_deterministic():
     spec = synth.tiny_qwen35(seed=7)
     arrays = arrays_of(spec)

@@ -286,7 +286,7 @@ def qwen3_8b_pair(seed=8, draft_seed=6, ctx_train=32768):
     return t, d
 
 
-def qwen3_8b_close_pair(layer_std=0.002, tail=0.05, seed=8, draft_seed=6, ctx_train=32768):
+def qwen3_8b_close_pair(layer_std=0.0003, tail=0.01, seed=8, draft_seed=6, ctx_train=32768):
     """The headline pair's shapes, formats and bytes, made to agree: small per-layer matrices (layer_std) keep both
     residual streams close to the token embedding, and the target's output norm weighs the 3072 embedding columns its
     draft does not have by `tail` (1.0 on the first 1024), so the target's head mostly sees what the draft's head sees.
