@@ -72,16 +72,16 @@ def test_c3_verify_rows_equal_single_passes_and_oracle(gpu, pair_8b, which):
 @pytest.mark.timeout(600)
 @pytest.mark.parametrize("which", ["target", "draft"])
 def test_prefill_chunks_of_64_equal_chunks_of_16(gpu, pair_8b, which):
-    """Prefill in chunks of 64 tokens (each weight read once per chunk on the GEMM) and of 16 (one GEMM launch per
-    chunk), and 16 tokens through the GEMV kernels alone (ZEROLLM_GEMM_MAXM=0: two passes of 8), all leave the same
-    KV cache: the next rows' logits are the same bits (prefillTokens, src/model/generate.js:18-31)."""
+    """Prefill in chunks of 64 tokens (each weight read once per chunk on the GEMM, score dots on the matrix cores) and
+    of 16, 16 tokens through the GEMV kernels alone (ZEROLLM_GEMM_MAXM=0: two passes of 8), and token by token all
+    leave the same KV cache: the next rows' logits are the same bits (prefillTokens, src/model/generate.js:18-31)."""
     import os
 
     spec = pair_8b[0] if which == "target" else pair_8b[1]
     ids = synth.seeded_ids(200, 41, spec.vocab)
     nxt = synth.seeded_ids(3, 42, spec.vocab)
     rows = {}
-    for mb, maxm in ((64, "64"), (16, "64"), (16, "0")):
+    for mb, maxm in ((1, "64"), (64, "64"), (16, "64"), (16, "0")):
         print(f"case prefill chunks {which} max_batch {mb} gemm {maxm}", flush=True)
         os.environ["ZEROLLM_GEMM_MAXM"] = maxm
         try:
@@ -92,7 +92,7 @@ def test_prefill_chunks_of_64_equal_chunks_of_16(gpu, pair_8b, which):
             m.close()
         finally:
             del os.environ["ZEROLLM_GEMM_MAXM"]
-    ref = rows[(64, "64")]
+    ref = rows[(1, "64")]  # token by token: the GEMV kernels and the lane-chain scores alone
     for k, v in rows.items():
         assert (_bits(v) == _bits(ref)).all(), k
 

@@ -78,6 +78,34 @@ def test_forward_batch_all_equals_sequential(gpu, tiny_files):
     b.close()
 
 
+@pytest.mark.parametrize("kv", ["f16", "f32"])
+def test_matrix_core_scores_equal_the_lane_chains(gpu, tiny_files, monkeypatch, kv):
+    """Passes of several tokens with their score dots on the matrix cores (k_attn_prep + k_attn_scores_mm, forced for
+    every pass of 2 tokens or more by ZEROLLM_ATTN_MM_B=2) give the rows of single-token passes (k_attn_scores) bit for
+    bit, over a prefix long enough for several position chunks, and match the oracle."""
+    monkeypatch.setenv("ZEROLLM_ATTN_MM_B", "2")
+    toks = prompt(600, seed=23)
+    print(f"case matrix-core scores kv {kv}", flush=True)
+    a = Mdl.HipModel.load(tiny_files[0], ctx=640, kv=kv)
+    b = Mdl.HipModel.load(tiny_files[0], ctx=640, kv=kv, max_batch=64)
+    for i in range(0, 590, 64):
+        b.forward_batch(toks[i:min(i + 64, 590)], logits="none")
+    for t in toks[:590]:
+        a.forward(t, logits=False)
+    seq = np.stack([a.forward(t).copy() for t in toks[590:]])
+    bat = b.forward_batch(toks[590:], logits="all").copy()
+    assert (bat.view(np.uint32) == seq.view(np.uint32)).all()
+    a.close()
+    b.close()
+    ref = O.OracleModel(tiny_files[0], ctx=640, kv=kv)
+    for t in toks[:596]:
+        ref.forward(t, logits=False)
+    want = np.stack([ref.forward(t) for t in toks[596:]])
+    got = bat[6:]
+    exact = np.mean(got.view(np.uint32) == want.view(np.uint32))
+    assert exact >= 0.999 and np.abs(got - want).max() <= 1e-6 * np.abs(want).max(), exact
+
+
 def test_rollback_equals_fresh_run(gpu, tiny_files):
     """50 random accept/reject cycles leave the same state as a fresh sequential run (test/spec-logits.test.js:97-139)."""
     rng = np.random.default_rng(4)

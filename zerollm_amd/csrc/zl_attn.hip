@@ -251,6 +251,146 @@ __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
   }
 }
 
+// ---- scores of passes of several tokens on the matrix cores. v_mfma_f64_16x16x4_f64 adds its four products to the
+// accumulator as four fused multiply-adds in k order (measured on gfx950, every element of random wide-range operands),
+// so eight of them over dimensions 32 j .. 32 j + 31 in order are exactly the per-lane f64 fma chain of k_attn_scores
+// (part j of a position's dot), and the parts are joined in the same butterfly order: the same bits. The pass's query
+// rows and keys are normed and rotated first (k_attn_prep, which also appends the pass's K and V to the cache, as
+// k_attn_scores' writer blocks do), so the score blocks only read.
+
+// One wave per (token, head): query heads are normed, rotated and stored f32 to qr [B][nHead][HD]; KV heads (blockIdx.y
+// >= nHead) have their key normed, rotated and appended to the cache in its format, and their value appended.
+template <int HD, bool F16KV>
+__global__ __launch_bounds__(64) void k_attn_prep(const AttnArgs a) {
+  __shared__ float v[HD];
+  const int b = blockIdx.x, hy = blockIdx.y, lane = threadIdx.x;
+  const Step *st = a.step;
+  if (b >= st->B) return;
+  const int pos = st->pos0 + b;
+  const bool isq = hy < a.nHead;
+  const int h = isq ? hy : hy - a.nHead;
+  const float *src = isq ? a.q + (long)b * a.ldq + (long)h * a.qhs : a.k + (long)b * a.ldkv + (long)h * HD;
+  for (int i = lane; i < HD; i += 64) v[i] = src[i];
+  __syncthreads();
+  norm_rope<HD>(v, isq ? a.qNorm : a.kNorm, a.eps, a.nRot, a.neox, a.cosT, a.sinT, pos, lane);
+  __syncthreads();
+  if (isq) {
+    for (int i = lane; i < HD; i += 64) a.qr[((long)b * a.nHead + h) * HD + i] = v[i];
+    return;
+  }
+  const long kvoff = ((long)a.layer * a.nHeadKv + h) * a.ctx * HD + (long)pos * HD;
+  const long voff = ((long)a.layer * a.nHeadKv + h) * HD;
+  for (int d = lane; d < HD; d += 64) {
+    const float vv = a.v[(long)b * a.ldkv + (long)h * HD + d];
+    if (F16KV) {
+      ((uint16_t *)a.kcache)[kvoff + d] = f2h(v[d]);
+      ((uint16_t *)a.vcache)[(voff + d) * a.vstride + pos] = f2h(vv);
+    } else {
+      ((float *)a.kcache)[kvoff + d] = v[d];
+      ((float *)a.vcache)[(voff + d) * a.vstride + pos] = vv;
+    }
+  }
+}
+
+// Block (position chunk of MM_PC, KV head, group of 4 row tiles); wave w computes row tile 4 z + w: 16 rows r = b G + g
+// (token b, query head kvh G + g) against every position of the chunk, 16 positions at a time. Lane l supplies A = the
+// row l mod 16's dimension 32 j + 4 m + l / 16 (its query values, f64, held for the whole chunk) and B = key value
+// [position l mod 16][dimension 32 j + 4 m + l / 16] from LDS, where the block has staged 64 positions' keys as f64;
+// the accumulator of lane l element v is (row 4 v + l / 16, position l mod 16).
+constexpr int MM_PC = 256;   // positions per block
+constexpr int MM_PT = 64;    // positions staged in LDS at a time
+template <int HD, bool F16KV>
+__global__ __launch_bounds__(256) void k_attn_scores_mm(const AttnArgs a, int nrows) {
+  constexpr int NP = HD / ATTN_VPL;    // parts (32 dimensions each)
+  constexpr int VB = F16KV ? 2 : 4;
+  constexpr int RAW = MM_PT * HD * VB / 16 / 256;  // 16-byte K pieces per thread per staged tile
+  typedef double d4 __attribute__((ext_vector_type(4)));
+  extern __shared__ __align__(16) uint8_t lds[];
+  double *kd = (double *)lds;          // [MM_PT][HD + 1] keys as f64 (the pad spreads a tile's rows over the banks)
+  constexpr int KP = HD + 1;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g = lane >> 4;
+  const int kvh = blockIdx.y, tile = blockIdx.z * 4 + wave;
+  const int G = a.nHead / a.nHeadKv;
+  const Step *st = a.step;
+  const int Bd = st->B, pos0 = st->pos0, nmax = pos0 + Bd;
+  const int c0 = blockIdx.x * MM_PC;
+  if (c0 >= nmax) return;
+  const int c1 = min(c0 + MM_PC, nmax);
+  const long kvoff = ((long)a.layer * a.nHeadKv + kvh) * a.ctx * HD;
+  const uint8_t *kbase = (const uint8_t *)a.kcache + kvoff * VB;
+  // A operands: row n16 of the tile, dimensions 32 j + 4 m + g
+  const int ra = tile * 16 + n16, ba = ra / G, ha = kvh * G + ra % G;
+  const bool rowok = ra < nrows && ba < Bd;
+  double A[NP][8];
+  #pragma unroll
+  for (int j = 0; j < NP; j++)
+    #pragma unroll
+    for (int m = 0; m < 8; m++)
+      A[j][m] = rowok ? (double)a.qr[((long)ba * a.nHead + ha) * HD + 32 * j + 4 * m + g] : 0.0;
+  // the rows whose accumulator elements this lane holds: 4 v + g, v = 0..3
+  int rb[4], rh[4], rn[4];
+  #pragma unroll
+  for (int v = 0; v < 4; v++) {
+    const int r = tile * 16 + 4 * v + g, bb = r / G;
+    rb[v] = bb; rh[v] = kvh * G + r % G;
+    rn[v] = (r < nrows && bb < Bd) ? pos0 + bb + 1 : 0;  // positions of the row (0: no row)
+  }
+  const bool waveok = tile * 16 < nrows;
+  uint4 raw[RAW];
+  auto fetch = [&](int t0) {
+    #pragma unroll
+    for (int k = 0; k < RAW; k++) {
+      const int e = (k * 256 + tid) * (16 / VB), p = e / HD, d = e % HD, t = t0 + p;
+      raw[k] = t < c1 ? *(const uint4 *)(kbase + ((long)t * HD + d) * VB) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store = [&]() {
+    #pragma unroll
+    for (int k = 0; k < RAW; k++) {
+      const int e = (k * 256 + tid) * (16 / VB), p = e / HD, d = e % HD;
+      const uint32_t w[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
+      #pragma unroll
+      for (int q = 0; q < 16 / VB; q++)
+        kd[p * KP + d + q] = F16KV ? (double)h2f((uint16_t)((w[q >> 1] >> (16 * (q & 1))) & 0xffff)) : (double)__uint_as_float(w[q]);
+    }
+  };
+  fetch(c0);
+  for (int t0 = c0; t0 < c1; t0 += MM_PT) {
+    __syncthreads();  // the previous tile's reads are done
+    store();
+    __syncthreads();
+    if (t0 + MM_PT < c1) fetch(t0 + MM_PT);
+    if (waveok) {
+      #pragma unroll 1
+      for (int pt = 0; pt < MM_PT && t0 + pt < c1; pt += 16) {
+        d4 acc[NP];
+        #pragma unroll
+        for (int j = 0; j < NP; j++) {
+          acc[j] = d4{0.0, 0.0, 0.0, 0.0};
+          #pragma unroll
+          for (int m = 0; m < 8; m++)
+            acc[j] = __builtin_amdgcn_mfma_f64_16x16x4f64(A[j][m], kd[(pt + n16) * KP + 32 * j + 4 * m + g], acc[j], 0, 0, 0);
+        }
+        const int t = t0 + pt + n16;
+        #pragma unroll
+        for (int v = 0; v < 4; v++) {
+          double sv[NP];
+          #pragma unroll
+          for (int j = 0; j < NP; j++) sv[j] = acc[j][v];
+          // the butterfly of k_attn_scores over the position's NP lanes: pairs, then pairs of pairs
+          #pragma unroll
+          for (int w = 1; w < NP; w *= 2)
+            #pragma unroll
+            for (int j = 0; j < NP; j += 2 * w) sv[j] = sv[j] + sv[j + w];
+          if (t < rn[v]) a.scores[((long)rb[v] * a.nHead + rh[v]) * a.sld + t] = (float)(sv[0] * a.scale);
+        }
+      }
+    }
+  }
+}
+
+size_t attention_mm_lds(int hd) { return (size_t)MM_PT * (hd + 1) * 8; }
+
 // One block per (32-dim slice, query head, token). The slice's V rows (dimension-major in the cache) are staged
 // through LDS in chunks of ROWB bytes per dimension (1024: 512 f16 or 256 f32 positions, at long contexts where the
 // softmax row leaves room; else 512), double buffered, the first chunk during the softmax; fewer chunks, fewer barriers in the
@@ -960,7 +1100,22 @@ AttnForm attention_form(int ctx, int hd) {
   while (fit < ctx && attention_lds(fit + AV_UNIT) <= ATTN_LDS_MAX) fit += AV_UNIT;
   f.head1Ctx = hd > 128 ? INT_MAX : e1 ? atoi(e1) : std::max(f.headCtx, fit);
   f.split = ctx > f.headCtx ? false : attention_lds(ctx) > ATTN_LDS_MAX;
+  // matrix-core score dots for passes of 16 tokens or more (prefill chunks), and of 2 or more where the context is long
+  // (verify passes at long contexts); ZEROLLM_ATTN_MM_B overrides the token count (tests)
+  const char *em = getenv("ZEROLLM_ATTN_MM_B");
+  f.mmMinB = em ? atoi(em) : ctx >= AVH_CTX ? 2 : 16;
   return f;
+}
+
+template <int HD, bool F16KV>
+static void launch_scores_mm(const AttnArgs &a, dim3 gp, dim3 gm, size_t lds, int nrows, hipStream_t st) {
+  static bool attr = false;  // dynamic LDS above 64 KB must be requested per kernel
+  if (!attr) {
+    ZL_HIP(hipFuncSetAttribute((const void *)k_attn_scores_mm<HD, F16KV>, hipFuncAttributeMaxDynamicSharedMemorySize, 140 * 1024));
+    attr = true;
+  }
+  hipLaunchKernelGGL((k_attn_prep<HD, F16KV>), gp, dim3(64), 0, st, a);
+  hipLaunchKernelGGL((k_attn_scores_mm<HD, F16KV>), gm, dim3(256), lds, st, a, nrows);
 }
 
 template <int HD, bool F16KV>
@@ -1012,14 +1167,29 @@ void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
   const int group = a.nHead / a.nHeadKv;
   a.hpb = attn_heads_per_block(group);
   const int chunks = (a.ctx + attn_score_chunk(a.hd) - 1) / attn_score_chunk(a.hd);
-  dim3 gs(chunks < 64 ? chunks : 64, a.nHead / a.hpb, B);
-  switch (a.hd * 2 + a.kvF16) {
-    case 128: launch_scores_k<64, false>(a, gs, B, st); break;
-    case 129: launch_scores_k<64, true>(a, gs, B, st); break;
-    case 256: launch_scores_k<128, false>(a, gs, B, st); break;
-    case 257: launch_scores_k<128, true>(a, gs, B, st); break;
-    case 512: launch_scores_k<256, false>(a, gs, B, st); break;
-    case 513: launch_scores_k<256, true>(a, gs, B, st); break;
+  if (a.qr && a.mmMinB > 0 && B >= a.mmMinB) {
+    const dim3 gp(B, a.nHead + a.nHeadKv);
+    const int nrows = B * group;
+    const dim3 gm((a.ctx + MM_PC - 1) / MM_PC, a.nHeadKv, (nrows + 63) / 64);
+    const size_t lm = attention_mm_lds(a.hd);
+    switch (a.hd * 2 + a.kvF16) {
+      case 128: launch_scores_mm<64, false>(a, gp, gm, lm, nrows, st); break;
+      case 129: launch_scores_mm<64, true>(a, gp, gm, lm, nrows, st); break;
+      case 256: launch_scores_mm<128, false>(a, gp, gm, lm, nrows, st); break;
+      case 257: launch_scores_mm<128, true>(a, gp, gm, lm, nrows, st); break;
+      case 512: launch_scores_mm<256, false>(a, gp, gm, lm, nrows, st); break;
+      case 513: launch_scores_mm<256, true>(a, gp, gm, lm, nrows, st); break;
+    }
+  } else {
+    dim3 gs(chunks < 64 ? chunks : 64, a.nHead / a.hpb, B);
+    switch (a.hd * 2 + a.kvF16) {
+      case 128: launch_scores_k<64, false>(a, gs, B, st); break;
+      case 129: launch_scores_k<64, true>(a, gs, B, st); break;
+      case 256: launch_scores_k<128, false>(a, gs, B, st); break;
+      case 257: launch_scores_k<128, true>(a, gs, B, st); break;
+      case 512: launch_scores_k<256, false>(a, gs, B, st); break;
+      case 513: launch_scores_k<256, true>(a, gs, B, st); break;
+    }
   }
   ZL_HIP(hipGetLastError());
   if (a.part) {
