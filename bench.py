@@ -301,7 +301,7 @@ def main():
                      "launch_ms": round(probe_ms, 5), "bytes_per_launch": bytes_per, "launches": iters,
                      "other_gemvs_GBps": {w: round(b / (ms * 1e-3) / 1e9, 1) for w, (ms, b) in others.items()}},
     }
-    speculation = {"headline_pair": paired_rounds(target, draft, prompt, args.rounds, args.gen)}
+    speculation = {"headline_pair": paired_rounds(target, draft, prompt, args.rounds, args.gen)} if args.rounds else {}
     target.close()
     draft.close()
     if args.rounds:

@@ -80,9 +80,10 @@ def test_forward_batch_all_equals_sequential(gpu, tiny_files):
 
 @pytest.mark.parametrize("kv", ["f16", "f32"])
 def test_matrix_core_scores_equal_the_lane_chains(gpu, tiny_files, monkeypatch, kv):
-    """Passes of several tokens with their score dots on the matrix cores (k_attn_prep + k_attn_scores_mm, forced for
-    every pass of 2 tokens or more by ZEROLLM_ATTN_MM_B=2) give the rows of single-token passes (k_attn_scores) bit for
-    bit, over a prefix long enough for several position chunks, and match the oracle."""
+    """Passes of several tokens with their score dots and weighted sums on the matrix cores (k_attn_prep +
+    k_attn_scores_mm, k_attn_softmax_rows + k_attn_av_mm; forced for every pass of 2 tokens or more by
+    ZEROLLM_ATTN_MM_B=2) give the rows of single-token passes (k_attn_scores, k_attn_av) bit for bit, over a prefix long
+    enough for several position chunks, and match the oracle."""
     monkeypatch.setenv("ZEROLLM_ATTN_MM_B", "2")
     toks = prompt(600, seed=23)
     print(f"case matrix-core scores kv {kv}", flush=True)

@@ -63,6 +63,35 @@ def test_logits_and_state_match_oracle(gpu, quant, kv):
     ref.close()
 
 
+@pytest.mark.parametrize("form", ["matrix-core", "per-head"])
+def test_gated_attention_forms_give_the_same_bits(gpu, monkeypatch, form):
+    """The gated attention's weighted sum on the matrix cores for every pass, single tokens included
+    (ZEROLLM_ATTN_MMAV_B=1: the form 256-dimension heads take beyond ~29,900 positions, where the slice form's softmax
+    row leaves LDS), and the per-head and grouped forms of long contexts (ZEROLLM_ATTN_HEAD_CTX=0,
+    ZEROLLM_ATTN_HEAD1_CTX=0) give the default forms' logits bit for bit (the slice form of single-token passes, the
+    lane chains of several-token passes), over single-token and 5-token passes."""
+    spec = synth.tiny_qwen35(seed=21, quant="q8_0")
+    toks = prompt(40, seed=6)
+
+    def run():
+        m = synth.build_on_device(spec, ctx=128, kv="f16")
+        a = np.stack([m.forward(t).copy() for t in toks[:30]])
+        b = m.forward_batch(toks[30:35], logits="all").copy()
+        c = np.stack([m.forward(t).copy() for t in toks[35:]])
+        m.close()
+        return np.concatenate([a, b, c])
+
+    print(f"case gated attention form {form}", flush=True)
+    want = run()
+    if form == "matrix-core":
+        monkeypatch.setenv("ZEROLLM_ATTN_MMAV_B", "1")
+    else:
+        monkeypatch.setenv("ZEROLLM_ATTN_HEAD_CTX", "0")
+        monkeypatch.setenv("ZEROLLM_ATTN_HEAD1_CTX", "0")
+    got = run()
+    assert (got.view(np.uint32) == want.view(np.uint32)).all()
+
+
 @pytest.mark.parametrize("d_state", [32, 128])
 def test_deltanet_head_sizes_match_oracle(gpu, d_state):
     """DeltaNet heads of 32 values (one workgroup per head: no exchange among workgroups) and of 128 (four workgroups

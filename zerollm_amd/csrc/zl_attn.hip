@@ -391,6 +391,7 @@ __global__ __launch_bounds__(256) void k_attn_scores_mm(const AttnArgs a, int nr
 
 size_t attention_mm_lds(int hd) { return (size_t)MM_PT * (hd + 1) * 8; }
 
+
 // One block per (32-dim slice, query head, token). The slice's V rows (dimension-major in the cache) are staged
 // through LDS in chunks of ROWB bytes per dimension (1024: 512 f16 or 256 f32 positions, at long contexts where the
 // softmax row leaves room; else 512), double buffered, the first chunk during the softmax; fewer chunks, fewer barriers in the
@@ -753,6 +754,7 @@ size_t attention_head_lds(int hd) { return (size_t)2 * hd * AV_PITCH + 2 * 256 *
 constexpr int AVG_ROWS = 8;   // rows (query head, token) per block of the grouped weighted sum
 constexpr int AVG_DIMS = 32;  // dimensions per block
 
+template <bool NORM>
 __global__ __launch_bounds__(256) void k_attn_softmax_rows(const AttnArgs a) {
   __shared__ double redd[4];
   __shared__ float redf[4];
@@ -793,8 +795,146 @@ __global__ __launch_bounds__(256) void k_attn_softmax_rows(const AttnArgs a) {
   sum = wave_sum_xor(sum, 64);
   if (lane == 0) redd[wave] = sum;
   __syncthreads();
-  if (tid == 0) a.pinv[(long)b * a.nHead + h] = 1.0 / ((redd[0] + redd[1]) + (redd[2] + redd[3]));
+  const double inv = 1.0 / ((redd[0] + redd[1]) + (redd[2] + redd[3]));
+  if (!NORM) {
+    if (tid == 0) a.pinv[(long)b * a.nHead + h] = inv;
+    return;
+  }
+  // the probabilities themselves, p = f32(e * inv), each thread over the positions it wrote
+  for (int t0 = tid; t0 < npos; t0 += 16 * 256) {
+    float v[16];
+    #pragma unroll
+    for (int k = 0; k < 16; k++) { const int t = t0 + 256 * k; v[k] = srow[t < npos ? t : t0]; }
+    #pragma unroll
+    for (int k = 0; k < 16; k++) {
+      const int t = t0 + 256 * k;
+      if (t < npos) srow[t] = (float)((double)v[k] * inv);
+    }
+  }
 }
+
+// ---- weighted sum of passes of several tokens on the matrix cores. v_mfma_f32_16x16x4_f32 adds its four products to
+// the accumulator as four fused multiply-adds in k order (measured on gfx950, every element of random wide-range
+// operands), so a chain of them over positions t, t + 1, ... in order is the reference's f32 chain out += p_t v_t
+// (one rounding per position, src/model/forward.js:131-134) for 16 rows x 16 dimensions at once: the bits of k_attn_av.
+// Block (pair of 64-dimension halves... see below): rows r = b G + g of a KV head (token b, query head kvh G + g) in
+// tiles of 16, wave w computing dimension tile (blockIdx.x * 4 + w) of 16 dimensions for the block's row tile; lane l
+// supplies A = p[row l mod 16][t + l / 16] and B = V[dimension l mod 16][t + l / 16] and holds the accumulator of
+// (row 4 (l / 16) + v, dimension l mod 16). The probabilities (already normalised: k_attn_softmax_rows<true>) and V
+// are staged in LDS chunk by chunk, the next chunk loaded into registers while the current one is summed; a row's
+// probabilities past its last position are zero, and so are V past the pass's last position.
+constexpr int MMV_CT = 128;   // positions per staged chunk
+template <bool F16KV>
+__global__ __launch_bounds__(256) void k_attn_av_mm(const AttnArgs a, int nrows) {
+  constexpr int VB = F16KV ? 2 : 4;
+  constexpr int PP = MMV_CT + 4;                      // LDS pitch (floats) of a staged probability row
+  constexpr int VP = MMV_CT * VB + 16;                // LDS pitch (bytes) of a staged V dimension row
+  constexpr int PL = 16 * MMV_CT / 4 / 256;           // 16-byte probability pieces per thread per chunk (2)
+  constexpr int VL = 64 * MMV_CT * VB / 16 / 256;     // 16-byte V pieces per thread per chunk
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  extern __shared__ __align__(16) uint8_t lds[];
+  float *pb = (float *)lds;                           // [2][16][PP]
+  uint8_t *vb = lds + 2 * 16 * PP * 4;                // [2][64][VP]
+  __shared__ float ot[16][65];                        // the block's outputs [row][dimension] for the epilogue
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g = lane >> 4;
+  const int kvh = blockIdx.y, rt = blockIdx.z, d0 = blockIdx.x * 64;
+  const int G = a.nHead / a.nHeadKv;
+  const Step *st = a.step;
+  const int Bd = st->B, pos0 = st->pos0, nmax = pos0 + Bd;
+  // the rows of the tile: scores row offsets and positions (0: no row)
+  __shared__ long roff[16];
+  __shared__ int rnp[16];
+  if (tid < 16) {
+    const int r = rt * 16 + tid, b = r / G, h = kvh * G + r % G;
+    const bool live = r < nrows && b < Bd;
+    roff[tid] = live ? ((long)b * a.nHead + h) * a.sld : 0;
+    rnp[tid] = live ? pos0 + b + 1 : 0;
+  }
+  __syncthreads();
+  const uint8_t *vbase = (const uint8_t *)a.vcache + (((long)a.layer * a.nHeadKv + kvh) * a.hd + d0) * a.vstride * VB;
+  float4 preP[PL];
+  uint4 preV[VL];
+  auto fetch = [&](int t0) {
+    #pragma unroll
+    for (int k = 0; k < PL; k++) {
+      const int idx = k * 256 + tid, r = idx / (MMV_CT / 4), t = t0 + (idx % (MMV_CT / 4)) * 4;
+      const float *src = a.scores + roff[r] + t;
+      float w[4];
+      #pragma unroll
+      for (int e = 0; e < 4; e++) w[e] = t + e < rnp[r] ? src[e] : 0.f;
+      preP[k] = make_float4(w[0], w[1], w[2], w[3]);
+    }
+    #pragma unroll
+    for (int k = 0; k < VL; k++) {
+      const int idx = k * 256 + tid, d = idx / (MMV_CT * VB / 16), t = t0 + (idx % (MMV_CT * VB / 16)) * (16 / VB);
+      uint4 v = t < nmax ? *(const uint4 *)(vbase + ((long)d * a.vstride + t) * VB) : make_uint4(0, 0, 0, 0);
+      if (t < nmax && t + 16 / VB > nmax) {  // the pieces past the pass's last position: zeros
+        uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        #pragma unroll
+        for (int e = 0; e < 16 / VB; e++)
+          if (t + e >= nmax) {
+            if (F16KV) w[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
+            else w[e] = 0u;
+          }
+        v = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+      preV[k] = v;
+    }
+  };
+  auto store = [&](int buf) {
+    #pragma unroll
+    for (int k = 0; k < PL; k++) {
+      const int idx = k * 256 + tid, r = idx / (MMV_CT / 4), t = (idx % (MMV_CT / 4)) * 4;
+      *(float4 *)(pb + (buf * 16 + r) * PP + t) = preP[k];
+    }
+    #pragma unroll
+    for (int k = 0; k < VL; k++) {
+      const int idx = k * 256 + tid, d = idx / (MMV_CT * VB / 16), o = (idx % (MMV_CT * VB / 16)) * 16;
+      *(uint4 *)(vb + (buf * 64 + d) * VP + o) = preV[k];
+    }
+  };
+  int nrmax = 0;
+  #pragma unroll
+  for (int i = 0; i < 16; i++) nrmax = max(nrmax, rnp[i]);
+  if (nrmax == 0) return;  // (uniform)
+  const int nch = (nrmax + MMV_CT - 1) / MMV_CT;
+  f4 acc = {0.f, 0.f, 0.f, 0.f};
+  fetch(0);
+  for (int c = 0; c < nch; c++) {
+    __syncthreads();  // the buffer about to be written was last read two chunks ago
+    store(c & 1);
+    __syncthreads();
+    if (c + 1 < nch) fetch((c + 1) * MMV_CT);
+    const float *pr = pb + ((c & 1) * 16 + n16) * PP + g;
+    const uint8_t *vr = vb + ((c & 1) * 64 + wave * 16 + n16) * VP + g * VB;
+    #pragma unroll 8
+    for (int t = 0; t < MMV_CT; t += 4) {
+      const float pa = pr[t];
+      float vv;
+      if (F16KV) vv = h2f(*(const uint16_t *)(vr + t * 2));
+      else vv = *(const float *)(vr + t * 4);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vv, acc, 0, 0, 0);
+    }
+  }
+  // ---- epilogue: the outputs through LDS, then per row 64 dimensions on the 64 lanes of a wave (quantizeAct blocks of
+  // 32 consecutive dimensions sit in 32 consecutive lanes)
+  #pragma unroll
+  for (int v = 0; v < 4; v++) ot[4 * g + v][wave * 16 + n16] = acc[v];
+  __syncthreads();
+  for (int i = wave; i < 16; i += 4) {
+    if (rnp[i] == 0) continue;
+    const int r = rt * 16 + i, b = r / G, h = kvh * G + r % G, dim = d0 + lane, col = h * a.hd + dim;
+    float o = ot[i][lane];
+    if (a.gate) {  // gated attention output (src/model/forward-qwen35.js:103): o * sigmoid(gate), f64, stored f32
+      const double gv = (double)a.gate[(long)b * a.ldq + (long)h * a.qhs + dim];
+      o = (float)((double)o * (1.0 / (1.0 + exp(-gv))));
+    }
+    if (a.out) a.out[(long)b * a.ldo + col] = o;
+    quant_block32(o, col, a.act, b);
+  }
+}
+
+size_t attention_av_mm_lds(int kvF16) { return (size_t)2 * 16 * (MMV_CT + 4) * 4 + (size_t)2 * 64 * (MMV_CT * (kvF16 ? 2 : 4) + 16); }
 
 // nrows: query heads per KV head x the launch's tokens (rows r = b G + g: token b, query head kvh G + g).
 // 512 threads: waves 0-3 run the chains of chunk c while waves 4-7 store chunk c + 1 (V and probabilities) into the
@@ -1104,7 +1244,28 @@ AttnForm attention_form(int ctx, int hd) {
   // (verify passes at long contexts); ZEROLLM_ATTN_MM_B overrides the token count (tests)
   const char *em = getenv("ZEROLLM_ATTN_MM_B");
   f.mmMinB = em ? atoi(em) : ctx >= AVH_CTX ? 2 : 16;
+  // their weighted sums on the matrix cores from 16 tokens on: below that a KV head has too few 16-row tiles for the
+  // chains of 4-position steps to fill the GPU (measured with 9-token verify passes at 16K positions: the cycle of the
+  // 8B/0.6B pair 42.7 -> 46.4 ms)
+  const char *ea = getenv("ZEROLLM_ATTN_MMAV_B");
+  f.mmAvMinB = ea ? atoi(ea) : em ? f.mmMinB : 16;
+  // where the slice form's softmax row would not fit LDS (256-dimension heads beyond ~29,900 positions) every pass
+  // takes the matrix-core weighted sum, whose staging does not grow with the context: the exact chain at any context
+  if (f.split) {
+    f.split = false;
+    f.mmAvMinB = 1;
+  }
   return f;
+}
+
+template <bool F16KV>
+static void launch_av_mm_k(const AttnArgs &a, dim3 grid, int nrows, hipStream_t st) {
+  static bool attr = false;  // dynamic LDS above 64 KB must be requested per kernel
+  if (!attr) {
+    ZL_HIP(hipFuncSetAttribute((const void *)k_attn_av_mm<F16KV>, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024));
+    attr = true;
+  }
+  hipLaunchKernelGGL((k_attn_av_mm<F16KV>), grid, dim3(256), attention_av_mm_lds(F16KV), st, a, nrows);
 }
 
 template <int HD, bool F16KV>
@@ -1158,7 +1319,10 @@ void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
   // the per-head form for passes of several tokens at long contexts (single-token passes keep the four slice blocks
   // per head, which stage a quarter of the rows each, wherever their softmax row fits LDS); both give the same bits
   const bool head = !a.part && a.ctx > (B > 1 ? a.headCtx : a.head1Ctx);
-  const size_t lds = a.part ? attention_split_lds(a.hd, a.kvF16) : head ? attention_head_lds(a.hd) : attention_lds(a.ctx);
+  // the weighted-sum form: split, the matrix cores, or the lane chains (grouped, per-head or slice form); only the
+  // slice form's LDS grows with the context
+  const bool avmm = !a.part && a.qr && a.mmAvMinB > 0 && B >= a.mmAvMinB;
+  const size_t lds = a.part ? attention_split_lds(a.hd, a.kvF16) : avmm ? 0 : head ? attention_head_lds(a.hd) : attention_lds(a.ctx);
   ZL_REQUIRE(lds <= ATTN_LDS_MAX, ZL_ERR_UNSUPPORTED, "context too long for the attention kernel");
   ZL_REQUIRE(!a.part || a.nch * ATTN_SPLIT_C >= a.ctx, ZL_ERR_ARG, "attention: split partials below the context");
   ZL_REQUIRE(a.hd == 64 || a.hd == 128 || a.hd == 256, ZL_ERR_UNSUPPORTED, "attention: head_dim must be 64, 128 or 256");
@@ -1201,9 +1365,19 @@ void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
     ZL_HIP(hipGetLastError());
     return;
   }
+  if (avmm) {
+    // the probabilities of every row, then the weighted sums on the matrix cores, 16 rows x 64 dimensions per block
+    hipLaunchKernelGGL(k_attn_softmax_rows<true>, dim3(1, a.nHead, B), dim3(256), 0, st, a);
+    const int nrows = group * B;
+    const dim3 gw(a.hd / 64, a.nHeadKv, (nrows + 15) / 16);
+    if (a.kvF16) launch_av_mm_k<true>(a, gw, nrows, st);
+    else launch_av_mm_k<false>(a, gw, nrows, st);
+    ZL_HIP(hipGetLastError());
+    return;
+  }
   if (head && B > 1 && a.pinv) {
     // grouped by KV head: the softmax rows, then each V chunk staged once for a group's rows
-    hipLaunchKernelGGL(k_attn_softmax_rows, dim3(1, a.nHead, B), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k_attn_softmax_rows<false>, dim3(1, a.nHead, B), dim3(256), 0, st, a);
     const int nrows = (a.nHead / a.nHeadKv) * B;
     const dim3 gg(a.hd / AVG_DIMS, a.nHeadKv, (nrows + AVG_ROWS - 1) / AVG_ROWS);
     // 1024-byte chunks (512 f16 / 256 f32 positions): each chunk's chain is long enough to cover the next chunk's loads

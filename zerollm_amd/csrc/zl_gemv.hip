@@ -79,10 +79,15 @@ static int gemm_max_m() {
   return m < GEMM_MIN_M ? 0 : std::min(m, 64);
 }
 
-// Launches of at least GEMM_MIN_M tokens of the formats the GEMM takes, without a fused prologue.
+// Launches of at least GEMM_MIN_M tokens (ZEROLLM_GEMM_MINM moves it, for measurements) of the formats the GEMM takes,
+// without a fused prologue.
+static int gemm_min_m() {
+  const char *e = getenv("ZEROLLM_GEMM_MINM");
+  return e ? std::max(1, atoi(e)) : GEMM_MIN_M;
+}
 bool gemm_takes(const GemvArgs &a) {
   const int t = a.seg[0].m.type;
-  return gemm_max_m() > 0 && a.M >= GEMM_MIN_M && !a.xf && (t == T_Q8_0 || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K);
+  return gemm_max_m() > 0 && a.M >= gemm_min_m() && !a.xf && (t == T_Q8_0 || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K);
 }
 
 long gemv_part_need(const GemvArgs &a) {

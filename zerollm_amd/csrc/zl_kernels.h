@@ -137,7 +137,7 @@ struct AttnArgs {
   int headCtx, head1Ctx;
   // passes of at least mmMinB tokens take the matrix-core score dots (k_attn_prep + k_attn_scores_mm), which need qr,
   // the pass's normed and rotated query rows [B][nHead][hd] f32
-  int mmMinB;
+  int mmMinB, mmAvMinB;  // ... and at least mmAvMinB tokens the matrix-core weighted sums (k_attn_av_mm)
   float *qr;
 };
 constexpr int ATTN_SPLIT_C = 256;  // positions per chunk of the position-split weighted sum
@@ -287,7 +287,7 @@ size_t attention_split_lds(int hd, int kvF16);
 // The attention form of a model, decided once at load from its context and head size (the environment overrides
 // ZEROLLM_ATTN_HEAD_CTX and ZEROLLM_ATTN_HEAD1_CTX move the thresholds, for tests): headCtx / head1Ctx as in AttnArgs
 // (INT_MAX: never), split = whether the model needs the position-split weighted sum (its exact chain would not fit).
-struct AttnForm { int headCtx, head1Ctx, mmMinB; bool split; };
+struct AttnForm { int headCtx, head1Ctx, mmMinB, mmAvMinB; bool split; };
 AttnForm attention_form(int ctx, int hd);
 void launch_norm_quant(const float *x, int ldx, int row0, int nrows, const float *w, double eps, int n, int npad,
                        const Act &act, hipStream_t st);
