@@ -381,6 +381,36 @@ def test_per_head_weighted_sum_equals_slice_form_and_oracle(gpu, tiny_files, mon
     assert exact >= 0.999 and np.abs(rows["head"] - want).max() <= 1e-6 * np.abs(want).max(), exact
 
 
+@pytest.mark.parametrize("kv", ["f16", "f32"])
+def test_matrix_core_slice_form_equals_lane_chains_and_oracle(gpu, tiny_files, monkeypatch, kv):
+    """The slice form's weighted sums with the chains on the matrix cores (k_attn_av_mfma: the default from 4096
+    positions, forced here by ZEROLLM_ATTN_AVMF=1) and on the lanes (k_attn_av, ZEROLLM_ATTN_AVMF=0) give the same rows
+    bit for bit, for single-token passes and a 6-token pass at a 1300-position context (three staged chunks), and match
+    the oracle."""
+    toks = prompt(1210, seed=29)
+    ref = O.OracleModel(tiny_files[0], ctx=1300, kv=kv)
+    for t in toks[:-6]:
+        ref.forward(t, logits=False)
+    want = np.stack([ref.forward(t) for t in toks[-6:]])
+    rows = {}
+    for form in ("mfma", "lanes"):
+        monkeypatch.setenv("ZEROLLM_ATTN_AVMF", "1" if form == "mfma" else "0")
+        print(f"case slice form {form} kv {kv}", flush=True)
+        m = Mdl.HipModel.load(tiny_files[0], ctx=1300, kv=kv)
+        for i in range(0, 1200, 16):
+            m.forward_batch(toks[i:i + 16], logits="none")
+        m.forward_batch(toks[1200:1204], logits="none")
+        single = np.stack([m.forward(t).copy() for t in toks[-6:]])
+        m.truncate(1204)
+        batched = m.forward_batch(toks[-6:], logits="all").copy()
+        m.close()
+        assert (single.view(np.uint32) == batched.view(np.uint32)).all(), form
+        rows[form] = single
+    assert (rows["mfma"].view(np.uint32) == rows["lanes"].view(np.uint32)).all()
+    exact = np.mean(rows["mfma"].view(np.uint32) == want.view(np.uint32))
+    assert exact >= 0.999 and np.abs(rows["mfma"] - want).max() <= 1e-6 * np.abs(want).max(), exact
+
+
 def test_16k_context_verify_width_9_equals_sequential_and_rolls_back(gpu, tiny_files):
     """At a 16384-token context a 9-row verify pass (k = 8) equals nine single-token passes bit for bit, and after a
     rollback to 3 accepted rows the next pass equals a fresh continuation (size-independent checks of the long-context

@@ -566,6 +566,206 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
   }
 }
 
+// ---- k_attn_av's weighted sum with the chains on the matrix cores: v_mfma_f32_16x16x4_f32 is four sequential fmaf in k
+// order (measured), so a chain of MFMAs whose A operand holds the row's probabilities in row 0 (rows 1-15 zero) and
+// whose B operand holds V of 16 dimensions computes the position-order f32 chain of every dimension bit for bit. A
+// dependent MFMA issues every 32 cycles (8 per position, where a dependent v_fma_mix_f32 takes 9) only while the wave
+// issues nothing else but LDS reads between them (a VALU instruction there costs ~12 cycles: measured), so V is staged
+// in LDS already converted to f32 and the chain waves only read and multiply.
+// One block per (32-dim slice, query head, token), as k_attn_av: the same softmax (the same max, the exponentials
+// summed in the same thread order, p = f32(f32(e) * inv)); then waves 0-1 run the chains of dimensions 16 w .. 16 w + 15
+// of chunk c while waves 2-3 stage chunk c + 1 (V as f32, and its probabilities, whose exponentials they compute again
+// from the scores: the same bits) and request chunk c + 2. One barrier per chunk; LDS does not grow with the context.
+// LDS holds V and the probabilities by position mod 4 (section k holds positions 4 m + k, m ascending), so the 16
+// lanes of MFMA k-group g read their own positions contiguously, 4 MFMAs' operands per 16-byte read.
+constexpr int AVM_CT = 512;                 // positions per chunk
+constexpr int AVM_SF = AVM_CT / 4 + 4;      // floats of one position section (16-byte pad)
+constexpr int AVM_UNIT = 32;                // positions per pipelined step of a chain (8 MFMAs)
+constexpr int AVM_MAX_CTX = 2 * 32 * 4 * AVM_SF;  // contexts this form takes: the scores row in the ring's LDS
+size_t attention_av_mfma_lds() { return (size_t)(2 * AV_DIMS * 4 + 2 * 4 + 1) * AVM_SF * 4; }
+
+template <bool F16KV>
+__global__ __launch_bounds__(256) void k_attn_av_mfma(const AttnArgs a) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  constexpr int VB = F16KV ? 2 : 4;
+  constexpr int CT = AVM_CT, SF = AVM_SF;
+  constexpr int EPP = 16 / VB;                      // positions per 16-byte piece
+  constexpr int PPR = CT / EPP;                     // pieces per dimension row of a chunk
+  constexpr int PLT = AV_DIMS * PPR / 128;          // pieces per producer thread per chunk (16 f16, 32 f32)
+  constexpr int SPT = CT / 128;                     // probabilities per producer thread per chunk
+  constexpr int NU = CT / AVM_UNIT;                 // units per chunk
+  float *vk = (float *)lds;                         // [2][AV_DIMS][4][SF]: V of position 4 m + k, dimension j at [j][k][m]
+  float *pk = vk + 2 * AV_DIMS * 4 * SF;            // [2][4][SF]: p of position 4 m + k at [k][m]
+  float *zb = pk + 2 * 4 * SF;                      // [SF] zeros: the A operand of rows 1-15
+  __shared__ double redd[4];
+  __shared__ float redf[4];
+  __shared__ float ot[AV_DIMS];
+  const int slice = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int n16 = lane & 15, g = lane >> 4;
+  const int hd = a.hd, kvh = h / (a.nHead / a.nHeadKv);
+  const uint8_t *vbase = (const uint8_t *)a.vcache + (((long)a.layer * a.nHeadKv + kvh) * hd + (long)slice * AV_DIMS) * a.vstride * VB;
+  const float *srow = a.scores + ((long)b * a.nHead + h) * a.sld;
+  const bool producer = wave >= 2;
+  const int pt = tid - 128;                         // producer thread 0..127
+  uint4 pre[PLT];
+  float sp[SPT];
+  int npos = 0;
+  double m = 0.0, inv = 0.0;
+  // chunk c's V pieces and scores, from in-range rows and positions (what lies past the last position is zeroed when
+  // the chunk is staged)
+  auto fetch = [&](int c, int lim) {
+    #pragma unroll
+    for (int k = 0; k < PLT; k++) {
+      const int idx = k * 128 + pt, dim = idx / PPR, t = c * CT + (idx % PPR) * EPP;
+      pre[k] = *(const uint4 *)(vbase + ((long)dim * a.vstride + (t < lim ? t : 0)) * VB);
+    }
+    #pragma unroll
+    for (int i = 0; i < SPT; i++) {
+      const int t = c * CT + i * 128 + pt;
+      sp[i] = srow[t < lim ? t : 0];
+    }
+  };
+  // producers: chunk c into slot c & 1 (V as f32, p = f32(f32(e) * inv), zeros past the last position)
+  auto stage = [&](int c) {
+    float *vs = vk + (c & 1) * AV_DIMS * 4 * SF;
+    #pragma unroll
+    for (int k = 0; k < PLT; k++) {
+      const int idx = k * 128 + pt, dim = idx / PPR, pc = idx % PPR, t = c * CT + pc * EPP;
+      const uint32_t w[4] = {pre[k].x, pre[k].y, pre[k].z, pre[k].w};
+      float f[EPP];
+      #pragma unroll
+      for (int e = 0; e < EPP; e++) {
+        const float x = F16KV ? h2f((uint16_t)((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffff))) : __uint_as_float(w[e]);
+        f[e] = t + e < npos ? x : 0.f;
+      }
+      float *drow = vs + dim * 4 * SF;
+      #pragma unroll
+      for (int q = 0; q < 4; q++) {
+        if (F16KV) *(float2 *)(drow + q * SF + 2 * pc) = make_float2(f[q], f[q + 4]);  // positions t + q, t + 4 + q
+        else drow[q * SF + pc] = f[q];                                                 // position t + q
+      }
+    }
+    float *ps = pk + (c & 1) * 4 * SF;
+    #pragma unroll
+    for (int i = 0; i < SPT; i++) {
+      const int tl = i * 128 + pt, t = c * CT + tl;
+      const double e = exp((double)sp[i] - m);
+      ps[(tl & 3) * SF + (tl >> 2)] = t < npos ? (float)((double)(float)e * inv) : 0.f;
+    }
+  };
+  if (producer) fetch(0, a.ctx);
+  const Step *st = a.step;
+  if (b >= st->B) return;
+  npos = st->pos0 + b + 1;
+  const int nch = (npos + CT - 1) / CT;
+  const int nend = (npos + AVM_UNIT - 1) / AVM_UNIT * AVM_UNIT;  // positions the chains run
+  // ---- softmax (src/compute/ref-kernels.js:313-320), k_attn_av's arithmetic on the scores row, which lies in the
+  // ring's LDS until the first chunk is staged: thread tid takes t = tid + 256 k, its exponentials added in k order
+  float *sc = vk;
+  float mx = -INFINITY;
+  for (int t0 = 0; t0 < npos; t0 += 64 * 256) {  // 64 loads per thread in flight at a time (a clamped load reads
+    float v[64];                                 // position 0, which leaves the maximum unchanged)
+    #pragma unroll
+    for (int k = 0; k < 64; k++) { const int t = t0 + k * 256 + tid; v[k] = srow[t < npos ? t : 0]; }
+    #pragma unroll
+    for (int k = 0; k < 64; k++) {
+      const int t = t0 + k * 256 + tid;
+      if (t < npos) sc[t] = v[k];
+      mx = fmaxf(mx, v[k]);
+    }
+  }
+  mx = group_fmax(mx, 64);
+  if (lane == 0) redf[wave] = mx;
+  __syncthreads();
+  m = (double)fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
+  double sum = 0.0;
+  for (int t0 = tid; t0 < npos; t0 += 4 * 256) {
+    double e[4];
+    #pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int t = t0 + 256 * k;
+      e[k] = exp((double)sc[t < npos ? t : t0] - m);
+    }
+    #pragma unroll
+    for (int k = 0; k < 4; k++)
+      if (t0 + 256 * k < npos) sum += e[k];
+  }
+  sum = wave_sum_xor(sum, 64);
+  if (lane == 0) redd[wave] = sum;
+  __syncthreads();  // also: every read of the scores row is done before chunk 0 is staged over it
+  inv = 1.0 / ((redd[0] + redd[1]) + (redd[2] + redd[3]));
+  if (producer) {
+    stage(0);
+    if (nch > 1) fetch(1, npos);
+  }
+  for (int i = tid; i < SF; i += 256) zb[i] = 0.f;
+  __syncthreads();
+  // ---- chains (waves 0-1) / staging (waves 2-3)
+  f4 acc = {0.f, 0.f, 0.f, 0.f};
+  auto mfma8 = [&](const f4 &p0, const f4 &p1, const f4 &v0, const f4 &v1) {
+    #pragma unroll
+    for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p0[i], v0[i], acc, 0, 0, 0);
+    #pragma unroll
+    for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p1[i], v1[i], acc, 0, 0, 0);
+  };
+  for (int c = 0; c < nch; c++) {
+    if (producer) {
+      if (c + 1 < nch) {
+        stage(c + 1);
+        if (c + 2 < nch) fetch(c + 2, npos);
+      }
+    } else {
+      // unit u: the 8 MFMAs of positions c CT + 32 u .. + 31; lane group g supplies positions 4 m + g, m = 8 u .. 8 u + 7
+      // (A: lanes of row 0 read the probabilities, the others the zeros). Units two at a time on two operand sets, the
+      // next unit's reads ahead of the current unit's MFMAs; a full chunk in straight-line code (constant offsets)
+      const float *vr = vk + ((c & 1) * AV_DIMS + wave * 16 + n16) * 4 * SF + g * SF;
+      const float *pr = n16 == 0 ? pk + ((c & 1) * 4 + g) * SF : zb;
+      auto ld = [&](const float *q, int off) { return *(const f4 *)(q + off); };
+      if (c * CT + CT <= nend) {
+        f4 a0 = ld(pr, 0), a1 = ld(pr, 4), a2 = ld(vr, 0), a3 = ld(vr, 4);
+        #pragma unroll
+        for (int u = 0; u < NU; u += 2) {
+          const f4 b0 = ld(pr, 8 * u + 8), b1 = ld(pr, 8 * u + 12), b2 = ld(vr, 8 * u + 8), b3 = ld(vr, 8 * u + 12);
+          __builtin_amdgcn_sched_barrier(0);
+          mfma8(a0, a1, a2, a3);
+          if (u + 2 < NU) { a0 = ld(pr, 8 * u + 16); a1 = ld(pr, 8 * u + 20); a2 = ld(vr, 8 * u + 16); a3 = ld(vr, 8 * u + 20); }
+          __builtin_amdgcn_sched_barrier(0);
+          mfma8(b0, b1, b2, b3);
+        }
+      } else {
+        const int nu = (nend - c * CT) / AVM_UNIT;
+        f4 a0 = ld(pr, 0), a1 = ld(pr, 4), a2 = ld(vr, 0), a3 = ld(vr, 4);
+        int u = 0;
+        for (; u + 2 <= nu; u += 2) {
+          const f4 b0 = ld(pr, 8 * u + 8), b1 = ld(pr, 8 * u + 12), b2 = ld(vr, 8 * u + 8), b3 = ld(vr, 8 * u + 12);
+          __builtin_amdgcn_sched_barrier(0);
+          mfma8(a0, a1, a2, a3);
+          const int un = min(u + 2, nu - 1);  // (a re-read of the last unit when past it)
+          a0 = ld(pr, 8 * un); a1 = ld(pr, 8 * un + 4); a2 = ld(vr, 8 * un); a3 = ld(vr, 8 * un + 4);
+          __builtin_amdgcn_sched_barrier(0);
+          mfma8(b0, b1, b2, b3);
+        }
+        if (u < nu) mfma8(a0, a1, a2, a3);
+      }
+    }
+    __syncthreads();
+  }
+  // ---- epilogue: row 0's outputs (element 0 of lanes 0-15 of each chain wave) to lanes 0-31 of wave 0
+  if (!producer && g == 0) ot[wave * 16 + n16] = acc[0];
+  __syncthreads();
+  if (wave == 0 && lane < AV_DIMS) {
+    const int col = h * hd + slice * AV_DIMS + lane;
+    float o = ot[lane];
+    if (a.gate) {  // gated attention output (src/model/forward-qwen35.js:103): o * sigmoid(gate), f64, stored f32
+      const double gv = (double)a.gate[(long)b * a.ldq + (long)h * a.qhs + slice * AV_DIMS + lane];
+      o = (float)((double)o * (1.0 / (1.0 + exp(-gv))));
+    }
+    if (a.out) a.out[(long)b * a.ldo + col] = o;
+    quant_block32(o, col, a.act, b);
+  }
+}
+
 // ---- the same weighted sum for long contexts, one block per (query head, token) over all HD dimensions. k_attn_av keeps
 // the block's softmax row in LDS, which at 16K positions leaves room for one block per CU, and its four slice blocks of
 // a head hold four copies. Here the exponentials are written back over the head's scores (one block per row, so no
@@ -1255,6 +1455,10 @@ AttnForm attention_form(int ctx, int hd) {
     f.split = false;
     f.mmAvMinB = 1;
   }
+  // the slice form's chains on the matrix cores from AV_BIG_CTX positions, where the lane-chain form's LDS already
+  // holds a CU to one block (ZEROLLM_ATTN_AVMF=1 / 0: at any context / never; the same bits)
+  const char *ev = getenv("ZEROLLM_ATTN_AVMF");
+  f.avmf = ctx <= AVM_MAX_CTX && (ev ? ev[0] == '1' : ctx >= AV_BIG_CTX);
   return f;
 }
 
@@ -1302,6 +1506,16 @@ static void launch_av_k(const AttnArgs &a, dim3 grid, size_t lds, hipStream_t st
   const size_t big = attention_lds(a.ctx, AV_ROW_BIG);
   if (a.ctx >= AV_BIG_CTX && big <= ATTN_LDS_MAX) launch_av_rows<F16KV, AV_ROW_BIG>(a, grid, big, st);
   else launch_av_rows<F16KV, AV_ROW>(a, grid, lds, st);
+}
+
+template <bool F16KV>
+static void launch_av_mfma_k(const AttnArgs &a, dim3 grid, size_t lds, hipStream_t st) {
+  static size_t attr = 64 * 1024;  // dynamic LDS above 64 KB must be requested per kernel
+  if (lds > attr) {
+    ZL_HIP(hipFuncSetAttribute((const void *)k_attn_av_mfma<F16KV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    attr = lds;
+  }
+  hipLaunchKernelGGL((k_attn_av_mfma<F16KV>), grid, dim3(256), lds, st, a);
 }
 
 template <bool F16KV>
@@ -1397,8 +1611,15 @@ void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
     return;
   }
   dim3 ga(a.hd / AV_DIMS, a.nHead, B);
-  if (a.kvF16) launch_av_k<true>(a, ga, lds, st);
-  else launch_av_k<false>(a, ga, lds, st);
+  if (a.avmf) {
+    const size_t lm = attention_av_mfma_lds();
+    if (a.kvF16) launch_av_mfma_k<true>(a, ga, lm, st);
+    else launch_av_mfma_k<false>(a, ga, lm, st);
+  } else if (a.kvF16) {
+    launch_av_k<true>(a, ga, lds, st);
+  } else {
+    launch_av_k<false>(a, ga, lds, st);
+  }
   ZL_HIP(hipGetLastError());
 }
 

@@ -139,6 +139,7 @@ struct AttnArgs {
   // the pass's normed and rotated query rows [B][nHead][hd] f32
   int mmMinB, mmAvMinB;  // ... and at least mmAvMinB tokens the matrix-core weighted sums (k_attn_av_mm)
   float *qr;
+  int avmf;  // the slice form's chains on the matrix cores (k_attn_av_mfma) instead of the lanes (k_attn_av)
 };
 constexpr int ATTN_SPLIT_C = 256;  // positions per chunk of the position-split weighted sum
 
@@ -287,7 +288,7 @@ size_t attention_split_lds(int hd, int kvF16);
 // The attention form of a model, decided once at load from its context and head size (the environment overrides
 // ZEROLLM_ATTN_HEAD_CTX and ZEROLLM_ATTN_HEAD1_CTX move the thresholds, for tests): headCtx / head1Ctx as in AttnArgs
 // (INT_MAX: never), split = whether the model needs the position-split weighted sum (its exact chain would not fit).
-struct AttnForm { int headCtx, head1Ctx, mmMinB, mmAvMinB; bool split; };
+struct AttnForm { int headCtx, head1Ctx, mmMinB, mmAvMinB; bool split, avmf; };
 AttnForm attention_form(int ctx, int hd);
 void launch_norm_quant(const float *x, int ldx, int row0, int nrows, const float *w, double eps, int n, int npad,
                        const Act &act, hipStream_t st);

@@ -232,6 +232,7 @@ struct zl_model {
   double *attnInv = nullptr;   // [maxBatch][n_head] 1 / sum of exponentials (grouped weighted sum)
   int attnNch = 0;
   int attnHeadCtx = 0, attnHead1Ctx = 0, attnMmMinB = 0, attnMmAvMinB = 0;  // attention form thresholds, at load
+  bool attnAvmf = false;
   float *qr = nullptr;  // the pass's normed and rotated query rows [maxBatch][n_head][head_dim] (matrix-core scores)
   zl::Act act{};    // quantised input of the q/k/v, attention-output and gate/up GEMVs
   zl::Act act2{};   // quantised FFN hidden state (written by the gate/up GEMV, read by the down GEMV)
@@ -416,6 +417,7 @@ static void finish_model(zl_model *m, const float *ropeFreqs) {
   m->attnHead1Ctx = form.head1Ctx;
   m->attnMmMinB = form.mmMinB;
   m->attnMmAvMinB = form.mmAvMinB;
+  m->attnAvmf = form.avmf;
   const int half = c.n_rot / 2;
   // RoPE tables exactly as ropeTables (src/compute/ref-kernels.js:329-342), in f64 on the host, stored f32
   std::vector<float> cs((size_t)m->ctx * half), sn((size_t)m->ctx * half);
@@ -715,6 +717,7 @@ static void enqueue_forward(zl_model *m, int B, int want) {
       aa.part = m->attnPart; aa.nch = m->attnNch; aa.pinv = m->attnInv;
       aa.headCtx = m->attnHeadCtx; aa.head1Ctx = m->attnHead1Ctx;
       aa.mmMinB = m->attnMmMinB; aa.mmAvMinB = m->attnMmAvMinB; aa.qr = m->qr;
+      aa.avmf = m->attnAvmf ? 1 : 0;
       launch_attention(aa, B, m->st);
       gemv_group(m, {{&L.wo, nullptr, 0, nullptr}}, B, EPI_RESID, m->act, m->act.f, m->act.ld);
     }
