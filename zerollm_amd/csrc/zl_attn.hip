@@ -581,7 +581,8 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
 constexpr int AVM_CT = 512;                 // positions per chunk
 constexpr int AVM_SF = AVM_CT / 4 + 4;      // floats of one position section (16-byte pad)
 constexpr int AVM_UNIT = 32;                // positions per pipelined step of a chain (8 MFMAs)
-constexpr int AVM_MAX_CTX = 2 * 32 * 4 * AVM_SF;  // contexts this form takes: the scores row in the ring's LDS
+constexpr int AVM_NK = 72;                  // scores per thread the softmax keeps in registers
+constexpr int AVM_MAX_CTX = AVM_NK * 256;   // contexts this form takes (18432 positions)
 size_t attention_av_mfma_lds() { return (size_t)(2 * AV_DIMS * 4 + 2 * 4 + 1) * AVM_SF * 4; }
 
 template <bool F16KV>
@@ -614,20 +615,22 @@ __global__ __launch_bounds__(256) void k_attn_av_mfma(const AttnArgs a) {
   double m = 0.0, inv = 0.0;
   // chunk c's V pieces and scores, from in-range rows and positions (what lies past the last position is zeroed when
   // the chunk is staged)
-  auto fetch = [&](int c, int lim) {
+  auto fetch_v = [&](int c, int lim) {
     #pragma unroll
     for (int k = 0; k < PLT; k++) {
       const int idx = k * 128 + pt, dim = idx / PPR, t = c * CT + (idx % PPR) * EPP;
       pre[k] = *(const uint4 *)(vbase + ((long)dim * a.vstride + (t < lim ? t : 0)) * VB);
     }
+  };
+  auto fetch_s = [&](int c, int lim) {
     #pragma unroll
     for (int i = 0; i < SPT; i++) {
       const int t = c * CT + i * 128 + pt;
       sp[i] = srow[t < lim ? t : 0];
     }
   };
-  // producers: chunk c into slot c & 1 (V as f32, p = f32(f32(e) * inv), zeros past the last position)
-  auto stage = [&](int c) {
+  // producers: chunk c into slot c & 1: V as f32 (zeros past the last position) ...
+  auto stage_v = [&](int c) {
     float *vs = vk + (c & 1) * AV_DIMS * 4 * SF;
     #pragma unroll
     for (int k = 0; k < PLT; k++) {
@@ -646,6 +649,9 @@ __global__ __launch_bounds__(256) void k_attn_av_mfma(const AttnArgs a) {
         else drow[q * SF + pc] = f[q];                                                 // position t + q
       }
     }
+  };
+  // ... and its probabilities p = f32(f32(e) * inv) (zeros past the last position)
+  auto stage_p = [&](int c) {
     float *ps = pk + (c & 1) * 4 * SF;
     #pragma unroll
     for (int i = 0; i < SPT; i++) {
@@ -654,50 +660,52 @@ __global__ __launch_bounds__(256) void k_attn_av_mfma(const AttnArgs a) {
       ps[(tl & 3) * SF + (tl >> 2)] = t < npos ? (float)((double)(float)e * inv) : 0.f;
     }
   };
-  if (producer) fetch(0, a.ctx);
+  if (producer) {
+    fetch_v(0, a.ctx);
+    fetch_s(0, a.ctx);
+  }
   const Step *st = a.step;
   if (b >= st->B) return;
   npos = st->pos0 + b + 1;
   const int nch = (npos + CT - 1) / CT;
   const int nend = (npos + AVM_UNIT - 1) / AVM_UNIT * AVM_UNIT;  // positions the chains run
-  // ---- softmax (src/compute/ref-kernels.js:313-320), k_attn_av's arithmetic on the scores row, which lies in the
-  // ring's LDS until the first chunk is staged: thread tid takes t = tid + 256 k, its exponentials added in k order
-  float *sc = vk;
-  float mx = -INFINITY;
-  for (int t0 = 0; t0 < npos; t0 += 64 * 256) {  // 64 loads per thread in flight at a time (a clamped load reads
-    float v[64];                                 // position 0, which leaves the maximum unchanged)
-    #pragma unroll
-    for (int k = 0; k < 64; k++) { const int t = t0 + k * 256 + tid; v[k] = srow[t < npos ? t : 0]; }
-    #pragma unroll
-    for (int k = 0; k < 64; k++) {
-      const int t = t0 + k * 256 + tid;
-      if (t < npos) sc[t] = v[k];
-      mx = fmaxf(mx, v[k]);
-    }
+  // ---- softmax (src/compute/ref-kernels.js:313-320), k_attn_av's arithmetic: thread tid takes t = tid + 256 k, its
+  // exponentials added in k order. The scores stay in registers (-inf past the last position: exp gives +0, which
+  // leaves the sum unchanged), so the producers stage chunk 0's V meanwhile.
+  float sv[AVM_NK];
+  #pragma unroll
+  for (int k = 0; k < AVM_NK; k++) { const int t = k * 256 + tid; sv[k] = srow[t < npos ? t : 0]; }
+  if (producer) {
+    stage_v(0);
+    if (nch > 1) fetch_v(1, npos);
   }
+  #pragma unroll
+  for (int k = 0; k < AVM_NK; k++) sv[k] = k * 256 + tid < npos ? sv[k] : -INFINITY;
+  float mx = -INFINITY;
+  #pragma unroll
+  for (int k = 0; k < AVM_NK; k++) mx = fmaxf(mx, sv[k]);
   mx = group_fmax(mx, 64);
   if (lane == 0) redf[wave] = mx;
   __syncthreads();
   m = (double)fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
   double sum = 0.0;
-  for (int t0 = tid; t0 < npos; t0 += 4 * 256) {
-    double e[4];
-    #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const int t = t0 + 256 * k;
-      e[k] = exp((double)sc[t < npos ? t : t0] - m);
+  #pragma unroll
+  for (int k0 = 0; k0 < AVM_NK; k0 += 8) {
+    if (k0 * 256 < npos) {  // (uniform)
+      double e[8];
+      #pragma unroll
+      for (int k = 0; k < 8; k++) e[k] = exp((double)sv[k0 + k] - m);
+      #pragma unroll
+      for (int k = 0; k < 8; k++) sum += e[k];
     }
-    #pragma unroll
-    for (int k = 0; k < 4; k++)
-      if (t0 + 256 * k < npos) sum += e[k];
   }
   sum = wave_sum_xor(sum, 64);
   if (lane == 0) redd[wave] = sum;
-  __syncthreads();  // also: every read of the scores row is done before chunk 0 is staged over it
+  __syncthreads();
   inv = 1.0 / ((redd[0] + redd[1]) + (redd[2] + redd[3]));
   if (producer) {
-    stage(0);
-    if (nch > 1) fetch(1, npos);
+    stage_p(0);
+    if (nch > 1) fetch_s(1, npos);
   }
   for (int i = tid; i < SF; i += 256) zb[i] = 0.f;
   __syncthreads();
@@ -712,8 +720,12 @@ __global__ __launch_bounds__(256) void k_attn_av_mfma(const AttnArgs a) {
   for (int c = 0; c < nch; c++) {
     if (producer) {
       if (c + 1 < nch) {
-        stage(c + 1);
-        if (c + 2 < nch) fetch(c + 2, npos);
+        stage_v(c + 1);
+        stage_p(c + 1);
+        if (c + 2 < nch) {
+          fetch_v(c + 2, npos);
+          fetch_s(c + 2, npos);
+        }
       }
     } else {
       // unit u: the 8 MFMAs of positions c CT + 32 u .. + 31; lane group g supplies positions 4 m + g, m = 8 u .. 8 u + 7
@@ -954,96 +966,126 @@ size_t attention_head_lds(int hd) { return (size_t)2 * hd * AV_PITCH + 2 * 256 *
 constexpr int AVG_ROWS = 8;   // rows (query head, token) per block of the grouped weighted sum
 constexpr int AVG_DIMS = 32;  // dimensions per block
 
+constexpr int SMR_T = 512;     // threads of k_attn_softmax_rows
+constexpr int SMR_RP = 4096;   // positions per round of its sum
+constexpr int SMR_NK = 40;     // positions per thread kept in registers (20480 per row)
 template <bool NORM>
-__global__ __launch_bounds__(256) void k_attn_softmax_rows(const AttnArgs a) {
+__global__ __launch_bounds__(SMR_T) void k_attn_softmax_rows(const AttnArgs a) {
+  // SMR_T threads: the exponentials on two waves per SIMD. The sum keeps k_attn_av's order (slot s = t mod 256 adds
+  // its positions s, s + 256, ... in order, then the 64-lane butterfly and (w0 + w1) + (w2 + w3)): each round of
+  // SMR_RP positions parks its exponentials in LDS by slot, and the 256 slot threads add them in position order.
+  constexpr int KR = SMR_RP / SMR_T;          // positions per thread per round (8)
+  constexpr int NQ = SMR_NK / KR;             // rounds kept in registers
+  __shared__ double ex[SMR_RP];               // a round's exponentials at [k][s], t = r0 + 256 k + s
   __shared__ double redd[4];
-  __shared__ float redf[4];
+  __shared__ float redf[SMR_T / 64];
   const int h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const Step *st = a.step;
   if (b >= st->B) return;
   const int npos = st->pos0 + b + 1;
   float *srow = a.scores + ((long)b * a.nHead + h) * a.sld;
+  // thread tid holds positions tid + SMR_T k (a clamped load reads position 0, which leaves the maximum unchanged)
+  float v[SMR_NK];
+  #pragma unroll
+  for (int k = 0; k < SMR_NK; k++) { const int t = tid + SMR_T * k; v[k] = srow[t < npos ? t : 0]; }
   float mx = -INFINITY;
-  for (int t0 = tid; t0 < npos; t0 += 16 * 256) {  // 16 loads per thread in flight at a time
-    float v[16];
-    #pragma unroll
-    for (int k = 0; k < 16; k++) { const int t = t0 + 256 * k; v[k] = srow[t < npos ? t : t0]; }
-    #pragma unroll
-    for (int k = 0; k < 16; k++) mx = fmaxf(mx, v[k]);  // (a clamped reload repeats a value already counted)
-  }
+  #pragma unroll
+  for (int k = 0; k < SMR_NK; k++) mx = fmaxf(mx, v[k]);
+  for (int t = SMR_NK * SMR_T + tid; t < npos; t += SMR_T) mx = fmaxf(mx, srow[t]);
   mx = group_fmax(mx, 64);
   if (lane == 0) redf[wave] = mx;
   __syncthreads();
-  const double m = (double)fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
+  float mf = redf[0];
+  #pragma unroll
+  for (int w = 1; w < SMR_T / 64; w++) mf = fmaxf(mf, redf[w]);
+  const double m = (double)mf;
+  // round q: thread tid computes t = q SMR_RP + tid + SMR_T i (slot tid mod 256, k = 2 i + tid / 256)
   double sum = 0.0;
-  for (int t0 = tid; t0 < npos; t0 += 16 * 256) {  // positions tid + 256 j added in j order, as k_attn_av does
-    float v[16];
-    #pragma unroll
-    for (int k = 0; k < 16; k++) { const int t = t0 + 256 * k; v[k] = srow[t < npos ? t : t0]; }
-    #pragma unroll
-    for (int q = 0; q < 16; q += 4) {
-      double e[4];
+  auto slot_add = [&]() {
+    __syncthreads();
+    if (tid < 256) {
       #pragma unroll
-      for (int k = 0; k < 4; k++) e[k] = exp((double)v[q + k] - m);
+      for (int k = 0; k < SMR_RP / 256; k++) sum += ex[k * 256 + tid];  // +0 past the last position: no change
+    }
+    __syncthreads();
+  };
+  #pragma unroll
+  for (int q = 0; q < NQ; q++) {
+    if (q * SMR_RP < npos) {  // (uniform)
       #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const int t = t0 + 256 * (q + k);
-        if (t < npos) { srow[t] = (float)e[k]; sum += e[k]; }
+      for (int i = 0; i < KR; i++) {
+        const int k = q * KR + i, t = tid + SMR_T * k;
+        const double e = exp((double)v[k] - m);
+        ex[(2 * i + (tid >> 8)) * 256 + (tid & 255)] = t < npos ? e : 0.0;
+        v[k] = (float)e;
+        if (!NORM && t < npos) srow[t] = v[k];
       }
+      slot_add();
     }
   }
-  sum = wave_sum_xor(sum, 64);
-  if (lane == 0) redd[wave] = sum;
+  for (int r0 = SMR_NK * SMR_T; r0 < npos; r0 += SMR_RP) {  // positions past the registers
+    #pragma unroll
+    for (int i = 0; i < KR; i++) {
+      const int t = r0 + tid + SMR_T * i;
+      const double e = t < npos ? exp((double)srow[t] - m) : 0.0;
+      ex[(2 * i + (tid >> 8)) * 256 + (tid & 255)] = e;
+      if (t < npos) srow[t] = (float)e;
+    }
+    slot_add();
+  }
+  if (tid < 256) {
+    sum = wave_sum_xor(sum, 64);
+    if (lane == 0) redd[wave] = sum;
+  }
   __syncthreads();
   const double inv = 1.0 / ((redd[0] + redd[1]) + (redd[2] + redd[3]));
   if (!NORM) {
     if (tid == 0) a.pinv[(long)b * a.nHead + h] = inv;
     return;
   }
-  // the probabilities themselves, p = f32(e * inv), each thread over the positions it wrote
-  for (int t0 = tid; t0 < npos; t0 += 16 * 256) {
-    float v[16];
-    #pragma unroll
-    for (int k = 0; k < 16; k++) { const int t = t0 + 256 * k; v[k] = srow[t < npos ? t : t0]; }
-    #pragma unroll
-    for (int k = 0; k < 16; k++) {
-      const int t = t0 + 256 * k;
-      if (t < npos) srow[t] = (float)((double)v[k] * inv);
-    }
+  // the probabilities themselves, p = f32(f32(e) * inv)
+  #pragma unroll
+  for (int k = 0; k < SMR_NK; k++) {
+    const int t = tid + SMR_T * k;
+    if (t < npos) srow[t] = (float)((double)v[k] * inv);
   }
+  for (int t = SMR_NK * SMR_T + tid; t < npos; t += SMR_T) srow[t] = (float)((double)srow[t] * inv);
 }
 
 // ---- weighted sum of passes of several tokens on the matrix cores. v_mfma_f32_16x16x4_f32 adds its four products to
 // the accumulator as four fused multiply-adds in k order (measured on gfx950, every element of random wide-range
 // operands), so a chain of them over positions t, t + 1, ... in order is the reference's f32 chain out += p_t v_t
 // (one rounding per position, src/model/forward.js:131-134) for 16 rows x 16 dimensions at once: the bits of k_attn_av.
-// Block (pair of 64-dimension halves... see below): rows r = b G + g of a KV head (token b, query head kvh G + g) in
-// tiles of 16, wave w computing dimension tile (blockIdx.x * 4 + w) of 16 dimensions for the block's row tile; lane l
-// supplies A = p[row l mod 16][t + l / 16] and B = V[dimension l mod 16][t + l / 16] and holds the accumulator of
-// (row 4 (l / 16) + v, dimension l mod 16). The probabilities (already normalised: k_attn_softmax_rows<true>) and V
-// are staged in LDS chunk by chunk, the next chunk loaded into registers while the current one is summed; a row's
-// probabilities past its last position are zero, and so are V past the pass's last position.
-constexpr int MMV_CT = 128;   // positions per staged chunk
+// Block: a 32-dimension slice of a KV head for a tile of 16 rows r = b G + g (token b, query head kvh G + g). Waves 0-1
+// run the chains of dimensions 16 w .. 16 w + 15 (lane l supplies A = p[row l mod 16][position 4 m + l / 16] and
+// B = V[dimension l mod 16][4 m + l / 16] and holds (row 4 (l / 16) + v, dimension l mod 16)) while waves 2-3 stage
+// chunk c + 1 (the probabilities, already normalised by k_attn_softmax_rows<true>, zero past each row's last position;
+// V as f32, zero past the pass's last position) and request chunk c + 2: as in k_attn_av_mfma the chain waves issue only
+// MFMAs and LDS reads, one barrier per chunk, operands by position mod 4 (section k holds positions 4 m + k).
+constexpr int MMV_CT = 256;                 // positions per chunk
+constexpr int MMV_SF = MMV_CT / 4 + 4;      // floats of one position section (16-byte pad)
 template <bool F16KV>
 __global__ __launch_bounds__(256) void k_attn_av_mm(const AttnArgs a, int nrows) {
-  constexpr int VB = F16KV ? 2 : 4;
-  constexpr int PP = MMV_CT + 4;                      // LDS pitch (floats) of a staged probability row
-  constexpr int VP = MMV_CT * VB + 16;                // LDS pitch (bytes) of a staged V dimension row
-  constexpr int PL = 16 * MMV_CT / 4 / 256;           // 16-byte probability pieces per thread per chunk (2)
-  constexpr int VL = 64 * MMV_CT * VB / 16 / 256;     // 16-byte V pieces per thread per chunk
-  typedef float f4 __attribute__((ext_vector_type(4)));
   extern __shared__ __align__(16) uint8_t lds[];
-  float *pb = (float *)lds;                           // [2][16][PP]
-  uint8_t *vb = lds + 2 * 16 * PP * 4;                // [2][64][VP]
-  __shared__ float ot[16][65];                        // the block's outputs [row][dimension] for the epilogue
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  constexpr int VB = F16KV ? 2 : 4;
+  constexpr int CT = MMV_CT, SF = MMV_SF;
+  constexpr int EPP = 16 / VB;                      // positions per 16-byte V piece
+  constexpr int PPR = CT / EPP;                     // V pieces per dimension row of a chunk
+  constexpr int PLT = AV_DIMS * PPR / 128;          // V pieces per producer thread per chunk (8 f16, 16 f32)
+  constexpr int QLT = 16 * (CT / 4) / 128;          // probability quads per producer thread per chunk (8)
+  constexpr int NU = CT / AVM_UNIT;                 // units (8 MFMAs) per chunk
+  float *vk = (float *)lds;                         // [2][AV_DIMS][4][SF]: V of position 4 m + k, dimension j at [j][k][m]
+  float *pk = vk + 2 * AV_DIMS * 4 * SF;            // [2][16][4][SF]: p of row i, position 4 m + k at [i][k][m]
+  __shared__ float ot[16][AV_DIMS + 1];             // the block's outputs [row][dimension] for the epilogue
+  __shared__ long roff[16];
+  __shared__ int rnp[16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g = lane >> 4;
-  const int kvh = blockIdx.y, rt = blockIdx.z, d0 = blockIdx.x * 64;
+  const int kvh = blockIdx.y, rt = blockIdx.z, d0 = blockIdx.x * AV_DIMS;
   const int G = a.nHead / a.nHeadKv;
   const Step *st = a.step;
   const int Bd = st->B, pos0 = st->pos0, nmax = pos0 + Bd;
   // the rows of the tile: scores row offsets and positions (0: no row)
-  __shared__ long roff[16];
-  __shared__ int rnp[16];
   if (tid < 16) {
     const int r = rt * 16 + tid, b = r / G, h = kvh * G + r % G;
     const bool live = r < nrows && b < Bd;
@@ -1051,80 +1093,127 @@ __global__ __launch_bounds__(256) void k_attn_av_mm(const AttnArgs a, int nrows)
     rnp[tid] = live ? pos0 + b + 1 : 0;
   }
   __syncthreads();
-  const uint8_t *vbase = (const uint8_t *)a.vcache + (((long)a.layer * a.nHeadKv + kvh) * a.hd + d0) * a.vstride * VB;
-  float4 preP[PL];
-  uint4 preV[VL];
-  auto fetch = [&](int t0) {
-    #pragma unroll
-    for (int k = 0; k < PL; k++) {
-      const int idx = k * 256 + tid, r = idx / (MMV_CT / 4), t = t0 + (idx % (MMV_CT / 4)) * 4;
-      const float *src = a.scores + roff[r] + t;
-      float w[4];
-      #pragma unroll
-      for (int e = 0; e < 4; e++) w[e] = t + e < rnp[r] ? src[e] : 0.f;
-      preP[k] = make_float4(w[0], w[1], w[2], w[3]);
-    }
-    #pragma unroll
-    for (int k = 0; k < VL; k++) {
-      const int idx = k * 256 + tid, d = idx / (MMV_CT * VB / 16), t = t0 + (idx % (MMV_CT * VB / 16)) * (16 / VB);
-      uint4 v = t < nmax ? *(const uint4 *)(vbase + ((long)d * a.vstride + t) * VB) : make_uint4(0, 0, 0, 0);
-      if (t < nmax && t + 16 / VB > nmax) {  // the pieces past the pass's last position: zeros
-        uint32_t w[4] = {v.x, v.y, v.z, v.w};
-        #pragma unroll
-        for (int e = 0; e < 16 / VB; e++)
-          if (t + e >= nmax) {
-            if (F16KV) w[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
-            else w[e] = 0u;
-          }
-        v = make_uint4(w[0], w[1], w[2], w[3]);
-      }
-      preV[k] = v;
-    }
-  };
-  auto store = [&](int buf) {
-    #pragma unroll
-    for (int k = 0; k < PL; k++) {
-      const int idx = k * 256 + tid, r = idx / (MMV_CT / 4), t = (idx % (MMV_CT / 4)) * 4;
-      *(float4 *)(pb + (buf * 16 + r) * PP + t) = preP[k];
-    }
-    #pragma unroll
-    for (int k = 0; k < VL; k++) {
-      const int idx = k * 256 + tid, d = idx / (MMV_CT * VB / 16), o = (idx % (MMV_CT * VB / 16)) * 16;
-      *(uint4 *)(vb + (buf * 64 + d) * VP + o) = preV[k];
-    }
-  };
   int nrmax = 0;
   #pragma unroll
   for (int i = 0; i < 16; i++) nrmax = max(nrmax, rnp[i]);
   if (nrmax == 0) return;  // (uniform)
-  const int nch = (nrmax + MMV_CT - 1) / MMV_CT;
-  f4 acc = {0.f, 0.f, 0.f, 0.f};
-  fetch(0);
-  for (int c = 0; c < nch; c++) {
-    __syncthreads();  // the buffer about to be written was last read two chunks ago
-    store(c & 1);
-    __syncthreads();
-    if (c + 1 < nch) fetch((c + 1) * MMV_CT);
-    const float *pr = pb + ((c & 1) * 16 + n16) * PP + g;
-    const uint8_t *vr = vb + ((c & 1) * 64 + wave * 16 + n16) * VP + g * VB;
-    #pragma unroll 8
-    for (int t = 0; t < MMV_CT; t += 4) {
-      const float pa = pr[t];
-      float vv;
-      if (F16KV) vv = h2f(*(const uint16_t *)(vr + t * 2));
-      else vv = *(const float *)(vr + t * 4);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vv, acc, 0, 0, 0);
+  const int nch = (nrmax + CT - 1) / CT;
+  const int nend = (nrmax + AVM_UNIT - 1) / AVM_UNIT * AVM_UNIT;  // positions the chains run
+  const uint8_t *vbase = (const uint8_t *)a.vcache + (((long)a.layer * a.nHeadKv + kvh) * a.hd + d0) * a.vstride * VB;
+  const bool producer = wave >= 2;
+  const int pt = tid - 128;                         // producer thread 0..127
+  uint4 preV[PLT];
+  float preP[QLT][4];
+  // chunk c's V pieces and probabilities, from in-range rows and positions (what lies past a row's or the pass's last
+  // position is zeroed when the chunk is staged)
+  auto fetch = [&](int c) {
+    #pragma unroll
+    for (int k = 0; k < PLT; k++) {
+      const int idx = k * 128 + pt, dim = idx / PPR, t = c * CT + (idx % PPR) * EPP;
+      preV[k] = *(const uint4 *)(vbase + ((long)dim * a.vstride + (t < nmax ? t : 0)) * VB);
     }
+    #pragma unroll
+    for (int k = 0; k < QLT; k++) {
+      const int idx = k * 128 + pt, r = idx / (CT / 4), t = c * CT + (idx % (CT / 4)) * 4;
+      const float *src = a.scores + roff[r];
+      #pragma unroll
+      for (int e = 0; e < 4; e++) preP[k][e] = src[t + e < rnp[r] ? t + e : 0];
+    }
+  };
+  auto stage = [&](int c) {
+    float *vs = vk + (c & 1) * AV_DIMS * 4 * SF;
+    #pragma unroll
+    for (int k = 0; k < PLT; k++) {
+      const int idx = k * 128 + pt, dim = idx / PPR, pc = idx % PPR, t = c * CT + pc * EPP;
+      const uint32_t w[4] = {preV[k].x, preV[k].y, preV[k].z, preV[k].w};
+      float f[EPP];
+      #pragma unroll
+      for (int e = 0; e < EPP; e++) {
+        const float x = F16KV ? h2f((uint16_t)((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffff))) : __uint_as_float(w[e]);
+        f[e] = t + e < nmax ? x : 0.f;
+      }
+      float *drow = vs + dim * 4 * SF;
+      #pragma unroll
+      for (int q = 0; q < 4; q++) {
+        if (F16KV) *(float2 *)(drow + q * SF + 2 * pc) = make_float2(f[q], f[q + 4]);  // positions t + q, t + 4 + q
+        else drow[q * SF + pc] = f[q];                                                 // position t + q
+      }
+    }
+    float *ps = pk + (c & 1) * 16 * 4 * SF;
+    #pragma unroll
+    for (int k = 0; k < QLT; k++) {
+      const int idx = k * 128 + pt, r = idx / (CT / 4), q = idx % (CT / 4), t = c * CT + q * 4;
+      #pragma unroll
+      for (int e = 0; e < 4; e++) ps[(r * 4 + e) * SF + q] = t + e < rnp[r] ? preP[k][e] : 0.f;
+    }
+  };
+  if (producer) {
+    fetch(0);
+    stage(0);
+    if (nch > 1) fetch(1);
   }
-  // ---- epilogue: the outputs through LDS, then per row 64 dimensions on the 64 lanes of a wave (quantizeAct blocks of
-  // 32 consecutive dimensions sit in 32 consecutive lanes)
-  #pragma unroll
-  for (int v = 0; v < 4; v++) ot[4 * g + v][wave * 16 + n16] = acc[v];
   __syncthreads();
-  for (int i = wave; i < 16; i += 4) {
+  f4 acc = {0.f, 0.f, 0.f, 0.f};
+  auto mfma8 = [&](const f4 &p0, const f4 &p1, const f4 &v0, const f4 &v1) {
+    #pragma unroll
+    for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p0[i], v0[i], acc, 0, 0, 0);
+    #pragma unroll
+    for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p1[i], v1[i], acc, 0, 0, 0);
+  };
+  for (int c = 0; c < nch; c++) {
+    if (producer) {
+      if (c + 1 < nch) {
+        stage(c + 1);
+        if (c + 2 < nch) fetch(c + 2);
+      }
+    } else {
+      // unit u: the 8 MFMAs of positions c CT + 32 u .. + 31 (lane group g: positions 4 m + g, m = 8 u .. 8 u + 7); two
+      // operand sets, the next unit's reads ahead of the current unit's MFMAs, a full chunk in straight-line code
+      const float *vr = vk + ((c & 1) * AV_DIMS + wave * 16 + n16) * 4 * SF + g * SF;
+      const float *pr = pk + ((c & 1) * 16 + n16) * 4 * SF + g * SF;
+      auto ld = [&](const float *q, int off) { return *(const f4 *)(q + off); };
+      if (c * CT + CT <= nend) {
+        f4 a0 = ld(pr, 0), a1 = ld(pr, 4), a2 = ld(vr, 0), a3 = ld(vr, 4);
+        #pragma unroll
+        for (int u = 0; u < NU; u += 2) {
+          const f4 b0 = ld(pr, 8 * u + 8), b1 = ld(pr, 8 * u + 12), b2 = ld(vr, 8 * u + 8), b3 = ld(vr, 8 * u + 12);
+          __builtin_amdgcn_sched_barrier(0);
+          mfma8(a0, a1, a2, a3);
+          if (u + 2 < NU) { a0 = ld(pr, 8 * u + 16); a1 = ld(pr, 8 * u + 20); a2 = ld(vr, 8 * u + 16); a3 = ld(vr, 8 * u + 20); }
+          __builtin_amdgcn_sched_barrier(0);
+          mfma8(b0, b1, b2, b3);
+        }
+      } else {
+        const int nu = (nend - c * CT) / AVM_UNIT;
+        f4 a0 = ld(pr, 0), a1 = ld(pr, 4), a2 = ld(vr, 0), a3 = ld(vr, 4);
+        int u = 0;
+        for (; u + 2 <= nu; u += 2) {
+          const f4 b0 = ld(pr, 8 * u + 8), b1 = ld(pr, 8 * u + 12), b2 = ld(vr, 8 * u + 8), b3 = ld(vr, 8 * u + 12);
+          __builtin_amdgcn_sched_barrier(0);
+          mfma8(a0, a1, a2, a3);
+          const int un = min(u + 2, nu - 1);  // (a re-read of the last unit when past it)
+          a0 = ld(pr, 8 * un); a1 = ld(pr, 8 * un + 4); a2 = ld(vr, 8 * un); a3 = ld(vr, 8 * un + 4);
+          __builtin_amdgcn_sched_barrier(0);
+          mfma8(b0, b1, b2, b3);
+        }
+        if (u < nu) mfma8(a0, a1, a2, a3);
+      }
+    }
+    __syncthreads();
+  }
+  // ---- epilogue: the outputs through LDS, then two rows per wave, a row's 32 dimensions on 32 consecutive lanes (one
+  // quantizeAct block)
+  if (!producer) {
+    #pragma unroll
+    for (int v = 0; v < 4; v++) ot[4 * g + v][wave * 16 + n16] = acc[v];
+  }
+  __syncthreads();
+  #pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int i = j * 8 + wave * 2 + (lane >> 5);
     if (rnp[i] == 0) continue;
-    const int r = rt * 16 + i, b = r / G, h = kvh * G + r % G, dim = d0 + lane, col = h * a.hd + dim;
-    float o = ot[i][lane];
+    const int r = rt * 16 + i, b = r / G, h = kvh * G + r % G, dim = d0 + (lane & 31), col = h * a.hd + dim;
+    float o = ot[i][lane & 31];
     if (a.gate) {  // gated attention output (src/model/forward-qwen35.js:103): o * sigmoid(gate), f64, stored f32
       const double gv = (double)a.gate[(long)b * a.ldq + (long)h * a.qhs + dim];
       o = (float)((double)o * (1.0 / (1.0 + exp(-gv))));
@@ -1134,7 +1223,7 @@ __global__ __launch_bounds__(256) void k_attn_av_mm(const AttnArgs a, int nrows)
   }
 }
 
-size_t attention_av_mm_lds(int kvF16) { return (size_t)2 * 16 * (MMV_CT + 4) * 4 + (size_t)2 * 64 * (MMV_CT * (kvF16 ? 2 : 4) + 16); }
+size_t attention_av_mm_lds(int) { return (size_t)2 * (AV_DIMS + 16) * 4 * MMV_SF * 4; }
 
 // nrows: query heads per KV head x the launch's tokens (rows r = b G + g: token b, query head kvh G + g).
 // 512 threads: waves 0-3 run the chains of chunk c while waves 4-7 store chunk c + 1 (V and probabilities) into the
@@ -1466,7 +1555,7 @@ template <bool F16KV>
 static void launch_av_mm_k(const AttnArgs &a, dim3 grid, int nrows, hipStream_t st) {
   static bool attr = false;  // dynamic LDS above 64 KB must be requested per kernel
   if (!attr) {
-    ZL_HIP(hipFuncSetAttribute((const void *)k_attn_av_mm<F16KV>, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024));
+    ZL_HIP(hipFuncSetAttribute((const void *)k_attn_av_mm<F16KV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)attention_av_mm_lds(F16KV)));
     attr = true;
   }
   hipLaunchKernelGGL((k_attn_av_mm<F16KV>), grid, dim3(256), attention_av_mm_lds(F16KV), st, a, nrows);
@@ -1580,10 +1669,10 @@ void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
     return;
   }
   if (avmm) {
-    // the probabilities of every row, then the weighted sums on the matrix cores, 16 rows x 64 dimensions per block
-    hipLaunchKernelGGL(k_attn_softmax_rows<true>, dim3(1, a.nHead, B), dim3(256), 0, st, a);
+    // the probabilities of every row, then the weighted sums on the matrix cores, 16 rows x 32 dimensions per block
+    hipLaunchKernelGGL(k_attn_softmax_rows<true>, dim3(1, a.nHead, B), dim3(SMR_T), 0, st, a);
     const int nrows = group * B;
-    const dim3 gw(a.hd / 64, a.nHeadKv, (nrows + 15) / 16);
+    const dim3 gw(a.hd / AV_DIMS, a.nHeadKv, (nrows + 15) / 16);
     if (a.kvF16) launch_av_mm_k<true>(a, gw, nrows, st);
     else launch_av_mm_k<false>(a, gw, nrows, st);
     ZL_HIP(hipGetLastError());
@@ -1591,7 +1680,7 @@ void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
   }
   if (head && B > 1 && a.pinv) {
     // grouped by KV head: the softmax rows, then each V chunk staged once for a group's rows
-    hipLaunchKernelGGL(k_attn_softmax_rows<false>, dim3(1, a.nHead, B), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k_attn_softmax_rows<false>, dim3(1, a.nHead, B), dim3(SMR_T), 0, st, a);
     const int nrows = (a.nHead / a.nHeadKv) * B;
     const dim3 gg(a.hd / AVG_DIMS, a.nHeadKv, (nrows + AVG_ROWS - 1) / AVG_ROWS);
     // 1024-byte chunks (512 f16 / 256 f32 positions): each chunk's chain is long enough to cover the next chunk's loads
@@ -1612,6 +1701,7 @@ void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
   }
   dim3 ga(a.hd / AV_DIMS, a.nHead, B);
   if (a.avmf) {
+    ZL_REQUIRE(a.ctx <= AVM_MAX_CTX, ZL_ERR_ARG, "attention: matrix-core slice form beyond its context");
     const size_t lm = attention_av_mfma_lds();
     if (a.kvF16) launch_av_mfma_k<true>(a, ga, lm, st);
     else launch_av_mfma_k<false>(a, ga, lm, st);
