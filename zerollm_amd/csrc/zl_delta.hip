@@ -186,11 +186,13 @@ __global__ __launch_bounds__(DELTA_LPR * DELTA_ROWS) void k_deltanet(const Delta
     if (a.capSsm) {  // the state after token b
       float *cs = a.capSsm + (long)b * a.capStride + ((long)hv * D + jg) * D + p * PER;
       #pragma unroll
-      for (int c = 0; c < PER; c += 4) *(float4 *)(cs + c) = make_float4(S[c], S[c + 1], S[c + 2], S[c + 3]);
+      for (int c = 0; c < PER; c++) __builtin_nontemporal_store(S[c], cs + c);
     }
   }
+  // the state and its captures with nontemporal stores: they are read only by later launches, and the arrival's
+  // agent-scope release below writes back the L2's dirty lines, which these would otherwise fill
   #pragma unroll
-  for (int c = 0; c < PER; c += 4) *(float4 *)(srow + c) = make_float4(S[c], S[c + 1], S[c + 2], S[c + 3]);
+  for (int c = 0; c < PER; c++) __builtin_nontemporal_store(S[c], srow + c);
 
   // ---- the head's last workgroup to arrive continues with the whole head
   if constexpr (R > 1) {
