@@ -3,11 +3,15 @@
 // in the same order (slab by slab, block 0 then block 1, in the reference's arithmetic, src/compute/ref-kernels.js:
 // 132-152, 210-240), the same halving-tree reduction over the waves and the same K parts.
 //
-// One MFMA multiplies an activation fragment A (16 rows rho = 2 t + b: token t's values of the slab's 32-value block b,
-// zero elsewhere in the slab) by a weight fragment B (16 rows of the tile, the slab's 64 values) into D[rho][row]: the
+// One MFMA multiplies an activation fragment A (16 rows rho: token t's values of the slab's 32-value block b, zero
+// elsewhere in the slab) by a weight fragment B (16 rows of the tile, the slab's 64 values) into D[rho][row]: the
 // integer dot of every (token, block) with every row at once. Lane l supplies A row l mod 16 and B row l mod 16 for the
-// value quarter l / 16 (16 bytes each), and receives D[4 (l / 16) + v][l mod 16], v = 0..3, i.e. tokens 2 (l / 16) and
-// 2 (l / 16) + 1, both blocks (measured on gfx950). A tile-slab is four MFMAs (row groups j = 0..3). The weights come
+// value quarter l / 16 (16 bytes each), and receives D[4 (l / 16) + v][l mod 16], v = 0..3 (measured on gfx950). Row
+// rho = 4 g + v holds token g (v = 0, 1) or token 4 + g (v = 2, 3), block v mod 2, so lane group g receives tokens g and
+// 4 + g, both blocks. Terms of tokens past M are not formed: at 2..4 tokens elements 2 and 3 are skipped (8 block
+// terms per lane and slab, not 16); at 5 tokens token 4 sits in lane group 0 of every row group's MFMA, and two
+// v_permlane16_swap and one v_permlane32_swap gather row group j's into lane group j, which then holds its own row
+// (10 terms per lane and slab). A tile-slab is four MFMAs (row groups j = 0..3). The weights come
 // from a second copy of the matrix's 4-bit plane in that operand order (DevMat::fq: per tile-slab, half h holds row
 // groups 2h and 2h + 1; lane L = n + 16 g of a half holds 8 bytes per group: the values 16 g .. 16 g + 15 of row
 // 16 j + n, value e and e + 4 in the low and high nibble of byte e of each 4-byte word, so two masks and a shift give
@@ -22,7 +26,8 @@ namespace zl {
 
 constexpr int MF_SLOTS = 8;  // sums per lane: 4 row groups x 2 tokens
 
-template <int FMT, int EPI>
+// MC: token class of the launch, 0 = 2..4 tokens, 1 = 5 tokens, 2 = 6..8 tokens
+template <int FMT, int EPI, int MC>
 __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, const int tile, uint8_t *xl) {
   static_assert(FMT == T_Q4_K || FMT == T_Q8_0, "matrix-core formats");
   constexpr int NR = EPI == EPI_SWIGLU ? 2 : 1;
@@ -96,12 +101,13 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the staged bytes are in LDS
   __syncthreads();
-  // A-fragment row rho = n16 of this lane: token n16 / 2, block n16 & 1; its quarter g holds values of that block
-  const int at = n16 >> 1;
+  // A-fragment row rho = n16 of this lane: token n16 / 4 (n16 mod 4 < 2) or 4 + n16 / 4, block n16 & 1; its quarter g
+  // holds values of that block
+  const int at = (n16 & 2) ? 4 + (n16 >> 2) : (n16 >> 2);
   const bool avalid = at < M && (g >> 1) == (n16 & 1);
   const uint8_t *abase = xl + (avalid ? at : 0) * nsl * GT_REC + 16 * g;
-  // records of this lane's D elements: tokens 2g and 2g + 1 (a token past M repeats the last one; not stored)
-  const int t0 = min(2 * g, M - 1), t1 = min(2 * g + 1, M - 1);
+  // records of this lane's D elements: tokens g and 4 + g (a token past M repeats the last one; not stored)
+  const int t0 = min(g, M - 1), t1 = min(4 + g, M - 1);
   const uint8_t *rb0 = xl + t0 * nsl * GT_REC + nsl * 64, *rb1 = xl + t1 * nsl * GT_REC + nsl * 64;
   double *fw = &fac[wave][0][0];
   #pragma unroll
@@ -134,9 +140,14 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
         const i32x4 A = {(int)av.x, (int)av.y, (int)av.z, (int)av.w};
         const uint4 r00 = *(const uint4 *)(rb0 + sl * 32), r01 = *(const uint4 *)(rb0 + sl * 32 + 16);
         const uint4 r10 = *(const uint4 *)(rb1 + sl * 32), r11 = *(const uint4 *)(rb1 + sl * 32 + 16);
-        // (xd, xs) of the elements v = 0..3: (token 2g, block 0), (2g, 1), (2g + 1, 0), (2g + 1, 1)
+        // (xd, xs) of the elements v = 0..3: (token g, block 0), (g, 1), (4 + g, 0), (4 + g, 1)
         const double xd[4] = {dbl(r00.x, r00.y), dbl(r01.x, r01.y), dbl(r10.x, r10.y), dbl(r11.x, r11.y)};
         const double xs[4] = {dbl(r00.z, r00.w), dbl(r01.z, r01.w), dbl(r10.z, r10.w), dbl(r11.z, r11.w)};
+        auto term = [&](double &acc1, double fa, double fb, double xdv, double xsv, int dv) {
+          if constexpr (FMT == T_Q4_K) acc1 = fma(xdv, fma(fa, (double)dv, -(fb * xsv)), acc1);
+          else acc1 = fma((double)dv * fa, xdv, acc1);  // Q8_0: (s * d) * xd
+        };
+        int d4[2][4];  // 5 tokens: token 4's elements (blocks 0, 1) of row group j, in lane group 0
         #pragma unroll
         for (int j = 0; j < 4; j++) {
           i32x4 B;
@@ -150,10 +161,24 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
           const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, (i32x4){0, 0, 0, 0}, 0, 0, 0);
           const double4 f = *(const double4 *)(fw + (16 * j + n16) * 4);  // row 16 j + n16: its factors
           #pragma unroll
-          for (int v = 0; v < 4; v++) {
+          for (int v = 0; v < (MC == 2 ? 4 : 2); v++) {
             const double fa = (v & 1) ? f.y : f.x, fb = (v & 1) ? f.w : f.z;
-            if constexpr (FMT == T_Q4_K) acc[j][v >> 1] = fma(xd[v], fma(fa, (double)D[v], -(fb * xs[v])), acc[j][v >> 1]);
-            else acc[j][v >> 1] = fma((double)D[v] * fa, xd[v], acc[j][v >> 1]);  // Q8_0: (s * d) * xd
+            term(acc[j][v >> 1], fa, fb, xd[v], xs[v], D[v]);
+          }
+          if constexpr (MC == 1) {
+            d4[0][j] = D[2];
+            d4[1][j] = D[3];
+          }
+        }
+        if constexpr (MC == 1) {
+          // token 4: row group j's from lane group 0 of MFMA j to lane group j, i.e. this lane's own row 16 g + n16,
+          // whose factors it formed itself
+          #pragma unroll
+          for (int bk = 0; bk < 2; bk++) {
+            const auto e01 = __builtin_amdgcn_permlane16_swap((unsigned)d4[bk][0], (unsigned)d4[bk][1], false, false);
+            const auto e23 = __builtin_amdgcn_permlane16_swap((unsigned)d4[bk][2], (unsigned)d4[bk][3], false, false);
+            const int c = (int)__builtin_amdgcn_permlane32_swap(e01[0], e23[0], false, false)[0];
+            term(acc[0][1], f4[bk], f4[2 + bk], xd[2 + bk], xs[2 + bk], c);
           }
         }
       }
@@ -168,9 +193,11 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
     #pragma unroll
     for (int tt = 0; tt < 2; tt++) red[(wave * MF_SLOTS + 2 * j + tt) * 64 + lane] = acc[j][tt];
   __syncthreads();
-  // (row = lane, token t) lives in lane 16 (t / 2) + row mod 16, slot 2 (row / 16) + t mod 2
+  // (row = lane, token t) lives in lane 16 t + row mod 16, slot 2 (row / 16) for t < 4; for t >= 4 in lane
+  // 16 (t - 4) + row mod 16, slot 2 (row / 16) + 1 (6..8 tokens), or in lane `row`, slot 1 (5 tokens: token 4)
   auto tree = [&](int r, int t) {
-    const int src = 16 * (t >> 1) + n16, slot = 2 * (lane >> 4) + (t & 1);
+    const int src = t < 4 ? 16 * t + n16 : MC == 1 ? lane : 16 * (t - 4) + n16;
+    const int slot = t < 4 ? 2 * (lane >> 4) : MC == 1 ? 1 : 2 * (lane >> 4) + 1;
     double v[16];
     #pragma unroll
     for (int w = 0; w < 16; w++) v[w] = red[((r * WH + min(w, WH - 1)) * MF_SLOTS + slot) * 64 + src];
@@ -241,10 +268,10 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
 #undef ZL_SEG
 }
 
-template <int FMT, int EPI>
+template <int FMT, int EPI, int MC>
 __global__ __launch_bounds__(1024) void k_gemv_mfma(const GemvArgs a) {
   extern __shared__ __align__(16) uint8_t xl[];
-  gemv_mfma_body<FMT, EPI>(a, blockIdx.x, blockIdx.y, xl);
+  gemv_mfma_body<FMT, EPI, MC>(a, blockIdx.x, blockIdx.y, xl);
 }
 
 // Two store launches reading the same activations in one kernel: a Q4_K launch on the matrix cores (a1) and a launch of
@@ -255,7 +282,7 @@ template <int FMT2, int MT2>
 __global__ __launch_bounds__(1024) void k_gemv_mix(const GemvArgs a1, const GemvArgs a2) {
   extern __shared__ __align__(16) uint8_t xl[];
   const int n1 = a1.ks * a1.ntiles, id = blockIdx.x;
-  if (id < n1) gemv_mfma_body<T_Q4_K, EPI_STORE>(a1, id % a1.ks, id / a1.ks, xl);
+  if (id < n1) gemv_mfma_body<T_Q4_K, EPI_STORE, MT2 <= 4 ? 0 : MT2 == 5 ? 1 : 2>(a1, id % a1.ks, id / a1.ks, xl);
   else gemv_tiles_body<FMT2, MT2, EPI_STORE, 4>(a2, (id - n1) % a2.ks, (id - n1) / a2.ks, xl);
 }
 
@@ -268,18 +295,25 @@ bool gemv_mfma_ok(const GemvArgs &a) {
   return true;
 }
 
+template <int FMT, int MC>
+static void launch_mfma_mc(const GemvArgs &a, int epi, dim3 grid, dim3 blk, size_t lds, hipStream_t st) {
+  if (epi == EPI_STORE) {
+    allow_big_lds(k_gemv_mfma<FMT, EPI_STORE, MC>);
+    hipLaunchKernelGGL((k_gemv_mfma<FMT, EPI_STORE, MC>), grid, blk, lds, st, a);
+  } else if (epi == EPI_RESID) {
+    allow_big_lds(k_gemv_mfma<FMT, EPI_RESID, MC>);
+    hipLaunchKernelGGL((k_gemv_mfma<FMT, EPI_RESID, MC>), grid, blk, lds, st, a);
+  } else {
+    allow_big_lds(k_gemv_mfma<FMT, EPI_SWIGLU, MC>);
+    hipLaunchKernelGGL((k_gemv_mfma<FMT, EPI_SWIGLU, MC>), grid, blk, lds, st, a);
+  }
+}
+
 template <int FMT>
 static void launch_mfma_fmt(const GemvArgs &a, int epi, dim3 grid, dim3 blk, size_t lds, hipStream_t st) {
-  if (epi == EPI_STORE) {
-    allow_big_lds(k_gemv_mfma<FMT, EPI_STORE>);
-    hipLaunchKernelGGL((k_gemv_mfma<FMT, EPI_STORE>), grid, blk, lds, st, a);
-  } else if (epi == EPI_RESID) {
-    allow_big_lds(k_gemv_mfma<FMT, EPI_RESID>);
-    hipLaunchKernelGGL((k_gemv_mfma<FMT, EPI_RESID>), grid, blk, lds, st, a);
-  } else {
-    allow_big_lds(k_gemv_mfma<FMT, EPI_SWIGLU>);
-    hipLaunchKernelGGL((k_gemv_mfma<FMT, EPI_SWIGLU>), grid, blk, lds, st, a);
-  }
+  if (a.M <= 4) launch_mfma_mc<FMT, 0>(a, epi, grid, blk, lds, st);
+  else if (a.M == 5) launch_mfma_mc<FMT, 1>(a, epi, grid, blk, lds, st);
+  else launch_mfma_mc<FMT, 2>(a, epi, grid, blk, lds, st);
 }
 
 void launch_gemv_mfma(const GemvArgs &a, int epi, hipStream_t st) {
