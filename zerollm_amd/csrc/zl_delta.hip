@@ -10,10 +10,11 @@
 // Row j of the delta rule reads only S[j][.], v_j and the head's q and k, so the rows split over workgroups without any
 // change of arithmetic: every workgroup convolves and normalises the head's q and k itself (the same bits in each), and
 // holds its rows of S in registers across the B tokens (read and written once per pass, captured per token when asked).
-// The gated norm needs the head's whole output row: each workgroup stores its rows' outputs to an exchange buffer at
-// agent scope and counts its arrival; the last to arrive for the head reads the other rows, norms, gates and quantises
-// the head's B rows, and writes back the head's q and k conv windows, which every workgroup of the head read at its
-// start, before it arrived. The arrival counter is back at zero when the launch ends.
+// The gated norm needs the head's whole output row, so it runs as a second launch (k_delta_norm, one workgroup per value
+// head) that reads the rows k_deltanet stored, and writes back the head's q and k conv windows, which every workgroup of
+// the first launch read. Two launches order this without any exchange among workgroups: a hand-off by an agent-scope
+// release/acquire counter inside one launch (the last workgroup of a head to arrive running the norm) measured ~6 us
+// more per launch than the kernel boundary.
 #include "zl_kernels.h"
 
 namespace zl {
@@ -29,10 +30,9 @@ __global__ __launch_bounds__(DELTA_LPR * DELTA_ROWS) void k_deltanet(const Delta
   static_assert(D % RW == 0, "head size is a multiple of the rows per workgroup");
   constexpr int NCH = 2 * D + RW;      // channels of the workgroup: the head's q and k, then its RW rows of v
   constexpr int EXT = M + DELTA_MAX_B;  // per channel: the window (oldest first), then the launch's inputs
-  __shared__ float cq[DELTA_MAX_B * ROW], ck[DELTA_MAX_B * ROW], cv[DELTA_MAX_B * RW], core[DELTA_MAX_B * D];
+  __shared__ float cq[DELTA_MAX_B * ROW], ck[DELTA_MAX_B * ROW], cv[DELTA_MAX_B * RW];
   __shared__ float ext[NCH * EXT], wts[NCH * CK];
   __shared__ double gexp[DELTA_MAX_B], bet[DELTA_MAX_B];
-  __shared__ uint32_t last;
   const int hv = blockIdx.x / R, r = blockIdx.x - hv * R, kh = hv % a.nK, tid = threadIdx.x, lane = tid & 63,
             wave = tid >> 6;
   const int B = a.B;
@@ -84,19 +84,6 @@ __global__ __launch_bounds__(DELTA_LPR * DELTA_ROWS) void k_deltanet(const Delta
     for (int k = 0; k < SW; k++) {
       const int idx = tid + k * NT, t = idx / NCH, c = idx - t * NCH;
       if (idx < CK * NCH) wts[c * CK + t] = vw[k];
-    }
-  }
-  // the gate values and norm weights of the lane's outputs in the gated norm (token wave + NW k, value 64 q + lane)
-  constexpr int ZB = ((DELTA_MAX_B + NW - 1) / NW + 1) / 2 * 2, ZI = (D + 63) / 64;
-  float zr[ZB][ZI], nwr[ZI];
-  #pragma unroll
-  for (int q = 0; q < ZI; q++) {
-    const int i = 64 * q + lane;
-    nwr[q] = a.normW[i < D ? i : 0];
-    #pragma unroll
-    for (int k = 0; k < ZB; k++) {
-      const int b = wave + NW * k;
-      zr[k][q] = a.z[(long)(b < B ? b : 0) * a.ldz + hv * D + (i < D ? i : 0)];
     }
   }
   // decay and write strength per token (src/model/forward-qwen35.js:55-56): beta = sigmoid(b),
@@ -179,52 +166,73 @@ __global__ __launch_bounds__(DELTA_LPR * DELTA_ROWS) void k_deltanet(const Delta
     o += __shfl_xor(o, 1);
     o += __shfl_xor(o, 2);
     o += __shfl_xor(o, 4);
-    if (p == 0) {
-      core[b * D + jg] = (float)o;
-      if (R > 1) __hip_atomic_store(a.xcore + ((long)hv * DELTA_MAX_B + b) * D + jg, (float)o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (p == 0) a.xcore[((long)hv * DELTA_MAX_B + b) * D + jg] = (float)o;  // (for k_delta_norm)
     if (a.capSsm) {  // the state after token b
       float *cs = a.capSsm + (long)b * a.capStride + ((long)hv * D + jg) * D + p * PER;
       #pragma unroll
       for (int c = 0; c < PER; c++) __builtin_nontemporal_store(S[c], cs + c);
     }
   }
-  // the state and its captures with nontemporal stores: they are read only by later launches, and the arrival's
-  // agent-scope release below writes back the L2's dirty lines, which these would otherwise fill
+  // the state and its captures with nontemporal stores: they are read only by later launches
   #pragma unroll
   for (int c = 0; c < PER; c++) __builtin_nontemporal_store(S[c], srow + c);
+}
 
-  // ---- the head's last workgroup to arrive continues with the whole head
-  if constexpr (R > 1) {
-    // the workgroup's exchange stores happen before its arrival (barrier), the arrival releases them at agent scope,
-    // and the last workgroup to arrive acquires every other workgroup's before it reads them
-    __syncthreads();
-    if (tid == 0) last = __hip_atomic_fetch_add(a.xcnt + hv, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(R - 1);
-    __syncthreads();
-    if (!last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    if (tid == 0) __hip_atomic_store(a.xcnt + hv, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    constexpr int XJ = (DELTA_MAX_B * D + NT - 1) / NT;
-    float xv[XJ];
+// The gated RMSNorm (gatedRmsNormHead, src/compute/ref-deltanet.js:102-106) + quantisation of one value head's B output
+// rows, one wave per token (the wave's tokens in pairs k, k + 1, their scales as independent chains), and the head's q
+// and k conv windows after the last token: the last M of [the window k_deltanet read, the launch's B inputs].
+template <int D, int CK>
+__global__ __launch_bounds__(256) void k_delta_norm(const DeltaArgs a) {
+  constexpr int NW = 4, M = CK - 1, ZB = ((DELTA_MAX_B + NW - 1) / NW + 1) / 2 * 2, ZI = (D + 63) / 64;
+  __shared__ float core[DELTA_MAX_B * D];
+  const int hv = blockIdx.x, kh = hv % a.nK, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, B = a.B;
+  const int keyDim = a.nK * D;
+  // every load first: the rows, the gate values and norm weights of the lane's outputs (token wave + NW k, value
+  // 64 q + lane), the window sources of the thread's q / k channel
+  constexpr int XJ = (DELTA_MAX_B * D + 255) / 256;
+  float xv[XJ];
+  #pragma unroll
+  for (int k = 0; k < XJ; k++) {
+    const int idx = tid + 256 * k;
+    xv[k] = a.xcore[(long)hv * DELTA_MAX_B * D + (idx < B * D ? idx : 0)];
+  }
+  float zr[ZB][ZI], nwr[ZI];
+  #pragma unroll
+  for (int q = 0; q < ZI; q++) {
+    const int i = 64 * q + lane;
+    nwr[q] = a.normW[i < D ? i : 0];
     #pragma unroll
-    for (int k = 0; k < XJ; k++) {  // every load issued before the first store
-      const int idx = tid + k * NT, b = idx / D, jj = idx - b * D;
-      xv[k] = idx < B * D && jj / RW != r ? __hip_atomic_load(a.xcore + ((long)hv * DELTA_MAX_B + b) * D + jj, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-    }
-    #pragma unroll
-    for (int k = 0; k < XJ; k++) {
-      const int idx = tid + k * NT, b = idx / D, jj = idx - b * D;
-      if (idx < B * D && jj / RW != r) core[b * D + jj] = xv[k];
+    for (int k = 0; k < ZB; k++) {
+      const int b = wave + NW * k;
+      zr[k][q] = a.z[(long)(b < B ? b : 0) * a.ldz + hv * D + (i < D ? i : 0)];
     }
   }
-  for (int idx = tid; idx < 2 * D * M; idx += NT) {  // the head's q and k windows after the last token
-    const int c = idx / M, t = idx - c * M, grp = c < D ? 0 : 1, i = c - grp * D;
-    a.conv[(((long)hv * 3 + grp) * D + i) * M + t] = ext[c * EXT + B + t];
+  constexpr int WJ = (2 * D + 255) / 256;
+  float wv[WJ][M];
+  #pragma unroll
+  for (int k = 0; k < WJ; k++) {
+    const int c = tid + 256 * k, grp = c < D ? 0 : 1, i = c < 2 * D ? c - grp * D : 0;
+    const int ch = grp == 0 ? kh * D + i : keyDim + kh * D + i;
+    #pragma unroll
+    for (int t = 0; t < M; t++) {
+      const int u = B + t;  // position in [window (M), inputs (B)]
+      wv[k][t] = u < M ? a.conv[(((long)hv * 3 + grp) * D + i) * M + u] : a.qkv[(long)(u - M) * a.ldqkv + ch];
+    }
+  }
+  #pragma unroll
+  for (int k = 0; k < XJ; k++) {
+    const int idx = tid + 256 * k;
+    if (idx < B * D) core[idx] = xv[k];
+  }
+  #pragma unroll
+  for (int k = 0; k < WJ; k++) {
+    const int c = tid + 256 * k, grp = c < D ? 0 : 1, i = c - grp * D;
+    if (c < 2 * D) {
+      #pragma unroll
+      for (int t = 0; t < M; t++) a.conv[(((long)hv * 3 + grp) * D + i) * M + t] = wv[k][t];
+    }
   }
   __syncthreads();
-
-  // ---- gated RMSNorm (gatedRmsNormHead, src/compute/ref-deltanet.js:102-106) + quantisation, one wave per token
-  // (the wave's tokens in pairs k, k + 1, their scales as independent chains)
   #pragma unroll
   for (int k = 0; k < ZB; k += 2) {
     const int b0 = wave + NW * k;
@@ -265,7 +273,7 @@ void launch_deltanet(const DeltaArgs &a0, int D, hipStream_t st) {
   ZL_REQUIRE(a0.nK >= 1 && a0.nV >= 1 && a0.nV % a0.nK == 0, ZL_ERR_ARG, "Gated DeltaNet: value heads must be a multiple of key heads");
   ZL_REQUIRE(a0.act.ld >= a0.nV * D && a0.act.ld % 64 == 0, ZL_ERR_ARG, "Gated DeltaNet: activation rows too short");
   ZL_REQUIRE(!a0.capConv || a0.B <= DELTA_MAX_B, ZL_ERR_ARG, "Gated DeltaNet: capture holds one launch of tokens");
-  ZL_REQUIRE(D <= DELTA_ROWS || (a0.xcore && a0.xcnt), ZL_ERR_ARG, "Gated DeltaNet: exchange buffer missing");
+  ZL_REQUIRE(a0.xcore, ZL_ERR_ARG, "Gated DeltaNet: output row buffer missing");
   for (int t0 = 0; t0 < a0.B; t0 += DELTA_MAX_B) {
     DeltaArgs a = a0;
     a.B = std::min(DELTA_MAX_B, a0.B - t0);
@@ -275,10 +283,17 @@ void launch_deltanet(const DeltaArgs &a0, int D, hipStream_t st) {
     a.beta += (long)t0 * a.ldab;
     a.act = act_rows(a0.act, t0);
     if (a.out) a.out += (long)t0 * a.ldo;
-    const dim3 grid((unsigned)(a.nV * (D / DELTA_ROWS))), blk(DELTA_LPR * DELTA_ROWS);
-    if (D == 128) hipLaunchKernelGGL((k_deltanet<128, 4>), grid, blk, 0, st, a);
-    else if (D == 64) hipLaunchKernelGGL((k_deltanet<64, 4>), grid, blk, 0, st, a);
-    else hipLaunchKernelGGL((k_deltanet<32, 4>), grid, blk, 0, st, a);
+    const dim3 grid((unsigned)(a.nV * (D / DELTA_ROWS))), blk(DELTA_LPR * DELTA_ROWS), gn((unsigned)a.nV), bn(256);
+    if (D == 128) {
+      hipLaunchKernelGGL((k_deltanet<128, 4>), grid, blk, 0, st, a);
+      hipLaunchKernelGGL((k_delta_norm<128, 4>), gn, bn, 0, st, a);
+    } else if (D == 64) {
+      hipLaunchKernelGGL((k_deltanet<64, 4>), grid, blk, 0, st, a);
+      hipLaunchKernelGGL((k_delta_norm<64, 4>), gn, bn, 0, st, a);
+    } else {
+      hipLaunchKernelGGL((k_deltanet<32, 4>), grid, blk, 0, st, a);
+      hipLaunchKernelGGL((k_delta_norm<32, 4>), gn, bn, 0, st, a);
+    }
     ZL_HIP(hipGetLastError());
   }
 }

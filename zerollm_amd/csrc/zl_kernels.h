@@ -167,10 +167,8 @@ struct DeltaArgs {
   // capConv / capSsm + b * capStride (floats; the same layout as conv / ssm), when set
   float *capConv, *capSsm;
   long capStride;
-  // exchange of the head's output rows among its workgroups ([nV][DELTA_MAX_B][D] floats) and the heads' arrival
-  // counters ([nV], zero between launches); needed when D is above 32
+  // the heads' output rows ([nV][DELTA_MAX_B][D] floats): written by k_deltanet, normed by k_delta_norm
   float *xcore;
-  uint32_t *xcnt;
 };
 constexpr int DELTA_MAX_B = 16;  // tokens per k_deltanet launch (longer passes run as several launches in order)
 void launch_deltanet(const DeltaArgs &a, int D, hipStream_t st);

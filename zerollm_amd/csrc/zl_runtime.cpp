@@ -250,8 +250,7 @@ struct zl_model {
   zl::Checkpoints ck;
   bool prevNoLogits = false;
   float *dqkv = nullptr, *dz = nullptr, *dalpha = nullptr, *dbeta = nullptr;
-  float *dxcore = nullptr;      // DeltaNet: exchange of a head's output rows among its workgroups
-  uint32_t *dxcnt = nullptr;    // and the heads' arrival counters
+  float *dxcore = nullptr;      // DeltaNet: the heads' output rows, between the recurrence and the gated norm
   zl::Step *dstep = nullptr;
   hipStream_t st = nullptr;
   hipStream_t cst = nullptr;  // graphs are captured on their own stream
@@ -466,8 +465,6 @@ static void finish_model(zl_model *m, const float *ropeFreqs) {
     m->dalpha = (float *)m->ar.alloc((size_t)B * c.ssm_dt_rank * 4);
     m->dbeta = (float *)m->ar.alloc((size_t)B * c.ssm_dt_rank * 4);
     m->dxcore = (float *)m->ar.alloc((size_t)c.ssm_dt_rank * DELTA_MAX_B * c.ssm_d_state * 4);
-    m->dxcnt = (uint32_t *)m->ar.alloc((size_t)c.ssm_dt_rank * 4);
-    zero_now(m->dxcnt, (size_t)c.ssm_dt_rank * 4);
   }
   m->x = (float *)m->ar.alloc((size_t)B * c.n_embd * 4);
   m->q = (float *)m->ar.alloc((size_t)B * qdim(m) * (m->hybrid ? 2 : 1) * 4);
@@ -689,7 +686,7 @@ static void enqueue_forward(zl_model *m, int B, int want) {
       da.dtBias = L.dtBias; da.ssmA = L.ssmA; da.normW = L.ssmNorm;
       da.nK = c.ssm_n_group; da.nV = nV; da.K = c.ssm_conv_kernel; da.B = B; da.eps = eps;
       da.act = m->act; da.out = m->act.f; da.ldo = m->act.ld;
-      da.xcore = m->dxcore; da.xcnt = m->dxcnt;
+      da.xcore = m->dxcore;
       if (want == 2 && m->capture && B <= m->capSlots) {
         const long stride = (long)m->nRec * (m->convFloats + m->ssmFloats);
         da.capConv = m->capture + (long)L.ri * m->convFloats;
