@@ -664,17 +664,20 @@ __global__ __launch_bounds__(256) void k_attn_av_mfma(const AttnArgs a) {
     fetch_v(0, a.ctx);
     fetch_s(0, a.ctx);
   }
-  const Step *st = a.step;
-  if (b >= st->B) return;
-  npos = st->pos0 + b + 1;
-  const int nch = (npos + CT - 1) / CT;
-  const int nend = (npos + AVM_UNIT - 1) / AVM_UNIT * AVM_UNIT;  // positions the chains run
   // ---- softmax (src/compute/ref-kernels.js:313-320), k_attn_av's arithmetic: thread tid takes t = tid + 256 k, its
   // exponentials added in k order. The scores stay in registers (-inf past the last position: exp gives +0, which
-  // leaves the sum unchanged), so the producers stage chunk 0's V meanwhile.
+  // leaves the sum unchanged), so the producers stage chunk 0's V meanwhile; they are requested before the pass's step
+  // record arrives (up to the cache's capacity).
+  const Step *st = a.step;
+  const int sB = st->B, sp0 = st->pos0;
   float sv[AVM_NK];
   #pragma unroll
-  for (int k = 0; k < AVM_NK; k++) { const int t = k * 256 + tid; sv[k] = srow[t < npos ? t : 0]; }
+  for (int k = 0; k < AVM_NK; k++) { const int t = k * 256 + tid; sv[k] = srow[t < a.ctx ? t : 0]; }
+  __asm__ volatile("" ::: "memory");  // keeps the loads above the branch (it would otherwise sink them past it)
+  if (b >= sB) return;
+  npos = sp0 + b + 1;
+  const int nch = (npos + CT - 1) / CT;
+  const int nend = (npos + AVM_UNIT - 1) / AVM_UNIT * AVM_UNIT;  // positions the chains run
   if (producer) {
     stage_v(0);
     if (nch > 1) fetch_v(1, npos);
@@ -984,7 +987,8 @@ __global__ __launch_bounds__(SMR_T) void k_attn_softmax_rows(const AttnArgs a) {
   if (b >= st->B) return;
   const int npos = st->pos0 + b + 1;
   float *srow = a.scores + ((long)b * a.nHead + h) * a.sld;
-  // thread tid holds positions tid + SMR_T k (a clamped load reads position 0, which leaves the maximum unchanged)
+  // thread tid holds positions tid + SMR_T k (a clamped load reads position 0, which leaves the maximum unchanged); the
+  // loads wait for the step record: the rows of a prefill chunk are far shorter than the cache
   float v[SMR_NK];
   #pragma unroll
   for (int k = 0; k < SMR_NK; k++) { const int t = tid + SMR_T * k; v[k] = srow[t < npos ? t : 0]; }

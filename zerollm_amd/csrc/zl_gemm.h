@@ -317,7 +317,7 @@ __global__ __launch_bounds__(W * 64) void k_gemm(const GemvArgs a) {
   }
   if (ks == 1) return;
 
-  // ---- K parts: the last part of the tile to arrive adds all parts' sums in part order (part_sum, as k_gemv_tiles)
+  // ---- K parts: the last part of the tile to arrive adds all parts' sums in part order (as k_gemv_tiles)
   __shared__ uint32_t last;
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores are complete
@@ -330,7 +330,18 @@ __global__ __launch_bounds__(W * 64) void k_gemm(const GemvArgs a) {
   for (int t = wave; t < M; t += W) {
     double sums[NR];
     #pragma unroll
-    for (int r = 0; r < NR; r++) sums[r] = part_sum(a.part + (long)tile * ks * PW + (r * MP + t) * 64 + lane, ks, PW);
+    for (int r = 0; r < NR; r++) {
+      const double *pt = a.part + (long)tile * ks * PW + (r * MP + t) * 64 + lane;
+      constexpr int KSMAX = 8;  // the parts' loads of one sum are issued together
+      double pv[KSMAX];
+      #pragma unroll
+      for (int k = 0; k < KSMAX; k++) pv[k] = __hip_atomic_load(pt + (long)min(k, ks - 1) * PW, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      double v = pv[0];
+      #pragma unroll
+      for (int k = 1; k < KSMAX; k++)
+        if (k < ks) v += pv[k];
+      sums[r] = v;
+    }
     epilogue(t, sums[0], sums[NR - 1]);
   }
 #undef ZL_SEG

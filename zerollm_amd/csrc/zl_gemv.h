@@ -25,38 +25,6 @@ typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
 constexpr int GT_KR_MAX = 96;        // slabs per K part at most (staged activations: M x 96 x 96 bytes of LDS)
 constexpr int GT_REC = 96;           // LDS bytes per (token, slab): 64 int8 values, then the two blocks' records
 
-// Split-K partial sums. A slot holds PART_EMPTY (all bits set: a NaN that no sum here produces, the device's f64
-// arithmetic giving the default NaN or an operand's payload, whose low bits an f16 or f32 source leaves clear) except
-// between its part's store and the read by the tile's last part to arrive. That workgroup waits for each slot of a sum
-// to be filled, adds the parts in part order and empties the slots for the next launch. The parts' sums reach it through
-// the slots themselves (relaxed agent-scope atomic accesses to the same locations, coherent across the XCDs' L2
-// caches), so the arrival counter only elects the workgroup; each part stores its sums before it counts itself in,
-// so the wait ends at once.
-constexpr unsigned long long PART_EMPTY = ~0ull;
-__device__ __forceinline__ double part_sum(double *pt, int ks, long stride) {
-  constexpr int KSMAX = 8;  // the parts' loads of one sum are issued together
-  unsigned long long u[KSMAX];
-  #pragma unroll
-  for (int k = 0; k < KSMAX; k++)
-    u[k] = __hip_atomic_load((unsigned long long *)(pt + (long)min(k, ks - 1) * stride), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  #pragma unroll
-  for (int k = 0; k < KSMAX; k++) {
-    if (k < ks) {
-      unsigned long long *slot = (unsigned long long *)(pt + (long)k * stride);
-      for (int it = 0; u[k] == PART_EMPTY && it < (1 << 20); it++) {  // bounded: a slot never filled leaves the NaN
-        __builtin_amdgcn_s_sleep(1);
-        u[k] = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      __hip_atomic_store(slot, PART_EMPTY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-  double v = __builtin_bit_cast(double, u[0]);
-  #pragma unroll
-  for (int k = 1; k < KSMAX; k++)
-    if (k < ks) v += __builtin_bit_cast(double, u[k]);
-  return v;
-}
-
 template <int FMT>
 struct Fmt {
   static constexpr int QW = FMT == T_Q8_0 ? 16 : 8;                                          // qs words per (row, slab)
@@ -413,8 +381,9 @@ __device__ __forceinline__ void gemv_tiles_body(const GemvArgs a, const int kp, 
     return v[0];
   };
 
-  // ---- K parts: the last part of the tile to arrive adds all parts' sums in part order (part_sum); each wave waits for
-  // its stores to complete before the workgroup counts itself in.
+  // ---- K parts: the last part of the tile to arrive adds all parts' sums in part order. Partial sums are written and
+  // read with device-scope (agent) atomic accesses, which are coherent across the XCDs' L2 caches without cache-wide
+  // fences; each wave waits for its stores to complete before the workgroup counts itself in.
   constexpr int PW = NR * MT * 64;  // doubles per part
   if (ks > 1) {
     __shared__ uint32_t last;
@@ -434,7 +403,16 @@ __device__ __forceinline__ void gemv_tiles_body(const GemvArgs a, const int kp, 
   }
   auto total = [&](int r, int t) {
     if (ks == 1) return tree(r, t);
-    return part_sum(a.part + (long)tile * ks * PW + (r * MT + t) * 64 + lane, ks, PW);
+    const double *pt = a.part + (long)tile * ks * PW + (r * MT + t) * 64 + lane;
+    constexpr int KSMAX = 8;  // the parts' loads of one sum are issued together
+    double pv[KSMAX];
+    #pragma unroll
+    for (int k = 0; k < KSMAX; k++) pv[k] = __hip_atomic_load(pt + (long)min(k, ks - 1) * PW, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    double v = pv[0];
+    #pragma unroll
+    for (int k = 1; k < KSMAX; k++)
+      if (k < ks) v += pv[k];
+    return v;
   };
 
   // ---- epilogue of token t on wave t (t, t + W, ...): lane = row of the tile

@@ -230,7 +230,16 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
   }
   auto total = [&](int r, int t) {
     if (ks == 1) return tree(r, t);
-    return part_sum(a.part + (long)tile * ks * PW + (r * GEMV_MAX_MT + t) * 64 + lane, ks, PW);
+    const double *pt = a.part + (long)tile * ks * PW + (r * GEMV_MAX_MT + t) * 64 + lane;
+    constexpr int KSMAX = 8;
+    double pv[KSMAX];
+    #pragma unroll
+    for (int k = 0; k < KSMAX; k++) pv[k] = __hip_atomic_load(pt + (long)min(k, ks - 1) * PW, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    double v = pv[0];
+    #pragma unroll
+    for (int k = 1; k < KSMAX; k++)
+      if (k < ks) v += pv[k];
+    return v;
   };
 
   // ---- epilogue of token t on wave t: lane = row of the tile (as k_gemv_tiles)

@@ -46,11 +46,6 @@ static void zero_now(void *p, size_t n) {
   ZL_HIP(hipMemset(p, 0, n));
   ZL_HIP(hipDeviceSynchronize());
 }
-// Split-K partial-sum slots start empty (PART_EMPTY: every byte 0xff).
-static void empty_parts_now(double *p, size_t n) {
-  ZL_HIP(hipMemset(p, 0xff, n * 8));
-  ZL_HIP(hipDeviceSynchronize());
-}
 
 struct Arena {
   std::vector<void *> ptrs;
@@ -397,7 +392,6 @@ static Act alloc_act(Arena &ar, int B, int ld, bool f32) {
 static GemvWork alloc_gemv_work(Arena &ar) {
   GemvWork w;
   w.part = (double *)ar.alloc(GEMV_PART_DOUBLES * 8);
-  empty_parts_now(w.part, GEMV_PART_DOUBLES);
   w.cnt = (uint32_t *)ar.alloc(GEMV_CNT_TILES * 4);
   zero_now(w.cnt, GEMV_CNT_TILES * 4);
   return w;
@@ -1663,9 +1657,8 @@ constexpr int NOALLOC_MAX_DEVICES = 64;
 static std::mutex g_scratch_mu;
 static unsigned char *g_scratch[NOALLOC_MAX_DEVICES];
 
-// Set-up, once per GPU with that GPU current: look up the array's address, clear the arrival counters and empty the
-// partial-sum slots (each split-K launch's last workgroup resets its own counters and slots, so they stay so between
-// calls).
+// Set-up, once per GPU with that GPU current: look up the array's address and clear the arrival counters (each
+// split-K launch's last workgroup resets its own counters, so they stay zero between calls).
 static unsigned char *noalloc_scratch() {
   int dev = -1;
   ZL_HIP(hipGetDevice(&dev));
@@ -1677,7 +1670,6 @@ static unsigned char *noalloc_scratch() {
     ZL_REQUIRE(p != nullptr, ZL_ERR_HIP, "static work space: no device address");
     unsigned char *b = (unsigned char *)p;
     launch_fill((float *)(b + NOALLOC_OFF_CNT), GEMV_CNT_TILES, 0.0f, nullptr);  // 0.0f is all-zero bits
-    launch_fill((float *)(b + NOALLOC_OFF_PART), (long)NOALLOC_PART_DOUBLES * 2, __builtin_bit_cast(float, 0xffffffffu), nullptr);
     ZL_HIP(hipStreamSynchronize(nullptr));
     g_scratch[dev] = b;
   }
