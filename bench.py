@@ -20,7 +20,7 @@ HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s
 # HBM bytes per launch of the roofline kernel (k_gemv_mfma<SWIGLU>, Q4_K ffn_gate + ffn_up at M = 5): FETCH_SIZE
 # and WRITE_SIZE counter runs over `bench.py --probe-only`, each scaled by the same counter's reading for a plain copy of
 # known size (profiles/gemv_gate_up_m5_traffic.md). A hardware counter cannot be read inside this timed run.
-ROOFLINE_TRAFFIC_BYTES = 59_249_000
+ROOFLINE_TRAFFIC_BYTES = 59_219_000
 PROMPT, GEN, K = 512, 256, 4
 
 
