@@ -1060,38 +1060,45 @@ __global__ __launch_bounds__(SMR_T) void k_attn_softmax_rows(const AttnArgs a) {
 // the accumulator as four fused multiply-adds in k order (measured on gfx950, every element of random wide-range
 // operands), so a chain of them over positions t, t + 1, ... in order is the reference's f32 chain out += p_t v_t
 // (one rounding per position, src/model/forward.js:131-134) for 16 rows x 16 dimensions at once: the bits of k_attn_av.
-// Block: a 32-dimension slice of a KV head for a tile of 16 rows r = b G + g (token b, query head kvh G + g). Waves 0-1
-// run the chains of dimensions 16 w .. 16 w + 15 (lane l supplies A = p[row l mod 16][position 4 m + l / 16] and
-// B = V[dimension l mod 16][4 m + l / 16] and holds (row 4 (l / 16) + v, dimension l mod 16)) while waves 2-3 stage
-// chunk c + 1 (the probabilities, already normalised by k_attn_softmax_rows<true>, zero past each row's last position;
-// V as f32, zero past the pass's last position) and request chunk c + 2: as in k_attn_av_mfma the chain waves issue only
-// MFMAs and LDS reads, one barrier per chunk, operands by position mod 4 (section k holds positions 4 m + k).
+// Block: a 32-dimension slice of a KV head for RB = 16 or 32 rows r = b G + g (token b, query head kvh G + g), one or two
+// 16-row tiles. Waves 0 .. 2 RB / 16 - 1 run the chains of (row tile w / 2, dimensions 16 (w mod 2) .. + 15) (lane l
+// supplies A = p[row l mod 16][position 4 m + l / 16] and B = V[dimension l mod 16][4 m + l / 16] and holds (row
+// 4 (l / 16) + v, dimension l mod 16)) while as many waves more stage chunk c + 1 (the probabilities, already normalised
+// by k_attn_softmax_rows<true>,
+// zero past each row's last position; V as f32, zero past the pass's last position) and request chunk c + 3: each
+// producer unit is 16 consecutive positions of one row or dimension (16-byte loads, one 16-byte LDS store per position
+// section), two register sets in turn. As in k_attn_av_mfma the chain waves issue only MFMAs and LDS reads, one barrier
+// per chunk, operands by position mod 4 (section k holds positions 4 m + k). 32-row blocks stage V once for two tiles
+// (prefill chunks); 16-row blocks keep the chain waves on SIMDs of their own (one block per CU), for passes of few rows.
 constexpr int MMV_CT = 256;                 // positions per chunk
 constexpr int MMV_SF = MMV_CT / 4 + 4;      // floats of one position section (16-byte pad)
-template <bool F16KV>
-__global__ __launch_bounds__(256) void k_attn_av_mm(const AttnArgs a, int nrows) {
+template <bool F16KV, int RB>
+__global__ __launch_bounds__(RB * 16) void k_attn_av_mm(const AttnArgs a, int nrows) {
   extern __shared__ __align__(16) uint8_t lds[];
   typedef float f4 __attribute__((ext_vector_type(4)));
+  typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));  // a row of scores starts at any float
   constexpr int VB = F16KV ? 2 : 4;
-  constexpr int CT = MMV_CT, SF = MMV_SF;
+  constexpr int CT = MMV_CT, SF = MMV_SF, NCW = RB / 8, NPT = NCW * 64;  // chain waves, producer threads
   constexpr int EPP = 16 / VB;                      // positions per 16-byte V piece
-  constexpr int PPR = CT / EPP;                     // V pieces per dimension row of a chunk
-  constexpr int PLT = AV_DIMS * PPR / 128;          // V pieces per producer thread per chunk (8 f16, 16 f32)
-  constexpr int QLT = 16 * (CT / 4) / 128;          // probability quads per producer thread per chunk (8)
+  constexpr int UL = 16 / EPP;                      // V pieces per unit of 16 positions (2 f16, 4 f32)
+  constexpr int UPR = CT / 16;                      // units per dimension or probability row of a chunk
+  constexpr int VU = AV_DIMS * UPR / NPT;           // V units per producer thread per chunk
+  constexpr int PU = RB * UPR / NPT;                // probability units per producer thread per chunk
   constexpr int NU = CT / AVM_UNIT;                 // units (8 MFMAs) per chunk
+  static_assert((RB == 16 || RB == 32) && VU * NPT == AV_DIMS * UPR && PU * NPT == RB * UPR, "producer units");
   float *vk = (float *)lds;                         // [2][AV_DIMS][4][SF]: V of position 4 m + k, dimension j at [j][k][m]
-  float *pk = vk + 2 * AV_DIMS * 4 * SF;            // [2][16][4][SF]: p of row i, position 4 m + k at [i][k][m]
-  __shared__ float ot[16][AV_DIMS + 1];             // the block's outputs [row][dimension] for the epilogue
-  __shared__ long roff[16];
-  __shared__ int rnp[16];
+  float *pk = vk + 2 * AV_DIMS * 4 * SF;            // [2][RB][4][SF]: p of row i, position 4 m + k at [i][k][m]
+  __shared__ float ot[RB][AV_DIMS + 1];             // the block's outputs [row][dimension] for the epilogue
+  __shared__ long roff[RB];
+  __shared__ int rnp[RB];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g = lane >> 4;
-  const int kvh = blockIdx.y, rt = blockIdx.z, d0 = blockIdx.x * AV_DIMS;
+  const int kvh = blockIdx.y, rbk = blockIdx.z, d0 = blockIdx.x * AV_DIMS;
   const int G = a.nHead / a.nHeadKv;
   const Step *st = a.step;
   const int Bd = st->B, pos0 = st->pos0, nmax = pos0 + Bd;
-  // the rows of the tile: scores row offsets and positions (0: no row)
-  if (tid < 16) {
-    const int r = rt * 16 + tid, b = r / G, h = kvh * G + r % G;
+  // the block's rows: scores row offsets and positions (0: no row)
+  if (tid < RB) {
+    const int r = rbk * RB + tid, b = r / G, h = kvh * G + r % G;
     const bool live = r < nrows && b < Bd;
     roff[tid] = live ? ((long)b * a.nHead + h) * a.sld : 0;
     rnp[tid] = live ? pos0 + b + 1 : 0;
@@ -1099,62 +1106,82 @@ __global__ __launch_bounds__(256) void k_attn_av_mm(const AttnArgs a, int nrows)
   __syncthreads();
   int nrmax = 0;
   #pragma unroll
-  for (int i = 0; i < 16; i++) nrmax = max(nrmax, rnp[i]);
+  for (int i = 0; i < RB; i++) nrmax = max(nrmax, rnp[i]);
   if (nrmax == 0) return;  // (uniform)
   const int nch = (nrmax + CT - 1) / CT;
   const int nend = (nrmax + AVM_UNIT - 1) / AVM_UNIT * AVM_UNIT;  // positions the chains run
   const uint8_t *vbase = (const uint8_t *)a.vcache + (((long)a.layer * a.nHeadKv + kvh) * a.hd + d0) * a.vstride * VB;
-  const bool producer = wave >= 2;
-  const int pt = tid - 128;                         // producer thread 0..127
-  uint4 preV[PLT];
-  float preP[QLT][4];
-  // chunk c's V pieces and probabilities, from in-range rows and positions (what lies past a row's or the pass's last
-  // position is zeroed when the chunk is staged)
-  auto fetch = [&](int c) {
+  const bool producer = wave >= NCW;
+  const int pt = tid - NPT;                         // producer thread 0 .. NPT - 1
+  const int tr = RB == 32 ? (wave >> 1) & 1 : 0, dg = wave & 1;  // a chain wave's row tile and dimension group
+  bool tlive = false;                               // the chain wave's tile holds a row
+  #pragma unroll
+  for (int i = 0; i < 16; i++) tlive |= rnp[16 * tr + i] > 0;
+  struct Pre {
+    uint4 v[VU][UL];
+    f4 p[PU][4];
+  };
+  // chunk c's V pieces and probabilities (loads stay inside the cache row and the scores row; what lies past a row's or
+  // the pass's last position is zeroed when the chunk is staged)
+  auto fetch = [&](int c, Pre &s) {
     #pragma unroll
-    for (int k = 0; k < PLT; k++) {
-      const int idx = k * 128 + pt, dim = idx / PPR, t = c * CT + (idx % PPR) * EPP;
-      preV[k] = *(const uint4 *)(vbase + ((long)dim * a.vstride + (t < nmax ? t : 0)) * VB);
+    for (int k = 0; k < VU; k++) {
+      const int u = k * NPT + pt, dim = u / UPR, t0 = c * CT + (u % UPR) * 16;
+      #pragma unroll
+      for (int l = 0; l < UL; l++) {
+        const int t = t0 + l * EPP;
+        s.v[k][l] = *(const uint4 *)(vbase + ((long)dim * a.vstride + (t < nmax ? t : 0)) * VB);
+      }
     }
     #pragma unroll
-    for (int k = 0; k < QLT; k++) {
-      const int idx = k * 128 + pt, r = idx / (CT / 4), t = c * CT + (idx % (CT / 4)) * 4;
+    for (int k = 0; k < PU; k++) {
+      const int u = k * NPT + pt, r = u / UPR, t0 = c * CT + (u % UPR) * 16;
       const float *src = a.scores + roff[r];
       #pragma unroll
-      for (int e = 0; e < 4; e++) preP[k][e] = src[t + e < rnp[r] ? t + e : 0];
+      for (int j = 0; j < 4; j++) {
+        const int tq = t0 + 4 * j;
+        s.p[k][j] = *(const f4u *)(src + (tq + 4 <= a.ctx ? tq : 0));
+      }
     }
   };
-  auto stage = [&](int c) {
+  auto stage = [&](int c, const Pre &s) {
     float *vs = vk + (c & 1) * AV_DIMS * 4 * SF;
     #pragma unroll
-    for (int k = 0; k < PLT; k++) {
-      const int idx = k * 128 + pt, dim = idx / PPR, pc = idx % PPR, t = c * CT + pc * EPP;
-      const uint32_t w[4] = {preV[k].x, preV[k].y, preV[k].z, preV[k].w};
-      float f[EPP];
+    for (int k = 0; k < VU; k++) {
+      const int u = k * NPT + pt, dim = u / UPR, uu = u % UPR, t0 = c * CT + uu * 16;
+      float f[16];
       #pragma unroll
-      for (int e = 0; e < EPP; e++) {
-        const float x = F16KV ? h2f((uint16_t)((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffff))) : __uint_as_float(w[e]);
-        f[e] = t + e < nmax ? x : 0.f;
+      for (int e = 0; e < 16; e++) {
+        const uint4 &pc = s.v[k][e / EPP];
+        const int w = e % EPP;
+        const uint32_t wd = (F16KV ? w >> 1 : w) == 0 ? pc.x : (F16KV ? w >> 1 : w) == 1 ? pc.y : (F16KV ? w >> 1 : w) == 2 ? pc.z : pc.w;
+        const float x = F16KV ? h2f((uint16_t)((w & 1) ? (wd >> 16) : (wd & 0xffff))) : __uint_as_float(wd);
+        f[e] = t0 + e < nmax ? x : 0.f;
       }
-      float *drow = vs + dim * 4 * SF;
+      float *drow = vs + dim * 4 * SF + uu * 4;
       #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        if (F16KV) *(float2 *)(drow + q * SF + 2 * pc) = make_float2(f[q], f[q + 4]);  // positions t + q, t + 4 + q
-        else drow[q * SF + pc] = f[q];                                                 // position t + q
-      }
+      for (int q = 0; q < 4; q++) *(f4 *)(drow + q * SF) = (f4){f[q], f[q + 4], f[q + 8], f[q + 12]};
     }
-    float *ps = pk + (c & 1) * 16 * 4 * SF;
+    float *ps = pk + (c & 1) * RB * 4 * SF;
     #pragma unroll
-    for (int k = 0; k < QLT; k++) {
-      const int idx = k * 128 + pt, r = idx / (CT / 4), q = idx % (CT / 4), t = c * CT + q * 4;
+    for (int k = 0; k < PU; k++) {
+      const int u = k * NPT + pt, r = u / UPR, uu = u % UPR, t0 = c * CT + uu * 16, np = rnp[r];
+      float *prow = ps + r * 4 * SF + uu * 4;
       #pragma unroll
-      for (int e = 0; e < 4; e++) ps[(r * 4 + e) * SF + q] = t + e < rnp[r] ? preP[k][e] : 0.f;
+      for (int e = 0; e < 4; e++) {
+        f4 w;
+        #pragma unroll
+        for (int j = 0; j < 4; j++) w[j] = t0 + 4 * j + e < np ? s.p[k][j][e] : 0.f;
+        *(f4 *)(prow + e * SF) = w;
+      }
     }
   };
+  Pre s0, s1;
   if (producer) {
-    fetch(0);
-    stage(0);
-    if (nch > 1) fetch(1);
+    fetch(0, s0);
+    if (nch > 1) fetch(1, s1);
+    stage(0, s0);
+    if (nch > 2) fetch(2, s0);
   }
   __syncthreads();
   f4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -1164,59 +1191,67 @@ __global__ __launch_bounds__(256) void k_attn_av_mm(const AttnArgs a, int nrows)
     #pragma unroll
     for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p1[i], v1[i], acc, 0, 0, 0);
   };
-  for (int c = 0; c < nch; c++) {
-    if (producer) {
-      if (c + 1 < nch) {
-        stage(c + 1);
-        if (c + 2 < nch) fetch(c + 2);
+  auto chains = [&](int c) {
+    // unit u: the 8 MFMAs of positions c CT + 32 u .. + 31 (lane group g: positions 4 m + g, m = 8 u .. 8 u + 7); two
+    // operand sets, the next unit's reads ahead of the current unit's MFMAs, a full chunk in straight-line code
+    const float *vr = vk + ((c & 1) * AV_DIMS + dg * 16 + n16) * 4 * SF + g * SF;
+    const float *pr = pk + ((c & 1) * RB + tr * 16 + n16) * 4 * SF + g * SF;
+    auto ld = [&](const float *q, int off) { return *(const f4 *)(q + off); };
+    if (c * CT + CT <= nend) {
+      f4 a0 = ld(pr, 0), a1 = ld(pr, 4), a2 = ld(vr, 0), a3 = ld(vr, 4);
+      #pragma unroll
+      for (int u = 0; u < NU; u += 2) {
+        const f4 b0 = ld(pr, 8 * u + 8), b1 = ld(pr, 8 * u + 12), b2 = ld(vr, 8 * u + 8), b3 = ld(vr, 8 * u + 12);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma8(a0, a1, a2, a3);
+        if (u + 2 < NU) { a0 = ld(pr, 8 * u + 16); a1 = ld(pr, 8 * u + 20); a2 = ld(vr, 8 * u + 16); a3 = ld(vr, 8 * u + 20); }
+        __builtin_amdgcn_sched_barrier(0);
+        mfma8(b0, b1, b2, b3);
       }
     } else {
-      // unit u: the 8 MFMAs of positions c CT + 32 u .. + 31 (lane group g: positions 4 m + g, m = 8 u .. 8 u + 7); two
-      // operand sets, the next unit's reads ahead of the current unit's MFMAs, a full chunk in straight-line code
-      const float *vr = vk + ((c & 1) * AV_DIMS + wave * 16 + n16) * 4 * SF + g * SF;
-      const float *pr = pk + ((c & 1) * 16 + n16) * 4 * SF + g * SF;
-      auto ld = [&](const float *q, int off) { return *(const f4 *)(q + off); };
-      if (c * CT + CT <= nend) {
-        f4 a0 = ld(pr, 0), a1 = ld(pr, 4), a2 = ld(vr, 0), a3 = ld(vr, 4);
-        #pragma unroll
-        for (int u = 0; u < NU; u += 2) {
-          const f4 b0 = ld(pr, 8 * u + 8), b1 = ld(pr, 8 * u + 12), b2 = ld(vr, 8 * u + 8), b3 = ld(vr, 8 * u + 12);
-          __builtin_amdgcn_sched_barrier(0);
-          mfma8(a0, a1, a2, a3);
-          if (u + 2 < NU) { a0 = ld(pr, 8 * u + 16); a1 = ld(pr, 8 * u + 20); a2 = ld(vr, 8 * u + 16); a3 = ld(vr, 8 * u + 20); }
-          __builtin_amdgcn_sched_barrier(0);
-          mfma8(b0, b1, b2, b3);
-        }
-      } else {
-        const int nu = (nend - c * CT) / AVM_UNIT;
-        f4 a0 = ld(pr, 0), a1 = ld(pr, 4), a2 = ld(vr, 0), a3 = ld(vr, 4);
-        int u = 0;
-        for (; u + 2 <= nu; u += 2) {
-          const f4 b0 = ld(pr, 8 * u + 8), b1 = ld(pr, 8 * u + 12), b2 = ld(vr, 8 * u + 8), b3 = ld(vr, 8 * u + 12);
-          __builtin_amdgcn_sched_barrier(0);
-          mfma8(a0, a1, a2, a3);
-          const int un = min(u + 2, nu - 1);  // (a re-read of the last unit when past it)
-          a0 = ld(pr, 8 * un); a1 = ld(pr, 8 * un + 4); a2 = ld(vr, 8 * un); a3 = ld(vr, 8 * un + 4);
-          __builtin_amdgcn_sched_barrier(0);
-          mfma8(b0, b1, b2, b3);
-        }
-        if (u < nu) mfma8(a0, a1, a2, a3);
+      const int nu = (nend - c * CT) / AVM_UNIT;
+      f4 a0 = ld(pr, 0), a1 = ld(pr, 4), a2 = ld(vr, 0), a3 = ld(vr, 4);
+      int u = 0;
+      for (; u + 2 <= nu; u += 2) {
+        const f4 b0 = ld(pr, 8 * u + 8), b1 = ld(pr, 8 * u + 12), b2 = ld(vr, 8 * u + 8), b3 = ld(vr, 8 * u + 12);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma8(a0, a1, a2, a3);
+        const int un = min(u + 2, nu - 1);  // (a re-read of the last unit when past it)
+        a0 = ld(pr, 8 * un); a1 = ld(pr, 8 * un + 4); a2 = ld(vr, 8 * un); a3 = ld(vr, 8 * un + 4);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma8(b0, b1, b2, b3);
       }
+      if (u < nu) mfma8(a0, a1, a2, a3);
+    }
+  };
+  // chunk c + 1 sits in register set (c + 1) mod 2, which then requests chunk c + 3
+  auto step = [&](int c, Pre &sn) {
+    if (producer) {
+      if (c + 1 < nch) {
+        stage(c + 1, sn);
+        if (c + 3 < nch) fetch(c + 3, sn);
+      }
+    } else if (tlive) {
+      chains(c);
     }
     __syncthreads();
+  };
+  for (int c = 0; c < nch; c += 2) {
+    step(c, s1);
+    if (c + 1 < nch) step(c + 1, s0);
   }
   // ---- epilogue: the outputs through LDS, then two rows per wave, a row's 32 dimensions on 32 consecutive lanes (one
   // quantizeAct block)
   if (!producer) {
     #pragma unroll
-    for (int v = 0; v < 4; v++) ot[4 * g + v][wave * 16 + n16] = acc[v];
+    for (int v = 0; v < 4; v++) ot[16 * tr + 4 * g + v][16 * dg + n16] = acc[v];
   }
   __syncthreads();
   #pragma unroll
   for (int j = 0; j < 2; j++) {
-    const int i = j * 8 + wave * 2 + (lane >> 5);
+    const int i = j * (RB / 2) + wave * 2 + (lane >> 5);  // (2 NCW waves: RB / 2 rows per pass)
     if (rnp[i] == 0) continue;
-    const int r = rt * 16 + i, b = r / G, h = kvh * G + r % G, dim = d0 + (lane & 31), col = h * a.hd + dim;
+    const int r = rbk * RB + i, b = r / G, h = kvh * G + r % G, dim = d0 + (lane & 31), col = h * a.hd + dim;
     float o = ot[i][lane & 31];
     if (a.gate) {  // gated attention output (src/model/forward-qwen35.js:103): o * sigmoid(gate), f64, stored f32
       const double gv = (double)a.gate[(long)b * a.ldq + (long)h * a.qhs + dim];
@@ -1227,7 +1262,7 @@ __global__ __launch_bounds__(256) void k_attn_av_mm(const AttnArgs a, int nrows)
   }
 }
 
-size_t attention_av_mm_lds(int) { return (size_t)2 * (AV_DIMS + 16) * 4 * MMV_SF * 4; }
+size_t attention_av_mm_lds(int rb) { return (size_t)2 * (AV_DIMS + rb) * 4 * MMV_SF * 4; }
 
 // nrows: query heads per KV head x the launch's tokens (rows r = b G + g: token b, query head kvh G + g).
 // 512 threads: waves 0-3 run the chains of chunk c while waves 4-7 store chunk c + 1 (V and probabilities) into the
@@ -1537,11 +1572,10 @@ AttnForm attention_form(int ctx, int hd) {
   // (verify passes at long contexts); ZEROLLM_ATTN_MM_B overrides the token count (tests)
   const char *em = getenv("ZEROLLM_ATTN_MM_B");
   f.mmMinB = em ? atoi(em) : ctx >= AVH_CTX ? 2 : 16;
-  // their weighted sums on the matrix cores from 16 tokens on: below that a KV head has too few 16-row tiles for the
-  // chains of 4-position steps to fill the GPU (measured with 9-token verify passes at 16K positions: the cycle of the
-  // 8B/0.6B pair 42.7 -> 46.4 ms)
+  // their weighted sums on the matrix cores likewise: from 16 tokens on (32-row blocks), and from 2 where the context
+  // is long (16-row blocks: 9-token verify passes at 16K positions 10.77 -> 10.52 ms against the grouped lane chains)
   const char *ea = getenv("ZEROLLM_ATTN_MMAV_B");
-  f.mmAvMinB = ea ? atoi(ea) : em ? f.mmMinB : 16;
+  f.mmAvMinB = ea ? atoi(ea) : em ? f.mmMinB : ctx >= AVH_CTX ? 2 : 16;
   // where the slice form's softmax row would not fit LDS (256-dimension heads beyond ~29,900 positions) every pass
   // takes the matrix-core weighted sum, whose staging does not grow with the context: the exact chain at any context
   if (f.split) {
@@ -1555,14 +1589,15 @@ AttnForm attention_form(int ctx, int hd) {
   return f;
 }
 
-template <bool F16KV>
-static void launch_av_mm_k(const AttnArgs &a, dim3 grid, int nrows, hipStream_t st) {
+template <bool F16KV, int RB>
+static void launch_av_mm_k(const AttnArgs &a, int nrows, hipStream_t st) {
   static bool attr = false;  // dynamic LDS above 64 KB must be requested per kernel
   if (!attr) {
-    ZL_HIP(hipFuncSetAttribute((const void *)k_attn_av_mm<F16KV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)attention_av_mm_lds(F16KV)));
+    ZL_HIP(hipFuncSetAttribute((const void *)k_attn_av_mm<F16KV, RB>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)attention_av_mm_lds(RB)));
     attr = true;
   }
-  hipLaunchKernelGGL((k_attn_av_mm<F16KV>), grid, dim3(256), attention_av_mm_lds(F16KV), st, a, nrows);
+  const dim3 grid(a.hd / AV_DIMS, a.nHeadKv, (nrows + RB - 1) / RB);
+  hipLaunchKernelGGL((k_attn_av_mm<F16KV, RB>), grid, dim3(RB * 16), attention_av_mm_lds(RB), st, a, nrows);
 }
 
 template <int HD, bool F16KV>
@@ -1673,12 +1708,17 @@ void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
     return;
   }
   if (avmm) {
-    // the probabilities of every row, then the weighted sums on the matrix cores, 16 rows x 32 dimensions per block
+    // the probabilities of every row, then the weighted sums on the matrix cores, 16 or 32 rows x 32 dimensions per block
     hipLaunchKernelGGL(k_attn_softmax_rows<true>, dim3(1, a.nHead, B), dim3(SMR_T), 0, st, a);
     const int nrows = group * B;
-    const dim3 gw(a.hd / AV_DIMS, a.nHeadKv, (nrows + 15) / 16);
-    if (a.kvF16) launch_av_mm_k<true>(a, gw, nrows, st);
-    else launch_av_mm_k<false>(a, gw, nrows, st);
+    // 32-row blocks for passes of 16 tokens or more (prefill chunks: V staged once for two tiles), 16-row blocks below
+    if (a.kvF16) {
+      if (B >= 16) launch_av_mm_k<true, 32>(a, nrows, st);
+      else launch_av_mm_k<true, 16>(a, nrows, st);
+    } else {
+      if (B >= 16) launch_av_mm_k<false, 32>(a, nrows, st);
+      else launch_av_mm_k<false, 16>(a, nrows, st);
+    }
     ZL_HIP(hipGetLastError());
     return;
   }
