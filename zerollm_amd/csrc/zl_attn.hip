@@ -292,12 +292,11 @@ __global__ __launch_bounds__(64) void k_attn_prep(const AttnArgs a) {
   }
 }
 
-// Block (position chunk of MM_PC, KV head, group of 4 row tiles); wave w computes row tile 4 z + w: 16 rows r = b G + g
-// (token b, query head kvh G + g) against every position of the chunk, 16 positions at a time. Lane l supplies A = the
-// row l mod 16's dimension 32 j + 4 m + l / 16 (its query values, f64, held for the whole chunk) and B = key value
+// Block (every X-th 64-position tile of the pass, KV head, group of 4 row tiles); wave w computes row tile 4 z + w: 16
+// rows r = b G + g (token b, query head kvh G + g) against every position of its tiles, 16 positions at a time. Lane l
+// supplies A = the row l mod 16's dimension 32 j + 4 m + l / 16 (its query values, f64, held for the whole block) and B = key value
 // [position l mod 16][dimension 32 j + 4 m + l / 16] from LDS, where the block has staged 64 positions' keys as f64;
 // the accumulator of lane l element v is (row 4 v + l / 16, position l mod 16).
-constexpr int MM_PC = 256;   // positions per block
 constexpr int MM_PT = 64;    // positions staged in LDS at a time
 template <int HD, bool F16KV>
 __global__ __launch_bounds__(256) void k_attn_scores_mm(const AttnArgs a, int nrows) {
@@ -313,9 +312,10 @@ __global__ __launch_bounds__(256) void k_attn_scores_mm(const AttnArgs a, int nr
   const int G = a.nHead / a.nHeadKv;
   const Step *st = a.step;
   const int Bd = st->B, pos0 = st->pos0, nmax = pos0 + Bd;
-  const int c0 = blockIdx.x * MM_PC;
-  if (c0 >= nmax) return;
-  const int c1 = min(c0 + MM_PC, nmax);
+  // the block's MM_PT-position tiles: bx, bx + X, ... of the pass's positions (the grid holds as many blocks per KV
+  // head and row group as stay resident at once, so the tiles of a pass of any length spread evenly over them)
+  const int X = gridDim.x, bx = blockIdx.x, ntile = (nmax + MM_PT - 1) / MM_PT;
+  if (bx >= ntile) return;
   const long kvoff = ((long)a.layer * a.nHeadKv + kvh) * a.ctx * HD;
   const uint8_t *kbase = (const uint8_t *)a.kcache + kvoff * VB;
   // A operands: row n16 of the tile, dimensions 32 j + 4 m + g
@@ -341,7 +341,7 @@ __global__ __launch_bounds__(256) void k_attn_scores_mm(const AttnArgs a, int nr
     #pragma unroll
     for (int k = 0; k < RAW; k++) {
       const int e = (k * 256 + tid) * (16 / VB), p = e / HD, d = e % HD, t = t0 + p;
-      raw[k] = t < c1 ? *(const uint4 *)(kbase + ((long)t * HD + d) * VB) : make_uint4(0, 0, 0, 0);
+      raw[k] = t < nmax ? *(const uint4 *)(kbase + ((long)t * HD + d) * VB) : make_uint4(0, 0, 0, 0);
     }
   };
   auto store = [&]() {
@@ -354,12 +354,13 @@ __global__ __launch_bounds__(256) void k_attn_scores_mm(const AttnArgs a, int nr
         kd[p * KP + d + q] = F16KV ? (double)h2f((uint16_t)((w[q >> 1] >> (16 * (q & 1))) & 0xffff)) : (double)__uint_as_float(w[q]);
     }
   };
-  fetch(c0);
-  for (int t0 = c0; t0 < c1; t0 += MM_PT) {
+  fetch(bx * MM_PT);
+  for (int ti = bx; ti < ntile; ti += X) {
+    const int t0 = ti * MM_PT, c1 = min(t0 + MM_PT, nmax);
     __syncthreads();  // the previous tile's reads are done
     store();
     __syncthreads();
-    if (t0 + MM_PT < c1) fetch(t0 + MM_PT);
+    if (ti + X < ntile) fetch((ti + X) * MM_PT);
     if (waveok) {
       #pragma unroll 1
       for (int pt = 0; pt < MM_PT && t0 + pt < c1; pt += 16) {
@@ -1676,7 +1677,11 @@ void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
   if (a.qr && a.mmMinB > 0 && B >= a.mmMinB) {
     const dim3 gp(B, a.nHead + a.nHeadKv);
     const int nrows = B * group;
-    const dim3 gm((a.ctx + MM_PC - 1) / MM_PC, a.nHeadKv, (nrows + 63) / 64);
+    // as many position blocks per (KV head, row group) as stay resident together (LDS bounds the blocks per CU), at most
+    // one per tile of the cache: a pass's tiles then spread over them in one round
+    const int zg = (nrows + 63) / 64, ntc = (a.ctx + MM_PT - 1) / MM_PT;
+    const int slots = 256 * std::max(1, (int)(160 * 1024 / attention_mm_lds(a.hd)));
+    const dim3 gm((unsigned)std::max(1, std::min(ntc, slots / (a.nHeadKv * zg))), a.nHeadKv, zg);
     const size_t lm = attention_mm_lds(a.hd);
     switch (a.hd * 2 + a.kvF16) {
       case 128: launch_scores_mm<64, false>(a, gp, gm, lm, nrows, st); break;
