@@ -1716,12 +1716,14 @@ void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
     // the probabilities of every row, then the weighted sums on the matrix cores, 16 or 32 rows x 32 dimensions per block
     hipLaunchKernelGGL(k_attn_softmax_rows<true>, dim3(1, a.nHead, B), dim3(SMR_T), 0, st, a);
     const int nrows = group * B;
-    // 32-row blocks for passes of 16 tokens or more (prefill chunks: V staged once for two tiles), 16-row blocks below
+    // 32-row blocks (V staged once for two tiles) where they still give every CU a block (prefill chunks of the 8B
+    // shapes), 16-row blocks otherwise (verify passes, the 0.6B shapes' chunks: 128 rows per KV head)
+    const bool rb32 = (nrows + 31) / 32 * (a.hd / AV_DIMS) * a.nHeadKv >= 256;
     if (a.kvF16) {
-      if (B >= 16) launch_av_mm_k<true, 32>(a, nrows, st);
+      if (rb32) launch_av_mm_k<true, 32>(a, nrows, st);
       else launch_av_mm_k<true, 16>(a, nrows, st);
     } else {
-      if (B >= 16) launch_av_mm_k<false, 32>(a, nrows, st);
+      if (rb32) launch_av_mm_k<false, 32>(a, nrows, st);
       else launch_av_mm_k<false, 16>(a, nrows, st);
     }
     ZL_HIP(hipGetLastError());
