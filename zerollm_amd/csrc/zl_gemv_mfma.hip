@@ -1,4 +1,4 @@
-// Q4_K and Q8_0 GEMVs for 2..8 tokens with the int8 block dots on the matrix cores (v_mfma_i32_16x16x64_i8), the same
+// Q4_K and Q8_0 GEMVs for 2..9 tokens with the int8 block dots on the matrix cores (v_mfma_i32_16x16x64_i8), the same
 // results bit for bit as k_gemv_tiles (zl_gemv.h): the same slabs per wave, the same f64 block terms per (row, token)
 // in the same order (slab by slab, block 0 then block 1, in the reference's arithmetic, src/compute/ref-kernels.js:
 // 132-152, 210-240), the same halving-tree reduction over the waves and the same K parts.
@@ -11,7 +11,9 @@
 // 4 + g, both blocks. Terms of tokens past M are not formed: at 2..4 tokens elements 2 and 3 are skipped (8 block
 // terms per lane and slab, not 16); at 5 tokens token 4 sits in lane group 0 of every row group's MFMA, and two
 // v_permlane16_swap and one v_permlane32_swap gather row group j's into lane group j, which then holds its own row
-// (10 terms per lane and slab). A tile-slab is four MFMAs (row groups j = 0..3). The weights come
+// (10 terms per lane and slab). At 9 tokens a second A fragment carries token 8 in the place of token 4, multiplied by
+// the same weight fragments and gathered the same way (18 terms per lane and slab). A tile-slab is four MFMAs (row
+// groups j = 0..3; eight at 9 tokens). The weights come
 // from a second copy of the matrix's 4-bit plane in that operand order (DevMat::fq: per tile-slab, half h holds row
 // groups 2h and 2h + 1; lane L = n + 16 g of a half holds 8 bytes per group: the values 16 g .. 16 g + 15 of row
 // 16 j + n, value e and e + 4 in the low and high nibble of byte e of each 4-byte word, so two masks and a shift give
@@ -24,14 +26,16 @@
 
 namespace zl {
 
-constexpr int MF_SLOTS = 8;  // sums per lane: 4 row groups x 2 tokens
+// sums per lane: 4 row groups x 2 tokens, and token 8 at 9 tokens
+constexpr int mf_slots(int mc) { return mc == 3 ? 9 : 8; }
 
-// MC: token class of the launch, 0 = 2..4 tokens, 1 = 5 tokens, 2 = 6..8 tokens
+// MC: token class of the launch, 0 = 2..4 tokens, 1 = 5 tokens, 2 = 6..8 tokens, 3 = 9 tokens
 template <int FMT, int EPI, int MC>
 __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, const int tile, uint8_t *xl) {
   static_assert(FMT == T_Q4_K || FMT == T_Q8_0, "matrix-core formats");
   constexpr int NR = EPI == EPI_SWIGLU ? 2 : 1;
   constexpr int DEPTH = FMT == T_Q4_K ? 4 : 3;  // Q8_0 slabs are 64 bytes per lane: three in flight
+  constexpr int MF_SLOTS = mf_slots(MC);
   typedef int i32x4 __attribute__((ext_vector_type(4)));
   // staged activations as in k_gemv_tiles; after the slab loop the same bytes hold the waves' sums ([W][8][64])
   __shared__ __align__(16) double fac[16][64][4];  // per wave: the factors of the tile's rows for one slab (Q4_K: fa0,
@@ -109,6 +113,11 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
   // records of this lane's D elements: tokens g and 4 + g (a token past M repeats the last one; not stored)
   const int t0 = min(g, M - 1), t1 = min(4 + g, M - 1);
   const uint8_t *rb0 = xl + t0 * nsl * GT_REC + nsl * 64, *rb1 = xl + t1 * nsl * GT_REC + nsl * 64;
+  // 9 tokens: the second fragment's row rho = n16 holds token 8 where n16 mod 16 is 2 or 3 (block n16 & 1), else zeros
+  const bool avalid8 = MC == 3 && M > 8 && (n16 & 14) == 2 && (g >> 1) == (n16 & 1);
+  const uint8_t *abase8 = xl + (avalid8 ? 8 : 0) * nsl * GT_REC + 16 * g;
+  const uint8_t *rb8 = xl + (MC == 3 && M > 8 ? 8 : 0) * nsl * GT_REC + nsl * 64;
+  double acc8 = 0.0;  // 9 tokens: (this lane's row 16 g + n16, token 8)
   double *fw = &fac[wave][0][0];
   #pragma unroll
   for (int i0 = 0; i0 < GT_NMAX; i0 += DEPTH) {
@@ -147,7 +156,16 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
           if constexpr (FMT == T_Q4_K) acc1 = fma(xdv, fma(fa, (double)dv, -(fb * xsv)), acc1);
           else acc1 = fma((double)dv * fa, xdv, acc1);  // Q8_0: (s * d) * xd
         };
-        int d4[2][4];  // 5 tokens: token 4's elements (blocks 0, 1) of row group j, in lane group 0
+        int d4[2][4];  // 5 tokens: token 4's elements (blocks 0, 1) of row group j, in lane group 0 (9 tokens: token 8's)
+        i32x4 A8 = {0, 0, 0, 0};
+        double xd8[2] = {0.0, 0.0}, xs8[2] = {0.0, 0.0};
+        if constexpr (MC == 3) {
+          const uint4 a8 = avalid8 ? *(const uint4 *)(abase8 + sl * 64) : make_uint4(0, 0, 0, 0);
+          A8 = (i32x4){(int)a8.x, (int)a8.y, (int)a8.z, (int)a8.w};
+          const uint4 r80 = *(const uint4 *)(rb8 + sl * 32), r81 = *(const uint4 *)(rb8 + sl * 32 + 16);
+          xd8[0] = dbl(r80.x, r80.y); xd8[1] = dbl(r81.x, r81.y);
+          xs8[0] = dbl(r80.z, r80.w); xs8[1] = dbl(r81.z, r81.w);
+        }
         #pragma unroll
         for (int j = 0; j < 4; j++) {
           i32x4 B;
@@ -161,7 +179,7 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
           const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, (i32x4){0, 0, 0, 0}, 0, 0, 0);
           const double4 f = *(const double4 *)(fw + (16 * j + n16) * 4);  // row 16 j + n16: its factors
           #pragma unroll
-          for (int v = 0; v < (MC == 2 ? 4 : 2); v++) {
+          for (int v = 0; v < (MC >= 2 ? 4 : 2); v++) {
             const double fa = (v & 1) ? f.y : f.x, fb = (v & 1) ? f.w : f.z;
             term(acc[j][v >> 1], fa, fb, xd[v], xs[v], D[v]);
           }
@@ -169,16 +187,22 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
             d4[0][j] = D[2];
             d4[1][j] = D[3];
           }
+          if constexpr (MC == 3) {
+            const i32x4 D8 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A8, B, (i32x4){0, 0, 0, 0}, 0, 0, 0);
+            d4[0][j] = D8[2];
+            d4[1][j] = D8[3];
+          }
         }
-        if constexpr (MC == 1) {
-          // token 4: row group j's from lane group 0 of MFMA j to lane group j, i.e. this lane's own row 16 g + n16,
-          // whose factors it formed itself
+        if constexpr (MC == 1 || MC == 3) {
+          // token 4 (token 8): row group j's from lane group 0 of MFMA j to lane group j, i.e. this lane's own row
+          // 16 g + n16, whose factors it formed itself
           #pragma unroll
           for (int bk = 0; bk < 2; bk++) {
             const auto e01 = __builtin_amdgcn_permlane16_swap((unsigned)d4[bk][0], (unsigned)d4[bk][1], false, false);
             const auto e23 = __builtin_amdgcn_permlane16_swap((unsigned)d4[bk][2], (unsigned)d4[bk][3], false, false);
             const int c = (int)__builtin_amdgcn_permlane32_swap(e01[0], e23[0], false, false)[0];
-            term(acc[0][1], f4[bk], f4[2 + bk], xd[2 + bk], xs[2 + bk], c);
+            if constexpr (MC == 1) term(acc[0][1], f4[bk], f4[2 + bk], xd[2 + bk], xs[2 + bk], c);
+            else term(acc8, f4[bk], f4[2 + bk], xd8[bk], xs8[bk], c);
           }
         }
       }
@@ -192,12 +216,14 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
   for (int j = 0; j < 4; j++)
     #pragma unroll
     for (int tt = 0; tt < 2; tt++) red[(wave * MF_SLOTS + 2 * j + tt) * 64 + lane] = acc[j][tt];
+  if constexpr (MC == 3) red[(wave * MF_SLOTS + 8) * 64 + lane] = acc8;
   __syncthreads();
-  // (row = lane, token t) lives in lane 16 t + row mod 16, slot 2 (row / 16) for t < 4; for t >= 4 in lane
-  // 16 (t - 4) + row mod 16, slot 2 (row / 16) + 1 (6..8 tokens), or in lane `row`, slot 1 (5 tokens: token 4)
+  // (row = lane, token t) lives in lane 16 t + row mod 16, slot 2 (row / 16) for t < 4; for 4 <= t < 8 in lane
+  // 16 (t - 4) + row mod 16, slot 2 (row / 16) + 1 (6..9 tokens), or in lane `row`, slot 1 (5 tokens: token 4); token 8
+  // in lane `row`, slot 8
   auto tree = [&](int r, int t) {
-    const int src = t < 4 ? 16 * t + n16 : MC == 1 ? lane : 16 * (t - 4) + n16;
-    const int slot = t < 4 ? 2 * (lane >> 4) : MC == 1 ? 1 : 2 * (lane >> 4) + 1;
+    const int src = t < 4 ? 16 * t + n16 : (MC == 1 || t == 8) ? lane : 16 * (t - 4) + n16;
+    const int slot = t < 4 ? 2 * (lane >> 4) : MC == 1 ? 1 : t == 8 ? 8 : 2 * (lane >> 4) + 1;
     double v[16];
     #pragma unroll
     for (int w = 0; w < 16; w++) v[w] = red[((r * WH + min(w, WH - 1)) * MF_SLOTS + slot) * 64 + src];
@@ -268,8 +294,9 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
 #undef ZL_SEG
 }
 
+// (9 tokens: at most 8 waves, so that the second fragment's sums stay in registers)
 template <int FMT, int EPI, int MC>
-__global__ __launch_bounds__(1024) void k_gemv_mfma(const GemvArgs a) {
+__global__ __launch_bounds__(MC == 3 ? 512 : 1024) void k_gemv_mfma(const GemvArgs a) {
   extern __shared__ __align__(16) uint8_t xl[];
   gemv_mfma_body<FMT, EPI, MC>(a, blockIdx.x, blockIdx.y, xl);
 }
@@ -279,17 +306,17 @@ __global__ __launch_bounds__(1024) void k_gemv_mfma(const GemvArgs a) {
 // for the second, each exactly as its own launch would run it (the verify pass's attn_q + attn_k and attn_v: the v
 // launch's workgroups no longer wait for a launch of their own). The launches' split-K work spaces are disjoint.
 template <int FMT2, int MT2>
-__global__ __launch_bounds__(1024) void k_gemv_mix(const GemvArgs a1, const GemvArgs a2) {
+__global__ __launch_bounds__(MT2 == 9 ? 512 : 1024) void k_gemv_mix(const GemvArgs a1, const GemvArgs a2) {
   extern __shared__ __align__(16) uint8_t xl[];
   const int n1 = a1.ks * a1.ntiles, id = blockIdx.x;
-  if (id < n1) gemv_mfma_body<T_Q4_K, EPI_STORE, MT2 <= 4 ? 0 : MT2 == 5 ? 1 : 2>(a1, id % a1.ks, id / a1.ks, xl);
+  if (id < n1) gemv_mfma_body<T_Q4_K, EPI_STORE, MT2 <= 4 ? 0 : MT2 == 5 ? 1 : MT2 == 9 ? 3 : 2>(a1, id % a1.ks, id / a1.ks, xl);
   else gemv_tiles_body<FMT2, MT2, EPI_STORE, 4>(a2, (id - n1) % a2.ks, (id - n1) / a2.ks, xl);
 }
 
-// Q4_K matrices with their fragment plane, and Q8_0 matrices, at 2..8 tokens without a fused prologue.
+// Q4_K matrices with their fragment plane, and Q8_0 matrices, at 2..9 tokens without a fused prologue.
 bool gemv_mfma_ok(const GemvArgs &a) {
   const int t = a.seg[0].m.type;
-  if ((t != T_Q4_K && t != T_Q8_0) || a.M < 2 || a.M > 8 || a.xf) return false;
+  if ((t != T_Q4_K && t != T_Q8_0) || a.M < 2 || a.M > 9 || (a.M == 9 && a.nwave > 8) || a.xf) return false;
   for (int i = 0; i < a.nseg; i++)
     if (a.seg[i].m.type != t || (t == T_Q4_K && !a.seg[i].m.fq)) return false;
   return true;
@@ -313,7 +340,8 @@ template <int FMT>
 static void launch_mfma_fmt(const GemvArgs &a, int epi, dim3 grid, dim3 blk, size_t lds, hipStream_t st) {
   if (a.M <= 4) launch_mfma_mc<FMT, 0>(a, epi, grid, blk, lds, st);
   else if (a.M == 5) launch_mfma_mc<FMT, 1>(a, epi, grid, blk, lds, st);
-  else launch_mfma_mc<FMT, 2>(a, epi, grid, blk, lds, st);
+  else if (a.M <= 8) launch_mfma_mc<FMT, 2>(a, epi, grid, blk, lds, st);
+  else launch_mfma_mc<FMT, 3>(a, epi, grid, blk, lds, st);
 }
 
 void launch_gemv_mfma(const GemvArgs &a, int epi, hipStream_t st) {
@@ -322,7 +350,7 @@ void launch_gemv_mfma(const GemvArgs &a, int epi, hipStream_t st) {
                  (epi != EPI_SWIGLU || (a.nwave % 2 == 0 && wpm <= 8)) && (a.kr + wpm - 1) / wpm <= GT_NMAX,
              ZL_ERR_ARG, "gemv (matrix cores): launch shape out of range");
   const dim3 grid((unsigned)a.ks, (unsigned)a.ntiles), blk((unsigned)a.nwave * 64);
-  const size_t lds = std::max((size_t)a.M * a.kr * GT_REC, (size_t)a.nwave * MF_SLOTS * 64 * 8);
+  const size_t lds = std::max((size_t)a.M * a.kr * GT_REC, (size_t)a.nwave * mf_slots(a.M == 9 ? 3 : 0) * 64 * 8);
   if (a.seg[0].m.type == T_Q4_K) launch_mfma_fmt<T_Q4_K>(a, epi, grid, blk, lds, st);
   else launch_mfma_fmt<T_Q8_0>(a, epi, grid, blk, lds, st);
 }
@@ -342,7 +370,7 @@ bool gemv_mix_ok(const GemvArgs &a1, const GemvArgs &a2) {
 
 template <int FMT2, int MT2>
 static void launch_mix_k(const GemvArgs &a1, const GemvArgs &a2, hipStream_t st) {
-  const size_t l1 = std::max((size_t)a1.M * a1.kr * GT_REC, (size_t)a1.nwave * MF_SLOTS * 64 * 8);
+  const size_t l1 = std::max((size_t)a1.M * a1.kr * GT_REC, (size_t)a1.nwave * mf_slots(MT2 == 9 ? 3 : 0) * 64 * 8);
   const size_t l2 = std::max((size_t)a2.M * a2.kr * GT_REC, (size_t)a2.nwave * MT2 * 64 * 8);
   allow_big_lds(k_gemv_mix<FMT2, MT2>);
   const unsigned n = (unsigned)(a1.ks * a1.ntiles + a2.ks * a2.ntiles);
@@ -357,6 +385,7 @@ static void launch_mix_fmt(const GemvArgs &a1, const GemvArgs &a2, hipStream_t s
     case 4: launch_mix_k<FMT2, 4>(a1, a2, st); break;
     case 5: launch_mix_k<FMT2, 5>(a1, a2, st); break;
     case 6: launch_mix_k<FMT2, 6>(a1, a2, st); break;
+    case 9: launch_mix_k<FMT2, 9>(a1, a2, st); break;
     default: launch_mix_k<FMT2, 8>(a1, a2, st); break;  // 7 and 8 tokens (token tile 8, as the tile launch)
   }
 }
