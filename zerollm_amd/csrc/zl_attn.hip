@@ -305,8 +305,10 @@ __global__ __launch_bounds__(256) void k_attn_scores_mm(const AttnArgs a, int nr
   constexpr int RAW = MM_PT * HD * VB / 16 / 256;  // 16-byte K pieces per thread per staged tile
   typedef double d4 __attribute__((ext_vector_type(4)));
   extern __shared__ __align__(16) uint8_t lds[];
-  double *kd = (double *)lds;          // [MM_PT][HD + 1] keys as f64 (the pad spreads a tile's rows over the banks)
-  constexpr int KP = HD + 1;
+  // [MM_PT][HD + 2] keys as f64: with rows 2 doubles (4 banks) apart, the 32 lanes of a half-wave's B read (16
+  // positions x 2 k-groups, one double each) fall on 64 distinct banks
+  double *kd = (double *)lds;
+  constexpr int KP = HD + 2;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g = lane >> 4;
   const int kvh = blockIdx.y, tile = blockIdx.z * 4 + wave;
   const int G = a.nHead / a.nHeadKv;
@@ -344,14 +346,30 @@ __global__ __launch_bounds__(256) void k_attn_scores_mm(const AttnArgs a, int nr
       raw[k] = t < nmax ? *(const uint4 *)(kbase + ((long)t * HD + d) * VB) : make_uint4(0, 0, 0, 0);
     }
   };
+  // A thread's 16 fetched bytes become PPL 16-byte pieces of f64 keys, one run of PPL * 16 bytes per lane: the runs of
+  // LPW neighbouring lanes fill a 256-byte bank window. Step s writes piece (s + rot) mod PPL, rot = (tid / LPW) mod PPL,
+  // so the lanes that share bank offsets write different pieces and each 16-lane group of a write covers 64 banks.
+  constexpr int PPL = 8 / VB, LPW = 256 / (PPL * 16);
+  const int rot = (tid / LPW) % PPL;
   auto store = [&]() {
     #pragma unroll
     for (int k = 0; k < RAW; k++) {
       const int e = (k * 256 + tid) * (16 / VB), p = e / HD, d = e % HD;
-      const uint32_t w[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
+      const uint32_t w0 = raw[k].x, w1 = raw[k].y, w2 = raw[k].z, w3 = raw[k].w;
       #pragma unroll
-      for (int q = 0; q < 16 / VB; q++)
-        kd[p * KP + d + q] = F16KV ? (double)h2f((uint16_t)((w[q >> 1] >> (16 * (q & 1))) & 0xffff)) : (double)__uint_as_float(w[q]);
+      for (int s = 0; s < PPL; s++) {
+        const int pc = (s + rot) % PPL;
+        double lo, hi;
+        if (F16KV) {  // piece pc = the two f16 keys of word pc
+          const uint32_t wd = pc == 0 ? w0 : pc == 1 ? w1 : pc == 2 ? w2 : w3;
+          lo = (double)h2f((uint16_t)(wd & 0xffff));
+          hi = (double)h2f((uint16_t)(wd >> 16));
+        } else {      // piece pc = the f32 keys of words 2 pc, 2 pc + 1
+          lo = (double)__uint_as_float(pc == 0 ? w0 : w2);
+          hi = (double)__uint_as_float(pc == 0 ? w1 : w3);
+        }
+        *(double2 *)(kd + p * KP + d + 2 * pc) = make_double2(lo, hi);
+      }
     }
   };
   fetch(bx * MM_PT);
@@ -390,7 +408,7 @@ __global__ __launch_bounds__(256) void k_attn_scores_mm(const AttnArgs a, int nr
   }
 }
 
-size_t attention_mm_lds(int hd) { return (size_t)MM_PT * (hd + 1) * 8; }
+size_t attention_mm_lds(int hd) { return (size_t)MM_PT * (hd + 2) * 8; }
 
 
 // One block per (32-dim slice, query head, token). The slice's V rows (dimension-major in the cache) are staged
