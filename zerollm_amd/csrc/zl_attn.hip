@@ -599,24 +599,26 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
 // lanes of MFMA k-group g read their own positions contiguously, 4 MFMAs' operands per 16-byte read.
 constexpr int AVM_CT = 512;                 // positions per chunk
 constexpr int AVM_SF = AVM_CT / 4 + 4;      // floats of one position section (16-byte pad)
+constexpr int AVM_RS = 4 * AVM_SF + 4;      // floats of one dimension row (4 x an odd number: the 16 lanes of a chain
+                                            // read, rows n16 = 0..15, fall on 64 distinct banks)
 constexpr int AVM_UNIT = 32;                // positions per pipelined step of a chain (8 MFMAs)
 constexpr int AVM_NK = 72;                  // scores per thread the softmax keeps in registers
 constexpr int AVM_MAX_CTX = AVM_NK * 256;   // contexts this form takes (18432 positions)
-size_t attention_av_mfma_lds() { return (size_t)(2 * AV_DIMS * 4 + 2 * 4 + 1) * AVM_SF * 4; }
+size_t attention_av_mfma_lds() { return ((size_t)2 * AV_DIMS * AVM_RS + (2 * 4 + 1) * AVM_SF) * 4; }
 
 template <bool F16KV>
 __global__ __launch_bounds__(256) void k_attn_av_mfma(const AttnArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
   typedef float f4 __attribute__((ext_vector_type(4)));
   constexpr int VB = F16KV ? 2 : 4;
-  constexpr int CT = AVM_CT, SF = AVM_SF;
+  constexpr int CT = AVM_CT, SF = AVM_SF, RS = AVM_RS;
   constexpr int EPP = 16 / VB;                      // positions per 16-byte piece
   constexpr int PPR = CT / EPP;                     // pieces per dimension row of a chunk
   constexpr int PLT = AV_DIMS * PPR / 128;          // pieces per producer thread per chunk (16 f16, 32 f32)
   constexpr int SPT = CT / 128;                     // probabilities per producer thread per chunk
   constexpr int NU = CT / AVM_UNIT;                 // units per chunk
-  float *vk = (float *)lds;                         // [2][AV_DIMS][4][SF]: V of position 4 m + k, dimension j at [j][k][m]
-  float *pk = vk + 2 * AV_DIMS * 4 * SF;            // [2][4][SF]: p of position 4 m + k at [k][m]
+  float *vk = (float *)lds;                         // [2][AV_DIMS][RS]: V of position 4 m + k, dimension j at j RS + k SF + m
+  float *pk = vk + 2 * AV_DIMS * RS;                // [2][4][SF]: p of position 4 m + k at [k][m]
   float *zb = pk + 2 * 4 * SF;                      // [SF] zeros: the A operand of rows 1-15
   __shared__ double redd[4];
   __shared__ float redf[4];
@@ -650,7 +652,7 @@ __global__ __launch_bounds__(256) void k_attn_av_mfma(const AttnArgs a) {
   };
   // producers: chunk c into slot c & 1: V as f32 (zeros past the last position) ...
   auto stage_v = [&](int c) {
-    float *vs = vk + (c & 1) * AV_DIMS * 4 * SF;
+    float *vs = vk + (c & 1) * AV_DIMS * RS;
     #pragma unroll
     for (int k = 0; k < PLT; k++) {
       const int idx = k * 128 + pt, dim = idx / PPR, pc = idx % PPR, t = c * CT + pc * EPP;
@@ -661,7 +663,7 @@ __global__ __launch_bounds__(256) void k_attn_av_mfma(const AttnArgs a) {
         const float x = F16KV ? h2f((uint16_t)((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffff))) : __uint_as_float(w[e]);
         f[e] = t + e < npos ? x : 0.f;
       }
-      float *drow = vs + dim * 4 * SF;
+      float *drow = vs + dim * RS;
       #pragma unroll
       for (int q = 0; q < 4; q++) {
         if (F16KV) *(float2 *)(drow + q * SF + 2 * pc) = make_float2(f[q], f[q + 4]);  // positions t + q, t + 4 + q
@@ -753,7 +755,7 @@ __global__ __launch_bounds__(256) void k_attn_av_mfma(const AttnArgs a) {
       // unit u: the 8 MFMAs of positions c CT + 32 u .. + 31; lane group g supplies positions 4 m + g, m = 8 u .. 8 u + 7
       // (A: lanes of row 0 read the probabilities, the others the zeros). Units two at a time on two operand sets, the
       // next unit's reads ahead of the current unit's MFMAs; a full chunk in straight-line code (constant offsets)
-      const float *vr = vk + ((c & 1) * AV_DIMS + wave * 16 + n16) * 4 * SF + g * SF;
+      const float *vr = vk + ((c & 1) * AV_DIMS + wave * 16 + n16) * RS + g * SF;
       const float *pr = n16 == 0 ? pk + ((c & 1) * 4 + g) * SF : zb;
       auto ld = [&](const float *q, int off) { return *(const f4 *)(q + off); };
       if (c * CT + CT <= nend) {
@@ -1091,13 +1093,14 @@ __global__ __launch_bounds__(SMR_T) void k_attn_softmax_rows(const AttnArgs a) {
 // (prefill chunks); 16-row blocks keep the chain waves on SIMDs of their own (one block per CU), for passes of few rows.
 constexpr int MMV_CT = 256;                 // positions per chunk
 constexpr int MMV_SF = MMV_CT / 4 + 4;      // floats of one position section (16-byte pad)
+constexpr int MMV_RS = 4 * MMV_SF + 4;      // floats of one dimension or row (4 x an odd number: conflict-free chain reads)
 template <bool F16KV, int RB>
 __global__ __launch_bounds__(RB * 16) void k_attn_av_mm(const AttnArgs a, int nrows) {
   extern __shared__ __align__(16) uint8_t lds[];
   typedef float f4 __attribute__((ext_vector_type(4)));
   typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));  // a row of scores starts at any float
   constexpr int VB = F16KV ? 2 : 4;
-  constexpr int CT = MMV_CT, SF = MMV_SF, NCW = RB / 8, NPT = NCW * 64;  // chain waves, producer threads
+  constexpr int CT = MMV_CT, SF = MMV_SF, RS = MMV_RS, NCW = RB / 8, NPT = NCW * 64;  // chain waves, producer threads
   constexpr int EPP = 16 / VB;                      // positions per 16-byte V piece
   constexpr int UL = 16 / EPP;                      // V pieces per unit of 16 positions (2 f16, 4 f32)
   constexpr int UPR = CT / 16;                      // units per dimension or probability row of a chunk
@@ -1105,8 +1108,8 @@ __global__ __launch_bounds__(RB * 16) void k_attn_av_mm(const AttnArgs a, int nr
   constexpr int PU = RB * UPR / NPT;                // probability units per producer thread per chunk
   constexpr int NU = CT / AVM_UNIT;                 // units (8 MFMAs) per chunk
   static_assert((RB == 16 || RB == 32) && VU * NPT == AV_DIMS * UPR && PU * NPT == RB * UPR, "producer units");
-  float *vk = (float *)lds;                         // [2][AV_DIMS][4][SF]: V of position 4 m + k, dimension j at [j][k][m]
-  float *pk = vk + 2 * AV_DIMS * 4 * SF;            // [2][RB][4][SF]: p of row i, position 4 m + k at [i][k][m]
+  float *vk = (float *)lds;                         // [2][AV_DIMS][RS]: V of position 4 m + k, dimension j at j RS + k SF + m
+  float *pk = vk + 2 * AV_DIMS * RS;                // [2][RB][RS]: p of row i, position 4 m + k at i RS + k SF + m
   __shared__ float ot[RB][AV_DIMS + 1];             // the block's outputs [row][dimension] for the epilogue
   __shared__ long roff[RB];
   __shared__ int rnp[RB];
@@ -1164,7 +1167,7 @@ __global__ __launch_bounds__(RB * 16) void k_attn_av_mm(const AttnArgs a, int nr
     }
   };
   auto stage = [&](int c, const Pre &s) {
-    float *vs = vk + (c & 1) * AV_DIMS * 4 * SF;
+    float *vs = vk + (c & 1) * AV_DIMS * RS;
     #pragma unroll
     for (int k = 0; k < VU; k++) {
       const int u = k * NPT + pt, dim = u / UPR, uu = u % UPR, t0 = c * CT + uu * 16;
@@ -1177,15 +1180,15 @@ __global__ __launch_bounds__(RB * 16) void k_attn_av_mm(const AttnArgs a, int nr
         const float x = F16KV ? h2f((uint16_t)((w & 1) ? (wd >> 16) : (wd & 0xffff))) : __uint_as_float(wd);
         f[e] = t0 + e < nmax ? x : 0.f;
       }
-      float *drow = vs + dim * 4 * SF + uu * 4;
+      float *drow = vs + dim * RS + uu * 4;
       #pragma unroll
       for (int q = 0; q < 4; q++) *(f4 *)(drow + q * SF) = (f4){f[q], f[q + 4], f[q + 8], f[q + 12]};
     }
-    float *ps = pk + (c & 1) * RB * 4 * SF;
+    float *ps = pk + (c & 1) * RB * RS;
     #pragma unroll
     for (int k = 0; k < PU; k++) {
       const int u = k * NPT + pt, r = u / UPR, uu = u % UPR, t0 = c * CT + uu * 16, np = rnp[r];
-      float *prow = ps + r * 4 * SF + uu * 4;
+      float *prow = ps + r * RS + uu * 4;
       #pragma unroll
       for (int e = 0; e < 4; e++) {
         f4 w;
@@ -1213,8 +1216,8 @@ __global__ __launch_bounds__(RB * 16) void k_attn_av_mm(const AttnArgs a, int nr
   auto chains = [&](int c) {
     // unit u: the 8 MFMAs of positions c CT + 32 u .. + 31 (lane group g: positions 4 m + g, m = 8 u .. 8 u + 7); two
     // operand sets, the next unit's reads ahead of the current unit's MFMAs, a full chunk in straight-line code
-    const float *vr = vk + ((c & 1) * AV_DIMS + dg * 16 + n16) * 4 * SF + g * SF;
-    const float *pr = pk + ((c & 1) * RB + tr * 16 + n16) * 4 * SF + g * SF;
+    const float *vr = vk + ((c & 1) * AV_DIMS + dg * 16 + n16) * RS + g * SF;
+    const float *pr = pk + ((c & 1) * RB + tr * 16 + n16) * RS + g * SF;
     auto ld = [&](const float *q, int off) { return *(const f4 *)(q + off); };
     if (c * CT + CT <= nend) {
       f4 a0 = ld(pr, 0), a1 = ld(pr, 4), a2 = ld(vr, 0), a3 = ld(vr, 4);
@@ -1281,7 +1284,7 @@ __global__ __launch_bounds__(RB * 16) void k_attn_av_mm(const AttnArgs a, int nr
   }
 }
 
-size_t attention_av_mm_lds(int rb) { return (size_t)2 * (AV_DIMS + rb) * 4 * MMV_SF * 4; }
+size_t attention_av_mm_lds(int rb) { return (size_t)2 * (AV_DIMS + rb) * MMV_RS * 4; }
 
 // nrows: query heads per KV head x the launch's tokens (rows r = b G + g: token b, query head kvh G + g).
 // 512 threads: waves 0-3 run the chains of chunk c while waves 4-7 store chunk c + 1 (V and probabilities) into the
