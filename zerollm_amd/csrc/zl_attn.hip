@@ -1092,6 +1092,7 @@ __global__ __launch_bounds__(SMR_T) void k_attn_softmax_rows(const AttnArgs a) {
 // per chunk, operands by position mod 4 (section k holds positions 4 m + k). 32-row blocks stage V once for two tiles
 // (prefill chunks); 16-row blocks keep the chain waves on SIMDs of their own (one block per CU), for passes of few rows.
 constexpr int MMV_CT = 256;                 // positions per chunk
+template <bool B> struct Whole { static constexpr bool value = B; };  // a chunk below every row's last position
 constexpr int MMV_SF = MMV_CT / 4 + 4;      // floats of one position section (16-byte pad)
 constexpr int MMV_RS = 4 * MMV_SF + 4;      // floats of one dimension or row (4 x an odd number: conflict-free chain reads)
 template <bool F16KV, int RB>
@@ -1114,7 +1115,14 @@ __global__ __launch_bounds__(RB * 16) void k_attn_av_mm(const AttnArgs a, int nr
   __shared__ long roff[RB];
   __shared__ int rnp[RB];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g = lane >> 4;
-  const int kvh = blockIdx.y, rbk = blockIdx.z, d0 = blockIdx.x * AV_DIMS;
+  // XCD-aware block order: workgroup i of the 1-D grid (a multiple of 8 long) goes to XCD i mod 8, and logical block
+  // L = (i mod 8) (grid / 8) + i / 8 gives each XCD a contiguous run of L, ordered slice fastest, then row block, then
+  // KV head, so the blocks that read the same probability rows (a row block's slices) and the same V (a KV head's row
+  // blocks) share one L2 instead of fetching them from HBM once per XCD
+  const int NS = a.hd / AV_DIMS, NZ = (nrows + RB - 1) / RB;
+  const int L = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+  if (L >= NS * NZ * a.nHeadKv) return;
+  const int kvh = L / (NS * NZ), rbk = (L / NS) % NZ, d0 = (L % NS) * AV_DIMS;
   const int G = a.nHead / a.nHeadKv;
   const Step *st = a.step;
   const int Bd = st->B, pos0 = st->pos0, nmax = pos0 + Bd;
@@ -1143,16 +1151,23 @@ __global__ __launch_bounds__(RB * 16) void k_attn_av_mm(const AttnArgs a, int nr
     uint4 v[VU][UL];
     f4 p[PU][4];
   };
+  // a chunk that ends at or before every live row's last position (all chunks but the last one or two) needs no load
+  // clamped and no value zeroed: fetch and stage take it in a form without those checks (rows without a live query read
+  // row 0 of the scores there; their outputs are never stored, and row i of an MFMA result depends on row i of A only)
+  int nrmin = INT_MAX;
+  #pragma unroll
+  for (int i = 0; i < RB; i++) nrmin = rnp[i] > 0 ? min(nrmin, rnp[i]) : nrmin;
   // chunk c's V pieces and probabilities (loads stay inside the cache row and the scores row; what lies past a row's or
   // the pass's last position is zeroed when the chunk is staged)
-  auto fetch = [&](int c, Pre &s) {
+  auto fetch_f = [&](auto whole, int c, Pre &s) {
+    constexpr bool W = decltype(whole)::value;
     #pragma unroll
     for (int k = 0; k < VU; k++) {
       const int u = k * NPT + pt, dim = u / UPR, t0 = c * CT + (u % UPR) * 16;
       #pragma unroll
       for (int l = 0; l < UL; l++) {
         const int t = t0 + l * EPP;
-        s.v[k][l] = *(const uint4 *)(vbase + ((long)dim * a.vstride + (t < nmax ? t : 0)) * VB);
+        s.v[k][l] = *(const uint4 *)(vbase + ((long)dim * a.vstride + (W || t < nmax ? t : 0)) * VB);
       }
     }
     #pragma unroll
@@ -1162,11 +1177,12 @@ __global__ __launch_bounds__(RB * 16) void k_attn_av_mm(const AttnArgs a, int nr
       #pragma unroll
       for (int j = 0; j < 4; j++) {
         const int tq = t0 + 4 * j;
-        s.p[k][j] = *(const f4u *)(src + (tq + 4 <= a.ctx ? tq : 0));
+        s.p[k][j] = *(const f4u *)(src + (W || tq + 4 <= a.ctx ? tq : 0));
       }
     }
   };
-  auto stage = [&](int c, const Pre &s) {
+  auto stage_f = [&](auto whole, int c, const Pre &s) {
+    constexpr bool W = decltype(whole)::value;
     float *vs = vk + (c & 1) * AV_DIMS * RS;
     #pragma unroll
     for (int k = 0; k < VU; k++) {
@@ -1178,7 +1194,7 @@ __global__ __launch_bounds__(RB * 16) void k_attn_av_mm(const AttnArgs a, int nr
         const int w = e % EPP;
         const uint32_t wd = (F16KV ? w >> 1 : w) == 0 ? pc.x : (F16KV ? w >> 1 : w) == 1 ? pc.y : (F16KV ? w >> 1 : w) == 2 ? pc.z : pc.w;
         const float x = F16KV ? h2f((uint16_t)((w & 1) ? (wd >> 16) : (wd & 0xffff))) : __uint_as_float(wd);
-        f[e] = t0 + e < nmax ? x : 0.f;
+        f[e] = W || t0 + e < nmax ? x : 0.f;
       }
       float *drow = vs + dim * RS + uu * 4;
       #pragma unroll
@@ -1187,16 +1203,31 @@ __global__ __launch_bounds__(RB * 16) void k_attn_av_mm(const AttnArgs a, int nr
     float *ps = pk + (c & 1) * RB * RS;
     #pragma unroll
     for (int k = 0; k < PU; k++) {
-      const int u = k * NPT + pt, r = u / UPR, uu = u % UPR, t0 = c * CT + uu * 16, np = rnp[r];
+      const int u = k * NPT + pt, r = u / UPR, uu = u % UPR, t0 = c * CT + uu * 16;
       float *prow = ps + r * RS + uu * 4;
-      #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        f4 w;
+      if (W) {
         #pragma unroll
-        for (int j = 0; j < 4; j++) w[j] = t0 + 4 * j + e < np ? s.p[k][j][e] : 0.f;
-        *(f4 *)(prow + e * SF) = w;
+        for (int e = 0; e < 4; e++) *(f4 *)(prow + e * SF) = (f4){s.p[k][0][e], s.p[k][1][e], s.p[k][2][e], s.p[k][3][e]};
+      } else {
+        const int np = rnp[r];
+        #pragma unroll
+        for (int e = 0; e < 4; e++) {
+          f4 w;
+          #pragma unroll
+          for (int j = 0; j < 4; j++) w[j] = t0 + 4 * j + e < np ? s.p[k][j][e] : 0.f;
+          *(f4 *)(prow + e * SF) = w;
+        }
       }
     }
+  };
+  // (f16 V only: with f32 V both forms do not fit the registers together)
+  auto fetch = [&](int c, Pre &s) {
+    if (F16KV && (c + 1) * CT <= nrmin) fetch_f(Whole<F16KV>{}, c, s);
+    else fetch_f(Whole<false>{}, c, s);
+  };
+  auto stage = [&](int c, const Pre &s) {
+    if (F16KV && (c + 1) * CT <= nrmin) stage_f(Whole<F16KV>{}, c, s);
+    else stage_f(Whole<false>{}, c, s);
   };
   Pre s0, s1;
   if (producer) {
@@ -1618,7 +1649,8 @@ static void launch_av_mm_k(const AttnArgs &a, int nrows, hipStream_t st) {
     ZL_HIP(hipFuncSetAttribute((const void *)k_attn_av_mm<F16KV, RB>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)attention_av_mm_lds(RB)));
     attr = true;
   }
-  const dim3 grid(a.hd / AV_DIMS, a.nHeadKv, (nrows + RB - 1) / RB);
+  const int nb = a.hd / AV_DIMS * a.nHeadKv * ((nrows + RB - 1) / RB);  // (slice, KV head, row block) blocks
+  const dim3 grid((nb + 7) / 8 * 8);
   hipLaunchKernelGGL((k_attn_av_mm<F16KV, RB>), grid, dim3(RB * 16), attention_av_mm_lds(RB), st, a, nrows);
 }
 
