@@ -1277,21 +1277,29 @@ __global__ __launch_bounds__(RB * 16) void k_attn_av_mm(const AttnArgs a, int nr
       if (u < nu) mfma8(a0, a1, a2, a3);
     }
   };
-  // chunk c + 1 sits in register set (c + 1) mod 2, which then requests chunk c + 3
-  auto step = [&](int c, Pre &sn) {
-    if (producer) {
+  // the producers and the chain waves run loops of their own with one barrier per chunk each (the same count), so the
+  // chains' accumulator stays in the matrix cores' registers from chunk to chunk; chunk c + 1 sits in register set
+  // (c + 1) mod 2, which then requests chunk c + 3
+  if (producer) {
+    for (int c = 0; c < nch; c += 2) {
       if (c + 1 < nch) {
-        stage(c + 1, sn);
-        if (c + 3 < nch) fetch(c + 3, sn);
+        stage(c + 1, s1);
+        if (c + 3 < nch) fetch(c + 3, s1);
       }
-    } else if (tlive) {
-      chains(c);
+      __syncthreads();
+      if (c + 1 < nch) {
+        if (c + 2 < nch) {
+          stage(c + 2, s0);
+          if (c + 4 < nch) fetch(c + 4, s0);
+        }
+        __syncthreads();
+      }
     }
-    __syncthreads();
-  };
-  for (int c = 0; c < nch; c += 2) {
-    step(c, s1);
-    if (c + 1 < nch) step(c + 1, s0);
+  } else {
+    for (int c = 0; c < nch; c++) {
+      if (tlive) chains(c);
+      __syncthreads();
+    }
   }
   // ---- epilogue: the outputs through LDS, then two rows per wave, a row's 32 dimensions on 32 consecutive lanes (one
   // quantizeAct block)
