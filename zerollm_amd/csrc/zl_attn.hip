@@ -598,6 +598,7 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
 // LDS holds V and the probabilities by position mod 4 (section k holds positions 4 m + k, m ascending), so the 16
 // lanes of MFMA k-group g read their own positions contiguously, 4 MFMAs' operands per 16-byte read.
 constexpr int AVM_CT = 512;                 // positions per chunk
+template <bool B> struct Whole { static constexpr bool value = B; };  // a chunk below every row's last position
 constexpr int AVM_SF = AVM_CT / 4 + 4;      // floats of one position section (16-byte pad)
 constexpr int AVM_RS = 4 * AVM_SF + 4;      // floats of one dimension row (4 x an odd number: the 16 lanes of a chain
                                             // read, rows n16 = 0..15, fall on 64 distinct banks)
@@ -741,8 +742,10 @@ __global__ __launch_bounds__(256) void k_attn_av_mfma(const AttnArgs a) {
     #pragma unroll
     for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p1[i], v1[i], acc, 0, 0, 0);
   };
-  for (int c = 0; c < nch; c++) {
-    if (producer) {
+  // the producers and the chain waves run loops of their own with one barrier per chunk each (the same count), so the
+  // chains' accumulator stays in the matrix cores' registers from chunk to chunk
+  if (producer) {
+    for (int c = 0; c < nch; c++) {
       if (c + 1 < nch) {
         stage_v(c + 1);
         stage_p(c + 1);
@@ -751,14 +754,18 @@ __global__ __launch_bounds__(256) void k_attn_av_mfma(const AttnArgs a) {
           fetch_s(c + 2, npos);
         }
       }
-    } else {
-      // unit u: the 8 MFMAs of positions c CT + 32 u .. + 31; lane group g supplies positions 4 m + g, m = 8 u .. 8 u + 7
-      // (A: lanes of row 0 read the probabilities, the others the zeros). Units two at a time on two operand sets, the
-      // next unit's reads ahead of the current unit's MFMAs; a full chunk in straight-line code (constant offsets)
+      __syncthreads();
+    }
+  } else {
+    // unit u: the 8 MFMAs of positions c CT + 32 u .. + 31; lane group g supplies positions 4 m + g, m = 8 u .. 8 u + 7
+    // (A: lanes of row 0 read the probabilities, the others the zeros). Units two at a time on two operand sets, the
+    // next unit's reads ahead of the current unit's MFMAs; a full chunk in straight-line code (constant offsets). The
+    // whole chunks run in a loop of their own, so the accumulator keeps one register assignment there.
+    auto chunk = [&](int c, auto whole) __attribute__((always_inline)) {
       const float *vr = vk + ((c & 1) * AV_DIMS + wave * 16 + n16) * RS + g * SF;
       const float *pr = n16 == 0 ? pk + ((c & 1) * 4 + g) * SF : zb;
       auto ld = [&](const float *q, int off) { return *(const f4 *)(q + off); };
-      if (c * CT + CT <= nend) {
+      if constexpr (decltype(whole)::value) {
         f4 a0 = ld(pr, 0), a1 = ld(pr, 4), a2 = ld(vr, 0), a3 = ld(vr, 4);
         #pragma unroll
         for (int u = 0; u < NU; u += 2) {
@@ -784,8 +791,12 @@ __global__ __launch_bounds__(256) void k_attn_av_mfma(const AttnArgs a) {
         }
         if (u < nu) mfma8(a0, a1, a2, a3);
       }
-    }
-    __syncthreads();
+      __syncthreads();
+    };
+    const int nwhole = min(nch, nend / CT);
+    int c = 0;
+    for (; c < nwhole; c++) chunk(c, Whole<true>{});
+    for (; c < nch; c++) chunk(c, Whole<false>{});
   }
   // ---- epilogue: row 0's outputs (element 0 of lanes 0-15 of each chain wave) to lanes 0-31 of wave 0
   if (!producer && g == 0) ot[wave * 16 + n16] = acc[0];
@@ -1092,7 +1103,6 @@ __global__ __launch_bounds__(SMR_T) void k_attn_softmax_rows(const AttnArgs a) {
 // per chunk, operands by position mod 4 (section k holds positions 4 m + k). 32-row blocks stage V once for two tiles
 // (prefill chunks); 16-row blocks keep the chain waves on SIMDs of their own (one block per CU), for passes of few rows.
 constexpr int MMV_CT = 256;                 // positions per chunk
-template <bool B> struct Whole { static constexpr bool value = B; };  // a chunk below every row's last position
 constexpr int MMV_SF = MMV_CT / 4 + 4;      // floats of one position section (16-byte pad)
 constexpr int MMV_RS = 4 * MMV_SF + 4;      // floats of one dimension or row (4 x an odd number: conflict-free chain reads)
 template <bool F16KV, int RB>
