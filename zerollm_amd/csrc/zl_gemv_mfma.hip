@@ -28,6 +28,10 @@ namespace zl {
 
 // sums per lane: 4 row groups x 2 tokens, and token 8 at 9 tokens
 constexpr int mf_slots(int mc) { return mc == 3 ? 9 : 8; }
+// LDS bytes between two tokens' staged rows past their nsl * GT_REC bytes: a stride of 16 x an odd number of bytes
+// modulo 256 puts the token rows that one A-fragment read takes (up to 8 in a 16-lane group) on disjoint banks, where
+// a multiple of 256 (nsl a multiple of 8) put them all on the same four
+constexpr int MF_TPAD = 16;
 
 // MC: token class of the launch, 0 = 2..4 tokens, 1 = 5 tokens, 2 = 6..8 tokens, 3 = 9 tokens
 template <int FMT, int EPI, int MC>
@@ -60,6 +64,7 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
                                  make_rsrc(a.seg[1].m.sc, a.seg[1].nsc), make_rsrc(a.seg[1].m.dd, a.seg[1].ndd)}
                           : R0;
   const int kr = a.kr, s0 = kp * kr, s1 = min(nslab, s0 + kr), nsl = s1 - s0;
+  const int ts = nsl * GT_REC + MF_TPAD;  // LDS bytes per token of the staged activations
   const int n = nsl > wl ? (nsl - wl + WH - 1) / WH : 0;
   const int M = a.M;
   const uint8_t *xq = (const uint8_t *)a.act.q, *xr = (const uint8_t *)a.act.ra;
@@ -97,7 +102,7 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
       const bool isx = k < xc;
       const int kk = isx ? k : k - xc, off = kk * 1024 + lane * 16;
       const uint8_t *src = (isx ? xq + t * ldq + s0 * 64 : xr + t * ldr + s0 * 32) + off;
-      uint8_t *dst = xl + t * nsl * GT_REC + (isx ? 0 : xb) + kk * 1024;
+      uint8_t *dst = xl + t * ts + (isx ? 0 : xb) + kk * 1024;
       if (off < (isx ? xb : rb))
         __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
                                          (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
@@ -109,14 +114,14 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
   // holds values of that block
   const int at = (n16 & 2) ? 4 + (n16 >> 2) : (n16 >> 2);
   const bool avalid = at < M && (g >> 1) == (n16 & 1);
-  const uint8_t *abase = xl + (avalid ? at : 0) * nsl * GT_REC + 16 * g;
+  const uint8_t *abase = xl + (avalid ? at : 0) * ts + 16 * g;
   // records of this lane's D elements: tokens g and 4 + g (a token past M repeats the last one; not stored)
   const int t0 = min(g, M - 1), t1 = min(4 + g, M - 1);
-  const uint8_t *rb0 = xl + t0 * nsl * GT_REC + nsl * 64, *rb1 = xl + t1 * nsl * GT_REC + nsl * 64;
+  const uint8_t *rb0 = xl + t0 * ts + nsl * 64, *rb1 = xl + t1 * ts + nsl * 64;
   // 9 tokens: the second fragment's row rho = n16 holds token 8 where n16 mod 16 is 2 or 3 (block n16 & 1), else zeros
   const bool avalid8 = MC == 3 && M > 8 && (n16 & 14) == 2 && (g >> 1) == (n16 & 1);
-  const uint8_t *abase8 = xl + (avalid8 ? 8 : 0) * nsl * GT_REC + 16 * g;
-  const uint8_t *rb8 = xl + (MC == 3 && M > 8 ? 8 : 0) * nsl * GT_REC + nsl * 64;
+  const uint8_t *abase8 = xl + (avalid8 ? 8 : 0) * ts + 16 * g;
+  const uint8_t *rb8 = xl + (MC == 3 && M > 8 ? 8 : 0) * ts + nsl * 64;
   double acc8 = 0.0;  // 9 tokens: (this lane's row 16 g + n16, token 8)
   double *fw = &fac[wave][0][0];
   #pragma unroll
@@ -144,7 +149,13 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
       load(i + DEPTH, buf[d]);  // past the wave's last slab: no memory access
       if (i < n) {
         const int sl = wl + WH * i;
-        *(double4 *)(fw + lane * 4) = make_double4(f4[0], f4[1], f4[2], f4[3]);
+        {  // the two 16-byte halves of a lane's 32-byte record swap places where (lane / 8) is odd, so lanes l and l + 8
+           // of a 16-lane access meet no bank twice (the readers swizzle by their row the same way)
+          double2 *fr = (double2 *)(fw + lane * 4);
+          const int sw = (lane >> 3) & 1;
+          fr[sw] = make_double2(f4[0], f4[1]);
+          fr[sw ^ 1] = make_double2(f4[2], f4[3]);
+        }
         const uint4 av = avalid ? *(const uint4 *)(abase + sl * 64) : make_uint4(0, 0, 0, 0);
         const i32x4 A = {(int)av.x, (int)av.y, (int)av.z, (int)av.w};
         const uint4 r00 = *(const uint4 *)(rb0 + sl * 32), r01 = *(const uint4 *)(rb0 + sl * 32 + 16);
@@ -177,7 +188,10 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
             B = (i32x4){(int)q[4 * j], (int)q[4 * j + 1], (int)q[4 * j + 2], (int)q[4 * j + 3]};
           }
           const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, (i32x4){0, 0, 0, 0}, 0, 0, 0);
-          const double4 f = *(const double4 *)(fw + (16 * j + n16) * 4);  // row 16 j + n16: its factors
+          const double2 *fr = (const double2 *)(fw + (16 * j + n16) * 4);  // row 16 j + n16: its factors
+          const int sw = (n16 >> 3) & 1;                                    // (the writer's swizzle, by row)
+          const double2 flo = fr[sw], fhi = fr[sw ^ 1];
+          const double4 f = make_double4(flo.x, flo.y, fhi.x, fhi.y);
           #pragma unroll
           for (int v = 0; v < (MC >= 2 ? 4 : 2); v++) {
             const double fa = (v & 1) ? f.y : f.x, fb = (v & 1) ? f.w : f.z;
@@ -350,7 +364,7 @@ void launch_gemv_mfma(const GemvArgs &a, int epi, hipStream_t st) {
                  (epi != EPI_SWIGLU || (a.nwave % 2 == 0 && wpm <= 8)) && (a.kr + wpm - 1) / wpm <= GT_NMAX,
              ZL_ERR_ARG, "gemv (matrix cores): launch shape out of range");
   const dim3 grid((unsigned)a.ks, (unsigned)a.ntiles), blk((unsigned)a.nwave * 64);
-  const size_t lds = std::max((size_t)a.M * a.kr * GT_REC, (size_t)a.nwave * mf_slots(a.M == 9 ? 3 : 0) * 64 * 8);
+  const size_t lds = std::max((size_t)a.M * (a.kr * GT_REC + MF_TPAD), (size_t)a.nwave * mf_slots(a.M == 9 ? 3 : 0) * 64 * 8);
   if (a.seg[0].m.type == T_Q4_K) launch_mfma_fmt<T_Q4_K>(a, epi, grid, blk, lds, st);
   else launch_mfma_fmt<T_Q8_0>(a, epi, grid, blk, lds, st);
 }
@@ -370,7 +384,7 @@ bool gemv_mix_ok(const GemvArgs &a1, const GemvArgs &a2) {
 
 template <int FMT2, int MT2>
 static void launch_mix_k(const GemvArgs &a1, const GemvArgs &a2, hipStream_t st) {
-  const size_t l1 = std::max((size_t)a1.M * a1.kr * GT_REC, (size_t)a1.nwave * mf_slots(MT2 == 9 ? 3 : 0) * 64 * 8);
+  const size_t l1 = std::max((size_t)a1.M * (a1.kr * GT_REC + MF_TPAD), (size_t)a1.nwave * mf_slots(MT2 == 9 ? 3 : 0) * 64 * 8);
   const size_t l2 = std::max((size_t)a2.M * a2.kr * GT_REC, (size_t)a2.nwave * MT2 * 64 * 8);
   allow_big_lds(k_gemv_mix<FMT2, MT2>);
   const unsigned n = (unsigned)(a1.ks * a1.ntiles + a2.ks * a2.ntiles);
