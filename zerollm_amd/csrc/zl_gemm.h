@@ -121,11 +121,14 @@ __global__ __launch_bounds__(W * 64) void k_gemm(const GemvArgs a) {
   constexpr int NG = FMT == T_Q6_K ? 4 : 2;                // dots per slab: 16-value groups or 32-value blocks
   static_assert(RB % 1024 == 0, "whole staging chunks");
   const int kp = blockIdx.x, tile = blockIdx.y;
+  // token group z of the launch's G (blockIdx.z): tokens tb .. tb + Ml - 1, staged as rows 0 .. MP - 1. A (row, token)
+  // sum does not depend on which workgroup holds the token, so the groups only spread a small matrix over more CUs.
+  const int zg = blockIdx.z, G = gridDim.z, tb = zg * MP, Ml = min(MP, a.M - tb);
   const int lane = threadIdx.x & 63, n16 = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = NR == 2 ? __builtin_amdgcn_readfirstlane(wave / WH) : 0;
   const int wl = wave - grp * WH;
-  const int ks = a.ks, M = a.M;
+  const int ks = a.ks, M = Ml;  // this group's tokens
   const int si = __builtin_amdgcn_readfirstlane(
       EPI == EPI_SWIGLU ? 0 : (a.nseg > 2 && tile >= a.seg[2].tile0) ? 2 : (a.nseg > 1 && tile >= a.seg[1].tile0) ? 1 : 0);
 #define ZL_SEG(f) (si == 0 ? a.seg[0].f : si == 1 ? a.seg[1].f : a.seg[2].f)
@@ -156,7 +159,7 @@ __global__ __launch_bounds__(W * 64) void k_gemm(const GemvArgs a) {
       const int per = isv ? MP * 64 : MP * 32, rb = isv ? 64 : 32;
       const int w_ = o / per, rem = o - w_ * per, t = min(rem / rb, M - 1), e = rem % rb;
       const int s = min(s0 + w_ + WH * r, nslab - 1);  // rounds past the last one read a slab in range (unused)
-      sg[k] = *(const u32x4 *)(isv ? xq + t * ldq + (long)s * 64 + e : xr + t * ldr + (long)s * 32 + e);
+      sg[k] = *(const u32x4 *)(isv ? xq + (long)(tb + t) * ldq + (long)s * 64 + e : xr + (long)(tb + t) * ldr + (long)s * 32 + e);
     }
   };
   auto stage_store = [&](int r, const u32x4 *sg) {
@@ -257,7 +260,7 @@ __global__ __launch_bounds__(W * 64) void k_gemm(const GemvArgs a) {
   // each matrix in the order of a halving tree (as k_gemv_tiles) and runs the epilogue (or stores a K part)
   double *red = (double *)xl;  // [W][4 j][4 v][64 lanes] of one token group
   const int PW = NR * MP * 64;  // doubles per K part
-  double *pp = a.part + ((long)tile * ks + kp) * PW;
+  double *pp = a.part + (((long)tile * G + zg) * ks + kp) * PW;
   const int row = lt * 64 + lane;
   const bool live = row < rows;
   auto epilogue = [&](int t, double g0, double u0) {
@@ -307,7 +310,7 @@ __global__ __launch_bounds__(W * 64) void k_gemm(const GemvArgs a) {
         sums[r] = vv[0];
       }
       if (ks == 1) {
-        epilogue(t, sums[0], sums[NR - 1]);
+        epilogue(tb + t, sums[0], sums[NR - 1]);
       } else {
         #pragma unroll
         for (int r = 0; r < NR; r++) __hip_atomic_store(pp + (r * MP + t) * 64 + lane, sums[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -323,15 +326,16 @@ __global__ __launch_bounds__(W * 64) void k_gemm(const GemvArgs a) {
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores are complete
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __syncthreads();
-  if (threadIdx.x == 0) last = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(ks - 1);
+  uint32_t *cnt = a.cnt + (long)tile * G + zg;
+  if (threadIdx.x == 0) last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(ks - 1);
   __syncthreads();
   if (!last) return;
-  if (threadIdx.x == 0) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   for (int t = wave; t < M; t += W) {
     double sums[NR];
     #pragma unroll
     for (int r = 0; r < NR; r++) {
-      const double *pt = a.part + (long)tile * ks * PW + (r * MP + t) * 64 + lane;
+      const double *pt = a.part + ((long)tile * G + zg) * ks * PW + (r * MP + t) * 64 + lane;
       constexpr int KSMAX = 8;  // the parts' loads of one sum are issued together
       double pv[KSMAX];
       #pragma unroll
@@ -342,7 +346,7 @@ __global__ __launch_bounds__(W * 64) void k_gemm(const GemvArgs a) {
         if (k < ks) v += pv[k];
       sums[r] = v;
     }
-    epilogue(t, sums[0], sums[NR - 1]);
+    epilogue(tb + t, sums[0], sums[NR - 1]);
   }
 #undef ZL_SEG
 }
@@ -354,23 +358,26 @@ constexpr size_t gemm_lds(bool swiglu) {
 }
 
 template <int FMT, int EPI, int W, int U>
-inline void launch_gemm_k(const GemvArgs &a, hipStream_t st) {
+inline void launch_gemm_k(const GemvArgs &a, int G, hipStream_t st) {
   const size_t lds = gemm_lds<W, U>(EPI == EPI_SWIGLU);
   static bool done = false;
   if (!done) {
     ZL_HIP(hipFuncSetAttribute((const void *)k_gemm<FMT, EPI, W, U>, hipFuncAttributeMaxDynamicSharedMemorySize, 112 * 1024));
     done = true;
   }
-  hipLaunchKernelGGL((k_gemm<FMT, EPI, W, U>), dim3((unsigned)a.ks, (unsigned)a.ntiles), dim3(W * 64), lds, st, a);
+  hipLaunchKernelGGL((k_gemm<FMT, EPI, W, U>), dim3((unsigned)a.ks, (unsigned)a.ntiles, (unsigned)G), dim3(W * 64), lds, st, a);
 }
 
 template <int FMT, int EPI, int W>
 inline void launch_gemm_w(const GemvArgs &a, hipStream_t st) {
-  switch ((a.M + 15) / 16) {
-    case 1: launch_gemm_k<FMT, EPI, W, 1>(a, st); break;
-    case 2: launch_gemm_k<FMT, EPI, W, 2>(a, st); break;
-    case 3: launch_gemm_k<FMT, EPI, W, 3>(a, st); break;
-    default: launch_gemm_k<FMT, EPI, W, 4>(a, st); break;
+  int U, G;
+  gemm_groups(a, U, G);
+  ZL_REQUIRE(a.ks == 1 || (long)a.ntiles * G <= GEMV_CNT_TILES, ZL_ERR_ARG, "gemm: too many split-K counters");
+  switch (U) {
+    case 1: launch_gemm_k<FMT, EPI, W, 1>(a, G, st); break;
+    case 2: launch_gemm_k<FMT, EPI, W, 2>(a, G, st); break;
+    case 3: launch_gemm_k<FMT, EPI, W, 3>(a, G, st); break;
+    default: launch_gemm_k<FMT, EPI, W, 4>(a, G, st); break;
   }
 }
 

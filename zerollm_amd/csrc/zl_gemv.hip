@@ -92,7 +92,13 @@ bool gemm_takes(const GemvArgs &a) {
 
 long gemv_part_need(const GemvArgs &a) {
   if (a.ks == 1) return 0;
-  if (gemm_takes(a)) return (long)a.ntiles * a.ks * 2 * 16 * ((std::min(a.M, gemm_max_m()) + 15) / 16) * 64;
+  if (gemm_takes(a)) {  // a chunk of at most min(M, cap) tokens in G groups of 16 U (the most for the largest chunk)
+    GemvArgs c = a;
+    c.M = std::min(a.M, gemm_max_m());
+    int U, G;
+    gemm_groups(c, U, G);
+    return (long)a.ntiles * a.ks * 2 * 16 * U * G * 64;
+  }
   return (long)a.ntiles * a.ks * 2 * GEMV_MAX_MT * 64;
 }
 

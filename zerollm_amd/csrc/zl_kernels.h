@@ -197,6 +197,16 @@ void launch_gemm_fmt(const GemvArgs &a, int epi, hipStream_t st);
 // Whether launch_gemv runs a launch of a.M tokens on the GEMM, and the split-K partial sums (doubles) a launch needs.
 bool gemm_takes(const GemvArgs &a);
 long gemv_part_need(const GemvArgs &a);
+// Token groups of a GEMM launch of a.M <= 64 tokens: G workgroups along the tokens per (K part, tile), 16 U tokens
+// each. A matrix of few (K part, tile) workgroups takes more groups (each re-reads the matrix): up to 4, while the
+// launch stays within 320 workgroups (the target's attn_v and the draft's projections would otherwise hold 16-64 of
+// the 256 CUs). No group is empty: G <= ceil(M / 16).
+inline void gemm_groups(const GemvArgs &a, int &U, int &G) {
+  const int n16 = (a.M + 15) / 16, blocks = a.ks * a.ntiles;
+  G = 1;
+  while (G < 4 && 2 * G <= n16 && 2 * G * blocks <= 320) G *= 2;
+  U = (n16 + G - 1) / G;
+}
 
 // quantizeAct of one 32-value block (src/compute/ref-kernels.js:44-62) held by 32 consecutive lanes: d = amax/127 (f64,
 // stored f32), q = round-half-away(v * (1/d)). Every lane gets its q; the block's first lane (i & 31 == 0) also gets
