@@ -204,7 +204,7 @@ long gemv_part_need(const GemvArgs &a);
 inline void gemm_groups(const GemvArgs &a, int &U, int &G) {
   const int n16 = (a.M + 15) / 16, blocks = a.ks * a.ntiles;
   G = 1;
-  while (G < 4 && 2 * G <= n16 && 2 * G * blocks <= 320) G *= 2;
+  while (G < 4 && 2 * G <= n16 && 2 * G * blocks <= 512) G *= 2;
   U = (n16 + G - 1) / G;
 }
 
