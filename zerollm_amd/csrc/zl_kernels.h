@@ -198,9 +198,11 @@ void launch_gemm_fmt(const GemvArgs &a, int epi, hipStream_t st);
 bool gemm_takes(const GemvArgs &a);
 long gemv_part_need(const GemvArgs &a);
 // Token groups of a GEMM launch of a.M <= 64 tokens: G workgroups along the tokens per (K part, tile), 16 U tokens
-// each. A matrix of few (K part, tile) workgroups takes more groups (each re-reads the matrix): up to 4, while the
-// launch stays within 320 workgroups (the target's attn_v and the draft's projections would otherwise hold 16-64 of
-// the 256 CUs). No group is empty: G <= ceil(M / 16).
+// each, each group re-reading the matrix. Up to 4 groups while the launch stays within 512 workgroups: at 64 tokens
+// the 8B-shaped target's attn_v takes 4 (64 workgroups otherwise), q/k, gate/up, attn_output and ffn_down 2, the
+// 0.6B-shaped draft's projections 4 (16-64 workgroups otherwise); measured on 16K-token prefills, target + draft:
+// 3.91 + 1.88 s in one group, 3.63 + 1.63 s within 320 workgroups, 3.23 + 1.55 s within 512, 3.31 + 1.59 s within
+// 1024. No group is empty: G <= ceil(M / 16).
 inline void gemm_groups(const GemvArgs &a, int &U, int &G) {
   const int n16 = (a.M + 15) / 16, blocks = a.ks * a.ntiles;
   G = 1;
