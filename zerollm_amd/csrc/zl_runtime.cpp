@@ -767,10 +767,20 @@ static bool use_graphs() {
   return v == 1;
 }
 
+// Passes of more than ZEROLLM_GRAPH_MAXB tokens are launched kernel by kernel (default: every pass from its graph).
+static int graph_max_b() {
+  static int v = -1;
+  if (v < 0) {
+    const char *e = getenv("ZEROLLM_GRAPH_MAXB");
+    v = e ? std::max(0, atoi(e)) : INT_MAX;
+  }
+  return v;
+}
+
 // One pass; the caller has set m->dstep.
 static void launch_pass(zl_model *m, int B, int want) {
   m->capN = 0;  // the pass moves the recurrent state: earlier captures no longer describe it
-  if (use_graphs()) ZL_HIP(hipGraphLaunch(graph_for(m, B, want), m->st));
+  if (use_graphs() && B <= graph_max_b()) ZL_HIP(hipGraphLaunch(graph_for(m, B, want), m->st));
   else enqueue_forward(m, B, want);
   if (want == 2 && m->capture && B <= m->capSlots) {
     m->capPos0 = (int)m->tokens.size();
