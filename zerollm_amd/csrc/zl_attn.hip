@@ -292,17 +292,21 @@ __global__ __launch_bounds__(64) void k_attn_prep(const AttnArgs a) {
   }
 }
 
-// Block (every X-th 64-position tile of the pass, KV head, group of 4 row tiles); wave w computes row tile 4 z + w: 16
+// Block (every X-th 64-position tile of the pass, KV head, group of NWV row tiles); wave w computes row tile NWV z + w: 16
 // rows r = b G + g (token b, query head kvh G + g) against every position of its tiles, 16 positions at a time. Lane l
 // supplies A = the row l mod 16's dimension 32 j + 4 m + l / 16 (its query values, f64, held for the whole block) and B = key value
 // [position l mod 16][dimension 32 j + 4 m + l / 16] from LDS, where the block has staged 64 positions' keys as f64;
 // the accumulator of lane l element v is (row 4 v + l / 16, position l mod 16).
 constexpr int MM_PT = 64;    // positions staged in LDS at a time
-template <int HD, bool F16KV>
-__global__ __launch_bounds__(256) void k_attn_scores_mm(const AttnArgs a, int nrows) {
+// NWV waves per block, one row tile each: 8 for passes of 128 rows or more per KV head (prefill chunks: every staged key
+// tile serves 8 row tiles), else 4
+template <int HD, bool F16KV, int NWV>
+__global__ __launch_bounds__(NWV * 64) void k_attn_scores_mm(const AttnArgs a, int nrows) {
   constexpr int NP = HD / ATTN_VPL;    // parts (32 dimensions each)
   constexpr int VB = F16KV ? 2 : 4;
-  constexpr int RAW = MM_PT * HD * VB / 16 / 256;  // 16-byte K pieces per thread per staged tile
+  constexpr int NT = NWV * 64;
+  constexpr int RAW = MM_PT * HD * VB / 16 / NT;  // 16-byte K pieces per thread per staged tile
+  static_assert(RAW >= 1 && RAW * NT * 16 == MM_PT * HD * VB, "staging geometry");
   typedef double d4 __attribute__((ext_vector_type(4)));
   extern __shared__ __align__(16) uint8_t lds[];
   // [MM_PT][HD + 2] keys as f64: with rows 2 doubles (4 banks) apart, the 32 lanes of a half-wave's B read (16
@@ -310,7 +314,7 @@ __global__ __launch_bounds__(256) void k_attn_scores_mm(const AttnArgs a, int nr
   double *kd = (double *)lds;
   constexpr int KP = HD + 2;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g = lane >> 4;
-  const int kvh = blockIdx.y, tile = blockIdx.z * 4 + wave;
+  const int kvh = blockIdx.y, tile = blockIdx.z * NWV + wave;
   const int G = a.nHead / a.nHeadKv;
   const Step *st = a.step;
   const int Bd = st->B, pos0 = st->pos0, nmax = pos0 + Bd;
@@ -342,7 +346,7 @@ __global__ __launch_bounds__(256) void k_attn_scores_mm(const AttnArgs a, int nr
   auto fetch = [&](int t0) {
     #pragma unroll
     for (int k = 0; k < RAW; k++) {
-      const int e = (k * 256 + tid) * (16 / VB), p = e / HD, d = e % HD, t = t0 + p;
+      const int e = (k * NT + tid) * (16 / VB), p = e / HD, d = e % HD, t = t0 + p;
       raw[k] = t < nmax ? *(const uint4 *)(kbase + ((long)t * HD + d) * VB) : make_uint4(0, 0, 0, 0);
     }
   };
@@ -354,7 +358,7 @@ __global__ __launch_bounds__(256) void k_attn_scores_mm(const AttnArgs a, int nr
   auto store = [&]() {
     #pragma unroll
     for (int k = 0; k < RAW; k++) {
-      const int e = (k * 256 + tid) * (16 / VB), p = e / HD, d = e % HD;
+      const int e = (k * NT + tid) * (16 / VB), p = e / HD, d = e % HD;
       const uint32_t w0 = raw[k].x, w1 = raw[k].y, w2 = raw[k].z, w3 = raw[k].w;
       #pragma unroll
       for (int s = 0; s < PPL; s++) {
@@ -1673,14 +1677,31 @@ static void launch_av_mm_k(const AttnArgs &a, int nrows, hipStream_t st) {
 }
 
 template <int HD, bool F16KV>
-static void launch_scores_mm(const AttnArgs &a, dim3 gp, dim3 gm, size_t lds, int nrows, hipStream_t st) {
+static void launch_scores_mm(const AttnArgs &a, dim3 gp, int nrows, hipStream_t st) {
+  constexpr bool canWide = HD <= 128;  // (256-dimension rows in 8-wave blocks would spill)
   static bool attr = false;  // dynamic LDS above 64 KB must be requested per kernel
   if (!attr) {
-    ZL_HIP(hipFuncSetAttribute((const void *)k_attn_scores_mm<HD, F16KV>, hipFuncAttributeMaxDynamicSharedMemorySize, 140 * 1024));
+    ZL_HIP(hipFuncSetAttribute((const void *)k_attn_scores_mm<HD, F16KV, 4>, hipFuncAttributeMaxDynamicSharedMemorySize, 140 * 1024));
+    if constexpr (canWide)
+      ZL_HIP(hipFuncSetAttribute((const void *)k_attn_scores_mm<HD, F16KV, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, 140 * 1024));
     attr = true;
   }
   hipLaunchKernelGGL((k_attn_prep<HD, F16KV>), gp, dim3(64), 0, st, a);
-  hipLaunchKernelGGL((k_attn_scores_mm<HD, F16KV>), gm, dim3(256), lds, st, a, nrows);
+  // as many position blocks per (KV head, row group) as stay resident together (LDS bounds the blocks per CU, and the
+  // registers of 8-wave blocks one per CU), at most one per tile of the cache: a pass's tiles then spread over them in
+  // one round
+  const bool wide = canWide && nrows >= 128;
+  const int nwv = wide ? 8 : 4, zg = (nrows + 16 * nwv - 1) / (16 * nwv), ntc = (a.ctx + MM_PT - 1) / MM_PT;
+  const size_t lds = attention_mm_lds(HD);
+  const int slots = 256 * (wide ? 1 : std::max(1, (int)(160 * 1024 / lds)));
+  const dim3 gm((unsigned)std::max(1, std::min(ntc, slots / (a.nHeadKv * zg))), a.nHeadKv, zg);
+  if constexpr (canWide) {
+    if (wide) {
+      hipLaunchKernelGGL((k_attn_scores_mm<HD, F16KV, 8>), gm, dim3(512), lds, st, a, nrows);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((k_attn_scores_mm<HD, F16KV, 4>), gm, dim3(256), lds, st, a, nrows);
 }
 
 template <int HD, bool F16KV>
@@ -1748,19 +1769,13 @@ void launch_attention(const AttnArgs &a0, int B, hipStream_t st) {
   if (a.qr && a.mmMinB > 0 && B >= a.mmMinB) {
     const dim3 gp(B, a.nHead + a.nHeadKv);
     const int nrows = B * group;
-    // as many position blocks per (KV head, row group) as stay resident together (LDS bounds the blocks per CU), at most
-    // one per tile of the cache: a pass's tiles then spread over them in one round
-    const int zg = (nrows + 63) / 64, ntc = (a.ctx + MM_PT - 1) / MM_PT;
-    const int slots = 256 * std::max(1, (int)(160 * 1024 / attention_mm_lds(a.hd)));
-    const dim3 gm((unsigned)std::max(1, std::min(ntc, slots / (a.nHeadKv * zg))), a.nHeadKv, zg);
-    const size_t lm = attention_mm_lds(a.hd);
     switch (a.hd * 2 + a.kvF16) {
-      case 128: launch_scores_mm<64, false>(a, gp, gm, lm, nrows, st); break;
-      case 129: launch_scores_mm<64, true>(a, gp, gm, lm, nrows, st); break;
-      case 256: launch_scores_mm<128, false>(a, gp, gm, lm, nrows, st); break;
-      case 257: launch_scores_mm<128, true>(a, gp, gm, lm, nrows, st); break;
-      case 512: launch_scores_mm<256, false>(a, gp, gm, lm, nrows, st); break;
-      case 513: launch_scores_mm<256, true>(a, gp, gm, lm, nrows, st); break;
+      case 128: launch_scores_mm<64, false>(a, gp, nrows, st); break;
+      case 129: launch_scores_mm<64, true>(a, gp, nrows, st); break;
+      case 256: launch_scores_mm<128, false>(a, gp, nrows, st); break;
+      case 257: launch_scores_mm<128, true>(a, gp, nrows, st); break;
+      case 512: launch_scores_mm<256, false>(a, gp, nrows, st); break;
+      case 513: launch_scores_mm<256, true>(a, gp, nrows, st); break;
     }
   } else {
     dim3 gs(chunks < 64 ? chunks : 64, a.nHead / a.hpb, B);
