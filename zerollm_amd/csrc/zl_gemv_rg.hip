@@ -5,8 +5,9 @@
 // matrix of R rows runs R / 16 workgroups (64 to 384 for the draft's projections) instead of R / 64: a single-token
 // GEMV of a few MB is bound by how many CUs stream it and by the critical path of each workgroup, not by arithmetic.
 //
-// Mapping. Wave w takes the slabs s_j = w + 4 j of K. Every weight load of the wave is issued at kernel entry (they do
-// not depend on the activations). The wave then quantises the activation values of its own slabs only, so no
+// Mapping. Wave w takes the slabs s_j = w + 4 j of K. Every weight load of the wave is issued at kernel entry, right
+// behind the wave's activation values (loads complete in order: the RMSNorm and quantisation wait for the activations
+// only and run while the weights arrive). The wave quantises the activation values of its own slabs only, so no
 // workgroup barrier stands between quantisation and use (one stands before it when the input is RMSNorm'd):
 //   - lane l loads x[64 s_j + l], which is x[tid + 256 j] for thread tid = 64 w + l: the element each thread adds in
 //     rms_scale256, so the RMSNorm scale is that function's bits;
@@ -53,6 +54,19 @@ __global__ __launch_bounds__(256) void k_gemv_rg_q8(const GemvArgs a) {
     qs[1] = make_rsrc(a.seg[1].m.qs, a.seg[1].nqs);
     dd[1] = make_rsrc(a.seg[1].m.dd, a.seg[1].ndd);
   }
+  // ---- this wave's activation values x[64 s_j + lane] (= x[tid + 256 j]) and norm weights, requested first: loads
+  // complete in order, so the prologue below waits for these alone while the weights are still on their way
+  const int n = a.n;
+  const float *xr = a.xf + (long)a.xrow0 * a.ldxf;
+  const float *wr = a.nw ? a.nw : xr;  // (no weights: a second read of x, unused; unconditional loads)
+  float xv[NSW], wn[NSW];
+  #pragma unroll
+  for (int j = 0; j < NSW; j++) {
+    const int i = 64 * (wave + 4 * j) + lane;
+    xv[j] = xr[i < n ? i : 0];
+    wn[j] = wr[i < n ? i : 0];
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep the weight loads behind these
   // ---- every weight load of this wave, issued before anything waits (past the wave's slabs: out-of-range offsets,
   // answered with zeros and no memory access)
   const int r64 = 16 * g + i16;
@@ -69,16 +83,7 @@ __global__ __launch_bounds__(256) void k_gemv_rg_q8(const GemvArgs a) {
       dv[r][j] = __builtin_amdgcn_raw_buffer_load_b16(dd[r], oob + (r64 * 2 + (p >> 1)) * 2, ts * 256, 0);
     }
   }
-  // ---- this wave's activation values: x[64 s_j + lane] (= x[tid + 256 j]), RMSNorm'd with nw when set
-  const int n = a.n;
-  const float *xr = a.xf + (long)a.xrow0 * a.ldxf;
-  float xv[NSW], wn[NSW] = {};
-  #pragma unroll
-  for (int j = 0; j < NSW; j++) {
-    const int i = 64 * (wave + 4 * j) + lane;
-    xv[j] = xr[i < n ? i : 0];
-    if (a.nw) wn[j] = a.nw[i < n ? i : 0];
-  }
+  // ---- the activation values, RMSNorm'd with nw when set
   double sc = 1.0;
   if (a.nw) {  // rms_scale256's order: this thread's squares in j order, the 64-lane butterfly, the four waves
     double ss = 0.0;
