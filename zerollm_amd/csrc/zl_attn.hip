@@ -155,7 +155,8 @@ __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
         u[r][k] = t < lim ? *(const uint4 *)(kbase + ((long)t * HD + part * ATTN_VPL) * VB + 16 * k) : make_uint4(0, 0, 0, 0);
     }
   };
-  fetch(bx * P, a.ctx);
+  // the query heads and the pass's keys, then the first chunk of cached keys: loads complete in order, so the query
+  // rotation below waits for the query values alone while the keys are on their way
   constexpr int QV = 8 * HD / 256;  // query values per thread (at most 8 heads of HD values per block)
   float qv[QV];
   #pragma unroll
@@ -173,6 +174,9 @@ __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
     const int e = tid + 256 * k, row = e / HD < nB ? e / HD : 0;
     kr[k] = a.k[(long)row * a.ldkv + (long)kvh * HD + e % HD];
   }
+  __builtin_amdgcn_sched_barrier(0);
+  fetch(bx * P, a.ctx);
+  __builtin_amdgcn_sched_barrier(0);
   const Step *st = a.step;
   if (b >= st->B) return;
   const int pos0 = st->pos0, npos = pos0 + b + 1;
@@ -461,30 +465,25 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
       *(uint4 *)(vbuf + buf * CHUNKB + (idx / PPR) * PITCH + (idx % PPR) * 16) = pre[k];
     }
   };
-  fetch(0, a.ctx);
+  // the first 1024 scores, then the first V chunk: loads complete in order, so the softmax below waits for the scores
+  // alone while the V chunk is on its way
   const float *srow = a.scores + ((long)b * a.nHead + h) * a.sld;
   float v0[4];
   #pragma unroll
-  for (int k = 0; k < 4; k++) { const int t = k * 256 + tid; v0[k] = t < a.ctx ? srow[t] : -INFINITY; }
+  for (int k = 0; k < 4; k++) { const int t = k * 256 + tid; v0[k] = srow[t < a.ctx ? t : 0]; }  // (t >= npos: unused)
+  __builtin_amdgcn_sched_barrier(0);
+  #pragma unroll
+  for (int k = 0; k < LPT; k++) {  // unconditional loads (pieces past the cache's positions read position 0, zeroed
+                                   // below with every piece at or past the last position): a load under a branch
+                                   // would make the first use of the scores wait for it too
+    const int idx = k * 256 + tid, dim = idx / PPR, t = (idx % PPR) * EPP;
+    pre[k] = *(const uint4 *)(vbase + ((long)dim * a.vstride + (t < a.ctx ? t : 0)) * VB);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   const Step *st = a.step;
   if (b >= st->B) return;
   npos = st->pos0 + b + 1;
   const int nch = (npos + CT - 1) / CT;
-  #pragma unroll
-  for (int k = 0; k < LPT; k++) {  // the first chunk's pieces from the last position on: zeros, as in later chunks
-    const int t = ((k * 256 + tid) % PPR) * EPP;
-    if (t >= npos) pre[k] = make_uint4(0, 0, 0, 0);
-    else if (t + EPP > npos) {
-      uint32_t w[4] = {pre[k].x, pre[k].y, pre[k].z, pre[k].w};
-      #pragma unroll
-      for (int e = 0; e < EPP; e++)
-        if (t + e >= npos) {
-          if (F16KV) w[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
-          else w[e] = 0u;
-        }
-      pre[k] = make_uint4(w[0], w[1], w[2], w[3]);
-    }
-  }
   // ---- softmax (src/compute/ref-kernels.js:313-320)
   float mx = -INFINITY;
   #pragma unroll
@@ -521,6 +520,21 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
   const double inv = 1.0 / ((redd[0] + redd[1]) + (redd[2] + redd[3]));
   for (int t = tid; t < npos; t += 256) p[t] = (float)((double)p[t] * inv);
   for (int t = npos + tid; t < (npos + AV_UNIT - 1) / AV_UNIT * AV_UNIT; t += 256) p[t] = 0.f;
+  #pragma unroll
+  for (int k = 0; k < LPT; k++) {  // the first chunk's pieces from the last position on: zeros, as in later chunks
+    const int t = ((k * 256 + tid) % PPR) * EPP;
+    if (t >= npos) pre[k] = make_uint4(0, 0, 0, 0);
+    else if (t + EPP > npos) {
+      uint32_t w[4] = {pre[k].x, pre[k].y, pre[k].z, pre[k].w};
+      #pragma unroll
+      for (int e = 0; e < EPP; e++)
+        if (t + e >= npos) {
+          if (F16KV) w[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
+          else w[e] = 0u;
+        }
+      pre[k] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
   store(0);
   __syncthreads();
   // ---- weighted sum of V: f32 fma chain in position order, one output dimension per lane (lanes 0-31 of wave 0)
