@@ -330,6 +330,10 @@ __device__ __forceinline__ void gemv_tiles_body(const GemvArgs a, const int kp, 
                                          (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
     }
   }
+  // the residual value of this lane's row for the wave's first token, requested now rather than after the reduction
+  // (and the K parts' hand-off), where its latency would follow the kernel's last step
+  float rres = 0.f;
+  if constexpr (EPI == EPI_RESID) rres = a.resid[(long)min(wave, M - 1) * a.ldr + min(lt * 64 + lane, rows - 1)];
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the staged bytes are in LDS
   __syncthreads();
   // fully unrolled over the most slabs a wave can hold (no loop-carried registers: each slot's reload lands in the
@@ -428,7 +432,7 @@ __device__ __forceinline__ void gemv_tiles_body(const GemvArgs a, const int kp, 
       const double y = (double)(float)total(0, t);
       if (live) {
         float *o = a.resid + (long)t * a.ldr + row;
-        *o = (float)((double)*o + y);
+        *o = (float)((double)(t == wave ? rres : *o) + y);
       }
     } else {
       const float y = (float)total(0, t);

@@ -108,6 +108,10 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
                                          (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
     }
   }
+  // the residual value of this lane's row for the wave's first token, requested now rather than after the reduction
+  // (and the K parts' hand-off), where its latency would follow the kernel's last step
+  float rres = 0.f;
+  if constexpr (EPI == EPI_RESID) rres = a.resid[(long)min(wave, M - 1) * a.ldr + min(lt * 64 + lane, rows - 1)];
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the staged bytes are in LDS
   __syncthreads();
   // A-fragment row rho = n16 of this lane: token n16 / 4 (n16 mod 4 < 2) or 4 + n16 / 4, block n16 & 1; its quarter g
@@ -295,7 +299,7 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs a, const int kp, c
       const double y = (double)(float)total(0, t);
       if (live) {
         float *o = a.resid + (long)t * a.ldr + row;
-        *o = (float)((double)*o + y);
+        *o = (float)((double)(t == wave ? rres : *o) + y);
       }
     } else {
       const float y = (float)total(0, t);

@@ -83,6 +83,10 @@ __global__ __launch_bounds__(256) void k_gemv_rg_q8(const GemvArgs a) {
       dv[r][j] = __builtin_amdgcn_raw_buffer_load_b16(dd[r], oob + (r64 * 2 + (p >> 1)) * 2, ts * 256, 0);
     }
   }
+  // the residual value this workgroup's epilogue adds to (threads 0-15: row 16 g + tid of the tile), requested with the
+  // weights rather than after the reduction, where its latency would follow the kernel's last step
+  float rres = 0.f;
+  if constexpr (EPI == EPI_RESID) rres = a.resid[min(lt * 64 + r64, rows - 1)];
   // ---- the activation values, RMSNorm'd with nw when set
   double sc = 1.0;
   if (a.nw) {  // rms_scale256's order: this thread's squares in j order, the 64-lane butterfly, the four waves
@@ -162,8 +166,7 @@ __global__ __launch_bounds__(256) void k_gemv_rg_q8(const GemvArgs a) {
         const double gv = (double)(float)tot[0], uu = (double)(float)tot[1];
         a.hb[row] = (float)(gv / (1.0 + exp(-gv)) * uu);  // src/compute/ref-kernels.js:322
       } else if constexpr (EPI == EPI_RESID) {
-        float *o = a.resid + row;
-        *o = (float)((double)*o + (double)(float)tot[0]);
+        a.resid[row] = (float)((double)rres + (double)(float)tot[0]);
       } else {
         const float y = (float)tot[0];
         const float *bias = ZL_SEG(bias);
