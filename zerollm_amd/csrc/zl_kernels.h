@@ -71,7 +71,8 @@ struct GemvSeg {
 // parts' f64 partial sums go to `part` and the last part to arrive (per-tile counters in `cnt`, left at zero) adds them
 // in part order and runs the epilogue.
 struct GemvArgs {
-  GemvSeg seg[3];
+  // (the fields a kernel needs before its first loads lead, so that they share the first cache lines of the
+  // argument block)
   int nseg;
   int ntiles;
   int nslab;
@@ -79,6 +80,13 @@ struct GemvArgs {
   int kr;           // slabs per K part: ceil(nslab / ks)
   int nwave;        // waves per workgroup
   int M;            // tokens (rows of the activation)
+  // Fused activation prologue: when xf is set, the workgroup quantises rows xf[xrow0 + t] (length n, stride ldxf)
+  // itself, after RMSNorm with weights nw when nw is set, exactly as k_norm_quant would, instead of reading `act`.
+  int ldxf, xrow0, n;
+  const float *xf;
+  const float *nw;
+  double eps;
+  GemvSeg seg[3];
   Act act;          // quantised activations read by the kernel
   float *resid;     // EPI_RESID: resid[t * ldr + row] += y
   int ldr;
@@ -87,12 +95,6 @@ struct GemvArgs {
   Act qout;         // EPI_SWIGLU: also quantise hb into qout (when qout.q is set)
   double *part;
   uint32_t *cnt;
-  // Fused activation prologue: when xf is set, the workgroup quantises rows xf[xrow0 + t] (length n, stride ldxf)
-  // itself, after RMSNorm with weights nw when nw is set, exactly as k_norm_quant would, instead of reading `act`.
-  const float *xf;
-  int ldxf, xrow0, n;
-  const float *nw;
-  double eps;
 };
 
 // Split-K work space of GEMV launches (partial sums and per-tile arrival counters, counters zero between launches).

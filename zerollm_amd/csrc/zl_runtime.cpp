@@ -502,6 +502,8 @@ static GemvArgs gemv_args(const SegSpec *segs, int nseg, int B, int epi, const A
   GemvArgs a;
   memset(&a, 0, sizeof(a));
   ZL_REQUIRE(nseg >= 1 && nseg <= 3, ZL_ERR_ARG, "gemv: 1 to 3 matrices per launch");
+  // the kernels take segment 0 alone in the residual and SwiGLU epilogues (no segment selection among the tiles)
+  ZL_REQUIRE(epi == EPI_STORE || nseg == (epi == EPI_SWIGLU ? 2 : 1), ZL_ERR_ARG, "gemv: one matrix per residual launch, two per gate/up launch");
   a.nseg = nseg;
   int t0 = 0;
   for (int i = 0; i < a.nseg; i++) {
