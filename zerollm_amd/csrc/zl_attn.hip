@@ -122,7 +122,9 @@ __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
   // L2s, the blocks of the pass's tokens that read the same key chunks are given consecutive linear ids of one XCD, so
   // their K reads meet in that XCD's L2 instead of each token streaming the keys from memory again (measured: 16K
   // context, 9 tokens, 0.24 ms less per verify pass; at ~700 positions the keys stay in L2 and the order costs 0.02 ms).
+  const int stB = a.step->B, stPos0 = a.step->pos0;  // the pass's step record (scalar loads, read before the pins)
   const int X = gridDim.x, XY = X * gridDim.y, Z = gridDim.z;
+  pin_args(Z, a.q, a.ldq, a.qhs, a.k, a.ldkv, a.kcache, a.hpb, a.layer, a.nHead, a.nHeadKv);
   const int L = blockIdx.x + X * (blockIdx.y + gridDim.y * blockIdx.z);
   int xy, b;
   if (a.ctx >= AV_BIG_CTX && XY % 8 == 0) {
@@ -177,9 +179,8 @@ __global__ __launch_bounds__(256) void k_attn_scores(const AttnArgs a) {
   __builtin_amdgcn_sched_barrier(0);
   fetch(bx * P, a.ctx);
   __builtin_amdgcn_sched_barrier(0);
-  const Step *st = a.step;
-  if (b >= st->B) return;
-  const int pos0 = st->pos0, npos = pos0 + b + 1;
+  if (b >= stB) return;
+  const int pos0 = stPos0, npos = pos0 + b + 1;
   if (bx * P >= npos) return;
   #pragma unroll
   for (int k = 0; k < QV; k++)
@@ -441,6 +442,8 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
   constexpr int PPR = ROWB / 16;       // pieces per row
   constexpr int LPT = AV_DIMS * PPR / 256;   // 16-byte loads per thread per chunk
   const int slice = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int stB = a.step->B, stPos0 = a.step->pos0;  // the pass's step record (scalar loads, read before the pins)
+  pin_args(a.hd, a.nHead, a.nHeadKv, a.layer, a.vstride, a.vcache, a.scores, a.sld, a.ctx);
   const int hd = a.hd, kvh = h / (a.nHead / a.nHeadKv);
   float *p = (float *)lds;                                // [ctx rounded up to AV_UNIT] probabilities
   uint8_t *vbuf = lds + (size_t)((a.ctx + AV_UNIT - 1) / AV_UNIT * AV_UNIT) * 4;  // [2][AV_DIMS][PITCH] staged V rows
@@ -480,9 +483,8 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
     pre[k] = *(const uint4 *)(vbase + ((long)dim * a.vstride + (t < a.ctx ? t : 0)) * VB);
   }
   __builtin_amdgcn_sched_barrier(0);
-  const Step *st = a.step;
-  if (b >= st->B) return;
-  npos = st->pos0 + b + 1;
+  if (b >= stB) return;
+  npos = stPos0 + b + 1;
   const int nch = (npos + CT - 1) / CT;
   // ---- softmax (src/compute/ref-kernels.js:313-320)
   float mx = -INFINITY;

@@ -131,6 +131,18 @@ __device__ inline T group_reduce(T v, int width, Op op) {
   return v;
 }
 
+// Uniform values (kernel arguments) needed right after a kernel's first branches: an empty asm that reads each in
+// scalar registers at this point, so the compiler issues their argument loads together with the first ones instead
+// of in later rounds behind the branches (each round of argument loads waits out a memory latency).
+template <typename T>
+__device__ __forceinline__ void pin_arg(const T &v) {
+  asm volatile("" ::"s"(v));
+}
+template <typename... T>
+__device__ __forceinline__ void pin_args(const T &...v) {
+  (pin_arg(v), ...);
+}
+
 template <typename T>
 __device__ inline T wave_sum_xor(T v, int width) {
   return group_reduce(v, width, [](T a, T b) { return a + b; });
