@@ -451,11 +451,11 @@ __global__ __launch_bounds__(1024) void k_gemv_tiles(const GemvArgs a) {
   gemv_tiles_body<FMT, MT, EPI, DEPTH>(a, blockIdx.x, blockIdx.y, xl);  // grid: (K parts, tiles)
 }
 
-template <typename K>
-inline void allow_big_lds(K kernel) {
-  static bool done = false;  // dynamic LDS beyond 64 KB must be allowed per kernel, once
+template <auto K>
+inline void allow_big_lds() {
+  static bool done = false;  // dynamic LDS beyond 64 KB must be allowed per kernel (one flag per kernel), once
   if (!done) {
-    ZL_HIP(hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 112 * 1024));
+    ZL_HIP(hipFuncSetAttribute((const void *)K, hipFuncAttributeMaxDynamicSharedMemorySize, 112 * 1024));
     done = true;
   }
 }
@@ -472,13 +472,13 @@ inline void launch_tiles_mt(const GemvArgs &a, int epi, hipStream_t st) {
   // [M][kr] staged records of 96 bytes, then (same bytes) the waves' sums
   const size_t lds = std::max((size_t)a.M * a.kr * GT_REC, (size_t)a.nwave * MT * 64 * 8);
   if (epi == EPI_STORE) {
-    allow_big_lds(k_gemv_tiles<FMT, MT, EPI_STORE, 4>);
+    allow_big_lds<k_gemv_tiles<FMT, MT, EPI_STORE, 4>>();
     hipLaunchKernelGGL((k_gemv_tiles<FMT, MT, EPI_STORE, 4>), grid, blk, lds, st, a);
   } else if (epi == EPI_RESID) {
-    allow_big_lds(k_gemv_tiles<FMT, MT, EPI_RESID, 4>);
+    allow_big_lds<k_gemv_tiles<FMT, MT, EPI_RESID, 4>>();
     hipLaunchKernelGGL((k_gemv_tiles<FMT, MT, EPI_RESID, 4>), grid, blk, lds, st, a);
   } else {
-    allow_big_lds(k_gemv_tiles<FMT, MT, EPI_SWIGLU, 4>);
+    allow_big_lds<k_gemv_tiles<FMT, MT, EPI_SWIGLU, 4>>();
     hipLaunchKernelGGL((k_gemv_tiles<FMT, MT, EPI_SWIGLU, 4>), grid, blk, lds, st, a);
   }
 }

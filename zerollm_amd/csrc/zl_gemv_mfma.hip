@@ -343,13 +343,13 @@ bool gemv_mfma_ok(const GemvArgs &a) {
 template <int FMT, int MC>
 static void launch_mfma_mc(const GemvArgs &a, int epi, dim3 grid, dim3 blk, size_t lds, hipStream_t st) {
   if (epi == EPI_STORE) {
-    allow_big_lds(k_gemv_mfma<FMT, EPI_STORE, MC>);
+    allow_big_lds<k_gemv_mfma<FMT, EPI_STORE, MC>>();
     hipLaunchKernelGGL((k_gemv_mfma<FMT, EPI_STORE, MC>), grid, blk, lds, st, a);
   } else if (epi == EPI_RESID) {
-    allow_big_lds(k_gemv_mfma<FMT, EPI_RESID, MC>);
+    allow_big_lds<k_gemv_mfma<FMT, EPI_RESID, MC>>();
     hipLaunchKernelGGL((k_gemv_mfma<FMT, EPI_RESID, MC>), grid, blk, lds, st, a);
   } else {
-    allow_big_lds(k_gemv_mfma<FMT, EPI_SWIGLU, MC>);
+    allow_big_lds<k_gemv_mfma<FMT, EPI_SWIGLU, MC>>();
     hipLaunchKernelGGL((k_gemv_mfma<FMT, EPI_SWIGLU, MC>), grid, blk, lds, st, a);
   }
 }
@@ -390,7 +390,7 @@ template <int FMT2, int MT2>
 static void launch_mix_k(const GemvArgs &a1, const GemvArgs &a2, hipStream_t st) {
   const size_t l1 = std::max((size_t)a1.M * (a1.kr * GT_REC + MF_TPAD), (size_t)a1.nwave * mf_slots(MT2 == 9 ? 3 : 0) * 64 * 8);
   const size_t l2 = std::max((size_t)a2.M * a2.kr * GT_REC, (size_t)a2.nwave * MT2 * 64 * 8);
-  allow_big_lds(k_gemv_mix<FMT2, MT2>);
+  allow_big_lds<k_gemv_mix<FMT2, MT2>>();
   const unsigned n = (unsigned)(a1.ks * a1.ntiles + a2.ks * a2.ntiles);
   hipLaunchKernelGGL((k_gemv_mix<FMT2, MT2>), dim3(n), dim3((unsigned)a1.nwave * 64), std::max(l1, l2), st, a1, a2);
 }
