@@ -130,7 +130,7 @@ __global__ __launch_bounds__(W * 64) void k_gemm(const GemvArgs a) {
   const int wl = wave - grp * WH;
   const int ks = a.ks, M = Ml;  // this group's tokens
   const int si = __builtin_amdgcn_readfirstlane(
-      EPI != EPI_STORE ? 0 : (a.nseg > 2 && tile >= a.seg[2].tile0) ? 2 : (a.nseg > 1 && tile >= a.seg[1].tile0) ? 1 : 0);
+      EPI == EPI_SWIGLU ? 0 : (a.nseg > 2 && tile >= a.seg[2].tile0) ? 2 : (a.nseg > 1 && tile >= a.seg[1].tile0) ? 1 : 0);
 #define ZL_SEG(f) (si == 0 ? a.seg[0].f : si == 1 ? a.seg[1].f : a.seg[2].f)
   const int lt = tile - ZL_SEG(tile0), rows = ZL_SEG(rows);
   const int nslab = a.nslab, nsb = nslab >> 2;
