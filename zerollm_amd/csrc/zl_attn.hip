@@ -601,7 +601,7 @@ __global__ __launch_bounds__(256) void k_attn_av(const AttnArgs a) {
       o = (float)((double)o * (1.0 / (1.0 + exp(-g))));
     }
     if (a.out) a.out[(long)b * a.ldo + col] = o;
-    quant_block32(o, col, a.act, b);
+    if (a.act.q) quant_block32(o, col, a.act, b);  // (unset: the output GEMV quantises the f32 rows itself)
   }
 }
 
@@ -829,7 +829,7 @@ __global__ __launch_bounds__(256) void k_attn_av_mfma(const AttnArgs a) {
       o = (float)((double)o * (1.0 / (1.0 + exp(-gv))));
     }
     if (a.out) a.out[(long)b * a.ldo + col] = o;
-    quant_block32(o, col, a.act, b);
+    if (a.act.q) quant_block32(o, col, a.act, b);  // (unset: the output GEMV quantises the f32 rows itself)
   }
 }
 
@@ -1003,7 +1003,7 @@ __global__ __launch_bounds__(256) void k_attn_av_head(const AttnArgs a) {
       o = (float)((double)o * (1.0 / (1.0 + exp(-g))));
     }
     if (a.out) a.out[(long)b * a.ldo + col] = o;
-    quant_block32(o, col, a.act, b);
+    if (a.act.q) quant_block32(o, col, a.act, b);  // (unset: the output GEMV quantises the f32 rows itself)
   }
 }
 
@@ -1349,7 +1349,7 @@ __global__ __launch_bounds__(RB * 16) void k_attn_av_mm(const AttnArgs a, int nr
       o = (float)((double)o * (1.0 / (1.0 + exp(-gv))));
     }
     if (a.out) a.out[(long)b * a.ldo + col] = o;
-    quant_block32(o, col, a.act, b);
+    if (a.act.q) quant_block32(o, col, a.act, b);  // (unset: the output GEMV quantises the f32 rows itself)
   }
 }
 
@@ -1514,7 +1514,7 @@ __global__ __launch_bounds__(AVG_THREADS) void k_attn_av_group(const AttnArgs a,
       o = (float)((double)o * (1.0 / (1.0 + exp(-g))));
     }
     if (a.out) a.out[(long)b * a.ldo + col] = o;
-    quant_block32(o, col, a.act, b);
+    if (a.act.q) quant_block32(o, col, a.act, b);  // (unset: the output GEMV quantises the f32 rows itself)
   }
 }
 
@@ -1634,7 +1634,7 @@ __global__ __launch_bounds__(256) void k_attn_merge(const AttnArgs a) {
     o = (float)((double)o * (1.0 / (1.0 + exp(-g))));
   }
   if (a.out) a.out[(long)b * a.ldo + col] = o;
-  quant_block32(o, col, a.act, b);
+  if (a.act.q) quant_block32(o, col, a.act, b);  // (unset: the output GEMV quantises the f32 rows itself)
 }
 
 size_t attention_split_lds(int hd, int kvF16) { return (size_t)hd * (ATTN_SPLIT_C * (kvF16 ? 2 : 4) + 4); }

@@ -717,6 +717,8 @@ static void enqueue_forward(zl_model *m, int B, int want) {
       aa.headCtx = m->attnHeadCtx; aa.head1Ctx = m->attnHead1Ctx;
       aa.mmMinB = m->attnMmMinB; aa.mmAvMinB = m->attnMmAvMinB; aa.qr = m->qr;
       aa.avmf = m->attnAvmf ? 1 : 0;
+      // a single-token Q8_0 attn_output GEMV quantises the f32 head outputs itself: the attention writes them alone
+      if (rg_path({&L.wo}, B)) aa.act.q = nullptr;
       launch_attention(aa, B, m->st);
       gemv_group(m, {{&L.wo, nullptr, 0, nullptr}}, B, EPI_RESID, m->act, m->act.f, m->act.ld);
     }
